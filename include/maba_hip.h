@@ -1,0 +1,154 @@
+/*
+ * maba_hip.h -- C ABI of the MI355X (gfx950) HIP backend for the Maba v2 hot path.
+ *
+ * Every entry point takes plain tensor descriptors (device pointer, dtype code,
+ * shape and element strides), scalar parameters and a hipStream_t passed as
+ * void*.  No entry point allocates persistent device memory; the ones that need
+ * scratch take a caller-provided workspace and have a *_workspace_size query.
+ * All work is enqueued on the given stream; nothing synchronises the host.
+ *
+ * Return value: 0 on success, MABA_ERR_* otherwise; the message of the last
+ * failure on the calling thread is returned by maba_hip_last_error().
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   maba_hip_dgda_prefill           maba_sparse/kernels/dispatcher.py:258-327
+ *                                   (op "dgda_prefill"; math common.py:229-268)
+ *   maba_hip_dgda_step              dispatcher.py:330-396
+ *                                   (op "dgda_step"; math common.py:271-309)
+ *   maba_hip_compute_centroids      dispatcher.py:399-421
+ *                                   (op "compute_centroids"; common.py:329-350)
+ *   maba_hip_index_topk             dispatcher.py:424-465
+ *                                   (op "index_topk"; cpu_indexer.py:53-112)
+ *   maba_hip_index_topk_decode      layers/indexer.py:391-402 (inline decode
+ *                                   scoring + torch.topk; no dispatcher op)
+ *   maba_hip_stream_superposition   dispatcher.py:468-508
+ *                                   (op "stream_superposition"; common.py:406-438)
+ *   maba_hip_hca_pool               layers/sparse_attention.py:206 (block means
+ *                                   of the latent cache for the HCA stream)
+ *   maba_hip_maba_sa_decode         layers/sparse_attention.py:79-219,263-275
+ *                                   (local + sparse + HCA decode streams and the
+ *                                   gate superposition; inline torch code in the
+ *                                   reference, no dispatcher op)
+ */
+#ifndef MABA_HIP_H
+#define MABA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum maba_dtype {
+  MABA_F32 = 0,
+  MABA_F16 = 1,
+  MABA_BF16 = 2,
+  MABA_F64 = 3,
+  MABA_I64 = 4,
+  MABA_I32 = 5
+};
+
+enum maba_status {
+  MABA_OK = 0,
+  MABA_ERR_INVALID = 1,     /* bad shape / argument (Python: ValueError) */
+  MABA_ERR_DTYPE = 2,       /* unsupported dtype (Python: TypeError) */
+  MABA_ERR_UNSUPPORTED = 3, /* valid but not implemented here (Python: NotImplementedError) */
+  MABA_ERR_HIP = 4,         /* HIP runtime error (Python: RuntimeError) */
+  MABA_ERR_WORKSPACE = 5    /* workspace too small (Python: RuntimeError) */
+};
+
+/* A strided view of device memory.  Unused trailing dims have shape 1. */
+typedef struct maba_tensor {
+  void* data;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t shape[4];
+  int64_t stride[4]; /* in elements */
+} maba_tensor;
+
+const char* maba_hip_last_error(void);
+int maba_hip_abi_version(void);
+
+/*
+ * DGDA chunked prefill.  q,k,alpha,log_alpha,b: [B,H,L,dk]; v,w: [B,H,L,dv];
+ * initial_state: [B,H,dk,dv] or NULL (zeros).  alpha or log_alpha may be NULL
+ * (not both); log_alpha wins when both are given.  Any of the gates may be a
+ * stride-0 broadcast along the channel axis.  out: [B,H,L,dv],
+ * final_state: [B,H,dk,dv]; dtypes f32/f16/bf16 independently per tensor.
+ * chunk_size is accepted for signature parity; the result does not depend on it.
+ */
+size_t maba_hip_dgda_prefill_workspace_size(const maba_tensor* q, const maba_tensor* v,
+                                            const maba_tensor* log_alpha_or_alpha,
+                                            const maba_tensor* b);
+int maba_hip_dgda_prefill(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
+                          const maba_tensor* alpha, const maba_tensor* log_alpha,
+                          const maba_tensor* b, const maba_tensor* w,
+                          const maba_tensor* initial_state, maba_tensor* out,
+                          maba_tensor* final_state, int chunk_size, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* DGDA single decode step.  q,k,alpha,log_alpha,b: [B,H,dk]; v,w: [B,H,dv];
+ * state / new_state: [B,H,dk,dv] (state NULL = zeros); out: [B,H,dv]. */
+int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
+                       const maba_tensor* alpha, const maba_tensor* log_alpha,
+                       const maba_tensor* b, const maba_tensor* w, const maba_tensor* state,
+                       maba_tensor* out, maba_tensor* new_state, void* stream);
+
+/* Block centroids 0.5*(mean+max) over block_size tokens, zero-padded tail.
+ * k_idx: [B,L,d]; out: [B,ceil(L/block_size),d] (same dtype as k_idx). */
+int maba_hip_compute_centroids(const maba_tensor* k_idx, maba_tensor* out, int block_size,
+                               void* stream);
+
+/* Causal prefill scoring + top-k.  q_idx: [B,L,d]; centroids: [B,nb,d];
+ * out_idx: int64 [B,L,min(top_k,nb)]; out_scores: [B,L,nb] or NULL. */
+int maba_hip_index_topk(const maba_tensor* q_idx, const maba_tensor* centroids,
+                        float lambda_dist, int top_k, int block_size, maba_tensor* out_idx,
+                        maba_tensor* out_scores, void* stream);
+
+/* Decode scoring (query block = nb-1, no mask) + top-k for Hq query heads
+ * sharing one centroid set.  q: [B,Hq,d]; centroids: [B,nb,d];
+ * out_idx: int64 [B,Hq,min(top_k,nb)]; out_scores: f32 [B,Hq,nb] or NULL. */
+size_t maba_hip_index_topk_decode_workspace_size(int64_t B, int64_t Hq, int64_t nb, int top_k);
+int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tensor* centroids,
+                               float lambda_dist, int top_k, maba_tensor* out_idx,
+                               maba_tensor* out_scores, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/* out = g0*o_local + g1*o_sparse + g2*o_hca; o_*: [B,H,L,D]; gate: [B,L,3] or
+ * [B,H,L,3] logits (softmax taken) or weights (is_weights != 0). */
+int maba_hip_stream_superposition(const maba_tensor* o_local, const maba_tensor* o_sparse,
+                                  const maba_tensor* o_hca, const maba_tensor* gate,
+                                  int is_weights, maba_tensor* out, void* stream);
+
+/* Means of complete pool-token blocks of a latent cache: c_kv [B,L,dc] ->
+ * out [B,L/pool,dc] (rounded to out's dtype). */
+int maba_hip_hca_pool(const maba_tensor* c_kv, maba_tensor* out, int pool, void* stream);
+
+/*
+ * Fused MABA-SA decode step over an MLA latent cache (latent absorption):
+ *   q_lat     [B,H,dc]  per-head query already mapped into latent space
+ *                       (W_k,h^T q_h, scale applied by the kernel)
+ *   c_kv      [B,Lmax,dc] latent cache, first L rows valid
+ *   hca       [B,>=L/pool,dc] means of complete pool-blocks
+ *   idx       int64 [B,Hi,K] selected blocks, Hi in {1,H}
+ *   gate      [B,3] or [B,H,3] gate logits
+ *   out_lat   f32 [B,H,dc]  sum_s g_s * sum_j p_sj c_j  (latent-space output;
+ *                       the caller applies W_v,h).  When L < pool the HCA
+ *                       stream is the running mean of c[0..L-1]
+ *                       (sparse_attention.py:189-199), computed in-kernel.
+ * scale = 1/sqrt(d_head) is passed explicitly.
+ */
+size_t maba_hip_maba_sa_decode_workspace_size(int64_t B, int64_t H, int64_t dc, int64_t L,
+                                              int64_t K, int window, int n_sink, int pool);
+int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                            const maba_tensor* hca, const maba_tensor* idx,
+                            const maba_tensor* gate, int64_t L, float scale, int window,
+                            int n_sink, int block_size, int pool, maba_tensor* out_lat,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MABA_HIP_H */

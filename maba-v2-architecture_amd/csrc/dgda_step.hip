@@ -1,0 +1,146 @@
+// DGDA single-token decode step (reference: maba_sparse/kernels/common.py:271-309,
+// cpu_dgda.py:200-261).
+//
+//   S'    = diag(alpha) S
+//   delta = w*v - (b*k)^T S'
+//   S_new = S' + k delta^T
+//   o     = S_new^T q
+//
+// One workgroup per (batch, head).  The [dk, dv] fp32 state is streamed once:
+// each thread owns one column c and a contiguous run of rows, keeps its slice
+// of S' in registers between the two reductions, and writes S_new once.  The
+// kernel is HBM-bound on the state read + write (8*dk*dv bytes per head).
+#include "maba_common.h"
+
+namespace maba {
+
+struct StepArgs {
+  View4 q, k, v, alpha, log_alpha, b, w, state;  // q..w are [B,H,d] (s2 = elem)
+  MView4 out, new_state;
+  int H, dk, dv;
+  int has_state, use_log;
+};
+
+template <int DVP>
+__global__ __launch_bounds__(256) void dgda_step_kernel(StepArgs a) {
+  constexpr int RG = 256 / DVP;          // row groups
+  constexpr int MAXR = 128 / RG;         // max rows per thread (dk <= 128)
+  __shared__ float s_a[128], s_bk[128], s_k[128], s_q[128], s_wv[128];
+  __shared__ float s_part[RG][DVP];
+
+  const int bh = blockIdx.x;
+  const int bi = bh / a.H, hi = bh % a.H;
+  const int tid = threadIdx.x;
+  const int dk = a.dk, dv = a.dv;
+
+  for (int r = tid; r < dk; r += 256) {
+    const float kk = a.k.at(bi, hi, r, 0);
+    const float al = a.use_log ? __expf(a.log_alpha.at(bi, hi, r, 0)) : a.alpha.at(bi, hi, r, 0);
+    s_a[r] = al;
+    s_k[r] = kk;
+    s_bk[r] = a.b.at(bi, hi, r, 0) * kk;
+    s_q[r] = a.q.at(bi, hi, r, 0);
+  }
+  for (int c = tid; c < dv; c += 256) s_wv[c] = a.w.at(bi, hi, c, 0) * a.v.at(bi, hi, c, 0);
+  __syncthreads();
+
+  const int c = tid % DVP;
+  const int rg = tid / DVP;
+  const int rows_per = (dk + RG - 1) / RG;
+  const int r0 = rg * rows_per;
+  const bool col_ok = c < dv;
+
+  float s[MAXR];
+  float pred = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    const int r = r0 + i;
+    float x = 0.f;
+    if (i < rows_per && r < dk && col_ok) {
+      x = a.has_state ? a.state.at(bi, hi, r, c) : 0.f;
+      x *= s_a[r];
+      pred = fmaf(s_bk[r], x, pred);
+    }
+    s[i] = x;
+  }
+  s_part[rg][c] = pred;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int g = 0; g < RG; ++g) tot += s_part[g][c];
+  const float delta = col_ok ? (s_wv[c] - tot) : 0.f;
+  __syncthreads();
+
+  float o = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    const int r = r0 + i;
+    if (i < rows_per && r < dk && col_ok) {
+      const float sn = fmaf(s_k[r], delta, s[i]);
+      a.new_state.put(bi, hi, r, c, sn);
+      o = fmaf(s_q[r], sn, o);
+    }
+  }
+  s_part[rg][c] = o;
+  __syncthreads();
+  if (rg == 0 && col_ok) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) t += s_part[g][c];
+    a.out.put(bi, hi, c, 0, t);
+  }
+}
+
+}  // namespace maba
+
+using namespace maba;
+
+extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
+                                  const maba_tensor* alpha, const maba_tensor* log_alpha,
+                                  const maba_tensor* b, const maba_tensor* w,
+                                  const maba_tensor* state, maba_tensor* out,
+                                  maba_tensor* new_state, void* stream) {
+  if (!q || q->ndim != 3) return fail(MABA_ERR_INVALID, "dgda_step: q must be [B,H,dk]");
+  const int64_t B = q->shape[0], H = q->shape[1], dk = q->shape[2];
+  if (!v || v->ndim != 3) return fail(MABA_ERR_INVALID, "dgda_step: v must be [B,H,dv]");
+  const int64_t dv = v->shape[2];
+  const int64_t sq[3] = {B, H, dk}, sv[3] = {B, H, dv}, ss[4] = {B, H, dk, dv};
+  if (!expect_shape(q, "q", 3, sq) || !expect_shape(k, "k", 3, sq) || !expect_shape(v, "v", 3, sv) ||
+      !expect_shape(b, "b", 3, sq) || !expect_shape(w, "w", 3, sv) ||
+      !expect_shape(out, "out", 3, sv) || !expect_shape(new_state, "new_state", 4, ss))
+    return MABA_ERR_INVALID;
+  if (!alpha && !log_alpha) return fail(MABA_ERR_INVALID, "dgda_step: alpha or log_alpha required");
+  if (log_alpha && !expect_shape(log_alpha, "log_alpha", 3, sq)) return MABA_ERR_INVALID;
+  if (!log_alpha && !expect_shape(alpha, "alpha", 3, sq)) return MABA_ERR_INVALID;
+  if (state && !expect_shape(state, "state", 4, ss)) return MABA_ERR_INVALID;
+  const maba_tensor* all[] = {q, k, v, b, w, out, new_state, log_alpha ? log_alpha : alpha, state};
+  for (const maba_tensor* t : all)
+    if (t && !expect_float(t, "dgda_step")) return MABA_ERR_DTYPE;
+  if (dk > 128 || dv > 128 || dk < 1 || dv < 1)
+    return fail(MABA_ERR_UNSUPPORTED, "dgda_step: dk, dv must be in [1,128], got %lld, %lld",
+                (long long)dk, (long long)dv);
+  if (B * H == 0) return MABA_OK;
+
+  StepArgs a;
+  a.q = view4(q); a.k = view4(k); a.v = view4(v); a.b = view4(b); a.w = view4(w);
+  a.alpha = view4(alpha); a.log_alpha = view4(log_alpha); a.state = view4(state);
+  // [B,H,d] views: move the element stride to slot 2 so .at(b,h,i,0) indexes them.
+  View4* vecs[] = {&a.q, &a.k, &a.v, &a.b, &a.w, &a.alpha, &a.log_alpha};
+  for (View4* x : vecs) { x->s3 = 0; }
+  a.q.s2 = q->stride[2]; a.k.s2 = k->stride[2]; a.v.s2 = v->stride[2];
+  a.b.s2 = b->stride[2]; a.w.s2 = w->stride[2];
+  if (alpha) a.alpha.s2 = alpha->stride[2];
+  if (log_alpha) a.log_alpha.s2 = log_alpha->stride[2];
+  a.out = mview4(out); a.out.s3 = 0;
+  a.new_state = mview4(new_state);
+  a.H = (int)H; a.dk = (int)dk; a.dv = (int)dv;
+  a.has_state = state != nullptr;
+  a.use_log = log_alpha != nullptr;
+
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)(B * H)), block(256);
+  if (dv <= 32) hipLaunchKernelGGL(dgda_step_kernel<32>, grid, block, 0, s, a);
+  else if (dv <= 64) hipLaunchKernelGGL(dgda_step_kernel<64>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(dgda_step_kernel<128>, grid, block, 0, s, a);
+  return check_launch("dgda_step");
+}

@@ -1,0 +1,253 @@
+// DG-Indexer scoring + top-k.
+//
+// Decode (reference: maba_sparse/layers/indexer.py:391-402):
+//   s[h,n] = (q_h / sqrt(d)) . c_n - lam * log1p(max(nb-1-n, 0))   (no mask)
+//   idx[h] = top min(K, nb) of s[h,:], score descending, ties -> lower index
+// Prefill (reference: maba_sparse/kernels/cpu_indexer.py:362-378):
+//   s[t,n] = (q_t / sqrt(d)) . c_n - lam * log1p(|t//bs - n|), -inf if n > t//bs
+//
+// Scores are fp32 dots of the stored inputs (bf16/f16/f32 converted exactly
+// to fp32).  The decode path streams the centroid set once per batch element:
+// each wave scores a 64-centroid tile for every query head (lane = centroid)
+// and folds it into per-head running top-64 lists (topk_wave.h); workgroup
+// results go to a workspace and a second kernel merges the splits.
+#include "maba_common.h"
+#include "topk_wave.h"
+
+namespace maba {
+
+constexpr int IDX_MAX_HEADS = 16;   // query heads per decode launch
+constexpr int IDX_MAX_D = 256;      // channels
+
+struct DecArgs {
+  const void* q; int qdt; int64_t qsb, qsh, qsd;
+  const void* c; int cdt; int64_t csb, csn, csd;
+  int64_t nb, d;
+  int Hq, K, nsplit, tiles_per_wave;
+  float scale, lam;
+  key64* ws;                           // [B, nsplit, Hq, 64]
+  float* scores; int64_t ssb, ssh, ssn; // optional fp32 scores
+};
+
+__global__ __launch_bounds__(256) void index_decode_score_kernel(DecArgs a) {
+  __shared__ float s_q[IDX_MAX_HEADS * IDX_MAX_D];
+  __shared__ key64 s_lists[4][64];
+  const int split = blockIdx.x;
+  const int64_t bi = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int Hq = a.Hq;
+  const int64_t d = a.d;
+  for (int64_t i = threadIdx.x; i < (int64_t)Hq * d; i += 256) {
+    const int h = (int)(i / d);
+    const int64_t c = i % d;
+    s_q[h * IDX_MAX_D + c] = load_elem(a.q, a.qdt, bi * a.qsb + h * a.qsh + c * a.qsd) * a.scale;
+  }
+  __syncthreads();
+
+  key64 list[IDX_MAX_HEADS];
+#pragma unroll
+  for (int h = 0; h < IDX_MAX_HEADS; ++h) list[h] = KEY_NONE;
+
+  const int64_t tile0 = ((int64_t)split * 4 + wave) * a.tiles_per_wave;
+  for (int tt = 0; tt < a.tiles_per_wave; ++tt) {
+    const int64_t n = (tile0 + tt) * 64 + lane;
+    const bool valid = n < a.nb;
+    float acc[IDX_MAX_HEADS];
+#pragma unroll
+    for (int h = 0; h < IDX_MAX_HEADS; ++h) acc[h] = 0.f;
+    if (valid) {
+      const int64_t cb = bi * a.csb + n * a.csn;
+      for (int64_t c = 0; c < d; ++c) {
+        const float x = load_elem(a.c, a.cdt, cb + c * a.csd);
+#pragma unroll
+        for (int h = 0; h < IDX_MAX_HEADS; ++h)
+          if (h < Hq) acc[h] = fmaf(s_q[h * IDX_MAX_D + c], x, acc[h]);
+      }
+    }
+    const float pen = valid ? a.lam * log1pf((float)(a.nb - 1 - n)) : 0.f;
+    if (__ballot(valid) == 0ull) break;
+#pragma unroll
+    for (int h = 0; h < IDX_MAX_HEADS; ++h) {
+      if (h < Hq) {
+        const float s = acc[h] - pen;
+        if (a.scores && valid) a.scores[bi * a.ssb + h * a.ssh + n * a.ssn] = s;
+        const key64 key = valid ? make_key(s, (uint32_t)n) : KEY_NONE;
+        list[h] = wave_merge_topk(list[h], key, a.K);
+      }
+    }
+  }
+  // merge the 4 wave lists per head, write the workgroup's top-64
+#pragma unroll
+  for (int h = 0; h < IDX_MAX_HEADS; ++h) {
+    if (h < Hq) {  // uniform across the workgroup
+      s_lists[wave][lane] = list[h];
+      __syncthreads();
+      if (wave == 0) {
+        key64 m = s_lists[0][lane];
+        for (int w = 1; w < 4; ++w) m = wave_merge_topk(m, s_lists[w][lane], a.K);
+        a.ws[(((int64_t)bi * a.nsplit + split) * Hq + h) * 64 + lane] = m;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void index_decode_merge_kernel(const key64* ws, int nsplit, int Hq, int K,
+                                                                int ak, int64_t* out, int64_t osb,
+                                                                int64_t osh, int64_t osk) {
+  const int64_t bi = blockIdx.x / Hq;
+  const int h = blockIdx.x % Hq;
+  const int lane = threadIdx.x;
+  key64 m = KEY_NONE;
+  for (int s = 0; s < nsplit; ++s) m = wave_merge_topk(m, ws[((bi * nsplit + s) * Hq + h) * 64 + lane], K);
+  if (lane < ak) out[bi * osb + h * osh + lane * osk] = (int64_t)key_index(m);
+}
+
+// Prefill: one wave per query row; lane = centroid within a 64-wide tile.
+struct PreArgs {
+  const void* q; int qdt; int64_t qsb, qsl, qsd;
+  const void* c; int cdt; int64_t csb, csn, csd;
+  int64_t B, L, nb, d;
+  int K, ak, bs;
+  float scale, lam;
+  int64_t* out; int64_t osb, osl, osk;
+  void* scores; int sdt; int64_t ssb, ssl, ssn;
+};
+
+__global__ __launch_bounds__(256) void index_prefill_kernel(PreArgs a) {
+  __shared__ float s_q[4][IDX_MAX_D];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;  // over B*L
+  const bool row_ok = row < a.B * a.L;
+  const int64_t bi = row_ok ? row / a.L : 0;
+  const int64_t t = row_ok ? row % a.L : 0;
+  for (int64_t c = lane; c < a.d; c += 64)
+    s_q[wave][c] = row_ok ? load_elem(a.q, a.qdt, bi * a.qsb + t * a.qsl + c * a.qsd) * a.scale : 0.f;
+  __syncthreads();
+  if (!row_ok) return;
+  const int64_t qblk = t / a.bs;
+  const int64_t nvalid = (qblk + 1 < a.nb) ? qblk + 1 : a.nb;  // blocks n <= qblk
+  key64 list = KEY_NONE;
+  for (int64_t n0 = 0; n0 < a.nb; n0 += 64) {
+    const int64_t n = n0 + lane;
+    float s = -INFINITY;
+    if (n < nvalid) {
+      float acc = 0.f;
+      const int64_t cb = bi * a.csb + n * a.csn;
+      for (int64_t c = 0; c < a.d; ++c) acc = fmaf(s_q[wave][c], load_elem(a.c, a.cdt, cb + c * a.csd), acc);
+      s = acc - a.lam * log1pf((float)(qblk - n));
+    }
+    if (a.scores && n < a.nb) store_elem(a.scores, a.sdt, bi * a.ssb + t * a.ssl + n * a.ssn, s);
+    if (n0 < nvalid) list = wave_merge_topk(list, n < nvalid ? make_key(s, (uint32_t)n) : KEY_NONE, a.K);
+  }
+  // Fewer valid blocks than ak: the remaining slots hold -inf blocks, lowest index first.
+  const int64_t nv = nvalid;
+  if (lane < a.ak) {
+    const int64_t idx = lane < nv ? (int64_t)key_index(list) : lane;  // masked blocks nv, nv+1, ...
+    a.out[bi * a.osb + t * a.osl + lane * a.osk] = idx;
+  }
+}
+
+}  // namespace maba
+
+using namespace maba;
+
+extern "C" size_t maba_hip_index_topk_decode_workspace_size(int64_t B, int64_t Hq, int64_t nb, int top_k) {
+  (void)top_k;
+  const int64_t tiles = ceil_div(nb, 64);
+  const int64_t nsplit = ceil_div(tiles, 4);
+  return (size_t)(B * (nsplit > 0 ? nsplit : 1) * Hq * 64) * sizeof(key64);
+}
+
+extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tensor* centroids,
+                                          float lambda_dist, int top_k, maba_tensor* out_idx,
+                                          maba_tensor* out_scores, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  if (!q || q->ndim != 3) return fail(MABA_ERR_INVALID, "index_topk_decode: q must be [B,Hq,d]");
+  if (!centroids || centroids->ndim != 3) return fail(MABA_ERR_INVALID, "index_topk_decode: centroids must be [B,nb,d]");
+  const int64_t B = q->shape[0], Hq = q->shape[1], d = q->shape[2], nb = centroids->shape[1];
+  if (centroids->shape[0] != B || centroids->shape[2] != d)
+    return fail(MABA_ERR_INVALID, "index_topk_decode: centroids shape mismatch");
+  if (top_k <= 0) return fail(MABA_ERR_INVALID, "index_topk_decode: top_k must be positive, got %d", top_k);
+  const int64_t ak = top_k < nb ? top_k : nb;
+  const int64_t so[3] = {B, Hq, ak};
+  if (!expect_shape(out_idx, "out_idx", 3, so)) return MABA_ERR_INVALID;
+  if (out_idx->dtype != MABA_I64) return fail(MABA_ERR_DTYPE, "index_topk_decode: out_idx must be int64");
+  if (!expect_float(q, "q") || !expect_float(centroids, "centroids")) return MABA_ERR_DTYPE;
+  if (top_k > 64) return fail(MABA_ERR_UNSUPPORTED, "index_topk_decode: top_k > 64 not supported");
+  if (Hq > IDX_MAX_HEADS || d > IDX_MAX_D)
+    return fail(MABA_ERR_UNSUPPORTED, "index_topk_decode: Hq <= %d and d <= %d required", IDX_MAX_HEADS, IDX_MAX_D);
+  if (out_scores) {
+    const int64_t ss[3] = {B, Hq, nb};
+    if (!expect_shape(out_scores, "out_scores", 3, ss)) return MABA_ERR_INVALID;
+    if (out_scores->dtype != MABA_F32) return fail(MABA_ERR_DTYPE, "index_topk_decode: out_scores must be f32");
+  }
+  if (B * Hq == 0 || nb == 0) return MABA_OK;
+  const size_t need = maba_hip_index_topk_decode_workspace_size(B, Hq, nb, top_k);
+  if (!workspace || workspace_bytes < need)
+    return fail(MABA_ERR_WORKSPACE, "index_topk_decode: workspace of %zu bytes required", need);
+  DecArgs a;
+  a.q = q->data; a.qdt = q->dtype; a.qsb = q->stride[0]; a.qsh = q->stride[1]; a.qsd = q->stride[2];
+  a.c = centroids->data; a.cdt = centroids->dtype;
+  a.csb = centroids->stride[0]; a.csn = centroids->stride[1]; a.csd = centroids->stride[2];
+  a.nb = nb; a.d = d; a.Hq = (int)Hq; a.K = top_k;
+  a.tiles_per_wave = 1;
+  a.nsplit = (int)ceil_div(ceil_div(nb, 64), 4);
+  a.scale = 1.0f / sqrtf((float)d);
+  a.lam = lambda_dist;
+  a.ws = (key64*)workspace;
+  a.scores = out_scores ? (float*)out_scores->data : nullptr;
+  a.ssb = out_scores ? out_scores->stride[0] : 0;
+  a.ssh = out_scores ? out_scores->stride[1] : 0;
+  a.ssn = out_scores ? out_scores->stride[2] : 0;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(index_decode_score_kernel, dim3((unsigned)a.nsplit, (unsigned)B), dim3(256), 0, s, a);
+  int rc = check_launch("index_topk_decode/score");
+  if (rc) return rc;
+  hipLaunchKernelGGL(index_decode_merge_kernel, dim3((unsigned)(B * Hq)), dim3(64), 0, s, a.ws, a.nsplit,
+                     (int)Hq, top_k, (int)ak, (int64_t*)out_idx->data, out_idx->stride[0],
+                     out_idx->stride[1], out_idx->stride[2]);
+  return check_launch("index_topk_decode/merge");
+}
+
+extern "C" int maba_hip_index_topk(const maba_tensor* q_idx, const maba_tensor* centroids,
+                                   float lambda_dist, int top_k, int block_size, maba_tensor* out_idx,
+                                   maba_tensor* out_scores, void* stream) {
+  if (!q_idx || q_idx->ndim != 3 || !centroids || centroids->ndim != 3)
+    return fail(MABA_ERR_INVALID, "index_topk: q_idx and centroids must be 3D");
+  const int64_t B = q_idx->shape[0], L = q_idx->shape[1], d = q_idx->shape[2], nb = centroids->shape[1];
+  if (centroids->shape[0] != B || centroids->shape[2] != d)
+    return fail(MABA_ERR_INVALID, "index_topk: dimension mismatch between q_idx and centroids");
+  if (top_k <= 0) return fail(MABA_ERR_INVALID, "index_topk: top_k must be positive, got %d", top_k);
+  if (block_size <= 0) return fail(MABA_ERR_INVALID, "index_topk: block_size must be positive, got %d", block_size);
+  const int64_t ak = top_k < nb ? top_k : nb;
+  const int64_t so[3] = {B, L, ak};
+  if (!expect_shape(out_idx, "out_idx", 3, so)) return MABA_ERR_INVALID;
+  if (out_idx->dtype != MABA_I64) return fail(MABA_ERR_DTYPE, "index_topk: out_idx must be int64");
+  if (!expect_float(q_idx, "q_idx") || !expect_float(centroids, "centroids")) return MABA_ERR_DTYPE;
+  if (top_k > 64 && nb > 64) return fail(MABA_ERR_UNSUPPORTED, "index_topk: top_k > 64 not supported");
+  if (d > IDX_MAX_D) return fail(MABA_ERR_UNSUPPORTED, "index_topk: d <= %d required", IDX_MAX_D);
+  if (out_scores) {
+    const int64_t ss[3] = {B, L, nb};
+    if (!expect_shape(out_scores, "out_scores", 3, ss)) return MABA_ERR_INVALID;
+    if (!expect_float(out_scores, "out_scores")) return MABA_ERR_DTYPE;
+  }
+  if (B * L == 0 || nb == 0) return MABA_OK;
+  PreArgs a;
+  a.q = q_idx->data; a.qdt = q_idx->dtype; a.qsb = q_idx->stride[0]; a.qsl = q_idx->stride[1]; a.qsd = q_idx->stride[2];
+  a.c = centroids->data; a.cdt = centroids->dtype;
+  a.csb = centroids->stride[0]; a.csn = centroids->stride[1]; a.csd = centroids->stride[2];
+  a.B = B; a.L = L; a.nb = nb; a.d = d;
+  a.K = (int)(top_k < 64 ? top_k : 64); a.ak = (int)ak; a.bs = block_size;
+  a.scale = 1.0f / sqrtf((float)d);
+  a.lam = lambda_dist;
+  a.out = (int64_t*)out_idx->data; a.osb = out_idx->stride[0]; a.osl = out_idx->stride[1]; a.osk = out_idx->stride[2];
+  a.scores = out_scores ? out_scores->data : nullptr;
+  a.sdt = out_scores ? out_scores->dtype : MABA_F32;
+  a.ssb = out_scores ? out_scores->stride[0] : 0;
+  a.ssl = out_scores ? out_scores->stride[1] : 0;
+  a.ssn = out_scores ? out_scores->stride[2] : 0;
+  hipLaunchKernelGGL(index_prefill_kernel, dim3((unsigned)ceil_div(B * L, 4)), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  return check_launch("index_topk");
+}

@@ -1,0 +1,170 @@
+"""ctypes binding of ``libmaba_hip.so`` (the gfx950 HIP kernels behind ``include/maba_hip.h``).
+
+The library is built in-tree by ``__graft_entry__.build()`` (or
+``python -m maba_sparse.build``) into ``maba_sparse/_lib/libmaba_hip.so``.  This
+module never compiles anything; a missing library raises ``HipLibraryMissing``
+when a HIP op is called, so a GPU run can never silently take another path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional, Sequence
+
+import torch
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
+LIB_PATH = os.path.join(LIB_DIR, "libmaba_hip.so")
+
+MABA_F32, MABA_F16, MABA_BF16, MABA_F64, MABA_I64, MABA_I32 = 0, 1, 2, 3, 4, 5
+_DTYPE_CODES = {
+    torch.float32: MABA_F32,
+    torch.float16: MABA_F16,
+    torch.bfloat16: MABA_BF16,
+    torch.float64: MABA_F64,
+    torch.int64: MABA_I64,
+    torch.int32: MABA_I32,
+}
+
+MABA_OK, MABA_ERR_INVALID, MABA_ERR_DTYPE, MABA_ERR_UNSUPPORTED, MABA_ERR_HIP, MABA_ERR_WORKSPACE = range(6)
+
+# Every symbol declared in include/maba_hip.h.
+EXPORTED_SYMBOLS = (
+    "maba_hip_last_error",
+    "maba_hip_abi_version",
+    "maba_hip_dgda_prefill_workspace_size",
+    "maba_hip_dgda_prefill",
+    "maba_hip_dgda_step",
+    "maba_hip_compute_centroids",
+    "maba_hip_index_topk",
+    "maba_hip_index_topk_decode_workspace_size",
+    "maba_hip_index_topk_decode",
+    "maba_hip_stream_superposition",
+    "maba_hip_hca_pool",
+    "maba_hip_maba_sa_decode_workspace_size",
+    "maba_hip_maba_sa_decode",
+)
+
+
+class HipLibraryMissing(RuntimeError):
+    """The HIP backend library is not built or cannot be loaded."""
+
+
+class MabaTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("shape", ctypes.c_int64 * 4),
+        ("stride", ctypes.c_int64 * 4),
+    ]
+
+
+_lib = None
+_lib_err: Optional[str] = None
+_lock = threading.Lock()
+
+
+def _declare(lib) -> None:
+    T = ctypes.POINTER(MabaTensor)
+    vp, i, f, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_size_t
+    sig = {
+        "maba_hip_last_error": ([], ctypes.c_char_p),
+        "maba_hip_abi_version": ([], i),
+        "maba_hip_dgda_prefill_workspace_size": ([T, T, T, T], sz),
+        "maba_hip_dgda_prefill": ([T, T, T, T, T, T, T, T, T, T, i, vp, sz, vp], i),
+        "maba_hip_dgda_step": ([T, T, T, T, T, T, T, T, T, T, vp], i),
+        "maba_hip_compute_centroids": ([T, T, i, vp], i),
+        "maba_hip_index_topk": ([T, T, f, i, i, T, T, vp], i),
+        "maba_hip_index_topk_decode_workspace_size": ([i64, i64, i64, i], sz),
+        "maba_hip_index_topk_decode": ([T, T, f, i, T, T, vp, sz, vp], i),
+        "maba_hip_stream_superposition": ([T, T, T, T, i, T, vp], i),
+        "maba_hip_hca_pool": ([T, T, i, vp], i),
+        "maba_hip_maba_sa_decode_workspace_size": ([i64, i64, i64, i64, i64, i, i, i], sz),
+        "maba_hip_maba_sa_decode": ([T, T, T, T, T, i64, f, i, i, i, i, T, vp, sz, vp], i),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+
+
+def load(required: bool = True):
+    """Load the library once; raise ``HipLibraryMissing`` when ``required``."""
+    global _lib, _lib_err
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None and _lib_err is None:
+            if not os.path.exists(LIB_PATH):
+                _lib_err = f"{LIB_PATH} not found; run __graft_entry__.build() first"
+            else:
+                try:
+                    lib = ctypes.CDLL(LIB_PATH)
+                    _declare(lib)
+                    _lib = lib
+                except OSError as exc:  # pragma: no cover - depends on the box
+                    _lib_err = f"cannot load {LIB_PATH}: {exc}"
+    if _lib is None and required:
+        raise HipLibraryMissing(_lib_err or "libmaba_hip.so unavailable")
+    return _lib
+
+
+def available() -> bool:
+    return load(required=False) is not None
+
+
+def desc(t: Optional[torch.Tensor]):
+    """Build a ``maba_tensor`` descriptor (pointer to it) for a tensor, or None."""
+    if t is None:
+        return None
+    if t.dim() > 4:
+        raise ValueError(f"descriptor supports at most 4 dims, got {t.dim()}")
+    code = _DTYPE_CODES.get(t.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    d = MabaTensor()
+    d.data = t.data_ptr() if t.numel() > 0 else 0
+    d.dtype = code
+    d.ndim = t.dim()
+    for k in range(4):
+        d.shape[k] = t.shape[k] if k < t.dim() else 1
+        d.stride[k] = t.stride(k) if k < t.dim() else 0
+    return ctypes.pointer(d)
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def check(rc: int, what: str) -> None:
+    """Map a status code to the Python exception the reference would raise."""
+    if rc == MABA_OK:
+        return
+    msg = (load().maba_hip_last_error() or b"").decode(errors="replace")
+    text = f"{what}: {msg}"
+    if rc == MABA_ERR_INVALID:
+        raise ValueError(text)
+    if rc == MABA_ERR_DTYPE:
+        raise TypeError(text)
+    if rc == MABA_ERR_UNSUPPORTED:
+        raise NotImplementedError(text)
+    raise RuntimeError(text)
+
+
+def require_device(tensors: Sequence[Optional[torch.Tensor]], op: str) -> torch.device:
+    """All tensors on one ROCm GPU device (the HIP kernels only run there)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{op}: HIP backend needs GPU tensors, got {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{op}: Expected all tensors to be on the same device, got {dev} and {t.device}")
+    if dev is None:
+        raise RuntimeError(f"{op}: no tensor given")
+    return dev

@@ -1,0 +1,236 @@
+"""The ``"hip"`` backend: registered wrappers around ``libmaba_hip.so``.
+
+Each wrapper keeps the reference op's keyword signature and return
+convention, allocates outputs (and any workspace) with torch on the inputs'
+device, and enqueues the HIP kernels on torch's current stream; the library
+itself never allocates.  The kernels are forward-only: when autograd needs
+gradients a wrapper raises ``NotImplementedError`` so that the dispatcher falls
+back to the differentiable reference path (reference tests check gradients
+through the dispatcher, tests/test_dispatcher.py:324-443).
+
+Reference wrappers mirrored (paths relative to the reference checkout):
+``triton_dgda_prefill``/``triton_dgda_step`` (kernels/triton_dgda.py:647-685),
+``triton_compute_centroids``/``triton_index_topk``/``triton_stream_superposition``
+(kernels/triton_indexer.py:558-693).
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, Optional, Tuple
+
+import torch
+
+from maba_sparse import _native as N
+from maba_sparse.kernels.common import (
+    validate_dgda_prefill_inputs,
+    validate_dgda_step_inputs,
+    validate_indexer_inputs,
+    validate_superposition_inputs,
+)
+from maba_sparse.kernels.dispatcher import register_kernel
+
+
+def _no_grad_needed(op: str, *tensors) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise NotImplementedError(f"{op}: HIP kernels are forward-only; autograd uses the reference path")
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+@register_kernel("hip", "dgda_prefill")
+def hip_dgda_prefill(q, k, v, alpha=None, b=None, w=None, chunk_size: int = 16, initial_state=None,
+                     log_alpha=None, out_dtype: Optional[torch.dtype] = None,
+                     state_dtype: Optional[torch.dtype] = None, allow_mixed_dtypes: bool = False,
+                     **kwargs: Any) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Chunked DGDA prefill on gfx950 (reference contract: dispatcher.py:258-327).
+
+    Outputs default to q's dtype like the reference (cpu_dgda.py:197);
+    ``out_dtype``/``state_dtype`` override them.  ``inversion_method`` and
+    ``adaptive_tol`` are accepted and ignored: the kernel's triangular solves
+    are exact.
+    """
+    validate_dgda_prefill_inputs(q, k, v, alpha, b, w, initial_state, log_alpha=log_alpha,
+                                 allow_mixed_dtypes=allow_mixed_dtypes)
+    _no_grad_needed("dgda_prefill", q, k, v, alpha, b, w, initial_state, log_alpha)
+    dev = N.require_device([q, k, v, alpha, b, w, initial_state, log_alpha], "dgda_prefill")
+    B, H, L, dk = q.shape
+    dv = v.shape[-1]
+    odt = out_dtype or q.dtype
+    sdt = state_dtype or q.dtype
+    if L == 0:
+        st = initial_state.clone().to(sdt) if initial_state is not None else \
+            torch.zeros(B, H, dk, dv, dtype=sdt, device=dev)
+        return torch.empty(B, H, 0, dv, dtype=odt, device=dev), st
+    lib = N.load()
+    out = torch.empty(B, H, L, dv, dtype=odt, device=dev)
+    state = torch.empty(B, H, dk, dv, dtype=sdt, device=dev)
+    dq, dk_, dvv = N.desc(q), N.desc(k), N.desc(v)
+    da, dla = N.desc(alpha), N.desc(log_alpha)
+    db, dw = N.desc(b), N.desc(w)
+    ds0 = N.desc(initial_state)
+    dout, dst = N.desc(out), N.desc(state)
+    gate = dla if log_alpha is not None else da
+    nbytes = lib.maba_hip_dgda_prefill_workspace_size(dq, dvv, gate, db)
+    ws = _workspace(nbytes, dev)
+    rc = lib.maba_hip_dgda_prefill(dq, dk_, dvv, da, dla, db, dw, ds0, dout, dst, int(chunk_size),
+                                   ws.data_ptr(), ws.numel(), N.stream_ptr(dev))
+    N.check(rc, "dgda_prefill")
+    return out, state
+
+
+def _squeeze_step(t):
+    if t is None:
+        return None
+    return t.squeeze(2) if (t.dim() == 4 and t.shape[2] == 1) else t
+
+
+@register_kernel("hip", "dgda_step")
+def hip_dgda_step(q, k, v, alpha=None, b=None, w=None, state=None, log_alpha=None,
+                  out_dtype: Optional[torch.dtype] = None, state_dtype: Optional[torch.dtype] = None,
+                  allow_mixed_dtypes: bool = False, **kwargs: Any) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One DGDA decode token (reference contract: dispatcher.py:330-396)."""
+    validate_dgda_step_inputs(q, k, v, alpha, b, w, state, log_alpha=log_alpha,
+                              allow_mixed_dtypes=allow_mixed_dtypes)
+    _no_grad_needed("dgda_step", q, k, v, alpha, b, w, state, log_alpha)
+    dev = N.require_device([q, k, v, alpha, b, w, state, log_alpha], "dgda_step")
+    q3, k3, v3, a3, b3, w3, la3 = (_squeeze_step(t) for t in (q, k, v, alpha, b, w, log_alpha))
+    B, H, dk = q3.shape
+    dv = v3.shape[-1]
+    out = torch.empty(B, H, dv, dtype=out_dtype or q.dtype, device=dev)
+    new_state = torch.empty(B, H, dk, dv, dtype=state_dtype or q.dtype, device=dev)
+    lib = N.load()
+    rc = lib.maba_hip_dgda_step(N.desc(q3), N.desc(k3), N.desc(v3), N.desc(a3), N.desc(la3), N.desc(b3),
+                                N.desc(w3), N.desc(state), N.desc(out), N.desc(new_state), N.stream_ptr(dev))
+    N.check(rc, "dgda_step")
+    return out, new_state
+
+
+@register_kernel("hip", "compute_centroids")
+def hip_compute_centroids(k_idx, block_size: int = 64, **kwargs: Any) -> torch.Tensor:
+    """Block centroids (reference contract: dispatcher.py:399-421, triton_indexer.py:558-578)."""
+    validate_indexer_inputs(k_idx=k_idx)
+    if block_size <= 0:
+        raise ValueError(f"block_size must be positive, got {block_size}")
+    _no_grad_needed("compute_centroids", k_idx)
+    dev = N.require_device([k_idx], "compute_centroids")
+    B, L, d = k_idx.shape
+    nb = (L + block_size - 1) // block_size
+    out = torch.empty(B, nb, d, dtype=k_idx.dtype, device=dev)
+    if L == 0:
+        return out
+    rc = N.load().maba_hip_compute_centroids(N.desc(k_idx), N.desc(out), int(block_size), N.stream_ptr(dev))
+    N.check(rc, "compute_centroids")
+    return out
+
+
+@register_kernel("hip", "index_topk")
+def hip_index_topk(q_idx, centroids, lambda_dist: float = 0.5, top_k: int = 32, block_size: int = 64,
+                   return_scores: bool = False, **kwargs: Any):
+    """Causal prefill scoring + top-k (reference contract: dispatcher.py:424-465)."""
+    lam = kwargs.get("dist_lambda", lambda_dist)
+    if q_idx.device != centroids.device:
+        raise RuntimeError(
+            f"Expected all tensors to be on the same device, got {q_idx.device} and {centroids.device}")
+    if q_idx.dim() != 3 or centroids.dim() != 3:
+        raise ValueError(f"q_idx and centroids must be 3D, got {q_idx.dim()}D and {centroids.dim()}D")
+    if q_idx.shape[0] != centroids.shape[0] or q_idx.shape[2] != centroids.shape[2]:
+        raise ValueError(
+            f"Dimension mismatch between q_idx {list(q_idx.shape)} and centroids {list(centroids.shape)}")
+    if top_k <= 0:
+        raise ValueError(f"top_k must be positive, got {top_k}")
+    if block_size <= 0:
+        raise ValueError(f"block_size must be positive, got {block_size}")
+    _no_grad_needed("index_topk", q_idx, centroids)
+    dev = N.require_device([q_idx, centroids], "index_topk")
+    B, L, d = q_idx.shape
+    nb = centroids.shape[1]
+    ak = min(top_k, nb)
+    idx = torch.zeros(B, L, ak, dtype=torch.long, device=dev)
+    scores = None
+    if return_scores:
+        scores = torch.zeros(B, L, nb, dtype=q_idx.dtype, device=dev)
+    if L == 0 or nb == 0:
+        return (idx, scores) if return_scores else idx
+    rc = N.load().maba_hip_index_topk(N.desc(q_idx), N.desc(centroids), float(lam), int(top_k),
+                                      int(block_size), N.desc(idx), N.desc(scores), N.stream_ptr(dev))
+    N.check(rc, "index_topk")
+    return (idx, scores) if return_scores else idx
+
+
+@register_kernel("hip", "index_topk_decode")
+def hip_index_topk_decode(q, centroids, lambda_dist: float = 0.5, top_k: int = 32,
+                          return_scores: bool = False, **kwargs: Any):
+    """Decode scoring + top-k over one centroid set per batch (layers/indexer.py:391-402)."""
+    lam = kwargs.get("dist_lambda", lambda_dist)
+    _no_grad_needed("index_topk_decode", q, centroids)
+    dev = N.require_device([q, centroids], "index_topk_decode")
+    B, Hq, d = q.shape
+    nb = centroids.shape[1]
+    ak = min(top_k, nb)
+    idx = torch.zeros(B, Hq, ak, dtype=torch.long, device=dev)
+    scores = torch.empty(B, Hq, nb, dtype=torch.float32, device=dev) if return_scores else None
+    if nb == 0 or B * Hq == 0:
+        return (idx, scores) if return_scores else idx
+    lib = N.load()
+    ws = _workspace(lib.maba_hip_index_topk_decode_workspace_size(B, Hq, nb, int(top_k)), dev)
+    rc = lib.maba_hip_index_topk_decode(N.desc(q), N.desc(centroids), float(lam), int(top_k), N.desc(idx),
+                                        N.desc(scores), ws.data_ptr(), ws.numel(), N.stream_ptr(dev))
+    N.check(rc, "index_topk_decode")
+    return (idx, scores) if return_scores else idx
+
+
+@register_kernel("hip", "stream_superposition")
+def hip_stream_superposition(o_local, o_sparse, o_hca, gate_logits=None, gate_weights=None,
+                             **kwargs: Any) -> torch.Tensor:
+    """Gate superposition (reference contract: dispatcher.py:468-508)."""
+    gate = gate_logits if gate_logits is not None else gate_weights
+    validate_superposition_inputs(o_local, o_sparse, o_hca, gate)
+    if gate is None:
+        raise ValueError("Either gate_logits or gate_weights must be provided")
+    if gate.dim() not in (3, 4):
+        raise ValueError(f"Gate tensor must be 3D or 4D, got {gate.dim()}D")
+    _no_grad_needed("stream_superposition", o_local, o_sparse, o_hca, gate)
+    dev = N.require_device([o_local, o_sparse, o_hca, gate], "stream_superposition")
+    out = torch.empty_like(o_local)
+    if o_local.shape[2] == 0 or o_local.numel() == 0:
+        return out
+    rc = N.load().maba_hip_stream_superposition(N.desc(o_local), N.desc(o_sparse), N.desc(o_hca), N.desc(gate),
+                                                int(gate_logits is None), N.desc(out), N.stream_ptr(dev))
+    N.check(rc, "stream_superposition")
+    return out
+
+
+@register_kernel("hip", "hca_pool")
+def hip_hca_pool(c_kv, pool: int = 64, **kwargs: Any) -> torch.Tensor:
+    """Means of complete ``pool``-token latent blocks (layers/sparse_attention.py:206)."""
+    _no_grad_needed("hca_pool", c_kv)
+    dev = N.require_device([c_kv], "hca_pool")
+    B, L, dc = c_kv.shape
+    out = torch.empty(B, L // pool, dc, dtype=kwargs.get("out_dtype") or c_kv.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    rc = N.load().maba_hip_hca_pool(N.desc(c_kv), N.desc(out), int(pool), N.stream_ptr(dev))
+    N.check(rc, "hca_pool")
+    return out
+
+
+@register_kernel("hip", "maba_sa_decode")
+def hip_maba_sa_decode(q_lat, c_kv, hca, idx, gate, L: int, scale: float, window: int = 128, n_sink: int = 4,
+                       block_size: int = 64, pool: int = 64, **kwargs: Any) -> torch.Tensor:
+    """Fused local + sparse + HCA decode streams with the gate superposition, in
+    latent space (layers/sparse_attention.py:79-219,263-275).  Returns fp32
+    ``[B, H, d_c]``; the caller applies the per-head value up-projection."""
+    _no_grad_needed("maba_sa_decode", q_lat, c_kv, hca, gate)
+    dev = N.require_device([q_lat, c_kv, hca, idx, gate], "maba_sa_decode")
+    B, H, dc = q_lat.shape
+    out = torch.empty(B, H, dc, dtype=torch.float32, device=dev)
+    lib = N.load()
+    K = idx.shape[-1]
+    ws = _workspace(lib.maba_hip_maba_sa_decode_workspace_size(B, H, dc, int(L), K, int(window), int(n_sink), int(pool)), dev)
+    rc = lib.maba_hip_maba_sa_decode(N.desc(q_lat), N.desc(c_kv), N.desc(hca), N.desc(idx), N.desc(gate),
+                                     int(L), float(scale), int(window), int(n_sink), int(block_size), int(pool),
+                                     N.desc(out), ws.data_ptr(), ws.numel(), N.stream_ptr(dev))
+    N.check(rc, "maba_sa_decode")
+    return out

@@ -1,0 +1,242 @@
+"""HIP kernels vs the CPU oracle on seeded inputs (runs on the GPU box).
+
+Tolerances: fp32 paths 1e-4 (reference test_cpu_dgda.py:469-470,
+test_triton_indexer.py:124-145); mixed bf16-input / fp32-accumulate paths
+rtol = atol = 2e-3; block indices bit-exact wherever the
+oracle's scores separate them by more than 1e-4.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_close, dgda_inputs, oracle_dgda_args, to_np, topk_agrees
+from oracle import dgda as odgda
+from oracle import indexer as oidx
+from oracle import sparse_attn as osa
+
+pytestmark = pytest.mark.gpu
+
+
+def _hip():
+    from maba_sparse.kernels import hip_backend
+    return hip_backend
+
+
+# ----------------------------------------------------------------------------- dgda_step
+
+@pytest.mark.parametrize("B,H,dk,dv", [(2, 3, 64, 64), (64, 10, 64, 64), (3, 2, 32, 128), (1, 1, 128, 16), (2, 2, 17, 33)])
+def test_dgda_step_fp32(dev, B, H, dk, dv):
+    g = torch.Generator().manual_seed(B * 100 + dk)
+    q = torch.randn(B, H, dk, generator=g)
+    k = torch.nn.functional.normalize(torch.randn(B, H, dk, generator=g), dim=-1)
+    v = torch.randn(B, H, dv, generator=g)
+    la = -torch.nn.functional.softplus(torch.randn(B, H, dk, generator=g) + 2)
+    b = torch.sigmoid(torch.randn(B, H, dk, generator=g))
+    w = torch.sigmoid(torch.randn(B, H, dv, generator=g))
+    S = torch.randn(B, H, dk, dv, generator=g)
+    o, Sn = _hip().hip_dgda_step(q.to(dev), k.to(dev), v.to(dev), log_alpha=la.to(dev), b=b.to(dev),
+                                 w=w.to(dev), state=S.to(dev))
+    eo, eS = odgda.dgda_step(q, k, v, alpha=np.exp(to_np(la)), b=b, w=w, state=to_np(S))
+    assert_close(o, eo, 1e-4, 1e-4, "out")
+    assert_close(Sn, eS, 1e-4, 1e-4, "state")
+
+
+def test_dgda_step_4d_alpha_no_state(dev):
+    g = torch.Generator().manual_seed(7)
+    B, H, d = 4, 2, 64
+    q, k, v = (torch.randn(B, H, 1, d, generator=g) for _ in range(3))
+    a = torch.rand(B, H, 1, d, generator=g)
+    b, w = torch.rand(B, H, 1, d, generator=g), torch.rand(B, H, 1, d, generator=g)
+    o, Sn = _hip().hip_dgda_step(*(t.to(dev) for t in (q, k, v)), alpha=a.to(dev), b=b.to(dev), w=w.to(dev))
+    eo, eS = odgda.dgda_step(q, k, v, alpha=a, b=b, w=w)
+    assert o.shape == (B, H, d)
+    assert_close(o, eo, 1e-4, 1e-4, "out")
+    assert_close(Sn, eS, 1e-4, 1e-4, "state")
+
+
+def test_dgda_step_mixed_bf16(dev):
+    """BASELINE decode microbench dtypes: bf16 q/k/v, fp32 gates and state."""
+    inp = dgda_inputs(64, 10, 1, seed=3, device=dev, with_state=True)
+    sq = lambda t: t[:, :, 0]
+    o, Sn = _hip().hip_dgda_step(sq(inp["q"]), sq(inp["k"]), sq(inp["v"]), log_alpha=sq(inp["log_alpha"]),
+                                 b=sq(inp["b"]), w=sq(inp["w"]), state=inp["initial_state"],
+                                 out_dtype=torch.float32, state_dtype=torch.float32, allow_mixed_dtypes=True)
+    ar = oracle_dgda_args(inp)
+    eo, eS = odgda.dgda_step(ar["q"][:, :, 0], ar["k"][:, :, 0], ar["v"][:, :, 0], alpha=ar["alpha"][:, :, 0],
+                             b=ar["b"][:, :, 0], w=ar["w"][:, :, 0], state=ar["initial_state"])
+    assert_close(o, eo, 2e-3, 2e-3, "out")
+    assert_close(Sn, eS, 2e-3, 2e-3, "state")
+
+
+# ----------------------------------------------------------------------------- dgda_prefill (general path)
+
+@pytest.mark.parametrize("gates", ["channel", "scalar"])
+@pytest.mark.parametrize("L", [1, 17, 200])
+def test_dgda_prefill_fp32(dev, gates, L):
+    inp = dgda_inputs(2, 3, L, 64, 64, qkv_dtype=torch.float32, gates=gates, seed=L, device=dev, with_state=True)
+    o, S = _hip().hip_dgda_prefill(**inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 1e-4, 1e-4, "out")
+    assert_close(S, eS, 1e-4, 1e-4, "state")
+
+
+def test_dgda_prefill_odd_dims(dev):
+    inp = dgda_inputs(1, 2, 33, 24, 40, qkv_dtype=torch.float32, gates="channel", seed=5, device=dev)
+    o, S = _hip().hip_dgda_prefill(**inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 1e-4, 1e-4, "out")
+    assert_close(S, eS, 1e-4, 1e-4, "state")
+
+
+def test_dgda_prefill_transposed_views(dev):
+    """The layer passes [B,L,H,d] storage viewed as [B,H,L,d] (dgda.py:199-205)."""
+    B, L, H, d = 2, 40, 3, 64
+    g = torch.Generator().manual_seed(11)
+    phys = [torch.randn(B, L, H, d, generator=g) for _ in range(3)]
+    q, k, v = (p.to(dev).transpose(1, 2) for p in phys)
+    k = k / k.norm(dim=-1, keepdim=True)
+    la = (-torch.nn.functional.softplus(torch.randn(B, L, H, d, generator=g))).to(dev).transpose(1, 2)
+    b = torch.rand(B, L, H, d, generator=g).to(dev).transpose(1, 2)
+    w = torch.rand(B, L, H, d, generator=g).to(dev).transpose(1, 2)
+    o, S = _hip().hip_dgda_prefill(q, k, v, log_alpha=la, b=b, w=w)
+    eo, eS = odgda.dgda_prefill_seq(to_np(q), to_np(k), to_np(v), alpha=np.exp(to_np(la)), b=to_np(b), w=to_np(w))
+    assert_close(o, eo, 1e-4, 1e-4, "out")
+    assert_close(S, eS, 1e-4, 1e-4, "state")
+
+
+# ----------------------------------------------------------------------------- pooling
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2), (torch.float16, 5e-3)])
+@pytest.mark.parametrize("B,L,d", [(1, 64, 64), (2, 100, 64), (3, 1, 128), (2, 4096, 128), (1, 70, 96), (2, 65, 30)])
+def test_compute_centroids(dev, dtype, tol, B, L, d):
+    x = torch.randn(B, L, d, generator=torch.Generator().manual_seed(L + d)).to(dtype)
+    c = _hip().hip_compute_centroids(x.to(dev), block_size=64)
+    exp = oidx.compute_centroids(to_np(x), 64)
+    assert c.dtype == dtype
+    assert_close(c, exp, 0, tol, "centroids")
+
+
+def test_compute_centroids_known_answers(dev):
+    k = torch.full((1, 256, 64), 0.01, device=dev)
+    k[0, 70, :] = 10.0
+    c = _hip().hip_compute_centroids(k, block_size=64)
+    pure_mean = (63 * 0.01 + 10.0) / 64.0
+    assert abs(c[0, 1, 0].item() - 0.5 * (pure_mean + 10.0)) < 1e-3       # test_triton_indexer.py:147-158
+    k = torch.full((1, 100, 64), -2.0, device=dev)
+    c = _hip().hip_compute_centroids(k, block_size=64)
+    assert torch.allclose(c[0, 0], torch.tensor(-2.0, device=dev), atol=1e-4)
+    assert torch.allclose(c[0, 1], torch.tensor(0.5 * (-72.0 / 64.0), device=dev), atol=1e-4)  # :160-168
+
+
+def test_hca_pool(dev):
+    x = torch.randn(3, 64 * 7 + 13, 128, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    m = _hip().hip_hca_pool(x.to(dev), pool=64)
+    exp = osa.hca_means(to_np(x), pool=64)
+    assert m.shape == (3, 7, 128)
+    assert_close(m, exp, 0, 1e-2, "hca means")
+
+
+# ----------------------------------------------------------------------------- superposition
+
+@pytest.mark.parametrize("gate_dim", [3, 4])
+@pytest.mark.parametrize("weights", [False, True])
+def test_stream_superposition(dev, gate_dim, weights):
+    B, H, L, D = 2, 4, 15, 64
+    g = torch.Generator().manual_seed(gate_dim + 10 * weights)
+    ol, os_, oh = (torch.randn(B, H, L, D, generator=g) for _ in range(3))
+    z = torch.randn(*((B, L, 3) if gate_dim == 3 else (B, H, L, 3)), generator=g)
+    gate = torch.softmax(z, -1) if weights else z
+    kw = {"gate_weights": gate.to(dev)} if weights else {"gate_logits": gate.to(dev)}
+    out = _hip().hip_stream_superposition(ol.to(dev), os_.to(dev), oh.to(dev), **kw)
+    exp = osa.superposition(to_np(ol), to_np(os_), to_np(oh), **({"gate_weights": to_np(gate)} if weights
+                                                                 else {"gate_logits": to_np(gate)}))
+    assert_close(out, exp, 1e-5, 1e-5, "superposition")
+
+
+def test_superposition_partition_of_unity(dev):
+    x = torch.randn(2, 4, 64, 64, device=dev)
+    out = _hip().hip_stream_superposition(x, x, x, gate_logits=torch.randn(2, 64, 3, device=dev))
+    assert torch.allclose(out, x, atol=1e-5)
+
+
+# ----------------------------------------------------------------------------- indexer
+
+@pytest.mark.parametrize("B,Hq,nb,d,k,lam,dtype", [
+    (2, 10, 15625 // 25, 128, 32, 0.1, torch.bfloat16),
+    (1, 1, 8, 64, 32, 0.5, torch.float32),
+    (3, 4, 300, 64, 8, 1.0, torch.float32),
+    (2, 16, 1000, 128, 64, 0.1, torch.bfloat16),
+    (1, 2, 64, 32, 1, 0.0, torch.float16),
+])
+def test_index_topk_decode(dev, B, Hq, nb, d, k, lam, dtype):
+    g = torch.Generator().manual_seed(nb + d)
+    q = torch.randn(B, Hq, d, generator=g).to(dtype)
+    c = torch.randn(B, nb, d, generator=g).to(dtype)
+    idx, sc = _hip().hip_index_topk_decode(q.to(dev), c.to(dev), lambda_dist=lam, top_k=k, return_scores=True)
+    ref = oidx.decode_scores(to_np(q), to_np(c), lam)
+    assert idx.shape == (B, Hq, min(k, nb)) and idx.dtype == torch.long
+    assert_close(sc, ref, 1e-5, 1e-4, "decode scores")
+    n = topk_agrees(idx.cpu().numpy(), ref, k)
+    assert n >= 1
+
+
+@pytest.mark.parametrize("B,L,nb_blocks,k,lam", [(1, 64, 1, 1, 0.5), (2, 128, 2, 2, 0.5), (3, 256, 4, 4, 0.5),
+                                                  (2, 512, 8, 8, 1.0), (1, 100, 2, 2, 0.25), (2, 65, 2, 2, 0.0),
+                                                  (2, 16, 1, 2, 0.5), (1, 512, 8, 32, 0.5), (2, 4096, 64, 32, 0.1)])
+def test_index_topk_prefill(dev, B, L, nb_blocks, k, lam):
+    g = torch.Generator().manual_seed(L + k)
+    q = torch.randn(B, L, 64, generator=g)
+    kk = torch.randn(B, L, 64, generator=g)
+    cent = torch.from_numpy(oidx.compute_centroids(to_np(kk), 64)).float()
+    idx, sc = _hip().hip_index_topk(q.to(dev), cent.to(dev), lambda_dist=lam, top_k=k, block_size=64,
+                                    return_scores=True)
+    ref = oidx.prefill_scores(to_np(q), to_np(cent), lam, 64)
+    fin = np.isfinite(ref)
+    assert_close(sc.cpu().numpy()[fin], ref[fin], 1e-5, 1e-4, "scores")
+    assert np.all(np.isneginf(sc.cpu().numpy()[~fin]))
+    topk_agrees(idx.cpu().numpy(), ref, k)
+    # causal: the first min(k, qblk+1) picks are past or current blocks
+    ii = idx.cpu().numpy()
+    for t in range(L):
+        avail = min(t // 64 + 1, ii.shape[-1])
+        assert (ii[:, t, :avail] <= t // 64).all()
+
+
+def test_index_topk_penalty_order(dev):
+    q = torch.ones(1, 256, 64, device=dev) / 8.0
+    c = torch.ones(1, 4, 64, device=dev) / 8.0
+    idx = _hip().hip_index_topk(q, c, lambda_dist=1.0, top_k=4, block_size=64)
+    assert idx[0, 255].tolist() == [3, 2, 1, 0]      # test_triton_indexer.py:247-255
+
+
+# ----------------------------------------------------------------------------- MABA-SA decode
+
+def _sa_case(B, H, dh, dc, L, K, Hi, seed, dev, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    c = torch.randn(B, L, dc, generator=g).to(dtype)
+    Wk = (torch.randn(H * dh, dc, generator=g) * 0.05)
+    Wv = (torch.randn(H * dh, dc, generator=g) * 0.05)
+    q = torch.randn(B, H, dh, generator=g)
+    nb = (L + 63) // 64
+    idx = torch.stack([torch.stack([torch.randperm(nb, generator=g)[: min(K, nb)] for _ in range(Hi)])
+                       for _ in range(B)])
+    gate = torch.randn(B, 3, generator=g)
+    return c, Wk, Wv, q, idx, gate
+
+
+@pytest.mark.parametrize("L,K,Hi", [(1, 32, 1), (50, 32, 1), (64, 32, 1), (200, 32, 1), (1000, 8, 1),
+                                    (3000, 32, 4), (5000, 32, 1)])
+def test_maba_sa_decode(dev, L, K, Hi):
+    B, H, dh, dc = 2, 4, 64, 128
+    c, Wk, Wv, q, idx, gate = _sa_case(B, H, dh, dc, L, K, Hi, L + K, dev)
+    hca = _hip().hip_hca_pool(c.to(dev), pool=64)
+    Wk_h = Wk.view(H, dh, dc)
+    q_lat = torch.einsum("bhd,hdc->bhc", q, Wk_h)          # W_k,h^T q_h
+    z = _hip().hip_maba_sa_decode(q_lat.to(dev), c.to(dev), hca, idx.to(dev), gate.to(dev), L=L,
+                                  scale=1.0 / math.sqrt(dh))
+    out = torch.einsum("bhc,hdc->bhd", z.cpu(), Wv.view(H, dh, dc))
+    exp = osa.maba_sa_decode(to_np(q), to_np(c), to_np(Wk), to_np(Wv), to_np(idx).astype(np.int64),
+                             to_np(gate), means=to_np(hca))
+    assert_close(out, exp, 2e-3, 2e-3, "maba_sa")
