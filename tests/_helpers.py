@@ -37,18 +37,21 @@ def dgda_inputs(B, H, L, dk=64, dv=64, qkv_dtype=torch.bfloat16, gate_dtype=torc
     else:
         raise ValueError(decay)
     beta = torch.sigmoid(z_b)
-    if gates == "scalar":
-        la_t = la.to(gate_dtype).expand(B, H, L, dk)
-        b_t = beta.to(gate_dtype).expand(B, H, L, dk)
-        w_t = beta.to(gate_dtype).expand(B, H, L, dv)
-    else:
-        la_t = la.to(gate_dtype)
-        b_t = beta[..., :dk].to(gate_dtype)
-        w_t = beta[..., :dv].to(gate_dtype)
     s0 = torch.randn(B, H, dk, dv, generator=g) * 0.1 if with_state else None
-    t = dict(q=q.to(qkv_dtype), k=k.to(qkv_dtype), v=v.to(qkv_dtype), log_alpha=la_t, b=b_t, w=w_t,
-             initial_state=s0)
-    return {k_: (v_.to(device) if v_ is not None else None) for k_, v_ in t.items()}
+    # move to the device before broadcasting: .to(device) would materialise a stride-0 view
+    la = la.to(device=device, dtype=gate_dtype)
+    beta = beta.to(device=device, dtype=gate_dtype)
+    if gates == "scalar":
+        la_t = la.expand(B, H, L, dk)
+        b_t = beta.expand(B, H, L, dk)
+        w_t = beta.expand(B, H, L, dv)
+    else:
+        la_t = la
+        b_t = beta[..., :dk]
+        w_t = beta[..., :dv]
+    return dict(q=q.to(device=device, dtype=qkv_dtype), k=k.to(device=device, dtype=qkv_dtype),
+                v=v.to(device=device, dtype=qkv_dtype), log_alpha=la_t, b=b_t, w=w_t,
+                initial_state=None if s0 is None else s0.to(device))
 
 
 def to_np(t):

@@ -1,0 +1,123 @@
+"""Chunked MFMA DGDA prefill (per-token gates, dk = dv = 64, bf16 q/k/v) vs the oracle.
+
+Tolerance: rtol = atol = 2e-3 on fp32 outputs and final states for bf16 inputs
+with fp32 accumulation.  bf16 outputs are checked to be
+the rounding of the fp32 results.  The full BASELINE shape (B=4, H=10,
+T=32768) is checked against the C oracle on two heads and through a
+size-independent property on all of them: a prefill split in two halves and
+chained through ``initial_state`` reproduces the single prefill.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_close, dgda_inputs, oracle_dgda_args, to_np
+from oracle import dgda as odgda
+from oracle import dgda_c
+
+pytestmark = pytest.mark.gpu
+
+
+def _hip():
+    from maba_sparse.kernels import hip_backend
+    return hip_backend
+
+
+def _run(inp, **kw):
+    return _hip().hip_dgda_prefill(**inp, out_dtype=kw.pop("out_dtype", torch.float32),
+                                   state_dtype=torch.float32, allow_mixed_dtypes=True, **kw)
+
+
+def test_chunk_path_is_selected(dev):
+    from maba_sparse import _native as N
+    inp = dgda_inputs(1, 2, 4096, seed=0, device=dev)
+    lib = N.load()
+    n = lib.maba_hip_dgda_prefill_workspace_size(N.desc(inp["q"]), N.desc(inp["v"]), N.desc(inp["log_alpha"]),
+                                                 N.desc(inp["b"]))
+    assert n > 16          # multi-segment chunked path needs aggregate/scan workspace
+    inp["b"] = inp["b"].contiguous()   # per-channel erase gate -> sequential path
+    n2 = lib.maba_hip_dgda_prefill_workspace_size(N.desc(inp["q"]), N.desc(inp["v"]), N.desc(inp["log_alpha"]),
+                                                  N.desc(inp["b"]))
+    assert n2 == 0
+
+
+@pytest.mark.parametrize("decay", ["baseline", "slow", "none"])
+@pytest.mark.parametrize("L", [1, 63, 64, 65, 200, 1024, 1025, 3000])
+def test_chunk_vs_oracle(dev, decay, L):
+    inp = dgda_inputs(1, 2, L, seed=L, decay=decay, device=dev, with_state=(L % 2 == 1))
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, f"out L={L} {decay}")
+    assert_close(S, eS, 2e-3, 2e-3, f"state L={L} {decay}")
+
+
+def test_chunk_alpha_instead_of_log_alpha(dev):
+    inp = dgda_inputs(2, 2, 700, seed=4, device=dev)
+    la = inp.pop("log_alpha")
+    inp["alpha"] = torch.exp(la[..., :1]).expand(la.shape)   # per-token, stride-0 broadcast
+    o, S = _run(inp)
+    args = oracle_dgda_args({**inp, "log_alpha": la})
+    eo, eS = odgda.dgda_prefill_seq(**args)
+    assert_close(o, eo, 2e-3, 2e-3, "out")
+    assert_close(S, eS, 2e-3, 2e-3, "state")
+
+
+def test_chunk_per_channel_write_gate(dev):
+    inp = dgda_inputs(1, 3, 300, seed=5, device=dev)
+    inp["w"] = torch.rand(1, 3, 300, 64, generator=torch.Generator().manual_seed(1)).to(dev)
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, "out")
+    assert_close(S, eS, 2e-3, 2e-3, "state")
+
+
+def test_chunk_bf16_output_is_rounded_fp32(dev):
+    inp = dgda_inputs(2, 2, 1500, seed=6, device=dev)
+    o32, _ = _run(inp)
+    o16, _ = _run(inp, out_dtype=torch.bfloat16)
+    assert o16.dtype == torch.bfloat16
+    assert torch.equal(o16, o32.to(torch.bfloat16))
+
+
+def test_chunk_transposed_views(dev):
+    """q/k/v as [B,L,H,d] storage viewed [B,H,L,d], as the DGDA layer passes them."""
+    B, L, H = 2, 777, 3
+    g = torch.Generator().manual_seed(8)
+    mk = lambda: torch.nn.functional.normalize(torch.randn(B, L, H, 64, generator=g), dim=-1)
+    q, k = (mk().bfloat16().to(dev).transpose(1, 2) for _ in range(2))
+    v = torch.randn(B, L, H, 64, generator=g).bfloat16().to(dev).transpose(1, 2)
+    la = (-torch.nn.functional.softplus(torch.randn(B, L, H, 1, generator=g) + 2)).to(dev).transpose(1, 2)
+    be = torch.sigmoid(torch.randn(B, L, H, 1, generator=g)).to(dev).transpose(1, 2)
+    inp = dict(q=q, k=k, v=v, log_alpha=la.expand(B, H, L, 64), b=be.expand(B, H, L, 64),
+               w=be.expand(B, H, L, 64), initial_state=None)
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, "out")
+    assert_close(S, eS, 2e-3, 2e-3, "state")
+
+
+def test_baseline_shape_two_heads_vs_c_oracle(dev):
+    """T = 32768 on (B=1, H=2) against the C chunked oracle (fp32)."""
+    inp = dgda_inputs(1, 2, 32768, seed=2, device=dev)
+    o, S = _run(inp)
+    f = lambda t: to_np(t).astype(np.float32)
+    eo, eS = dgda_c.dgda_prefill_chunked_c(f(inp["q"]), f(inp["k"]), f(inp["v"]), f(inp["log_alpha"][..., :1]),
+                                           f(inp["b"][..., :1]), f(inp["w"][..., :1]), chunk_size=64)
+    assert_close(o, eo, 2e-3, 2e-3, "out")
+    assert_close(S, eS, 2e-3, 2e-3, "state")
+
+
+def test_baseline_shape_split_chaining(dev):
+    """Full BASELINE config 2 shape: prefill(T) == prefill(T/2) -> prefill(T/2, initial_state)."""
+    B, H, T = 4, 10, 32768
+    inp = dgda_inputs(B, H, T, seed=3, decay="slow", device=dev)
+    o, S = _run(inp)
+    assert torch.isfinite(o).all() and torch.isfinite(S).all()
+    h = T // 2
+    first = {k: (v[:, :, :h] if (v is not None and v.dim() == 4 and k != "initial_state") else v) for k, v in inp.items()}
+    second = {k: (v[:, :, h:] if (v is not None and v.dim() == 4 and k != "initial_state") else v) for k, v in inp.items()}
+    o1, S1 = _run(first)
+    second["initial_state"] = S1
+    o2, S2 = _run(second)
+    assert_close(torch.cat([o1, o2], dim=2), to_np(o), 2e-3, 2e-3, "chained out")
+    assert_close(S2, to_np(S), 2e-3, 2e-3, "chained state")
