@@ -1,0 +1,255 @@
+"""Benchmark of the Maba v2 hot path on one MI355X.
+
+Headline (BASELINE.json ``metric``): DGDA chunked prefill throughput at
+T = 32k: B=4, H=10, T=32768, d_k=d_v=64, bf16 q/k/v,
+fp32 per-token gates (stride-0 broadcast over channels), fp32 state, output in
+q's dtype (bf16).  One step = one ``dgda_prefill`` over the whole batch with
+inputs resident in HBM.  ``value`` = B*T / step time (tokens/s).
+
+Also reported in the same JSON line:
+  * ``roofline``   -- the DGDA prefill op (three launches: segment aggregate,
+                      segment scan, segment output) against HBM: algorithmic
+                      bytes per step / step time (HIP events on the launch
+                      stream), plus the bf16-MFMA fraction of the algorithmic
+                      flops;
+  * ``cpu_baseline`` -- the C/OpenMP restatement of the reference CPU chunked
+                      algorithm (oracle/dgda_chunked.c) on a bounded sample of the
+                      same workload, on the host cores;
+  * ``decode``     -- BASELINE configs 2b-4: the B=64 DGDA decode microbench
+                      (10,000 steps), the DG-Indexer decode scoring + top-32 at
+                      1M context and the fused MABA-SA decode step at 1M context
+                      (us/step and HBM GB/s each).
+
+``python bench.py --gpus N --steps K --warmup W``; only N = 1 is supported.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "maba-v2-architecture_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--skip-cpu", action="store_true", help="do not time the CPU baseline")
+    ap.add_argument("--skip-decode", action="store_true", help="do not run the decode benchmarks")
+    ap.add_argument("--only-prefill", action="store_true", help="time only the DGDA prefill step (for profiling)")
+    return ap.parse_args()
+
+
+def time_op(fn, steps: int, warmup: int):
+    """Mean ms per call over ``steps`` calls, HIP events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - w0) * 1e3 / steps
+    return e0.elapsed_time(e1) / steps, wall
+
+
+def dgda_prefill_case(dev, B=4, H=10, T=32768, d=64, seed=0):
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    q = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1).to(dev, torch.bfloat16)
+    k = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1).to(dev, torch.bfloat16)
+    v = torch.randn(B, H, T, d, generator=g).to(dev, torch.bfloat16)
+    la = (-F.softplus(torch.randn(B, H, T, 1, generator=g) + 2.0)).to(dev)
+    beta = torch.sigmoid(torch.randn(B, H, T, 1, generator=g)).to(dev)
+    return dict(q=q, k=k, v=v, log_alpha=la.expand(B, H, T, d), b=beta.expand(B, H, T, d),
+                w=beta.expand(B, H, T, d))
+
+
+def prefill_bytes(B, H, T, d):
+    """Algorithmic HBM bytes of one prefill step: q,k,v bf16 + two per-token fp32
+    gates (log-decay, beta) + bf16 output + fp32 final state."""
+    return B * H * T * (3 * d * 2 + 2 * 4 + d * 2) + B * H * d * d * 4
+
+
+def prefill_flops(B, H, T, d, C=64):
+    """Chunked-algorithm flops, (8 C^2 d + 6 C d^2) per (b, h, chunk)."""
+    return B * H * (T // C) * (8 * C * C * d + 6 * C * d * d)
+
+
+def cpu_baseline(B=4, H=10, T=16384, d=64):
+    import numpy as np
+    from oracle import dgda_c
+    dgda_c.build()
+    r = np.random.default_rng(0)
+    q = r.standard_normal((B, H, T, d), dtype=np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k = r.standard_normal((B, H, T, d), dtype=np.float32)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = r.standard_normal((B, H, T, d), dtype=np.float32)
+    la = (-np.log1p(np.exp(r.standard_normal((B, H, T, 1), dtype=np.float32) + 2))).astype(np.float32)
+    be = (1 / (1 + np.exp(-r.standard_normal((B, H, T, 1), dtype=np.float32)))).astype(np.float32)
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(os.cpu_count() or 1, omp if omp > 0 else (os.cpu_count() or 1), B * H)
+    t0 = time.perf_counter()
+    dgda_c.dgda_prefill_chunked_c(q, k, v, la, be, be, chunk_size=64, nthreads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": B * T / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"dgda_prefill B={B} H={H} T={T} d={d} (first {T} tokens of config 2), fp32, chunk 64, "
+                      f"{dt:.1f} s, oracle/dgda_chunked.c"}
+
+
+def decode_benches(dev, steps: int):
+    import torch
+    import torch.nn.functional as F
+    from maba_sparse.kernels import hip_backend as hb
+    out = {}
+    # --- config 2b: 10,000 DGDA decode steps at B=64, H=10, d=64 (bf16 q/k/v, fp32 gates/state)
+    B, H, d = 64, 10, 64
+    g = torch.Generator().manual_seed(1)
+    q = F.normalize(torch.randn(B, H, d, generator=g), dim=-1).to(dev, torch.bfloat16)
+    k = F.normalize(torch.randn(B, H, d, generator=g), dim=-1).to(dev, torch.bfloat16)
+    v = torch.randn(B, H, d, generator=g).to(dev, torch.bfloat16)
+    la = (-F.softplus(torch.randn(B, H, 1, generator=g) + 2)).to(dev).expand(B, H, d)
+    be = torch.sigmoid(torch.randn(B, H, 1, generator=g)).to(dev).expand(B, H, d)
+    S = torch.zeros(B, H, d, d, device=dev)
+    S2 = torch.zeros_like(S)
+    o = torch.empty(B, H, d, device=dev)
+    from maba_sparse import _native as N
+    lib = N.load()
+    dq, dk_, dv_, dla, db = N.desc(q), N.desc(k), N.desc(v), N.desc(la), N.desc(be)
+    dS, dS2, do = N.desc(S), N.desc(S2), N.desc(o)
+    sp = N.stream_ptr(dev)
+
+    def step():
+        rc = lib.maba_hip_dgda_step(dq, dk_, dv_, None, dla, db, db, dS, do, dS2, sp)
+        rc |= lib.maba_hip_dgda_step(dq, dk_, dv_, None, dla, db, db, dS2, do, dS, sp)
+        if rc:
+            N.check(rc, "dgda_step")
+    ms, _ = time_op(step, 5000, 100)   # 10,000 state updates
+    us = ms * 1e3 / 2
+    byts = 2 * B * H * d * d * 4 + B * H * (3 * d * 2 + 2 * 4 + d * 4)
+    out["dgda_step_B64"] = {"us_per_step": us, "gbs": byts / (us * 1e-6) / 1e9, "steps": 10000}
+    log(f"dgda_step B=64: {us:.2f} us/step")
+
+    # --- configs 3/4: 1M-token latent cache, B=8, d_c=128
+    B, L, dc, Hq, H, dh, K = 8, 1_000_000, 128, 10, 10, 64, 32
+    gen = torch.Generator(device=dev).manual_seed(2)
+    c_kv = torch.randn(B, L, dc, device=dev, generator=gen, dtype=torch.bfloat16)
+    pos = torch.randint(0, L, (B,), generator=torch.Generator().manual_seed(3))
+    for b in range(B):   # one salient token per sequence, norm x8
+        c_kv[b, pos[b]] *= 8
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    cent = hb.hip_compute_centroids(c_kv, block_size=64)
+    hca = hb.hip_hca_pool(c_kv, pool=64)
+    torch.cuda.synchronize()
+    pool_ms, _ = time_op(lambda: hb.hip_compute_centroids(c_kv, block_size=64), 10, 2)
+    out["centroid_pool_1M"] = {"us": pool_ms * 1e3, "gbs": B * L * dc * 2 / (pool_ms * 1e-3) / 1e9}
+    log(f"centroid pooling 1M: {pool_ms * 1e3:.1f} us")
+    q_idx = torch.randn(B, Hq, dc, device=dev, generator=gen, dtype=torch.bfloat16)
+    idx_ms, _ = time_op(lambda: hb.hip_index_topk_decode(q_idx, cent, lambda_dist=0.1, top_k=K), steps * 10, 5)
+    nb = cent.shape[1]
+    out["index_topk_decode_1M"] = {"us_per_step": idx_ms * 1e3, "gbs": B * nb * dc * 2 / (idx_ms * 1e-3) / 1e9}
+    log(f"indexer decode 1M: {idx_ms * 1e3:.1f} us")
+    idx = hb.hip_index_topk_decode(q_idx, cent, lambda_dist=0.1, top_k=K)        # [B, 10, 32] per head
+    q_lat = torch.randn(B, H, dc, device=dev, generator=gen) * 0.1
+    gate = torch.randn(B, 3, device=dev, generator=gen)
+    scale = 1.0 / math.sqrt(dh)
+    sa_ms, _ = time_op(lambda: hb.hip_maba_sa_decode(q_lat, c_kv, hca, idx, gate, L=L, scale=scale),
+                       steps * 10, 5)
+    nloc = 132
+    sa_bytes = B * (hca.shape[1] * dc * 2 + H * K * 64 * dc * 2 + nloc * dc * 2)
+    out["maba_sa_decode_1M"] = {"us_per_step": sa_ms * 1e3, "gbs": sa_bytes / (sa_ms * 1e-3) / 1e9,
+                                "index_sets": "per head [8,10,32]"}
+    log(f"MABA-SA decode 1M: {sa_ms * 1e3:.1f} us")
+    both = idx_ms + sa_ms
+    tot_bytes = sa_bytes + B * nb * dc * 2
+    out["indexer_plus_maba_sa_1M"] = {"us_per_step": both * 1e3, "gbs": tot_bytes / (both * 1e-3) / 1e9,
+                                      "hbm_frac": tot_bytes / (both * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del c_kv
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); multi-GPU sharding is "
+              f"described in DESIGN.md but not launched", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from maba_sparse.kernels import hip_backend as hb
+    dev = torch.device("cuda:0")
+    B, H, T, d = 4, 10, 32768, 64
+    inp = dgda_prefill_case(dev, B, H, T, d)
+    log("dgda_prefill config 2 inputs ready")
+
+    def step():
+        return hb.hip_dgda_prefill(**inp, chunk_size=64, out_dtype=torch.bfloat16, state_dtype=torch.float32,
+                                   allow_mixed_dtypes=True)
+
+    ms, wall_ms = time_op(step, args.steps, args.warmup)
+    log(f"dgda_prefill: {ms:.3f} ms/step (wall {wall_ms:.3f})")
+    tok_s = B * T / (ms * 1e-3)
+    nbytes = prefill_bytes(B, H, T, d)
+    flops = prefill_flops(B, H, T, d)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as fh:
+            traffic = json.load(fh).get("dgda_prefill_bytes_per_step")
+    res = {
+        "metric": "DGDA prefill tok/s @T=32k; MABA-SA decode us/step @1M ctx; % roofline",
+        "value": tok_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded BASELINE config 2 distributions)",
+        "config": {"workload": "dgda_prefill BASELINE config 2", "batch": B, "heads": H, "seq_len": T,
+                   "d_k": d, "d_v": d, "chunk": 64, "qkv": "bf16", "gates": "fp32 per-token (stride-0)",
+                   "state": "fp32", "out": "bf16", "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "dgda_prefill op (aggregate + scan + output launches)",
+                     "algorithmic_bytes": nbytes},
+        "mfma": {"achieved": flops / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                 "frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "algorithmic_flops": flops},
+    }
+    if not args.only_prefill and not args.skip_decode:
+        res["decode"] = decode_benches(dev, args.steps)
+    if not args.only_prefill and not args.skip_cpu:
+        log("timing the CPU baseline")
+        res["cpu_baseline"] = cpu_baseline()
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

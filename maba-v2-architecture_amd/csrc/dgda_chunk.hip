@@ -51,8 +51,14 @@ constexpr int CPS = 16;       // chunks per segment
 struct ChunkArgs {
   const uint16_t* q; int64_t qs0, qs1, qs2;   // bf16 [B,H,L,64], channel stride 1
   const uint16_t* k; int64_t ks0, ks1, ks2;
-  View4 v, gate, b, w, s0;                    // gate: log_alpha (use_log) or alpha
-  MView4 out, sf;
+  const uint16_t* vp; int64_t vs0, vs1, vs2;
+  const float* gp; int64_t gs0, gs1, gs2;    // log_alpha (use_log) or alpha, fp32, per token
+  const float* bp; int64_t bs0, bs1, bs2;     // erase gate b, fp32, per token
+  const float* wp; int64_t ws0, ws1, ws2, ws3;  // write gate w, fp32 (per token when ws3 == 0)
+  View4 s0;
+  int w_tok;                                  // write gate is per token (stride-0 channels)
+  void* op; int64_t os0, os1, os2, os3;       // output (bf16 or fp32, see OBF)
+  MView4 sf;
   float* agg;      // [BH, nseg, 64, 128]
   float* sstart;   // [BH, nseg, 64, 64]
   int H, L, nseg, nchunks, use_log, has_s0;
@@ -69,17 +75,17 @@ __device__ __forceinline__ f32x4 mma16(f32x4 c, i16x4 a, i16x4 b) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ short bf16_rn(float f) { return (short)f32_to_bf16_bits(f); }
+__device__ __forceinline__ short bf16_rn(float f) { return __builtin_bit_cast(short, (__bf16)f); }
 __device__ __forceinline__ float bf16_val(short h) { return bf16_bits_to_f32((uint16_t)h); }
 
-// Split four fp32 values into bf16 hi and lo parts (x ~= hi + lo).
+// Split four fp32 values into bf16 hi and lo parts (x ~= hi + lo), using the
+// hardware round-to-nearest-even conversion (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ void split4(f32x4 x, i16x4& hi, i16x4& lo) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const short h = bf16_rn(x[i]);
-    hi[i] = h;
-    lo[i] = bf16_rn(x[i] - bf16_val(h));
-  }
+  const bf16x4 h = __builtin_convertvector(x, bf16x4);
+  const f32x4 hf = __builtin_convertvector(h, f32x4);
+  const bf16x4 l = __builtin_convertvector(x - hf, bf16x4);
+  hi = __builtin_bit_cast(i16x4, h);
+  lo = __builtin_bit_cast(i16x4, l);
 }
 
 __device__ __forceinline__ i16x8 cat8(i16x4 a, i16x4 b) {
@@ -100,25 +106,78 @@ __device__ __forceinline__ i16x8 lds4x2(const short* base, int row, int c0, int 
   return cat8(lds4(base, row, c0, pitch), lds4(base, row, c0 + 16, pitch));
 }
 
+// Lower-triangular 64x64 matrices are stored as their 10 lower 16x16 tiles
+// (tile (I,J), J <= I, at index I(I+1)/2 + J), rows padded to TPITCH.
+__device__ __forceinline__ int tri_tile(int I, int J) { return I * (I + 1) / 2 + J; }
+constexpr int TILE_ELEMS = 16 * TPITCH;
+
+// Columns 4g..4g+3 of row r of tile (I,J).
+__device__ __forceinline__ i16x4 tri4(const short* base, int I, int J, int r, int g) {
+  return *(const i16x4*)(base + tri_tile(I, J) * TILE_ELEMS + r * TPITCH + 4 * g);
+}
+// Permuted-K operand spanning tiles (I,J) and (I,J+1).
+__device__ __forceinline__ i16x8 tri4x2(const short* base, int I, int J, int r, int g) {
+  return cat8(tri4(base, I, J, r, g), tri4(base, I, J + 1, r, g));
+}
+
+
+// T = (I + N)^-1 for the strictly lower 16x16 block N = nh + nl (bf16 hi/lo, row
+// pitch TPITCH), by forward substitution on one wave: lane c16 owns column j, and
+// the four lane groups g split each row's sum over the column range m in
+// [4g, 4g+4) (one 8-byte read per plane), combined with two shuffles.  Every lane
+// ends with the whole column; group g writes rows 4g..4g+3.
+__device__ __forceinline__ void diag_block_inverse(const short* nh, const short* nl, short* th, short* tl,
+                                                   int j, int g) {
+  float xg[4] = {0.f, 0.f, 0.f, 0.f};  // x[4g + r] of this lane's column, filled as rows complete
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float part = 0.f;
+    if (4 * g < i) {
+      const i16x4 h = *(const i16x4*)(nh + i * TPITCH + 4 * g);
+      const i16x4 l = *(const i16x4*)(nl + i * TPITCH + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float n = (4 * g + r < i) ? bf16_val(h[r]) + bf16_val(l[r]) : 0.f;  // N is strictly lower
+        part = fmaf(n, xg[r], part);
+      }
+    }
+    part += __shfl_xor(part, 16);
+    part += __shfl_xor(part, 32);
+    const float xi = ((i == j) ? 1.f : 0.f) - part;
+    xg[i & 3] = ((i >> 2) == g) ? xi : xg[i & 3];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const short h = bf16_rn(xg[r]);
+    th[(4 * g + r) * TPITCH + j] = h;
+    tl[(4 * g + r) * TPITCH + j] = bf16_rn(xg[r] - bf16_val(h));
+  }
+}
+
 // ------------------------------------------------------------------ shared memory
 
 template <bool AGG>
 struct ChunkSmem {
   short K[CH * PITCH];        // k rows (token-major)
   short KT[DK * PITCH];       // k^T (channel-major)
+  short V[CH * PITCH];        // v rows
   short Q[AGG ? 1 : CH * PITCH];
-  short LH[CH * PITCH], LL[CH * PITCH];              // L hi/lo, strictly lower
-  short AH[AGG ? 1 : CH * PITCH], AL[AGG ? 1 : CH * PITCH];  // A hi/lo, lower incl. diagonal
-  short TH[4 * 16 * TPITCH], TL[4 * 16 * TPITCH];   // (I + L_II)^-1 hi/lo
-  float LD[4][16][17];                               // diagonal blocks of L, fp32
-  float lam[CH], elam[CH], eend[CH], beta[CH];
+  short LH[10 * TILE_ELEMS], LL[10 * TILE_ELEMS];                      // L hi/lo, strictly lower
+  short AH[AGG ? 1 : 10 * TILE_ELEMS], AL[AGG ? 1 : 10 * TILE_ELEMS];  // A hi/lo, lower incl. diagonal
+  short TH[4 * TILE_ELEMS], TL[4 * TILE_ELEMS];                        // (I + L_II)^-1 hi/lo
+  float lam[CH], elam[CH], eend[CH], beta[CH], wtok[CH];
 };
 
 // ------------------------------------------------------------------ the chunk kernel
 
-template <bool AGG>
-__global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a) {
+// LDS-only barrier: waits for this wave's LDS operations, not for its outstanding
+// global loads (the next chunk's prefetch stays in flight across it).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <bool AGG, bool WTOK, bool OBF>
+__global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kernel(ChunkArgs a) {
   constexpr int NW = AGG ? 8 : 4;
+  constexpr int IPT = (CH * 8) / (NW * 64);  // 16-byte staging items per thread
   __shared__ ChunkSmem<AGG> sm;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c16 = lane & 15;
@@ -130,6 +189,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
   // Carried state slab: S[16kt + 4g + i][col0 + c16] in Sr[kt][i].
   f32x4 Sr[4];
   const int col0 = (wave & 3) * 16;
+  const int col = col0 + c16;
   const bool is_m = AGG && wave >= 4;  // pass 1: M half of [N | M]
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
@@ -138,11 +198,11 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
       const int r = 16 * kt + 4 * g + i;
       float x = 0.f;
       if (AGG) {
-        x = (is_m && r == col0 + c16) ? 1.f : 0.f;
+        x = (is_m && r == col) ? 1.f : 0.f;
       } else if (seg == 0) {
-        x = a.has_s0 ? a.s0.at(bi, hi, r, col0 + c16) : 0.f;
+        x = a.has_s0 ? a.s0.at(bi, hi, r, col) : 0.f;
       } else {
-        x = a.sstart[(((int64_t)bh * a.nseg + seg) * 64 + r) * 64 + col0 + c16];
+        x = a.sstart[(((int64_t)bh * a.nseg + seg) * 64 + r) * 64 + col];
       }
       Sr[kt][i] = x;
     }
@@ -152,32 +212,73 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
   const int c_end = min(a.nchunks, c_begin + CPS);
   const uint16_t* qb = a.q + bi * a.qs0 + hi * a.qs1;
   const uint16_t* kb = a.k + bi * a.ks0 + hi * a.ks1;
-
-  for (int c = c_begin; c < c_end; ++c) {
-    const int t0 = c * CH;
-    __syncthreads();  // previous chunk is done with the shared buffers
-    // ---- stage k (and q) rows, k^T, gates
-    for (int i = tid; i < CH * 8; i += NW * 64) {
-      const int t = i >> 3, c8 = (i & 7) * 8;
-      i16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0}, qv = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (t0 + t < a.L) {
-        kv = *(const i16x8*)(kb + (int64_t)(t0 + t) * a.ks2 + c8);
-        if (!AGG) qv = *(const i16x8*)(qb + (int64_t)(t0 + t) * a.qs2 + c8);
-      }
-      *(i16x8*)(sm.K + t * PITCH + c8) = kv;
-      if (!AGG) *(i16x8*)(sm.Q + t * PITCH + c8) = qv;
+  const uint16_t* vb = a.vp + bi * a.vs0 + hi * a.vs1;
+  const float* gb = a.gp + bi * a.gs0 + hi * a.gs1;
+  const float* bb = a.bp + bi * a.bs0 + hi * a.bs1;
+  const float* wb = a.wp + bi * a.ws0 + hi * a.ws1 + (WTOK ? 0 : (int64_t)col * a.ws3);
+  // output: this lane's column and rows 4g..4g+3 of a 16-row block, advanced per block
+  const int64_t obase = bi * a.os0 + hi * a.os1 + (int64_t)col * a.os3;
+  int64_t orow[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sm.KT[(c8 + j) * PITCH + t] = kv[j];
+  for (int i = 0; i < 4; ++i) orow[i] = (int64_t)(4 * g + i) * a.os2;
+
+  // ---- register prefetch of one chunk's k, v, q rows and per-token gates
+  i16x8 pk[IPT], pv[IPT], pq[IPT];
+  float pla = 0.f, pbe = 0.f, pwt = 0.f;
+  auto prefetch = [&](int cc) {
+    const int t0 = cc * CH;
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      const int i = tid + it * NW * 64;
+      const int t = i >> 3, c8 = (i & 7) * 8;
+      const i16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+      pk[it] = z; pv[it] = z; pq[it] = z;
+      if (t0 + t < a.L) {
+        pk[it] = *(const i16x8*)(kb + (int64_t)(t0 + t) * a.ks2 + c8);
+        pv[it] = *(const i16x8*)(vb + (int64_t)(t0 + t) * a.vs2 + c8);
+        if (!AGG) pq[it] = *(const i16x8*)(qb + (int64_t)(t0 + t) * a.qs2 + c8);
+      }
     }
     if (tid < CH) {
       const int t = t0 + tid;
-      float la = 0.f, be = 0.f;
+      pla = 0.f; pbe = 0.f; pwt = 0.f;
       if (t < a.L) {
-        const float gv = a.gate.at(bi, hi, t, 0);
-        la = a.use_log ? gv : __logf(fmaxf(gv, 1e-20f));
-        la = fminf(la, 0.f);
-        be = a.b.at(bi, hi, t, 0);
+        pla = gb[(int64_t)t * a.gs2];
+        pbe = bb[(int64_t)t * a.bs2];
+        if (WTOK) pwt = wb[(int64_t)t * a.ws2];
       }
+    }
+  };
+  prefetch(c_begin);
+
+  for (int c = c_begin; c < c_end; ++c) {
+    const int t0 = c * CH;
+    // per-channel write gate: this wave's 16 values, fetched before the staging barrier
+    f32x4 wreg[4];
+    if (!WTOK && !is_m) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = t0 + 16 * tt + 4 * g + i;
+          wreg[tt][i] = t < a.L ? wb[(int64_t)t * a.ws2] : 0.f;
+        }
+    }
+    lds_barrier();  // previous chunk is done with the shared buffers
+    // ---- stage the prefetched rows (k, v, q, k^T) and gates, then prefetch the next chunk
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      const int i = tid + it * NW * 64;
+      const int t = i >> 3, c8 = (i & 7) * 8;
+      *(i16x8*)(sm.K + t * PITCH + c8) = pk[it];
+      *(i16x8*)(sm.V + t * PITCH + c8) = pv[it];
+      if (!AGG) *(i16x8*)(sm.Q + t * PITCH + c8) = pq[it];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sm.KT[(c8 + j) * PITCH + t] = pk[it][j];
+    }
+    if (tid < CH) {
+      float la = a.use_log ? pla : __logf(fmaxf(pla, 1e-20f));
+      la = (t0 + tid < a.L) ? fminf(la, 0.f) : 0.f;
       // inclusive prefix sum of the log decay across the wave
       float s = la;
 #pragma unroll
@@ -189,83 +290,76 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
       sm.lam[tid] = s;
       sm.elam[tid] = __expf(s);
       sm.eend[tid] = __expf(last - s);
-      sm.beta[tid] = be;
+      sm.beta[tid] = pbe;
+      sm.wtok[tid] = pwt;
     }
-    __syncthreads();
+    if (c + 1 < c_end) prefetch(c + 1);
+    lds_barrier();
 
     // ---- L = beta_i (k k^T) decay (strict lower) and A = (q k^T) decay (lower)
     // Tile (I,J) is computed as D = k_J x k_I^T (or k_J x q_I^T) so each lane holds
-    // row i = 16I + c16 and columns 16J + 4g..+3: a contiguous 8-byte store.
+    // row 16I + c16 and columns 16J + 4g..+3: one 8-byte store into the tile.
+    auto build_tile = [&](int tix, bool isA) {
+      int tt = tix, I = 0;
+      while (tt > I) { tt -= I + 1; ++I; }
+      const int J = tt;  // J <= I
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const short* Bsrc = isA ? sm.Q : sm.K;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const i16x8 av = lds8(sm.K, 16 * J + c16, 32 * p + 8 * g, PITCH);
+        const i16x8 bv = lds8(Bsrc, 16 * I + c16, 32 * p + 8 * g, PITCH);
+        acc = mma32(acc, av, bv);
+      }
+      const int i = 16 * I + c16;
+      const float li = sm.lam[i];
+      const float be = sm.beta[i];
+      f32x4 val;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * J + 4 * g + r;
+        const float x = acc[r] * __expf(fminf(li - sm.lam[j], 0.f));
+        val[r] = isA ? ((j <= i) ? x : 0.f) : ((j < i) ? x * be : 0.f);
+      }
+      i16x4 h, l;
+      split4(val, h, l);
+      const int off = tri_tile(I, J) * TILE_ELEMS + c16 * TPITCH + 4 * g;
+      *(i16x4*)((isA ? sm.AH : sm.LH) + off) = h;
+      *(i16x4*)((isA ? sm.AL : sm.LL) + off) = l;
+    };
     {
-      constexpr int NT = AGG ? 10 : 20;
-      for (int tix = wave; tix < NT; tix += NW) {
-        const bool isA = tix >= 10;
-        int tt = isA ? tix - 10 : tix;
-        int I = 0;
-        while (tt > I) { tt -= I + 1; ++I; }
-        const int J = tt;  // J <= I
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const short* Bsrc = isA ? sm.Q : sm.K;
+      constexpr int NTILE = AGG ? 10 : 20;
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const i16x8 av = lds8(sm.K, 16 * J + c16, 32 * p + 8 * g, PITCH);
-          const i16x8 bv = lds8(Bsrc, 16 * I + c16, 32 * p + 8 * g, PITCH);
-          acc = mma32(acc, av, bv);
-        }
-        const int i = 16 * I + c16;
-        const float li = sm.lam[i];
-        const float be = sm.beta[i];
-        i16x4 h, l;
-        f32x4 val;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * J + 4 * g + r;
-          const float dec = __expf(fminf(li - sm.lam[j], 0.f));
-          float x = acc[r] * dec;
-          if (isA) {
-            x = (j <= i) ? x : 0.f;
-          } else {
-            x = (j < i) ? x * be : 0.f;
-          }
-          val[r] = x;
-        }
-        split4(val, h, l);
-        short* dh = isA ? sm.AH : sm.LH;
-        short* dl = isA ? sm.AL : sm.LL;
-        *(i16x4*)(dh + i * PITCH + 16 * J + 4 * g) = h;
-        *(i16x4*)(dl + i * PITCH + 16 * J + 4 * g) = l;
-        if (!isA && I == J) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sm.LD[I][c16][4 * g + r] = bf16_val(h[r]) + bf16_val(l[r]);
-        }
+      for (int k = 0; k < (NTILE + NW - 1) / NW; ++k) {
+        const int tix = wave + k * NW;
+        if (tix < NTILE) build_tile(tix % 10, tix >= 10);
       }
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ---- T_II = (I + L_II)^-1 by forward substitution, one column per lane.
-    if (wave < 4 && lane < 16) {
-      const int I = wave, j = lane;
-      float x[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float s = (i == j) ? 1.f : 0.f;
-#pragma unroll
-        for (int m = 0; m < i; ++m) s = fmaf(-sm.LD[I][i][m], x[m], s);
-        x[i] = s;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const short h = bf16_rn(x[i]);
-        sm.TH[(I * 16 + i) * TPITCH + j] = h;
-        sm.TL[(I * 16 + i) * TPITCH + j] = bf16_rn(x[i] - bf16_val(h));
-      }
-    }
-    __syncthreads();
-
-    // ---- per-wave column slab: v_e = w*v - diag(beta e^Lam) (k S)
+    // ---- T_II = (I + L_II)^-1 (waves 0..3, block I = wave), overlapped with the
+    // state-dependent products that do not need it: v_e = w*v - diag(beta e^Lam)(k S)
+    // and q S.
+    if (wave < 4)
+      diag_block_inverse(sm.LH + tri_tile(wave, wave) * TILE_ELEMS, sm.LL + tri_tile(wave, wave) * TILE_ELEMS,
+                         sm.TH + wave * TILE_ELEMS, sm.TL + wave * TILE_ELEMS, c16, g);
     i16x4 Sh[4], Sl[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
+    f32x4 qsr[4];
+    if (!AGG) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        f32x4 qs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const i16x8 av = lds4x2(sm.Q, 16 * I + c16, 32 * p + 4 * g, PITCH);
+          qs = mma32(qs, av, cat8(Sh[2 * p], Sh[2 * p + 1]));
+          qs = mma32(qs, av, cat8(Sl[2 * p], Sl[2 * p + 1]));
+        }
+        qsr[I] = qs;
+      }
+    }
     f32x4 u[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
@@ -279,12 +373,15 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tl = 16 * tt + 4 * g + i;
-        const int t = t0 + tl;
         float y = 0.f;
-        if (!is_m && t < a.L) y = a.w.at(bi, hi, t, col0 + c16) * a.v.at(bi, hi, t, col0 + c16);
+        if (!is_m) {
+          const float wv = WTOK ? sm.wtok[tl] : wreg[tt][i];
+          y = wv * bf16_val(sm.V[tl * PITCH + col]);
+        }
         u[tt][i] = y - sm.beta[tl] * sm.elam[tl] * acc[i];
       }
     }
+    lds_barrier();
 
     // ---- blocked forward substitution, u_I = T_II (v_e_I - sum_{J<I} L_IJ u_J)
     i16x4 uh[4], ul[4];
@@ -294,26 +391,26 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
       if (I >= 1) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         if (I >= 2) {  // J = 0,1 as one K = 32 step
-          const int row = 16 * I + c16;
-          const i16x8 ah = lds4x2(sm.LH, row, 4 * g, PITCH), al = lds4x2(sm.LL, row, 4 * g, PITCH);
+          const i16x8 ah = tri4x2(sm.LH, I, 0, c16, g), al = tri4x2(sm.LL, I, 0, c16, g);
           const i16x8 bh8 = cat8(uh[0], uh[1]), bl8 = cat8(ul[0], ul[1]);
           acc = mma32(acc, ah, bh8);
           acc = mma32(acc, ah, bl8);
           acc = mma32(acc, al, bh8);
         }
-        if (I == 1 || I == 3) {  // the remaining single 16-wide step J = I-1 (I=3: J=2)
-          const int J = I == 1 ? 0 : 2;
-          const int row = 16 * I + c16;
-          const i16x4 ah = lds4(sm.LH, row, 16 * J + 4 * g, PITCH), al = lds4(sm.LL, row, 16 * J + 4 * g, PITCH);
-          acc = mma16(acc, ah, uh[J]);
-          acc = mma16(acc, ah, ul[J]);
-          acc = mma16(acc, al, uh[J]);
+        f32x4 acc16 = {0.f, 0.f, 0.f, 0.f};  // K=16 products never accumulate onto a K=32 result
+        if (I == 1 || I == 3) {  // the remaining 16-wide step J = I-1
+          const int J = I - 1;
+          const i16x4 ah = tri4(sm.LH, I, J, c16, g), al = tri4(sm.LL, I, J, c16, g);
+          acc16 = mma16(acc16, ah, uh[J]);
+          acc16 = mma16(acc16, ah, ul[J]);
+          acc16 = mma16(acc16, al, uh[J]);
         }
-        rhs = rhs - acc;
+        rhs = rhs - acc - acc16;
       }
       i16x4 rh, rl;
       split4(rhs, rh, rl);
-      const i16x4 th = lds4(sm.TH, I * 16 + c16, 4 * g, TPITCH), tl = lds4(sm.TL, I * 16 + c16, 4 * g, TPITCH);
+      const i16x4 th = lds4(sm.TH + I * TILE_ELEMS, c16, 4 * g, TPITCH);
+      const i16x4 tl = lds4(sm.TL + I * TILE_ELEMS, c16, 4 * g, TPITCH);
       f32x4 x = {0.f, 0.f, 0.f, 0.f};
       x = mma16(x, th, rh);
       x = mma16(x, th, rl);
@@ -326,36 +423,35 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
     if (!AGG) {
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
-        f32x4 qs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const i16x8 av = lds4x2(sm.Q, 16 * I + c16, 32 * p + 4 * g, PITCH);
-          qs = mma32(qs, av, cat8(Sh[2 * p], Sh[2 * p + 1]));
-          qs = mma32(qs, av, cat8(Sl[2 * p], Sl[2 * p + 1]));
-        }
+        const f32x4 qs = qsr[I];
         f32x4 au = {0.f, 0.f, 0.f, 0.f};
-        const int row = 16 * I + c16;
 #pragma unroll
         for (int P = 0; P < 2; ++P) {  // J pairs (0,1), (2,3)
           if (2 * P + 1 <= I) {
-            const i16x8 ah = lds4x2(sm.AH, row, 32 * P + 4 * g, PITCH), al = lds4x2(sm.AL, row, 32 * P + 4 * g, PITCH);
+            const i16x8 ah = tri4x2(sm.AH, I, 2 * P, c16, g), al = tri4x2(sm.AL, I, 2 * P, c16, g);
             const i16x8 bh8 = cat8(uh[2 * P], uh[2 * P + 1]), bl8 = cat8(ul[2 * P], ul[2 * P + 1]);
             au = mma32(au, ah, bh8);
             au = mma32(au, ah, bl8);
             au = mma32(au, al, bh8);
           }
         }
+        f32x4 au16 = {0.f, 0.f, 0.f, 0.f};  // separate K=16 accumulator (see the solve)
         if ((I & 1) == 0) {  // single J = I
-          const i16x4 ah = lds4(sm.AH, row, 16 * I + 4 * g, PITCH), al = lds4(sm.AL, row, 16 * I + 4 * g, PITCH);
-          au = mma16(au, ah, uh[I]);
-          au = mma16(au, ah, ul[I]);
-          au = mma16(au, al, uh[I]);
+          const i16x4 ah = tri4(sm.AH, I, I, c16, g), al = tri4(sm.AL, I, I, c16, g);
+          au16 = mma16(au16, ah, uh[I]);
+          au16 = mma16(au16, ah, ul[I]);
+          au16 = mma16(au16, al, uh[I]);
         }
+        au = au + au16;
+        const int64_t oblk = obase + (int64_t)(t0 + 16 * I) * a.os2;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int tl = 16 * I + 4 * g + i;
-          const int t = t0 + tl;
-          if (t < a.L) a.out.put(bi, hi, t, col0 + c16, sm.elam[tl] * qs[i] + au[i]);
+          if (t0 + tl < a.L) {
+            const float ov = sm.elam[tl] * qs[i] + au[i];
+            if (OBF) ((short*)a.op)[oblk + orow[i]] = bf16_rn(ov);
+            else ((float*)a.op)[oblk + orow[i]] = ov;
+          }
         }
       }
     }
@@ -386,7 +482,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
   // ---- segment results
   if (AGG) {
     float* dst = a.agg + ((int64_t)bh * a.nseg + seg) * 64 * 128;
-    const int cc = (is_m ? 64 : 0) + col0 + c16;
+    const int cc = (is_m ? 64 : 0) + col;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -395,7 +491,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256) void dgda_chunk_kernel(ChunkArgs a
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a.sf.put(bi, hi, 16 * kt + 4 * g + i, col0 + c16, Sr[kt][i]);
+      for (int i = 0; i < 4; ++i) a.sf.put(bi, hi, 16 * kt + 4 * g + i, col, Sr[kt][i]);
   }
 }
 
@@ -456,12 +552,13 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 bool dgda_chunk_supported(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                           const maba_tensor* gate, const maba_tensor* b) {
   if (!q || !k || !v || !gate || !b) return false;
-  if (q->dtype != MABA_BF16 || k->dtype != MABA_BF16) return false;
+  if (q->dtype != MABA_BF16 || k->dtype != MABA_BF16 || v->dtype != MABA_BF16) return false;
   if (q->shape[3] != DK || v->shape[3] != DK) return false;
-  if (q->stride[3] != 1 || k->stride[3] != 1) return false;
+  if (q->stride[3] != 1 || k->stride[3] != 1 || v->stride[3] != 1) return false;
   if (gate->stride[3] != 0 || b->stride[3] != 0) return false;  // per-token decay and erase gate
+  if (gate->dtype != MABA_F32 || b->dtype != MABA_F32) return false;
   if (q->shape[2] > (int64_t)1 << 30) return false;
-  for (const maba_tensor* t : {q, k}) {
+  for (const maba_tensor* t : {q, k, v}) {
     if (!aligned16(t->data)) return false;
     for (int d = 0; d < 3; ++d)
       if (t->shape[d] > 1 && (t->stride[d] % 8) != 0) return false;
@@ -489,8 +586,15 @@ int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_ten
   ChunkArgs a;
   a.q = (const uint16_t*)q->data; a.qs0 = q->stride[0]; a.qs1 = q->stride[1]; a.qs2 = q->stride[2];
   a.k = (const uint16_t*)k->data; a.ks0 = k->stride[0]; a.ks1 = k->stride[1]; a.ks2 = k->stride[2];
-  a.v = view4(v); a.gate = view4(gate); a.b = view4(b); a.w = view4(w); a.s0 = view4(s0);
-  a.out = mview4(out); a.sf = mview4(sf);
+  a.vp = (const uint16_t*)v->data; a.vs0 = v->stride[0]; a.vs1 = v->stride[1]; a.vs2 = v->stride[2];
+  a.gp = (const float*)gate->data; a.gs0 = gate->stride[0]; a.gs1 = gate->stride[1]; a.gs2 = gate->stride[2];
+  a.bp = (const float*)b->data; a.bs0 = b->stride[0]; a.bs1 = b->stride[1]; a.bs2 = b->stride[2];
+  a.wp = (const float*)w->data; a.ws0 = w->stride[0]; a.ws1 = w->stride[1]; a.ws2 = w->stride[2];
+  a.ws3 = w->stride[3];
+  a.s0 = view4(s0);
+  a.w_tok = w->stride[3] == 0;
+  a.op = out->data; a.os0 = out->stride[0]; a.os1 = out->stride[1]; a.os2 = out->stride[2]; a.os3 = out->stride[3];
+  a.sf = mview4(sf);
   a.H = (int)H; a.L = (int)L;
   a.nchunks = (int)ceil_div(L, CH);
   a.nseg = nseg_for(L);
@@ -499,15 +603,21 @@ int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_ten
   if (ws_bytes < need) return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace too small");
   a.agg = (float*)ws;
   a.sstart = a.agg + BH * a.nseg * 64 * 128;
+  const dim3 grid((unsigned)(BH * a.nseg));
   if (a.nseg > 1) {
-    hipLaunchKernelGGL(dgda_chunk_kernel<true>, dim3((unsigned)(BH * a.nseg)), dim3(512), 0, stream, a);
+    if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<true, true, true>), grid, dim3(512), 0, stream, a);
+    else hipLaunchKernelGGL((dgda_chunk_kernel<true, false, true>), grid, dim3(512), 0, stream, a);
     int rc = check_launch("dgda_prefill/aggregate");
     if (rc) return rc;
     hipLaunchKernelGGL(dgda_segment_scan_kernel, dim3((unsigned)(BH * 4)), dim3(64), 0, stream, a);
     rc = check_launch("dgda_prefill/scan");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(dgda_chunk_kernel<false>, dim3((unsigned)(BH * a.nseg)), dim3(256), 0, stream, a);
+  const bool obf = out->dtype == MABA_BF16;
+  if (a.w_tok && obf) hipLaunchKernelGGL((dgda_chunk_kernel<false, true, true>), grid, dim3(256), 0, stream, a);
+  else if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<false, true, false>), grid, dim3(256), 0, stream, a);
+  else if (obf) hipLaunchKernelGGL((dgda_chunk_kernel<false, false, true>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((dgda_chunk_kernel<false, false, false>), grid, dim3(256), 0, stream, a);
   return check_launch("dgda_prefill/output");
 }
 
