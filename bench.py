@@ -53,6 +53,7 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true", help="do not time the CPU baseline")
     ap.add_argument("--skip-decode", action="store_true", help="do not run the decode benchmarks")
     ap.add_argument("--only-prefill", action="store_true", help="time only the DGDA prefill step (for profiling)")
+    ap.add_argument("--only-decode", action="store_true", help="run only the decode benchmarks (for profiling)")
     return ap.parse_args()
 
 
@@ -200,6 +201,9 @@ def main():
     import torch
     from maba_sparse.kernels import hip_backend as hb
     dev = torch.device("cuda:0")
+    if args.only_decode:
+        print(json.dumps({"decode": decode_benches(dev, args.steps)}), flush=True)
+        return
     B, H, T, d = 4, 10, 32768, 64
     inp = dgda_prefill_case(dev, B, H, T, d)
     log("dgda_prefill config 2 inputs ready")

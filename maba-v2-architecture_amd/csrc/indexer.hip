@@ -18,6 +18,7 @@ namespace maba {
 
 constexpr int IDX_MAX_HEADS = 16;   // query heads per decode launch
 constexpr int IDX_MAX_D = 256;      // channels
+constexpr int DEC_TPW = 2;          // 64-centroid tiles per wave (MFMA decode path)
 
 struct DecArgs {
   const void* q; int qdt; int64_t qsb, qsh, qsd;
@@ -103,6 +104,93 @@ __global__ __launch_bounds__(64) void index_decode_merge_kernel(const key64* ws,
   if (lane < ak) out[bi * osb + h * osh + lane * osk] = (int64_t)key_index(m);
 }
 
+// Decode scoring on MFMA (bf16 q and centroids, d a multiple of 32, <= 256).
+// Each wave scores TPW consecutive 64-centroid tiles against all query heads as
+// D = C x Q^T with v_mfma_f32_16x16x32_bf16: the A operand is read straight from
+// global memory (lane = centroid row, 16 contiguous bytes), the B operand (the
+// queries, heads padded to 16) stays in registers.  Scores go through a per-wave
+// LDS tile so that, per head, each lane holds one centroid's score for the wave
+// top-k merge.  bf16 x bf16 products are exact and accumulate in fp32.
+typedef __attribute__((ext_vector_type(8))) short i16x8_t;
+
+struct DecMfmaArgs {
+  const uint16_t* q; int64_t qsb, qsh;   // [B, Hq, d] bf16, channel stride 1
+  const uint16_t* c; int64_t csb, csn;   // [B, nb, d] bf16, channel stride 1
+  int64_t nb;
+  int d, Hq, K, nsplit, tpw;
+  float scale, lam;
+  key64* ws;
+  float* scores; int64_t ssb, ssh, ssn;
+};
+
+template <int NP>  // NP = d / 32
+__global__ __launch_bounds__(256) void index_decode_mfma_kernel(DecMfmaArgs a) {
+  __shared__ float s_tile[4][16][65];
+  __shared__ key64 s_lists[4][64];
+  const int split = blockIdx.x;
+  const int64_t bi = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  // B operand: Q^T, lane (head c16, group g) holds dims 32p + 8g .. +7
+  i16x8_t qb[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    i16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (c16 < a.Hq) z = *(const i16x8_t*)(a.q + bi * a.qsb + c16 * a.qsh + 32 * p + 8 * g);
+    qb[p] = z;
+  }
+  key64 list[IDX_MAX_HEADS];
+#pragma unroll
+  for (int h = 0; h < IDX_MAX_HEADS; ++h) list[h] = KEY_NONE;
+  const uint16_t* cb = a.c + bi * a.csb;
+  const int64_t tile0 = ((int64_t)split * 4 + wave) * a.tpw;
+  for (int tt = 0; tt < a.tpw; ++tt) {
+    const int64_t n0 = (tile0 + tt) * 64;
+    if (n0 >= a.nb) break;
+    // scores for 4 row blocks of 16 centroids
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const int64_t n = n0 + 16 * rb + c16;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        i16x8_t av = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (n < a.nb) av = *(const i16x8_t*)(cb + n * a.csn + 32 * p + 8 * g);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, qb[p]),
+                                                      acc, 0, 0, 0);
+      }
+      // lane holds D[centroid 16rb + 4g + i][head c16]
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_tile[wave][c16][16 * rb + 4 * g + i] = acc[i];
+    }
+    // per head: lane = centroid
+    const int64_t n = n0 + lane;
+    const bool valid = n < a.nb;
+    const float pen = valid ? a.lam * log1pf((float)(a.nb - 1 - n)) : 0.f;
+#pragma unroll
+    for (int h = 0; h < IDX_MAX_HEADS; ++h) {
+      if (h < a.Hq) {
+        const float sc = s_tile[wave][h][lane] * a.scale - pen;
+        if (a.scores && valid) a.scores[bi * a.ssb + h * a.ssh + n * a.ssn] = sc;
+        list[h] = wave_merge_topk(list[h], valid ? make_key(sc, (uint32_t)n) : KEY_NONE, a.K);
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < IDX_MAX_HEADS; ++h) {
+    if (h < a.Hq) {
+      s_lists[wave][lane] = list[h];
+      __syncthreads();
+      if (wave == 0) {
+        key64 m = s_lists[0][lane];
+        for (int w = 1; w < 4; ++w) m = wave_merge_topk(m, s_lists[w][lane], a.K);
+        a.ws[(((int64_t)bi * a.nsplit + split) * a.Hq + h) * 64 + lane] = m;
+      }
+      __syncthreads();
+    }
+  }
+}
+
 // Prefill: one wave per query row; lane = centroid within a 64-wide tile.
 struct PreArgs {
   const void* q; int qdt; int64_t qsb, qsl, qsd;
@@ -155,7 +243,7 @@ using namespace maba;
 extern "C" size_t maba_hip_index_topk_decode_workspace_size(int64_t B, int64_t Hq, int64_t nb, int top_k) {
   (void)top_k;
   const int64_t tiles = ceil_div(nb, 64);
-  const int64_t nsplit = ceil_div(tiles, 4);
+  const int64_t nsplit = ceil_div(tiles, 4);  // scalar path (the MFMA path uses fewer splits)
   return (size_t)(B * (nsplit > 0 ? nsplit : 1) * Hq * 64) * sizeof(key64);
 }
 
@@ -186,6 +274,43 @@ extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tenso
   const size_t need = maba_hip_index_topk_decode_workspace_size(B, Hq, nb, top_k);
   if (!workspace || workspace_bytes < need)
     return fail(MABA_ERR_WORKSPACE, "index_topk_decode: workspace of %zu bytes required", need);
+  hipStream_t s = (hipStream_t)stream;
+  const bool mfma_ok = q->dtype == MABA_BF16 && centroids->dtype == MABA_BF16 && q->stride[2] == 1 &&
+                       centroids->stride[2] == 1 && d % 32 == 0 && d <= 256 && (uintptr_t)q->data % 16 == 0 &&
+                       (uintptr_t)centroids->data % 16 == 0 && q->stride[0] % 8 == 0 && q->stride[1] % 8 == 0 &&
+                       centroids->stride[0] % 8 == 0 && centroids->stride[1] % 8 == 0;
+  if (mfma_ok) {
+    DecMfmaArgs m;
+    m.q = (const uint16_t*)q->data; m.qsb = q->stride[0]; m.qsh = q->stride[1];
+    m.c = (const uint16_t*)centroids->data; m.csb = centroids->stride[0]; m.csn = centroids->stride[1];
+    m.nb = nb; m.d = (int)d; m.Hq = (int)Hq; m.K = top_k;
+    m.tpw = DEC_TPW;
+    m.nsplit = (int)ceil_div(ceil_div(nb, 64), 4 * DEC_TPW);
+    m.scale = 1.0f / sqrtf((float)d);
+    m.lam = lambda_dist;
+    m.ws = (key64*)workspace;
+    m.scores = out_scores ? (float*)out_scores->data : nullptr;
+    m.ssb = out_scores ? out_scores->stride[0] : 0;
+    m.ssh = out_scores ? out_scores->stride[1] : 0;
+    m.ssn = out_scores ? out_scores->stride[2] : 0;
+    const dim3 grid((unsigned)m.nsplit, (unsigned)B);
+    switch (d / 32) {
+      case 1: hipLaunchKernelGGL(index_decode_mfma_kernel<1>, grid, dim3(256), 0, s, m); break;
+      case 2: hipLaunchKernelGGL(index_decode_mfma_kernel<2>, grid, dim3(256), 0, s, m); break;
+      case 3: hipLaunchKernelGGL(index_decode_mfma_kernel<3>, grid, dim3(256), 0, s, m); break;
+      case 4: hipLaunchKernelGGL(index_decode_mfma_kernel<4>, grid, dim3(256), 0, s, m); break;
+      case 5: hipLaunchKernelGGL(index_decode_mfma_kernel<5>, grid, dim3(256), 0, s, m); break;
+      case 6: hipLaunchKernelGGL(index_decode_mfma_kernel<6>, grid, dim3(256), 0, s, m); break;
+      case 7: hipLaunchKernelGGL(index_decode_mfma_kernel<7>, grid, dim3(256), 0, s, m); break;
+      default: hipLaunchKernelGGL(index_decode_mfma_kernel<8>, grid, dim3(256), 0, s, m); break;
+    }
+    int rc = check_launch("index_topk_decode/score");
+    if (rc) return rc;
+    hipLaunchKernelGGL(index_decode_merge_kernel, dim3((unsigned)(B * Hq)), dim3(64), 0, s, m.ws, m.nsplit,
+                       (int)Hq, top_k, (int)ak, (int64_t*)out_idx->data, out_idx->stride[0],
+                       out_idx->stride[1], out_idx->stride[2]);
+    return check_launch("index_topk_decode/merge");
+  }
   DecArgs a;
   a.q = q->data; a.qdt = q->dtype; a.qsb = q->stride[0]; a.qsh = q->stride[1]; a.qsd = q->stride[2];
   a.c = centroids->data; a.cdt = centroids->dtype;
@@ -200,7 +325,6 @@ extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tenso
   a.ssb = out_scores ? out_scores->stride[0] : 0;
   a.ssh = out_scores ? out_scores->stride[1] : 0;
   a.ssn = out_scores ? out_scores->stride[2] : 0;
-  hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(index_decode_score_kernel, dim3((unsigned)a.nsplit, (unsigned)B), dim3(256), 0, s, a);
   int rc = check_launch("index_topk_decode/score");
   if (rc) return rc;

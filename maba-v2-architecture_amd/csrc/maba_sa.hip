@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void maba_sa_tile_kernel(SaArgs a) {
 }
 
 // One workgroup per (b, h): merge partials per stream, apply the gate.
-__global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a) {
+__global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a, int p1, int p2, int p3) {
   const int64_t b = blockIdx.x / a.H;
   const int h = blockIdx.x % a.H;
   const int dc = a.dc;
@@ -161,8 +161,9 @@ __global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a) {
   z0 = __expf(z0 - gm); z1 = __expf(z1 - gm); z2 = __expf(z2 - gm);
   const float gi = 1.f / (z0 + z1 + z2);
   const float g[3] = {z0 * gi, z1 * gi, z2 * gi};
-  const int t_begin[3] = {0, a.t_loc, a.t_loc + a.t_sp};
-  const int t_end[3] = {a.t_loc, a.t_loc + a.t_sp, a.t_loc + a.t_sp + a.t_hca};
+  // partials [0, p1) local, [p1, p2) sparse, [p2, p3) HCA
+  const int t_begin[3] = {0, p1, p2};
+  const int t_end[3] = {p1, p2, p3};
   for (int d = threadIdx.x; d < dc; d += blockDim.x) {
     float res = 0.f;
     for (int st = 0; st < 3; ++st) {
@@ -190,6 +191,204 @@ __global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a) {
       res = fmaf(g[st], zs, res);
     }
     a.out[b * a.osb + h * a.osh + d * a.osd] = res;
+  }
+}
+
+// ------------------------------------------------------------------ MFMA path
+// Used when c_kv / hca are bf16 rows with unit channel stride, d_c <= 128 (a
+// multiple of 32) and H <= 16.  Every stream of every batch element is cut into
+// segments of up to SA_TPS 64-key tiles; one wave runs one segment with an online
+// softmax and writes one partial (max, sum, weighted latent sum) per head.
+//   scores  D[key][head] = C Q^T   (A: key rows straight from global memory,
+//                                   B: the queries, bf16 hi + lo, in registers)
+//   values  Z[dim][head] += C^T P  (A: the tile transposed into per-wave LDS,
+//                                   B: the probabilities, bf16 hi + lo, used in
+//                                   place from the score accumulators)
+typedef __attribute__((ext_vector_type(8))) short s16x8;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+constexpr int SA_TPS = 8;        // tiles per segment
+constexpr int SA_CTP = 72;       // row pitch (bf16) of the transposed tile
+
+struct SaSeg {
+  int stream, head_only;
+  int64_t t_begin, t_end;  // tile range within the stream (sparse: index slots)
+  int hs;                  // sparse index row
+};
+
+__device__ __forceinline__ SaSeg sa_segment(const SaArgs& a, int sid, int s_sp1) {
+  SaSeg g;
+  g.head_only = -1;
+  g.hs = 0;
+  const int s_sp = (a.Hi == 1) ? s_sp1 : a.H * s_sp1;
+  if (sid == 0) {
+    g.stream = 0; g.t_begin = 0; g.t_end = a.t_loc;
+  } else if (sid < 1 + s_sp) {
+    const int r = sid - 1;
+    g.stream = 1;
+    g.hs = (a.Hi == 1) ? 0 : r / s_sp1;
+    const int rr = (a.Hi == 1) ? r : r % s_sp1;
+    if (a.Hi > 1) g.head_only = g.hs;
+    g.t_begin = (int64_t)rr * SA_TPS;
+    g.t_end = min((int64_t)a.K, g.t_begin + SA_TPS);
+  } else {
+    const int r = sid - 1 - s_sp;
+    g.stream = 2;
+    g.t_begin = (int64_t)r * SA_TPS;
+    g.t_end = min((int64_t)a.t_hca, g.t_begin + SA_TPS);
+  }
+  return g;
+}
+
+template <int NP>  // d_c = 32 * NP
+__global__ __launch_bounds__(256) void maba_sa_mfma_kernel(SaArgs a, int nseg, int s_sp1) {
+  constexpr int DC = 32 * NP;
+  __shared__ short s_ct[4][DC * SA_CTP];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t b = blockIdx.y;
+  const int sid = blockIdx.x * 4 + wave;
+  if (sid >= nseg) return;
+  const SaSeg sg = sa_segment(a, sid, s_sp1);
+  short* ct = s_ct[wave];
+
+  // queries (B operand of the scores): head c16, dims 32p + 8g .. +7, split hi/lo
+  s16x8 qh[NP], ql[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = (c16 < a.H) ? load_elem(a.q, a.qdt, b * a.qsb + c16 * a.qsh + (32 * p + 8 * g + j) * a.qsd) : 0.f;
+      const short h = __builtin_bit_cast(short, (__bf16)x);
+      qh[p][j] = h;
+      ql[p][j] = __builtin_bit_cast(short, (__bf16)(x - bf16_bits_to_f32((uint16_t)h)));
+    }
+  }
+  const bool head_on = c16 < a.H && (sg.head_only < 0 || sg.head_only == c16);
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 z[DC / 16];
+#pragma unroll
+  for (int dt = 0; dt < DC / 16; ++dt) z[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t tix = sg.t_begin; tix < sg.t_end; ++tix) {
+    // key rows of this tile: row r = 16 rb + c16
+    const uint16_t* base;
+    int64_t rstride;
+    int64_t pos[4];
+    bool ok[4];
+    if (sg.stream == 2) {
+      base = (const uint16_t*)a.hca + b * a.hsb;
+      rstride = a.hsn;
+    } else {
+      base = (const uint16_t*)a.c + b * a.csb;
+      rstride = a.csl;
+    }
+    int64_t blk = 0;
+    if (sg.stream == 1) blk = a.idx[b * a.isb + sg.hs * a.ish + tix * a.isk];
+    const int64_t nblk = (a.L + a.bs - 1) / a.bs;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const int j = 16 * rb + c16;
+      if (sg.stream == 0) {
+        const int64_t li = tix * 64 + j;
+        ok[rb] = li < a.nloc;
+        pos[rb] = li < a.ns ? li : a.loc_start + (li - a.ns);
+      } else if (sg.stream == 1) {
+        pos[rb] = blk * a.bs + j;
+        ok[rb] = blk >= 0 && blk < nblk && j < a.bs && pos[rb] < a.L;
+      } else {
+        pos[rb] = tix * 64 + j;
+        ok[rb] = pos[rb] < a.nc;
+      }
+    }
+    f32x4 sc[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        s16x8 cv = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (ok[rb]) cv = *(const s16x8*)(base + pos[rb] * rstride + 32 * p + 8 * g);
+        // transposed copy for the value product: ct[dim][key]
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) ct[(32 * p + 8 * g + jj) * SA_CTP + 16 * rb + c16] = cv[jj];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv), __builtin_bit_cast(bf16x8, qh[p]),
+                                                      acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv), __builtin_bit_cast(bf16x8, ql[p]),
+                                                      acc, 0, 0, 0);
+      }
+      sc[rb] = acc;
+    }
+    // lane (head c16, group g) holds scores of keys 16 rb + 4g + i
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // key row 16 rb + 4g + i is valid iff the loading lane c16' = 4g + i had ok[rb]
+        const bool kv = __shfl(ok[rb] ? 1 : 0, 4 * g + i) != 0;
+        const float x = (kv && head_on) ? sc[rb][i] * a.scale : -INFINITY;
+        sc[rb][i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float corr = (m_new == -INFINITY) ? 1.f : __expf(m_run - m_new);
+    float psum = 0.f;
+    s16x4 ph[4], pl[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      f32x4 pv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pe = (sc[rb][i] == -INFINITY) ? 0.f : __expf(sc[rb][i] - m_new);
+        pv[i] = pe;
+        psum += pe;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const short h = __builtin_bit_cast(short, (__bf16)pv[i]);
+        ph[rb][i] = h;
+        pl[rb][i] = __builtin_bit_cast(short, (__bf16)(pv[i] - bf16_bits_to_f32((uint16_t)h)));
+      }
+    }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+    // z[dim][head] = corr * z + C^T P  (K = 64 keys as two permuted 32-steps)
+#pragma unroll
+    for (int dt = 0; dt < DC / 16; ++dt) {
+      f32x4 acc = z[dt] * corr;
+#pragma unroll
+      for (int p2 = 0; p2 < 2; ++p2) {
+        const s16x4 a0 = *(const s16x4*)(ct + (16 * dt + c16) * SA_CTP + 32 * p2 + 4 * g);
+        const s16x4 a1 = *(const s16x4*)(ct + (16 * dt + c16) * SA_CTP + 32 * p2 + 16 + 4 * g);
+        const s16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        const s16x8 bh = {ph[2 * p2][0], ph[2 * p2][1], ph[2 * p2][2], ph[2 * p2][3],
+                          ph[2 * p2 + 1][0], ph[2 * p2 + 1][1], ph[2 * p2 + 1][2], ph[2 * p2 + 1][3]};
+        const s16x8 bl = {pl[2 * p2][0], pl[2 * p2][1], pl[2 * p2][2], pl[2 * p2][3],
+                          pl[2 * p2 + 1][0], pl[2 * p2 + 1][1], pl[2 * p2 + 1][2], pl[2 * p2 + 1][3]};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bh),
+                                                      acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bl),
+                                                      acc, 0, 0, 0);
+      }
+      z[dt] = acc;
+    }
+  }
+  // partial for head c16: lane (c16, g) holds dims 16 dt + 4g + i
+  if (c16 < a.H) {
+    const int64_t o = (((b * a.ntiles) + sid) * a.H + c16) * (int64_t)(a.dc + 2);
+    if (g == 0) {
+      a.ws[o] = m_run;
+      a.ws[o + 1] = l_run;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DC / 16; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a.ws[o + 2 + 16 * dt + 4 * g + i] = z[dt][i];
   }
 }
 
@@ -263,11 +462,34 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
   if (!workspace || workspace_bytes < need)
     return fail(MABA_ERR_WORKSPACE, "maba_sa_decode: workspace of %zu bytes required", need);
   hipStream_t s = (hipStream_t)stream;
+  const bool mfma_ok = c_kv->dtype == MABA_BF16 && hca->dtype == MABA_BF16 && c_kv->stride[2] == 1 &&
+                       hca->stride[2] == 1 && dc % 32 == 0 && dc <= 128 && (uintptr_t)c_kv->data % 16 == 0 &&
+                       (uintptr_t)hca->data % 16 == 0 && c_kv->stride[0] % 8 == 0 && c_kv->stride[1] % 8 == 0 &&
+                       hca->stride[0] % 8 == 0 && hca->stride[1] % 8 == 0 && block_size <= 64;
+  if (mfma_ok) {
+    const int s_sp1 = (int)ceil_div(a.K, SA_TPS);
+    const int s_sp = a.Hi == 1 ? s_sp1 : (int)H * s_sp1;
+    const int s_hca = (int)ceil_div(a.t_hca, SA_TPS);
+    const int nseg = 1 + s_sp + s_hca;
+    a.ntiles = nseg;  // partial slots are segments
+    const dim3 grid((unsigned)ceil_div(nseg, 4), (unsigned)B);
+    switch (dc / 32) {
+      case 1: hipLaunchKernelGGL(maba_sa_mfma_kernel<1>, grid, dim3(256), 0, s, a, nseg, s_sp1); break;
+      case 2: hipLaunchKernelGGL(maba_sa_mfma_kernel<2>, grid, dim3(256), 0, s, a, nseg, s_sp1); break;
+      case 3: hipLaunchKernelGGL(maba_sa_mfma_kernel<3>, grid, dim3(256), 0, s, a, nseg, s_sp1); break;
+      default: hipLaunchKernelGGL(maba_sa_mfma_kernel<4>, grid, dim3(256), 0, s, a, nseg, s_sp1); break;
+    }
+    int rc = check_launch("maba_sa_decode/segments");
+    if (rc) return rc;
+    hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(128), 0, s, a, 1, 1 + s_sp, nseg);
+    return check_launch("maba_sa_decode/combine");
+  }
   if (a.ntiles > 0) {
     hipLaunchKernelGGL(maba_sa_tile_kernel, dim3((unsigned)a.ntiles, (unsigned)B), dim3(256), 0, s, a);
     int rc = check_launch("maba_sa_decode/tiles");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(128), 0, s, a);
+  hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(128), 0, s, a, a.t_loc,
+                     a.t_loc + a.t_sp, a.t_loc + a.t_sp + a.t_hca);
   return check_launch("maba_sa_decode/combine");
 }
