@@ -74,6 +74,38 @@ def time_op(fn, steps: int, warmup: int):
     return e0.elapsed_time(e1) / steps, wall
 
 
+def graph_time(fn, reps: int, check: bool = True):
+    """Mean ms per replay of ``fn`` captured in a HIP graph (events on the replay stream).
+
+    With ``check``, the graph's outputs of the first replay must equal an eager call's
+    outputs (``fn`` must then be a pure function of its inputs)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            ref = fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        res = fn()
+    g.replay()
+    torch.cuda.synchronize()
+    if check and not torch.equal(res, ref):
+        raise RuntimeError("graph replay differs from the eager result")
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
 def dgda_prefill_case(dev, B=4, H=10, T=32768, d=64, seed=0):
     import torch
     import torch.nn.functional as F
@@ -140,17 +172,25 @@ def decode_benches(dev, steps: int):
     lib = N.load()
     dq, dk_, dv_, dla, db = N.desc(q), N.desc(k), N.desc(v), N.desc(la), N.desc(be)
     dS, dS2, do = N.desc(S), N.desc(S2), N.desc(o)
-    sp = N.stream_ptr(dev)
-
     def step():
+        sp = N.stream_ptr(dev)   # the capture stream while a graph is recorded
         rc = lib.maba_hip_dgda_step(dq, dk_, dv_, None, dla, db, db, dS, do, dS2, sp)
         rc |= lib.maba_hip_dgda_step(dq, dk_, dv_, None, dla, db, db, dS2, do, dS, sp)
         if rc:
             N.check(rc, "dgda_step")
-    ms, _ = time_op(step, 5000, 100)   # 10,000 state updates
-    us = ms * 1e3 / 2
+
+    def hundred_steps():
+        for _ in range(50):
+            step()
+        return o
+
+    # 10,000 state updates: a HIP graph of 100 launches replayed 100 times
+    ms = graph_time(hundred_steps, 100, check=False)
+    us = ms * 1e3 / 100
+    eager_ms, _ = time_op(step, 500, 10)
     byts = 2 * B * H * d * d * 4 + B * H * (3 * d * 2 + 2 * 4 + d * 4)
-    out["dgda_step_B64"] = {"us_per_step": us, "gbs": byts / (us * 1e-6) / 1e9, "steps": 10000}
+    out["dgda_step_B64"] = {"us_per_step": us, "gbs": byts / (us * 1e-6) / 1e9, "steps": 10000,
+                            "eager_us_per_step": eager_ms * 1e3 / 2, "algorithmic_bytes": byts}
     log(f"dgda_step B=64: {us:.2f} us/step")
 
     # --- configs 3/4: 1M-token latent cache, B=8, d_c=128
@@ -169,25 +209,43 @@ def decode_benches(dev, steps: int):
     out["centroid_pool_1M"] = {"us": pool_ms * 1e3, "gbs": B * L * dc * 2 / (pool_ms * 1e-3) / 1e9}
     log(f"centroid pooling 1M: {pool_ms * 1e3:.1f} us")
     q_idx = torch.randn(B, Hq, dc, device=dev, generator=gen, dtype=torch.bfloat16)
-    idx_ms, _ = time_op(lambda: hb.hip_index_topk_decode(q_idx, cent, lambda_dist=0.1, top_k=K), steps * 10, 5)
-    nb = cent.shape[1]
-    out["index_topk_decode_1M"] = {"us_per_step": idx_ms * 1e3, "gbs": B * nb * dc * 2 / (idx_ms * 1e-3) / 1e9}
-    log(f"indexer decode 1M: {idx_ms * 1e3:.1f} us")
-    idx = hb.hip_index_topk_decode(q_idx, cent, lambda_dist=0.1, top_k=K)        # [B, 10, 32] per head
     q_lat = torch.randn(B, H, dc, device=dev, generator=gen) * 0.1
     gate = torch.randn(B, 3, device=dev, generator=gen)
     scale = 1.0 / math.sqrt(dh)
-    sa_ms, _ = time_op(lambda: hb.hip_maba_sa_decode(q_lat, c_kv, hca, idx, gate, L=L, scale=scale),
-                       steps * 10, 5)
+    nb = cent.shape[1]
+
+    def indexer():
+        return hb.hip_index_topk_decode(q_idx, cent, lambda_dist=0.1, top_k=K)     # [B, 10, 32] per head
+
+    idx_fixed = indexer()
+
+    def maba_sa():
+        return hb.hip_maba_sa_decode(q_lat, c_kv, hca, idx_fixed, gate, L=L, scale=scale)
+
+    def decode_step():
+        return hb.hip_maba_sa_decode(q_lat, c_kv, hca, indexer(), gate, L=L, scale=scale)
+
+    reps = max(steps * 10, 50)
+    idx_ms = graph_time(indexer, reps)
+    sa_ms = graph_time(maba_sa, reps)
+    step_ms = graph_time(decode_step, reps)
+    idx_eager_ms, _ = time_op(indexer, reps, 5)
+    sa_eager_ms, _ = time_op(maba_sa, reps, 5)
+    idx_bytes = B * nb * dc * 2
     nloc = 132
     sa_bytes = B * (hca.shape[1] * dc * 2 + H * K * 64 * dc * 2 + nloc * dc * 2)
+    out["index_topk_decode_1M"] = {"us_per_step": idx_ms * 1e3, "gbs": idx_bytes / (idx_ms * 1e-3) / 1e9,
+                                   "eager_us_per_step": idx_eager_ms * 1e3}
     out["maba_sa_decode_1M"] = {"us_per_step": sa_ms * 1e3, "gbs": sa_bytes / (sa_ms * 1e-3) / 1e9,
-                                "index_sets": "per head [8,10,32]"}
-    log(f"MABA-SA decode 1M: {sa_ms * 1e3:.1f} us")
-    both = idx_ms + sa_ms
-    tot_bytes = sa_bytes + B * nb * dc * 2
-    out["indexer_plus_maba_sa_1M"] = {"us_per_step": both * 1e3, "gbs": tot_bytes / (both * 1e-3) / 1e9,
-                                      "hbm_frac": tot_bytes / (both * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                                "eager_us_per_step": sa_eager_ms * 1e3, "index_sets": "per head [8,10,32]"}
+    tot_bytes = sa_bytes + idx_bytes
+    out["indexer_plus_maba_sa_1M"] = {"us_per_step": step_ms * 1e3, "gbs": tot_bytes / (step_ms * 1e-3) / 1e9,
+                                      "hbm_frac": tot_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                      "algorithmic_bytes": tot_bytes,
+                                      "timing": "HIP graph replay of the two entry points, events on the stream"}
+    log(f"indexer decode 1M: {idx_ms * 1e3:.1f} us (eager {idx_eager_ms * 1e3:.1f})")
+    log(f"MABA-SA decode 1M: {sa_ms * 1e3:.1f} us (eager {sa_eager_ms * 1e3:.1f})")
+    log(f"indexer + MABA-SA decode step 1M: {step_ms * 1e3:.1f} us")
     del c_kv
     return out
 

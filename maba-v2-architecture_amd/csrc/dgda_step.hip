@@ -91,6 +91,79 @@ __global__ __launch_bounds__(256) void dgda_step_kernel(StepArgs a) {
   }
 }
 
+// Fast path for dk = dv = 64 with fp32 state rows of unit column stride, q/k/v of
+// one dtype (bf16 or fp32) and fp32 gates: one wave per (b, h), lane = state
+// column.  All 64 row loads of the column are issued at once and the state stays
+// in registers; per-row scalars (decay, b*k, k, q) are broadcast from the lane
+// that loaded them with readlane, so neither reduction leaves the lane.
+struct StepFast {
+  const void* q; const void* k; const void* v;
+  int64_t qsb, qsh, qsd, ksb, ksh, ksd, vsb, vsh, vsd;
+  const float* gate; int64_t gsb, gsh, gsd;   // log_alpha (use_log) or alpha
+  const float* bb; int64_t bsb, bsh, bsd;
+  const float* ww; int64_t wsb, wsh, wsd;
+  const float* state; int64_t ssb, ssh, ssr;  // may be null (zero state)
+  float* nst; int64_t nsb, nsh, nsr;
+  void* out; int odt; int64_t osb, osh, osd;
+  int64_t BH;
+  int H, use_log;
+};
+
+template <typename T>
+__device__ __forceinline__ float ldf(const void* p, int64_t i);
+template <>
+__device__ __forceinline__ float ldf<float>(const void* p, int64_t i) { return ((const float*)p)[i]; }
+template <>
+__device__ __forceinline__ float ldf<uint16_t>(const void* p, int64_t i) {
+  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+__device__ __forceinline__ float bcast(float x, int r) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), r));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t bh = (int64_t)blockIdx.x * 4 + wave;
+  if (bh >= a.BH) return;  // wave-uniform; no barriers
+  const int64_t bi = bh / a.H, hi = bh % a.H;
+  float s[64];
+  if (a.state) {
+    const float* S = a.state + bi * a.ssb + hi * a.ssh + lane;
+#pragma unroll
+    for (int r = 0; r < 64; ++r) s[r] = S[r * a.ssr];
+  } else {
+#pragma unroll
+    for (int r = 0; r < 64; ++r) s[r] = 0.f;
+  }
+  // lane r holds the row-r scalars; lane c holds w_c v_c
+  const float kr = ldf<T>(a.k, bi * a.ksb + hi * a.ksh + lane * a.ksd);
+  const float qr = ldf<T>(a.q, bi * a.qsb + hi * a.qsh + lane * a.qsd);
+  const float vc = ldf<T>(a.v, bi * a.vsb + hi * a.vsh + lane * a.vsd);
+  const float gr = a.gate[bi * a.gsb + hi * a.gsh + lane * a.gsd];
+  const float br = a.bb[bi * a.bsb + hi * a.bsh + lane * a.bsd];
+  const float wc = a.ww[bi * a.wsb + hi * a.wsh + lane * a.wsd];
+  const float al = a.use_log ? __expf(gr) : gr;
+  const float bk = br * kr;
+  float pred = 0.f;
+#pragma unroll
+  for (int r = 0; r < 64; ++r) {
+    s[r] *= bcast(al, r);
+    pred = fmaf(bcast(bk, r), s[r], pred);
+  }
+  const float delta = wc * vc - pred;
+  float o = 0.f;
+  float* N = a.nst + bi * a.nsb + hi * a.nsh + lane;
+#pragma unroll
+  for (int r = 0; r < 64; ++r) {
+    const float sn = fmaf(bcast(kr, r), delta, s[r]);
+    N[r * a.nsr] = sn;
+    o = fmaf(bcast(qr, r), sn, o);
+  }
+  store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
+}
+
 }  // namespace maba
 
 using namespace maba;
@@ -138,6 +211,30 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
   a.use_log = log_alpha != nullptr;
 
   hipStream_t s = (hipStream_t)stream;
+  const maba_tensor* gate = log_alpha ? log_alpha : alpha;
+  const bool qkv_same = q->dtype == k->dtype && q->dtype == v->dtype && (q->dtype == MABA_BF16 || q->dtype == MABA_F32);
+  const bool fast = dk == 64 && dv == 64 && qkv_same && gate->dtype == MABA_F32 && b->dtype == MABA_F32 &&
+                    w->dtype == MABA_F32 && new_state->dtype == MABA_F32 && new_state->stride[3] == 1 &&
+                    (!state || (state->dtype == MABA_F32 && state->stride[3] == 1));
+  if (fast) {
+    StepFast f;
+    f.q = q->data; f.qsb = q->stride[0]; f.qsh = q->stride[1]; f.qsd = q->stride[2];
+    f.k = k->data; f.ksb = k->stride[0]; f.ksh = k->stride[1]; f.ksd = k->stride[2];
+    f.v = v->data; f.vsb = v->stride[0]; f.vsh = v->stride[1]; f.vsd = v->stride[2];
+    f.gate = (const float*)gate->data; f.gsb = gate->stride[0]; f.gsh = gate->stride[1]; f.gsd = gate->stride[2];
+    f.bb = (const float*)b->data; f.bsb = b->stride[0]; f.bsh = b->stride[1]; f.bsd = b->stride[2];
+    f.ww = (const float*)w->data; f.wsb = w->stride[0]; f.wsh = w->stride[1]; f.wsd = w->stride[2];
+    f.state = state ? (const float*)state->data : nullptr;
+    f.ssb = state ? state->stride[0] : 0; f.ssh = state ? state->stride[1] : 0; f.ssr = state ? state->stride[2] : 0;
+    f.nst = (float*)new_state->data; f.nsb = new_state->stride[0]; f.nsh = new_state->stride[1];
+    f.nsr = new_state->stride[2];
+    f.out = out->data; f.odt = out->dtype; f.osb = out->stride[0]; f.osh = out->stride[1]; f.osd = out->stride[2];
+    f.BH = B * H; f.H = (int)H; f.use_log = log_alpha != nullptr;
+    const dim3 g4((unsigned)ceil_div(B * H, 4));
+    if (q->dtype == MABA_BF16) hipLaunchKernelGGL(dgda_step_wave_kernel<uint16_t>, g4, dim3(256), 0, s, f);
+    else hipLaunchKernelGGL(dgda_step_wave_kernel<float>, g4, dim3(256), 0, s, f);
+    return check_launch("dgda_step");
+  }
   dim3 grid((unsigned)(B * H)), block(256);
   if (dv <= 32) hipLaunchKernelGGL(dgda_step_kernel<32>, grid, block, 0, s, a);
   else if (dv <= 64) hipLaunchKernelGGL(dgda_step_kernel<64>, grid, block, 0, s, a);

@@ -1,6 +1,6 @@
 // DG-Indexer scoring + top-k.
 //
-// Decode (reference: maba_sparse/layers/indexer.py:391-402):
+// Decode (reference: maba_sparse/layers/indexer.py:101-112):
 //   s[h,n] = (q_h / sqrt(d)) . c_n - lam * log1p(max(nb-1-n, 0))   (no mask)
 //   idx[h] = top min(K, nb) of s[h,:], score descending, ties -> lower index
 // Prefill (reference: maba_sparse/kernels/cpu_indexer.py:362-378):
@@ -18,7 +18,6 @@ namespace maba {
 
 constexpr int IDX_MAX_HEADS = 16;   // query heads per decode launch
 constexpr int IDX_MAX_D = 256;      // channels
-constexpr int DEC_TPW = 2;          // 64-centroid tiles per wave (MFMA decode path)
 
 struct DecArgs {
   const void* q; int qdt; int64_t qsb, qsh, qsd;
@@ -104,34 +103,56 @@ __global__ __launch_bounds__(64) void index_decode_merge_kernel(const key64* ws,
   if (lane < ak) out[bi * osb + h * osh + lane * osk] = (int64_t)key_index(m);
 }
 
-// Decode scoring on MFMA (bf16 q and centroids, d a multiple of 32, <= 256).
-// Each wave scores TPW consecutive 64-centroid tiles against all query heads as
-// D = C x Q^T with v_mfma_f32_16x16x32_bf16: the A operand is read straight from
-// global memory (lane = centroid row, 16 contiguous bytes), the B operand (the
-// queries, heads padded to 16) stays in registers.  Scores go through a per-wave
-// LDS tile so that, per head, each lane holds one centroid's score for the wave
-// top-k merge.  bf16 x bf16 products are exact and accumulate in fp32.
+// Decode on MFMA (bf16 q and centroids, d a multiple of 32, <= 256), two launches.
+//
+// index_decode_tile_kernel -- one wave per 64-centroid tile: D = C x Q^T with
+//   v_mfma_f32_16x16x32_bf16 (A: centroid rows straight from global memory, B:
+//   the queries, heads padded to 16, in registers).  bf16 x bf16 products are
+//   exact and accumulate in fp32.  Writes every score to a workspace row per
+//   (b, head) and the tile's best key per head.
+// index_decode_select_kernel -- one workgroup per (b, head).  tau = the K-th
+//   largest of the tile maxima bounds the K-th largest key from below (K tiles
+//   each hold a key >= tau), so the top K are among the keys >= tau: collect
+//   those (typically a few dozen), rank them by counting, write ranks < K.  If
+//   more than SEL_CAP keys pass (heavily tied scores), the workgroup falls back
+//   to wave top-k merges over the whole row.
 typedef __attribute__((ext_vector_type(8))) short i16x8_t;
+constexpr int SEL_CAP = 1024;     // candidate slots of the select kernel
+constexpr int SEL_GROUPS = 64;    // tile maxima are folded into at most this many groups (<= 256)
+constexpr int SEL_V = 16;         // float4 score loads in flight per thread in the select kernel
 
-struct DecMfmaArgs {
+struct DecTileArgs {
   const uint16_t* q; int64_t qsb, qsh;   // [B, Hq, d] bf16, channel stride 1
   const uint16_t* c; int64_t csb, csn;   // [B, nb, d] bf16, channel stride 1
   int64_t nb;
-  int d, Hq, K, nsplit, tpw;
+  int ntiles, Hq;
   float scale, lam;
-  key64* ws;
-  float* scores; int64_t ssb, ssh, ssn;
+  float* sc;                              // [B, Hq, ntiles * 64] workspace scores
+  key64* tmax;                            // [B, Hq, ntiles] best key per tile
+  float* scores; int64_t ssb, ssh, ssn;   // optional caller scores [B, Hq, nb]
 };
 
 template <int NP>  // NP = d / 32
-__global__ __launch_bounds__(256) void index_decode_mfma_kernel(DecMfmaArgs a) {
-  __shared__ float s_tile[4][16][65];
-  __shared__ key64 s_lists[4][64];
-  const int split = blockIdx.x;
-  const int64_t bi = blockIdx.y;
+__global__ __launch_bounds__(256) void index_decode_tile_kernel(DecTileArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  // B operand: Q^T, lane (head c16, group g) holds dims 32p + 8g .. +7
+  const int tile = blockIdx.x * 4 + wave;
+  const int64_t bi = blockIdx.y;
+  if (tile >= a.ntiles) return;  // wave-uniform; the kernel has no barrier
+  const int64_t n0 = (int64_t)tile * 64;
+  const uint16_t* cb = a.c + bi * a.csb;
+  // all centroid loads of the tile first: lane (c16, g) reads row 16 rb + c16, dims 32 p + 8 g .. +7
+  i16x8_t av[4][NP];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int64_t n = n0 + 16 * rb + c16;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      i16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (n < a.nb) z = *(const i16x8_t*)(cb + n * a.csn + 32 * p + 8 * g);
+      av[rb][p] = z;
+    }
+  }
   i16x8_t qb[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
@@ -139,55 +160,155 @@ __global__ __launch_bounds__(256) void index_decode_mfma_kernel(DecMfmaArgs a) {
     if (c16 < a.Hq) z = *(const i16x8_t*)(a.q + bi * a.qsb + c16 * a.qsh + 32 * p + 8 * g);
     qb[p] = z;
   }
-  key64 list[IDX_MAX_HEADS];
+  const bool hv = c16 < a.Hq;
+  float* srow = a.sc + (bi * a.Hq + c16) * (int64_t)a.ntiles * 64 + n0;
+  key64 best = KEY_NONE;
 #pragma unroll
-  for (int h = 0; h < IDX_MAX_HEADS; ++h) list[h] = KEY_NONE;
-  const uint16_t* cb = a.c + bi * a.csb;
-  const int64_t tile0 = ((int64_t)split * 4 + wave) * a.tpw;
-  for (int tt = 0; tt < a.tpw; ++tt) {
-    const int64_t n0 = (tile0 + tt) * 64;
-    if (n0 >= a.nb) break;
-    // scores for 4 row blocks of 16 centroids
+  for (int rb = 0; rb < 4; ++rb) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const int64_t n = n0 + 16 * rb + c16;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < NP; ++p)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[rb][p]),
+                                                    __builtin_bit_cast(bf16x8, qb[p]), acc, 0, 0, 0);
+    // lane holds D[centroid n0 + 16 rb + 4 g + i][head c16]
+    f32x4 sv;
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        i16x8_t av = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (n < a.nb) av = *(const i16x8_t*)(cb + n * a.csn + 32 * p + 8 * g);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, qb[p]),
-                                                      acc, 0, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = n0 + 16 * rb + 4 * g + i;
+      float sc = -INFINITY;
+      if (n < a.nb) {
+        // log1p(m) = log(1 + m) with 1 + m exact for integer block distances m < 2^24
+        sc = acc[i] * a.scale - a.lam * __logf(1.f + (float)(a.nb - 1 - n));
+        best = kmax(best, make_key(sc, (uint32_t)n));
+        if (hv && a.scores) a.scores[bi * a.ssb + c16 * a.ssh + n * a.ssn] = sc;
       }
-      // lane holds D[centroid 16rb + 4g + i][head c16]
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s_tile[wave][c16][16 * rb + 4 * g + i] = acc[i];
+      sv[i] = sc;
     }
-    // per head: lane = centroid
-    const int64_t n = n0 + lane;
-    const bool valid = n < a.nb;
-    const float pen = valid ? a.lam * log1pf((float)(a.nb - 1 - n)) : 0.f;
+    if (hv) *(f32x4*)(srow + 16 * rb + 4 * g) = sv;
+  }
+  best = kmax(best, __shfl_xor(best, 16));
+  best = kmax(best, __shfl_xor(best, 32));
+  if (hv && g == 0) a.tmax[(bi * a.Hq + c16) * a.ntiles + tile] = best;
+}
+
+// Number of keys in s[0, n8) greater than k; n8 is a multiple of 8 and s 16-byte
+// aligned.  Eight keys per step through 128-bit LDS reads, all lanes reading the
+// same address (broadcast).
+__device__ __forceinline__ int count_greater(const key64* s, int n8, key64 k) {
+  typedef __attribute__((ext_vector_type(2))) unsigned long long u64x2;
+  int r = 0;
+  for (int i = 0; i < n8; i += 8) {
+    const u64x2 x0 = *(const u64x2*)(s + i), x1 = *(const u64x2*)(s + i + 2);
+    const u64x2 x2 = *(const u64x2*)(s + i + 4), x3 = *(const u64x2*)(s + i + 6);
+    r += (x0.x > k) + (x0.y > k) + (x1.x > k) + (x1.y > k) + (x2.x > k) + (x2.y > k) + (x3.x > k) + (x3.y > k);
+  }
+  return r;
+}
+
+struct DecSelArgs {
+  const float* sc; const key64* tmax;
+  int64_t nb;
+  int ntiles, Hq, K, ak;
+  int64_t* out; int64_t osb, osh, osk;
+};
+
+__global__ __launch_bounds__(256) void index_decode_select_kernel(DecSelArgs a) {
+  __shared__ __attribute__((aligned(16))) key64 s_c[SEL_CAP + 8];
+  __shared__ __attribute__((aligned(16))) key64 s_g[SEL_GROUPS];
+  __shared__ key64 s_tau;
+  __shared__ int s_cnt;
+  const int64_t row = blockIdx.x;  // b * Hq + h
+  const int64_t bi = row / a.Hq;
+  const int h = (int)(row % a.Hq);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const key64* tm = a.tmax + row * a.ntiles;
+  const float* sc = a.sc + row * (int64_t)a.ntiles * 64;
+  const int G = a.ntiles < SEL_GROUPS ? a.ntiles : SEL_GROUPS;
+  const int G8 = (G + 7) & ~7;
+  // first pass of score loads, issued before the tile maxima so that both are in flight together
+  f32x4 v[SEL_V];
 #pragma unroll
-    for (int h = 0; h < IDX_MAX_HEADS; ++h) {
-      if (h < a.Hq) {
-        const float sc = s_tile[wave][h][lane] * a.scale - pen;
-        if (a.scores && valid) a.scores[bi * a.ssb + h * a.ssh + n * a.ssn] = sc;
-        list[h] = wave_merge_topk(list[h], valid ? make_key(sc, (uint32_t)n) : KEY_NONE, a.K);
+  for (int j = 0; j < SEL_V; ++j) {
+    const int64_t n = 1024 * j + 4 * tid;
+    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    if (n < a.nb) z = *(const f32x4*)(sc + n);   // rows are padded to whole tiles
+    v[j] = z;
+  }
+  if (tid == 0) { s_cnt = 0; s_tau = KEY_NONE; }
+  if (tid < G8) {   // group j = tiles [j*ntiles/G, (j+1)*ntiles/G); padding slots hold KEY_NONE
+    key64 m = KEY_NONE;
+    if (tid < G) {
+      const int t0 = (int)((int64_t)tid * a.ntiles / G), t1 = (int)((int64_t)(tid + 1) * a.ntiles / G);
+      for (int t = t0; t < t1; ++t) m = kmax(m, tm[t]);
+    }
+    s_g[tid] = m;
+  }
+  __syncthreads();
+  if (G >= a.K && tid < G) {  // tau = K-th largest group maximum (keys are distinct)
+    if (count_greater(s_g, G8, s_g[tid]) == a.K - 1) s_tau = s_g[tid];
+  }
+  __syncthreads();
+  const key64 tau = s_tau;
+  // keys >= tau have scores >= tau's score: a branch-free float prefilter marks the
+  // survivors of each pass in a bit mask, and only those take the exact key test
+  const float tau_s = tau == KEY_NONE ? -INFINITY : key_score(tau);
+  for (int64_t base = 0; base < a.nb; base += 1024 * SEL_V) {
+    if (base > 0) {
+#pragma unroll
+      for (int j = 0; j < SEL_V; ++j) {
+        const int64_t n = base + 1024 * j + 4 * tid;
+        f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        if (n < a.nb) z = *(const f32x4*)(sc + n);
+        v[j] = z;
+      }
+    }
+    unsigned long long mask = 0ull;
+#pragma unroll
+    for (int j = 0; j < SEL_V; ++j) {
+      const int64_t n = base + 1024 * j + 4 * tid;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        mask |= (unsigned long long)(n + i < a.nb && v[j][i] >= tau_s) << (4 * j + i);
+    }
+    while (mask) {
+      const int bit = __builtin_ctzll(mask);
+      mask &= mask - 1ull;
+      const int64_t n = base + 1024 * (bit >> 2) + 4 * tid + (bit & 3);
+      const key64 key = make_key(sc[n], (uint32_t)n);
+      if (key >= tau) {
+        const int pos = atomicAdd(&s_cnt, 1);
+        if (pos < SEL_CAP) s_c[pos] = key;
       }
     }
   }
-#pragma unroll
-  for (int h = 0; h < IDX_MAX_HEADS; ++h) {
-    if (h < a.Hq) {
-      s_lists[wave][lane] = list[h];
-      __syncthreads();
-      if (wave == 0) {
-        key64 m = s_lists[0][lane];
-        for (int w = 1; w < 4; ++w) m = wave_merge_topk(m, s_lists[w][lane], a.K);
-        a.ws[(((int64_t)bi * a.nsplit + split) * a.Hq + h) * 64 + lane] = m;
-      }
-      __syncthreads();
+  __syncthreads();
+  const int cnt = s_cnt;
+  int64_t* orow = a.out + bi * a.osb + h * a.osh;
+  if (cnt <= SEL_CAP) {
+    const int c8 = (cnt + 7) & ~7;
+    if (tid < c8 - cnt) s_c[cnt + tid] = KEY_NONE;   // pad to whole groups of 8
+    __syncthreads();
+    for (int j = tid; j < cnt; j += 256) {
+      const key64 kj = s_c[j];
+      const int rank = count_greater(s_c, c8, kj);
+      if (rank < a.ak) orow[rank * a.osk] = (int64_t)key_index(kj);
     }
+    return;
+  }
+  // fallback: each wave merges a quarter of the row, then wave 0 merges the four lists
+  key64 list = KEY_NONE;
+  for (int64_t base = (int64_t)wave * 64; base < a.nb; base += 256) {
+    const int64_t n = base + lane;
+    const key64 key = n < a.nb ? make_key(sc[n], (uint32_t)n) : KEY_NONE;
+    list = wave_merge_topk(list, key >= tau ? key : KEY_NONE, a.K);
+  }
+  __syncthreads();
+  s_c[wave * 64 + lane] = list;
+  __syncthreads();
+  if (wave == 0) {
+    key64 m = s_c[lane];
+    for (int w = 1; w < 4; ++w) m = wave_merge_topk(m, s_c[w * 64 + lane], a.K);
+    if (lane < a.ak) orow[lane * a.osk] = (int64_t)key_index(m);
   }
 }
 
@@ -240,11 +361,18 @@ __global__ __launch_bounds__(256) void index_prefill_kernel(PreArgs a) {
 
 using namespace maba;
 
+static size_t decode_scores_bytes(int64_t B, int64_t Hq, int64_t nb) {
+  return (size_t)(B * Hq * ceil_div(nb, 64) * 64) * sizeof(float);
+}
+
 extern "C" size_t maba_hip_index_topk_decode_workspace_size(int64_t B, int64_t Hq, int64_t nb, int top_k) {
   (void)top_k;
   const int64_t tiles = ceil_div(nb, 64);
-  const int64_t nsplit = ceil_div(tiles, 4);  // scalar path (the MFMA path uses fewer splits)
-  return (size_t)(B * (nsplit > 0 ? nsplit : 1) * Hq * 64) * sizeof(key64);
+  // MFMA path: scores + per-tile maxima; scalar path: per-split top-64 lists
+  const size_t mfma = decode_scores_bytes(B, Hq, nb) + (size_t)(B * Hq * tiles) * sizeof(key64);
+  const int64_t nsplit = ceil_div(tiles, 4);
+  const size_t scalar = (size_t)(B * (nsplit > 0 ? nsplit : 1) * Hq * 64) * sizeof(key64);
+  return mfma > scalar ? mfma : scalar;
 }
 
 extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tensor* centroids,
@@ -280,36 +408,37 @@ extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tenso
                        (uintptr_t)centroids->data % 16 == 0 && q->stride[0] % 8 == 0 && q->stride[1] % 8 == 0 &&
                        centroids->stride[0] % 8 == 0 && centroids->stride[1] % 8 == 0;
   if (mfma_ok) {
-    DecMfmaArgs m;
+    DecTileArgs m;
     m.q = (const uint16_t*)q->data; m.qsb = q->stride[0]; m.qsh = q->stride[1];
     m.c = (const uint16_t*)centroids->data; m.csb = centroids->stride[0]; m.csn = centroids->stride[1];
-    m.nb = nb; m.d = (int)d; m.Hq = (int)Hq; m.K = top_k;
-    m.tpw = DEC_TPW;
-    m.nsplit = (int)ceil_div(ceil_div(nb, 64), 4 * DEC_TPW);
+    m.nb = nb; m.ntiles = (int)ceil_div(nb, 64); m.Hq = (int)Hq;
     m.scale = 1.0f / sqrtf((float)d);
     m.lam = lambda_dist;
-    m.ws = (key64*)workspace;
+    m.sc = (float*)workspace;
+    m.tmax = (key64*)((char*)workspace + decode_scores_bytes(B, Hq, nb));
     m.scores = out_scores ? (float*)out_scores->data : nullptr;
     m.ssb = out_scores ? out_scores->stride[0] : 0;
     m.ssh = out_scores ? out_scores->stride[1] : 0;
     m.ssn = out_scores ? out_scores->stride[2] : 0;
-    const dim3 grid((unsigned)m.nsplit, (unsigned)B);
+    const dim3 grid((unsigned)ceil_div(m.ntiles, 4), (unsigned)B);
     switch (d / 32) {
-      case 1: hipLaunchKernelGGL(index_decode_mfma_kernel<1>, grid, dim3(256), 0, s, m); break;
-      case 2: hipLaunchKernelGGL(index_decode_mfma_kernel<2>, grid, dim3(256), 0, s, m); break;
-      case 3: hipLaunchKernelGGL(index_decode_mfma_kernel<3>, grid, dim3(256), 0, s, m); break;
-      case 4: hipLaunchKernelGGL(index_decode_mfma_kernel<4>, grid, dim3(256), 0, s, m); break;
-      case 5: hipLaunchKernelGGL(index_decode_mfma_kernel<5>, grid, dim3(256), 0, s, m); break;
-      case 6: hipLaunchKernelGGL(index_decode_mfma_kernel<6>, grid, dim3(256), 0, s, m); break;
-      case 7: hipLaunchKernelGGL(index_decode_mfma_kernel<7>, grid, dim3(256), 0, s, m); break;
-      default: hipLaunchKernelGGL(index_decode_mfma_kernel<8>, grid, dim3(256), 0, s, m); break;
+      case 1: hipLaunchKernelGGL(index_decode_tile_kernel<1>, grid, dim3(256), 0, s, m); break;
+      case 2: hipLaunchKernelGGL(index_decode_tile_kernel<2>, grid, dim3(256), 0, s, m); break;
+      case 3: hipLaunchKernelGGL(index_decode_tile_kernel<3>, grid, dim3(256), 0, s, m); break;
+      case 4: hipLaunchKernelGGL(index_decode_tile_kernel<4>, grid, dim3(256), 0, s, m); break;
+      case 5: hipLaunchKernelGGL(index_decode_tile_kernel<5>, grid, dim3(256), 0, s, m); break;
+      case 6: hipLaunchKernelGGL(index_decode_tile_kernel<6>, grid, dim3(256), 0, s, m); break;
+      case 7: hipLaunchKernelGGL(index_decode_tile_kernel<7>, grid, dim3(256), 0, s, m); break;
+      default: hipLaunchKernelGGL(index_decode_tile_kernel<8>, grid, dim3(256), 0, s, m); break;
     }
-    int rc = check_launch("index_topk_decode/score");
+    int rc = check_launch("index_topk_decode/tiles");
     if (rc) return rc;
-    hipLaunchKernelGGL(index_decode_merge_kernel, dim3((unsigned)(B * Hq)), dim3(64), 0, s, m.ws, m.nsplit,
-                       (int)Hq, top_k, (int)ak, (int64_t*)out_idx->data, out_idx->stride[0],
-                       out_idx->stride[1], out_idx->stride[2]);
-    return check_launch("index_topk_decode/merge");
+    DecSelArgs e;
+    e.sc = m.sc; e.tmax = m.tmax; e.nb = nb; e.ntiles = m.ntiles; e.Hq = (int)Hq; e.K = top_k; e.ak = (int)ak;
+    e.out = (int64_t*)out_idx->data; e.osb = out_idx->stride[0]; e.osh = out_idx->stride[1];
+    e.osk = out_idx->stride[2];
+    hipLaunchKernelGGL(index_decode_select_kernel, dim3((unsigned)(B * Hq)), dim3(256), 0, s, e);
+    return check_launch("index_topk_decode/select");
   }
   DecArgs a;
   a.q = q->data; a.qdt = q->dtype; a.qsb = q->stride[0]; a.qsh = q->stride[1]; a.qsd = q->stride[2];

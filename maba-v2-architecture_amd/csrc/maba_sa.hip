@@ -19,6 +19,8 @@
 // latent sum) per head.  Kernel 2 merges the partials of each (b, h, stream),
 // applies the gate softmax and writes z.  Traffic is one read of the selected
 // latent rows (bf16) plus small partials: HBM-bound.
+#include <algorithm>
+
 #include "maba_common.h"
 
 namespace maba {
@@ -148,57 +150,102 @@ __global__ __launch_bounds__(256) void maba_sa_tile_kernel(SaArgs a) {
   }
 }
 
-// One workgroup per (b, h): merge partials per stream, apply the gate.
+// One workgroup per (b, h): merge the partials of each stream, apply the gate.
+// Partials [0, p1) are the local stream, [p1, p2) sparse, [p2, p3) HCA.  Waves
+// 0-2 reduce the (max, sum) pairs of one stream each; then, in chunks of 256
+// partials, every partial's weight g_s exp(m - M_s) / L_s goes to LDS and the
+// threads (dim d, sub-slice) accumulate the weighted latent sums.
 __global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a, int p1, int p2, int p3) {
+  __shared__ float s_w[256];
+  __shared__ float s_M[3], s_S[3];
+  __shared__ float s_acc[256];
   const int64_t b = blockIdx.x / a.H;
   const int h = blockIdx.x % a.H;
   const int dc = a.dc;
-  // gate softmax
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t gb = b * a.gsb + h * a.gsh;
   float z0 = load_elem(a.gate, a.gdt, gb), z1 = load_elem(a.gate, a.gdt, gb + a.gsm),
         z2 = load_elem(a.gate, a.gdt, gb + 2 * a.gsm);
   const float gm = fmaxf(z0, fmaxf(z1, z2));
   z0 = __expf(z0 - gm); z1 = __expf(z1 - gm); z2 = __expf(z2 - gm);
   const float gi = 1.f / (z0 + z1 + z2);
-  const float g[3] = {z0 * gi, z1 * gi, z2 * gi};
-  // partials [0, p1) local, [p1, p2) sparse, [p2, p3) HCA
+  const float gate[3] = {z0 * gi, z1 * gi, z2 * gi};
   const int t_begin[3] = {0, p1, p2};
   const int t_end[3] = {p1, p2, p3};
-  for (int d = threadIdx.x; d < dc; d += blockDim.x) {
-    float res = 0.f;
-    for (int st = 0; st < 3; ++st) {
-      float zs = 0.f;
-      if (st == 2 && a.L - 1 < a.pool - 1) {
-        // early HCA: running mean of c[0..L-1] (sparse_attention.py:189-199)
-        for (int64_t t = 0; t < a.L; ++t) zs += load_elem(a.c, a.cdt, b * a.csb + t * a.csl + d * a.csd);
-        zs /= (float)a.L;
-      } else {
-        float M = -INFINITY;
-        for (int t = t_begin[st]; t < t_end[st]; ++t) M = fmaxf(M, a.ws[sa_part_off(a, b, t, h)]);
-        if (M != -INFINITY) {
-          float Ls = 0.f, Z = 0.f;
-          for (int t = t_begin[st]; t < t_end[st]; ++t) {
-            const int64_t o = sa_part_off(a, b, t, h);
-            const float m = a.ws[o];
-            if (m == -INFINITY) continue;
-            const float e = __expf(m - M);
-            Ls = fmaf(a.ws[o + 1], e, Ls);
-            Z = fmaf(a.ws[o + 2 + d], e, Z);
-          }
-          zs = Ls > 0.f ? Z / Ls : 0.f;
+  // partial headers of the first chunk, loaded alongside the stream reductions
+  float m_first = -INFINITY;
+  if (tid < p3) m_first = a.ws[sa_part_off(a, b, tid, h)];
+  if (wave < 3) {  // online (max, sum) over the stream's partials, one pass
+    float M = -INFINITY, S = 0.f;
+    for (int t = t_begin[wave] + lane; t < t_end[wave]; t += 64) {
+      const int64_t o = sa_part_off(a, b, t, h);
+      const float m = a.ws[o], l = a.ws[o + 1];
+      if (m != -INFINITY) {
+        if (m > M) {
+          S = S * __expf(M - m) + l;
+          M = m;
+        } else {
+          S = fmaf(l, __expf(m - M), S);
         }
       }
-      res = fmaf(g[st], zs, res);
     }
-    a.out[b * a.osb + h * a.osh + d * a.osd] = res;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float M2 = __shfl_xor(M, o), S2 = __shfl_xor(S, o);
+      const float Mn = fmaxf(M, M2);
+      S = (M == -INFINITY ? 0.f : S * __expf(M - Mn)) + (M2 == -INFINITY ? 0.f : S2 * __expf(M2 - Mn));
+      M = Mn;
+    }
+    if (lane == 0) {
+      s_M[wave] = M;
+      s_S[wave] = S;
+    }
+  }
+  __syncthreads();
+  const int nsub = 256 / dc;  // threads per latent dim
+  const int d = tid % dc, sub = tid / dc;
+  const bool active = sub < nsub;
+  float acc = 0.f;
+  for (int c0 = 0; c0 < p3; c0 += 256) {
+    const int t = c0 + tid;
+    float w = 0.f;
+    if (t < p3) {
+      const int st = t < p1 ? 0 : (t < p2 ? 1 : 2);
+      const float m = c0 == 0 ? m_first : a.ws[sa_part_off(a, b, t, h)];
+      if (m != -INFINITY && s_S[st] > 0.f) w = gate[st] * __expf(m - s_M[st]) / s_S[st];
+    }
+    s_w[tid] = w;
+    __syncthreads();
+    const int cn = (p3 - c0) < 256 ? (p3 - c0) : 256;
+    // every partial slot is written by the segment kernel, so the loads need no guard
+    if (active) {
+#pragma unroll 8
+      for (int j = sub; j < cn; j += nsub) acc = fmaf(s_w[j], a.ws[sa_part_off(a, b, c0 + j, h) + 2 + d], acc);
+    }
+    __syncthreads();
+  }
+  s_acc[tid] = active ? acc : 0.f;
+  __syncthreads();
+  if (tid < dc) {
+    float r = 0.f;
+    for (int k = 0; k < nsub; ++k) r += s_acc[k * dc + tid];
+    if (a.L - 1 < a.pool - 1) {
+      // early HCA: running mean of c[0..L-1] (sparse_attention.py:189-199)
+      float zs = 0.f;
+      for (int64_t t = 0; t < a.L; ++t) zs += load_elem(a.c, a.cdt, b * a.csb + t * a.csl + tid * a.csd);
+      r = fmaf(gate[2], zs / (float)a.L, r);
+    }
+    a.out[b * a.osb + h * a.osh + tid * a.osd] = r;
   }
 }
 
 // ------------------------------------------------------------------ MFMA path
 // Used when c_kv / hca are bf16 rows with unit channel stride, d_c <= 128 (a
 // multiple of 32) and H <= 16.  Every stream of every batch element is cut into
-// segments of up to SA_TPS 64-key tiles; one wave runs one segment with an online
-// softmax and writes one partial (max, sum, weighted latent sum) per head.
+// segments of up to 4 * tpw 64-key tiles, one workgroup per segment.  Each wave
+// runs tpw consecutive tiles with an online softmax, loading tile t+1 into
+// registers while it computes tile t; the four wave partials are merged in LDS
+// and the workgroup writes one partial (max, sum, weighted latent sum) per head.
 //   scores  D[key][head] = C Q^T   (A: key rows straight from global memory,
 //                                   B: the queries, bf16 hi + lo, in registers)
 //   values  Z[dim][head] += C^T P  (A: the tile transposed into per-wave LDS,
@@ -206,8 +253,7 @@ __global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a, int p1, 
 //                                   place from the score accumulators)
 typedef __attribute__((ext_vector_type(8))) short s16x8;
 typedef __attribute__((ext_vector_type(4))) short s16x4;
-constexpr int SA_TPS = 8;        // tiles per segment
-constexpr int SA_CTP = 72;       // row pitch (bf16) of the transposed tile
+constexpr int SA_CTP = 68;  // row pitch (bf16) of the transposed tile: 34 words, so rows 8 apart start 16 banks apart
 
 struct SaSeg {
   int stream, head_only;
@@ -215,7 +261,7 @@ struct SaSeg {
   int hs;                  // sparse index row
 };
 
-__device__ __forceinline__ SaSeg sa_segment(const SaArgs& a, int sid, int s_sp1) {
+__device__ __forceinline__ SaSeg sa_segment(const SaArgs& a, int sid, int s_sp1, int span) {
   SaSeg g;
   g.head_only = -1;
   g.hs = 0;
@@ -228,27 +274,68 @@ __device__ __forceinline__ SaSeg sa_segment(const SaArgs& a, int sid, int s_sp1)
     g.hs = (a.Hi == 1) ? 0 : r / s_sp1;
     const int rr = (a.Hi == 1) ? r : r % s_sp1;
     if (a.Hi > 1) g.head_only = g.hs;
-    g.t_begin = (int64_t)rr * SA_TPS;
-    g.t_end = min((int64_t)a.K, g.t_begin + SA_TPS);
+    g.t_begin = (int64_t)rr * span;
+    g.t_end = min((int64_t)a.K, g.t_begin + span);
   } else {
     const int r = sid - 1 - s_sp;
     g.stream = 2;
-    g.t_begin = (int64_t)r * SA_TPS;
-    g.t_end = min((int64_t)a.t_hca, g.t_begin + SA_TPS);
+    g.t_begin = (int64_t)r * span;
+    g.t_end = min((int64_t)a.t_hca, g.t_begin + span);
   }
   return g;
 }
 
+// Key rows 16 rb + c16 of tile tix of a segment, dims 32 p + 8 g .. +7; invalid rows read as zeros.
+// blk is the tile's block index for the sparse stream.
+template <int NP>
+__device__ __forceinline__ void sa_load_tile(const SaArgs& a, const SaSeg& sg, int64_t b, int64_t tix, int64_t blk,
+                                             int c16, int g, s16x8 (&cv)[4][NP], bool (&ok)[4]) {
+  const uint16_t* base;
+  int64_t rstride;
+  if (sg.stream == 2) {
+    base = (const uint16_t*)a.hca + b * a.hsb;
+    rstride = a.hsn;
+  } else {
+    base = (const uint16_t*)a.c + b * a.csb;
+    rstride = a.csl;
+  }
+  const int64_t nblk = (a.L + a.bs - 1) / a.bs;
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int j = 16 * rb + c16;
+    int64_t pos;
+    if (sg.stream == 0) {
+      const int64_t li = tix * 64 + j;
+      ok[rb] = li < a.nloc;
+      pos = li < a.ns ? li : a.loc_start + (li - a.ns);
+    } else if (sg.stream == 1) {
+      pos = blk * a.bs + j;
+      ok[rb] = blk >= 0 && blk < nblk && j < a.bs && pos < a.L;
+    } else {
+      pos = tix * 64 + j;
+      ok[rb] = pos < a.nc;
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (ok[rb]) v = *(const s16x8*)(base + pos * rstride + 32 * p + 8 * g);
+      cv[rb][p] = v;
+    }
+  }
+}
+
 template <int NP>  // d_c = 32 * NP
-__global__ __launch_bounds__(256) void maba_sa_mfma_kernel(SaArgs a, int nseg, int s_sp1) {
+__global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg, int s_sp1, int tpw) {
   constexpr int DC = 32 * NP;
-  __shared__ short s_ct[4][DC * SA_CTP];
+  __shared__ __attribute__((aligned(16))) short s_ct[4][DC * SA_CTP];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 4, c16 = lane & 15;
+  const int sid = blockIdx.x;
   const int64_t b = blockIdx.y;
-  const int sid = blockIdx.x * 4 + wave;
-  if (sid >= nseg) return;
-  const SaSeg sg = sa_segment(a, sid, s_sp1);
+  if (sid >= nseg) return;  // uniform per workgroup
+  const SaSeg sg = sa_segment(a, sid, s_sp1, 4 * tpw);
+  const int64_t t0 = sg.t_begin + (int64_t)wave * tpw;
+  const int64_t t1 = min(sg.t_end, t0 + tpw);
   short* ct = s_ct[wave];
 
   // queries (B operand of the scores): head c16, dims 32p + 8g .. +7, split hi/lo
@@ -269,52 +356,32 @@ __global__ __launch_bounds__(256) void maba_sa_mfma_kernel(SaArgs a, int nseg, i
 #pragma unroll
   for (int dt = 0; dt < DC / 16; ++dt) z[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t tix = sg.t_begin; tix < sg.t_end; ++tix) {
-    // key rows of this tile: row r = 16 rb + c16
-    const uint16_t* base;
-    int64_t rstride;
-    int64_t pos[4];
-    bool ok[4];
-    if (sg.stream == 2) {
-      base = (const uint16_t*)a.hca + b * a.hsb;
-      rstride = a.hsn;
-    } else {
-      base = (const uint16_t*)a.c + b * a.csb;
-      rstride = a.csl;
-    }
-    int64_t blk = 0;
-    if (sg.stream == 1) blk = a.idx[b * a.isb + sg.hs * a.ish + tix * a.isk];
-    const int64_t nblk = (a.L + a.bs - 1) / a.bs;
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const int j = 16 * rb + c16;
-      if (sg.stream == 0) {
-        const int64_t li = tix * 64 + j;
-        ok[rb] = li < a.nloc;
-        pos[rb] = li < a.ns ? li : a.loc_start + (li - a.ns);
-      } else if (sg.stream == 1) {
-        pos[rb] = blk * a.bs + j;
-        ok[rb] = blk >= 0 && blk < nblk && j < a.bs && pos[rb] < a.L;
-      } else {
-        pos[rb] = tix * 64 + j;
-        ok[rb] = pos[rb] < a.nc;
-      }
-    }
+  // sparse block indices of this wave's tiles, one per lane, fetched up front so that
+  // the tile loads do not wait on a dependent index load
+  int64_t blk_l = 0;
+  if (sg.stream == 1 && lane < t1 - t0) blk_l = a.idx[b * a.isb + sg.hs * a.ish + (t0 + lane) * a.isk];
+  s16x8 cv[4][NP];
+  bool ok[4];
+  if (t0 < t1) sa_load_tile<NP>(a, sg, b, t0, __shfl(blk_l, 0), c16, g, cv, ok);
+  for (int64_t tix = t0; tix < t1; ++tix) {
+    // prefetch the next tile (the current one is re-read when there is none: in bounds, unused)
+    s16x8 nv[4][NP];
+    bool nok[4];
+    const int64_t tn = tix + 1 < t1 ? tix + 1 : tix;
+    sa_load_tile<NP>(a, sg, b, tn, __shfl(blk_l, (int)(tn - t0)), c16, g, nv, nok);
     f32x4 sc[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        s16x8 cv = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (ok[rb]) cv = *(const s16x8*)(base + pos[rb] * rstride + 32 * p + 8 * g);
         // transposed copy for the value product: ct[dim][key]
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) ct[(32 * p + 8 * g + jj) * SA_CTP + 16 * rb + c16] = cv[jj];
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv), __builtin_bit_cast(bf16x8, qh[p]),
-                                                      acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv), __builtin_bit_cast(bf16x8, ql[p]),
-                                                      acc, 0, 0, 0);
+        for (int jj = 0; jj < 8; ++jj) ct[(32 * p + 8 * g + jj) * SA_CTP + 16 * rb + c16] = cv[rb][p][jj];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
+                                                      __builtin_bit_cast(bf16x8, qh[p]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
+                                                      __builtin_bit_cast(bf16x8, ql[p]), acc, 0, 0, 0);
       }
       sc[rb] = acc;
     }
@@ -377,18 +444,52 @@ __global__ __launch_bounds__(256) void maba_sa_mfma_kernel(SaArgs a, int nseg, i
       }
       z[dt] = acc;
     }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      ok[rb] = nok[rb];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) cv[rb][p] = nv[rb][p];
+    }
   }
-  // partial for head c16: lane (c16, g) holds dims 16 dt + 4g + i
-  if (c16 < a.H) {
-    const int64_t o = (((b * a.ntiles) + sid) * a.H + c16) * (int64_t)(a.dc + 2);
-    if (g == 0) {
-      a.ws[o] = m_run;
-      a.ws[o + 1] = l_run;
+  // merge the four wave partials: s_z[wave][head][dim], s_m / s_l[wave][head]
+  __syncthreads();
+  float* s_z = (float*)&s_ct[0][0];
+  float* s_m = s_z + 4 * 16 * DC;
+  float* s_l = s_m + 64;
+#pragma unroll
+  for (int dt = 0; dt < DC / 16; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_z[(wave * 16 + c16) * DC + 16 * dt + 4 * g + i] = z[dt][i];
+  if (g == 0) {
+    s_m[wave * 16 + c16] = m_run;
+    s_l[wave * 16 + c16] = l_run;
+  }
+  __syncthreads();
+  const int h = threadIdx.x >> 4, part = threadIdx.x & 15;  // 16 threads per head
+  if (h < a.H) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w * 16 + h]);
+    float e[4], Ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float m = s_m[w * 16 + h];
+      e[w] = (m == -INFINITY) ? 0.f : __expf(m - M);
+      Ls = fmaf(e[w], s_l[w * 16 + h], Ls);
+    }
+    const int64_t o = (((b * a.ntiles) + sid) * a.H + h) * (int64_t)(a.dc + 2);
+    if (part == 0) {
+      a.ws[o] = M;
+      a.ws[o + 1] = Ls;
     }
 #pragma unroll
-    for (int dt = 0; dt < DC / 16; ++dt)
+    for (int j = 0; j < DC / 16; ++j) {
+      const int dd = part * (DC / 16) + j;
+      float zz = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a.ws[o + 2 + 16 * dt + 4 * g + i] = z[dt][i];
+      for (int w = 0; w < 4; ++w) zz = fmaf(e[w], s_z[(w * 16 + h) * DC + dd], zz);
+      a.ws[o + 2 + dd] = zz;
+    }
   }
 }
 
@@ -467,21 +568,25 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
                        (uintptr_t)hca->data % 16 == 0 && c_kv->stride[0] % 8 == 0 && c_kv->stride[1] % 8 == 0 &&
                        hca->stride[0] % 8 == 0 && hca->stride[1] % 8 == 0 && block_size <= 64;
   if (mfma_ok) {
-    const int s_sp1 = (int)ceil_div(a.K, SA_TPS);
+    // tiles per wave: enough segments to cover the machine about twice, at most 8
+    const int64_t tiles = B * (a.t_loc + (int64_t)a.Hi * a.K + a.t_hca);
+    const int tpw = (int)std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(tiles, 2048)));
+    const int span = 4 * tpw;
+    const int s_sp1 = (int)ceil_div(a.K, span);
     const int s_sp = a.Hi == 1 ? s_sp1 : (int)H * s_sp1;
-    const int s_hca = (int)ceil_div(a.t_hca, SA_TPS);
+    const int s_hca = (int)ceil_div(a.t_hca, span);
     const int nseg = 1 + s_sp + s_hca;
     a.ntiles = nseg;  // partial slots are segments
-    const dim3 grid((unsigned)ceil_div(nseg, 4), (unsigned)B);
+    const dim3 grid((unsigned)nseg, (unsigned)B);
     switch (dc / 32) {
-      case 1: hipLaunchKernelGGL(maba_sa_mfma_kernel<1>, grid, dim3(256), 0, s, a, nseg, s_sp1); break;
-      case 2: hipLaunchKernelGGL(maba_sa_mfma_kernel<2>, grid, dim3(256), 0, s, a, nseg, s_sp1); break;
-      case 3: hipLaunchKernelGGL(maba_sa_mfma_kernel<3>, grid, dim3(256), 0, s, a, nseg, s_sp1); break;
-      default: hipLaunchKernelGGL(maba_sa_mfma_kernel<4>, grid, dim3(256), 0, s, a, nseg, s_sp1); break;
+      case 1: hipLaunchKernelGGL(maba_sa_mfma_kernel<1>, grid, dim3(256), 0, s, a, nseg, s_sp1, tpw); break;
+      case 2: hipLaunchKernelGGL(maba_sa_mfma_kernel<2>, grid, dim3(256), 0, s, a, nseg, s_sp1, tpw); break;
+      case 3: hipLaunchKernelGGL(maba_sa_mfma_kernel<3>, grid, dim3(256), 0, s, a, nseg, s_sp1, tpw); break;
+      default: hipLaunchKernelGGL(maba_sa_mfma_kernel<4>, grid, dim3(256), 0, s, a, nseg, s_sp1, tpw); break;
     }
     int rc = check_launch("maba_sa_decode/segments");
     if (rc) return rc;
-    hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(128), 0, s, a, 1, 1 + s_sp, nseg);
+    hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(256), 0, s, a, 1, 1 + s_sp, nseg);
     return check_launch("maba_sa_decode/combine");
   }
   if (a.ntiles > 0) {
@@ -489,7 +594,7 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
     int rc = check_launch("maba_sa_decode/tiles");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(128), 0, s, a, a.t_loc,
+  hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(256), 0, s, a, a.t_loc,
                      a.t_loc + a.t_sp, a.t_loc + a.t_sp + a.t_hca);
   return check_launch("maba_sa_decode/combine");
 }

@@ -162,14 +162,14 @@ def hip_index_topk(q_idx, centroids, lambda_dist: float = 0.5, top_k: int = 32, 
 @register_kernel("hip", "index_topk_decode")
 def hip_index_topk_decode(q, centroids, lambda_dist: float = 0.5, top_k: int = 32,
                           return_scores: bool = False, **kwargs: Any):
-    """Decode scoring + top-k over one centroid set per batch (layers/indexer.py:391-402)."""
+    """Decode scoring + top-k over one centroid set per batch (layers/indexer.py:101-112)."""
     lam = kwargs.get("dist_lambda", lambda_dist)
     _no_grad_needed("index_topk_decode", q, centroids)
     dev = N.require_device([q, centroids], "index_topk_decode")
     B, Hq, d = q.shape
     nb = centroids.shape[1]
     ak = min(top_k, nb)
-    idx = torch.zeros(B, Hq, ak, dtype=torch.long, device=dev)
+    idx = torch.empty(B, Hq, ak, dtype=torch.long, device=dev)   # every slot is written
     scores = torch.empty(B, Hq, nb, dtype=torch.float32, device=dev) if return_scores else None
     if nb == 0 or B * Hq == 0:
         return (idx, scores) if return_scores else idx

@@ -182,6 +182,35 @@ def test_index_topk_decode(dev, B, Hq, nb, d, k, lam, dtype):
     assert n >= 1
 
 
+@pytest.mark.parametrize("nb,lam", [(100, 0.0), (4000, 0.0), (15625, 0.0), (4000, 0.1)])
+def test_index_topk_decode_ties(dev, nb, lam):
+    """Zero centroids: every score is the penalty alone.  With lam = 0 all scores tie and
+    the order is index ascending (nb = 4000 and 15625 exceed the select kernel's
+    candidate slots and take the merge fallback); with lam > 0 the penalty decreases
+    toward the last block, so the picks are the last blocks, newest first."""
+    q = torch.randn(2, 10, 128, generator=torch.Generator().manual_seed(5)).to(dev, torch.bfloat16)
+    c = torch.zeros(2, nb, 128, device=dev, dtype=torch.bfloat16)
+    idx = _hip().hip_index_topk_decode(q, c, lambda_dist=lam, top_k=32)
+    exp = torch.arange(32) if lam == 0.0 else torch.arange(nb - 1, nb - 33, -1)
+    assert torch.equal(idx.cpu(), exp.expand(2, 10, 32))
+
+
+def test_index_topk_decode_baseline_needle(dev):
+    """BASELINE config 3 shape for one batch element pair: 15,625 bf16 centroids with a
+    planted block; the needle block is selected first for every head aligned with it and
+    the full top-32 matches the oracle wherever its scores separate."""
+    g = torch.Generator().manual_seed(11)
+    B, Hq, nb, d = 2, 10, 15625, 128
+    c = torch.randn(B, nb, d, generator=g).bfloat16()
+    q = torch.randn(B, Hq, d, generator=g).bfloat16()
+    c[0, 777] = (q[0, 3].float() * 4).bfloat16()          # needle aligned with head 3
+    idx, sc = _hip().hip_index_topk_decode(q.to(dev), c.to(dev), lambda_dist=0.1, top_k=32, return_scores=True)
+    ref = oidx.decode_scores(to_np(q), to_np(c), 0.1)
+    assert_close(sc, ref, 1e-5, 1e-4, "decode scores")
+    assert idx[0, 3, 0].item() == 777
+    assert topk_agrees(idx.cpu().numpy(), ref, 32) >= B * Hq - 2
+
+
 @pytest.mark.parametrize("B,L,nb_blocks,k,lam", [(1, 64, 1, 1, 0.5), (2, 128, 2, 2, 0.5), (3, 256, 4, 4, 0.5),
                                                   (2, 512, 8, 8, 1.0), (1, 100, 2, 2, 0.25), (2, 65, 2, 2, 0.0),
                                                   (2, 16, 1, 2, 0.5), (1, 512, 8, 32, 0.5), (2, 4096, 64, 32, 0.1)])
@@ -234,6 +263,22 @@ def test_maba_sa_decode(dev, L, K, Hi):
     hca = _hip().hip_hca_pool(c.to(dev), pool=64)
     Wk_h = Wk.view(H, dh, dc)
     q_lat = torch.einsum("bhd,hdc->bhc", q, Wk_h)          # W_k,h^T q_h
+    z = _hip().hip_maba_sa_decode(q_lat.to(dev), c.to(dev), hca, idx.to(dev), gate.to(dev), L=L,
+                                  scale=1.0 / math.sqrt(dh))
+    out = torch.einsum("bhc,hdc->bhd", z.cpu(), Wv.view(H, dh, dc))
+    exp = osa.maba_sa_decode(to_np(q), to_np(c), to_np(Wk), to_np(Wv), to_np(idx).astype(np.int64),
+                             to_np(gate), means=to_np(hca))
+    assert_close(out, exp, 2e-3, 2e-3, "maba_sa")
+
+
+@pytest.mark.parametrize("L,K,Hi", [(8192, 64, 10), (20000, 64, 1)])
+def test_maba_sa_decode_many_segments(dev, L, K, Hi):
+    """Enough tiles that every wave runs several tiles (register prefetch path) and the
+    combine merges partials from many workgroups."""
+    B, H, dh, dc = 4, 10, 64, 128
+    c, Wk, Wv, q, idx, gate = _sa_case(B, H, dh, dc, L, K, Hi, L + K + 1, dev)
+    hca = _hip().hip_hca_pool(c.to(dev), pool=64)
+    q_lat = torch.einsum("bhd,hdc->bhc", q, Wk.view(H, dh, dc))
     z = _hip().hip_maba_sa_decode(q_lat.to(dev), c.to(dev), hca, idx.to(dev), gate.to(dev), L=L,
                                   scale=1.0 / math.sqrt(dh))
     out = torch.einsum("bhc,hdc->bhd", z.cpu(), Wv.view(H, dh, dc))
