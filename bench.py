@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--skip-decode", action="store_true", help="do not run the decode benchmarks")
     ap.add_argument("--only-prefill", action="store_true", help="time only the DGDA prefill step (for profiling)")
     ap.add_argument("--only-decode", action="store_true", help="run only the decode benchmarks (for profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 256 MiB device-to-device copy (calibrates FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -259,6 +261,14 @@ def main():
     import torch
     from maba_sparse.kernels import hip_backend as hb
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)     # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "copies": 5}), flush=True)
+        return
     if args.only_decode:
         print(json.dumps({"decode": decode_benches(dev, args.steps)}), flush=True)
         return

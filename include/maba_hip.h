@@ -19,7 +19,7 @@
  *                                   (op "compute_centroids"; common.py:329-350)
  *   maba_hip_index_topk             dispatcher.py:424-465
  *                                   (op "index_topk"; cpu_indexer.py:53-112)
- *   maba_hip_index_topk_decode      layers/indexer.py:391-402 (inline decode
+ *   maba_hip_index_topk_decode      layers/indexer.py:101-112 (inline decode
  *                                   scoring + torch.topk; no dispatcher op)
  *   maba_hip_stream_superposition   dispatcher.py:468-508
  *                                   (op "stream_superposition"; common.py:406-438)

@@ -3,7 +3,7 @@
 // Decode (reference: maba_sparse/layers/indexer.py:101-112):
 //   s[h,n] = (q_h / sqrt(d)) . c_n - lam * log1p(max(nb-1-n, 0))   (no mask)
 //   idx[h] = top min(K, nb) of s[h,:], score descending, ties -> lower index
-// Prefill (reference: maba_sparse/kernels/cpu_indexer.py:362-378):
+// Prefill (reference: maba_sparse/kernels/cpu_indexer.py:91-108):
 //   s[t,n] = (q_t / sqrt(d)) . c_n - lam * log1p(|t//bs - n|), -inf if n > t//bs
 //
 // Scores are fp32 dots of the stored inputs (bf16/f16/f32 converted exactly

@@ -3,7 +3,7 @@
 //  * compute_centroids: c_n = 0.5*(mean + max) over a block of block_size
 //    tokens; the tail block is zero-padded and the padding takes part in both
 //    the mean (divide by block_size) and the max
-//    (reference: maba_sparse/kernels/common.py:343-350, cpu_indexer.py:306-320).
+//    (reference: maba_sparse/kernels/common.py:343-350, cpu_indexer.py:38-50).
 //  * hca_pool: mean of each complete pool-token block of the MLA latent cache
 //    (reference: layers/sparse_attention.py:206).
 //

@@ -211,7 +211,7 @@ def ref_dgda_sequential(q, k, v, alpha=None, b=None, w=None, initial_state=None,
 
 def ref_compute_centroids(k_idx, block_size: int = 64, **kwargs: Any) -> torch.Tensor:
     """``0.5*(mean+max)`` over zero-padded blocks, in fp32, returned in the input dtype
-    (reference common.py:329-350, cpu_indexer.py:306-320)."""
+    (reference common.py:329-350, cpu_indexer.py:38-50)."""
     if k_idx.dim() != 3:
         raise ValueError(f"k_idx must be 3D [B, L, d_idx], got {list(k_idx.shape)}")
     if block_size <= 0:
@@ -264,7 +264,7 @@ def ref_index_topk(q_idx, centroids, lambda_dist: float = 0.5, top_k: int = 32, 
 def ref_index_topk_decode(q, centroids, lambda_dist: float = 0.5, top_k: int = 32,
                           return_scores: bool = False, **kwargs: Any):
     """Decode scoring (query block = nb-1, no mask) + top-k for ``q [B, Hq, d]``
-    (reference layers/indexer.py:391-402, computed in fp32)."""
+    (reference layers/indexer.py:101-112, computed in fp32)."""
     lam = kwargs.get("dist_lambda", lambda_dist)
     nb = centroids.shape[1]
     d = q.shape[-1]

@@ -16,7 +16,7 @@ Differences, all deliberate:
 * A missing HIP library is never papered over: ``HipLibraryMissing`` propagates
   instead of falling back, so a GPU run cannot silently take a non-HIP path.
 * Three ops the reference only has as inline torch code get dispatcher entries:
-  ``index_topk_decode`` (layers/indexer.py:391-402), ``hca_pool``
+  ``index_topk_decode`` (layers/indexer.py:101-112), ``hca_pool``
   (layers/sparse_attention.py:206) and ``maba_sa_decode``
   (layers/sparse_attention.py:79-219,263-275).
 * ``allow_mixed_dtypes=True`` (keyword) lets ``dgda_prefill``/``dgda_step``

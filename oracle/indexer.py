@@ -8,28 +8,28 @@ Functions
 ``compute_centroids``  ``c_n = 0.5*(mean + max)`` over 64-token blocks; the
                        last block is zero-padded and the zeros take part in
                        both the mean (divide by block size) and the max
-                       (common.py:343-350, cpu_indexer.py:306-320).  Output
+                       (common.py:343-350, cpu_indexer.py:38-50).  Output
                        is rounded to the input dtype by the caller
-                       (cpu_indexer.py:320).  Pinned by the needle and padding
+                       (cpu_indexer.py:50).  Pinned by the needle and padding
                        known answers (test_triton_indexer.py:147-168) and
                        zeros-in/zeros-out (test_triton_indexer.py:488-497).
 ``prefill_scores``     causal prefill scores ``(q_t/sqrt d).c_n -
                        lam*log1p(|t//bs - n|)``, ``-inf`` for ``n > t//bs``
-                       (cpu_indexer.py:362-375), in float64.  Pinned by the
+                       (cpu_indexer.py:91-102), in float64.  Pinned by the
                        ``-0.75*ln 3`` known answer (test_indexer.py:143-164),
                        the causal pattern (test_triton_indexer.py:222-244) and
                        the penalty order ``[3,2,1,0]``
                        (test_triton_indexer.py:247-255).
 ``decode_scores``      decode scores with ``q_blk = nb-1`` and no mask
-                       (layers/indexer.py:391-397).  Pinned by the same
+                       (layers/indexer.py:101-107).  Pinned by the same
                        penalty closed form and brute force on tiny inputs.
 ``topk_desc``          selection of the top ``min(K, nb)`` entries sorted by
                        score descending, ties by index ascending.  torch.topk
-                       leaves tie order unspecified (cpu_indexer.py:378), so
+                       leaves tie order unspecified (cpu_indexer.py:107-108), so
                        tied orders are "parity unpinned" and the tests compare
                        selections only where the score gap exceeds 1e-4.
 ``decode_centroid_cache`` the per-step centroid cache of
-                       layers/indexer.py:352-372: complete blocks plus the
+                       layers/indexer.py:62-81: complete blocks plus the
                        zero-padded partial tail block.
 """
 from __future__ import annotations
@@ -53,7 +53,7 @@ def compute_centroids(k_idx, block_size=64):
 
 
 def prefill_scores(q_idx, centroids, lam, block_size=64):
-    """Causal prefill score matrix ``[B, L, nb]`` (cpu_indexer.py:362-375)."""
+    """Causal prefill score matrix ``[B, L, nb]`` (cpu_indexer.py:91-102)."""
     q = np.asarray(q_idx, np.float64)
     c = np.asarray(centroids, np.float64)
     B, L, d = q.shape
@@ -72,7 +72,7 @@ def decode_scores(q, centroids, lam):
     """Decode scores ``[B, Hq, nb]`` for queries ``q [B, Hq, d]``.
 
     ``q_blk = nb - 1``; ``dist = max(q_blk - n, 0)``; no causal mask
-    (layers/indexer.py:391-397).  ``Hq`` generalises the reference's single
+    (layers/indexer.py:101-107).  ``Hq`` generalises the reference's single
     indexer query to several query heads sharing one centroid set.
     """
     q = np.asarray(q, np.float64)
@@ -106,7 +106,7 @@ def decode_centroid_cache(k_idx_cache, block_size=64):
     """Centroids seen by a decode step whose key cache is ``k_idx_cache [B, L, d]``.
 
     Complete blocks each give one centroid; a partial tail block gives the
-    zero-padded tail centroid (layers/indexer.py:355-372).  The result equals
+    zero-padded tail centroid (layers/indexer.py:62-81).  The result equals
     ``compute_centroids`` over the whole cache because a block's centroid only
     depends on its own tokens.
     """

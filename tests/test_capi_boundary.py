@@ -1,0 +1,148 @@
+"""The C-ABI boundary on the CPU: the library loads, exports every symbol that
+``include/maba_hip.h`` declares, and its host-side validation and workspace
+sizing behave as documented.  No call here launches GPU work: every entry point
+exercised returns before its first HIP call.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from maba_sparse import _native as N
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "maba_hip.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)      # drop comments
+    text = re.sub(r"//[^\n]*", "", text)
+    return set(re.findall(r"\b(maba_hip_\w+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip("libmaba_hip.so not built (run __graft_entry__.build())")
+    return N.load()
+
+
+def test_header_matches_binding_table():
+    declared = _declared_symbols()
+    assert declared, "no declarations parsed"
+    assert declared == set(N.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(N.LIB_PATH)
+    for name in sorted(_declared_symbols()):
+        assert hasattr(raw, name), f"{name} declared in maba_hip.h but not exported"
+
+
+def test_abi_version(lib):
+    assert lib.maba_hip_abi_version() == 1
+
+
+def _t(shape, dtype=N.MABA_BF16, strides=None, data=0x10000):
+    """A descriptor that is never dereferenced (validation-only calls)."""
+    t = N.MabaTensor()
+    t.data = data
+    t.dtype = dtype
+    t.ndim = len(shape)
+    if strides is None:
+        strides, acc = [], 1
+        for s in reversed(shape):
+            strides.insert(0, acc)
+            acc *= s
+    for i, (s, st) in enumerate(zip(shape, strides)):
+        t.shape[i] = s
+        t.stride[i] = st
+    return ctypes.byref(t)
+
+
+def test_prefill_rejects_bad_rank_with_message(lib):
+    q = _t([2, 3, 4])
+    rc = lib.maba_hip_dgda_prefill(q, q, q, None, q, q, q, None, q, q, 64, None, 0, None)
+    assert rc == N.MABA_ERR_INVALID
+    assert b"q must be [B,H,L,dk]" in lib.maba_hip_last_error()
+
+
+def test_prefill_requires_a_decay_gate(lib):
+    B, H, L, d = 1, 2, 8, 64
+    q = _t([B, H, L, d])
+    s = _t([B, H, d, d], N.MABA_F32)
+    rc = lib.maba_hip_dgda_prefill(q, q, q, None, None, q, q, None, q, s, 64, None, 0, None)
+    assert rc == N.MABA_ERR_INVALID
+    assert b"alpha or log_alpha" in lib.maba_hip_last_error()
+
+
+def test_prefill_shape_mismatch(lib):
+    q = _t([1, 2, 8, 64])
+    k = _t([1, 2, 9, 64])
+    s = _t([1, 2, 64, 64], N.MABA_F32)
+    rc = lib.maba_hip_dgda_prefill(q, k, q, None, q, q, q, None, q, s, 64, None, 0, None)
+    assert rc == N.MABA_ERR_INVALID
+
+
+def test_prefill_workspace_size_at_baseline_shape(lib):
+    """B=4, H=10, T=32768: 32 segments of 1024 tokens per head, each carrying a
+    [64, 128] fp32 aggregate plus a [64, 64] fp32 start state."""
+    B, H, T, d = 4, 10, 32768, 64
+    q = _t([B, H, T, d])
+    gate = _t([B, H, T, d], N.MABA_F32, strides=[H * T, T, 1, 0])   # per-token, stride-0 channels
+    n = lib.maba_hip_dgda_prefill_workspace_size(q, q, gate, gate)
+    nseg = T // 1024
+    assert n == B * H * nseg * 64 * (128 + 64) * 4
+    per_channel = _t([B, H, T, d], N.MABA_F32)
+    assert lib.maba_hip_dgda_prefill_workspace_size(q, q, per_channel, gate) == 0   # sequential path
+
+
+def test_index_topk_decode_validation(lib):
+    q = _t([2, 4, 128])
+    c = _t([2, 100, 128])
+    out = _t([2, 4, 32], N.MABA_I64)
+    rc = lib.maba_hip_index_topk_decode(q, c, 0.1, 0, out, None, None, 0, None)
+    assert rc == N.MABA_ERR_INVALID and b"top_k must be positive" in lib.maba_hip_last_error()
+    rc = lib.maba_hip_index_topk_decode(q, c, 0.1, 65, _t([2, 4, 65], N.MABA_I64), None, None, 0, None)
+    assert rc == N.MABA_ERR_UNSUPPORTED
+    rc = lib.maba_hip_index_topk_decode(q, c, 0.1, 32, _t([2, 4, 32], N.MABA_F32), None, None, 0, None)
+    assert rc == N.MABA_ERR_DTYPE
+    rc = lib.maba_hip_index_topk_decode(q, c, 0.1, 32, out, None, None, 0, None)
+    assert rc == N.MABA_ERR_WORKSPACE
+
+
+def test_index_topk_decode_workspace_covers_scores_and_tile_maxima(lib):
+    B, Hq, nb = 8, 10, 15625
+    tiles = (nb + 63) // 64
+    n = lib.maba_hip_index_topk_decode_workspace_size(B, Hq, nb, 32)
+    assert n >= B * Hq * tiles * 64 * 4 + B * Hq * tiles * 8
+
+
+def test_maba_sa_decode_validation(lib):
+    B, H, dc, L = 2, 4, 128, 1000
+    q = _t([B, H, dc], N.MABA_F32)
+    c = _t([B, L, dc])
+    hca = _t([B, L // 64, dc])
+    idx = _t([B, 3, 32], N.MABA_I64)      # neither 1 nor H index rows
+    gate = _t([B, 3], N.MABA_F32)
+    out = _t([B, H, dc], N.MABA_F32)
+    rc = lib.maba_hip_maba_sa_decode(q, c, hca, idx, gate, L, 0.125, 128, 4, 64, 64, out, None, 0, None)
+    assert rc == N.MABA_ERR_INVALID and b"idx must be [B,1|H,K]" in lib.maba_hip_last_error()
+    idx = _t([B, 1, 32], N.MABA_I64)
+    rc = lib.maba_hip_maba_sa_decode(q, c, hca, idx, gate, L + 1, 0.125, 128, 4, 64, 64, out, None, 0, None)
+    assert rc == N.MABA_ERR_INVALID and b"L out of range" in lib.maba_hip_last_error()
+    rc = lib.maba_hip_maba_sa_decode(q, c, hca, idx, gate, L, 0.125, 128, 4, 64, 64, out, None, 0, None)
+    assert rc == N.MABA_ERR_WORKSPACE
+
+
+def test_check_maps_status_to_python_exceptions(lib):
+    q = _t([2, 3, 4])
+    rc = lib.maba_hip_dgda_prefill(q, q, q, None, q, q, q, None, q, q, 64, None, 0, None)
+    with pytest.raises(ValueError, match="dgda_prefill"):
+        N.check(rc, "dgda_prefill")
+    rc = lib.maba_hip_index_topk_decode(_t([2, 4, 128]), _t([2, 100, 128]), 0.1, 65,
+                                        _t([2, 4, 65], N.MABA_I64), None, None, 0, None)
+    with pytest.raises(NotImplementedError):
+        N.check(rc, "index_topk_decode")
