@@ -132,7 +132,10 @@ def prefill_flops(B, H, T, d, C=64):
     return B * H * (T // C) * (8 * C * C * d + 6 * C * d * d)
 
 
-def cpu_baseline(B=4, H=10, T=16384, d=64):
+def cpu_baseline(B=4, H=10, T=32768, d=64, min_seconds=10.0):
+    """The C/OpenMP restatement of the reference CPU chunked prefill (oracle/dgda_chunked.c,
+    cpu_dgda.py:33-197 streamed per chunk) on the config-2 shape in fp32: 2 untimed
+    repeats, then repeats until ``min_seconds`` have elapsed (benchmark.py:684-745 method)."""
     import numpy as np
     from oracle import dgda_c
     dgda_c.build()
@@ -145,13 +148,31 @@ def cpu_baseline(B=4, H=10, T=16384, d=64):
     la = (-np.log1p(np.exp(r.standard_normal((B, H, T, 1), dtype=np.float32) + 2))).astype(np.float32)
     be = (1 / (1 + np.exp(-r.standard_normal((B, H, T, 1), dtype=np.float32)))).astype(np.float32)
     omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-    threads = min(os.cpu_count() or 1, omp if omp > 0 else (os.cpu_count() or 1), B * H)
-    t0 = time.perf_counter()
-    dgda_c.dgda_prefill_chunked_c(q, k, v, la, be, be, chunk_size=64, nthreads=threads)
-    dt = time.perf_counter() - t0
-    return {"value": B * T / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"dgda_prefill B={B} H={H} T={T} d={d} (first {T} tokens of config 2), fp32, chunk 64, "
-                      f"{dt:.1f} s, oracle/dgda_chunked.c"}
+    ncpu = os.cpu_count() or 1
+    threads = min(ncpu, omp if omp > 0 else ncpu, B * H)
+
+    def run():
+        dgda_c.dgda_prefill_chunked_c(q, k, v, la, be, be, chunk_size=64, nthreads=threads)
+
+    for _ in range(2):
+        run()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds and reps >= 3:
+            break
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in fh if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": reps * B * T / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"dgda_prefill config 2 shape B={B} H={H} T={T} d={d}, fp32, chunk 64, "
+                      f"{reps} timed repeats in {dt:.1f} s after 2 warm-ups, oracle/dgda_chunked.c (OpenMP over b*h)",
+            "host": {"cpu_model": cpu_model, "os_cpu_count": ncpu, "omp_num_threads": omp or None}}
 
 
 def decode_benches(dev, steps: int):

@@ -1,0 +1,224 @@
+"""MABA-SA layer: the caller of the indexer, the three attention streams and the
+gate superposition (reference: layers/sparse_attention.py:11-277).
+
+Decode (one token): everything runs in latent space through the fused
+``maba_sa_decode`` op.  ``q_lat[b,h] = W_k,h^T q[b,h]`` (absorbed key
+up-projection), the op returns ``z[b,h] = sum_s g_s sum_j p_sj c_j`` over the
+latent rows of the local window + sinks, the indexer's gathered blocks and the
+HCA block means, and the layer applies ``W_v,h`` and ``o_proj``.  This replaces
+the reference's per-step concatenation of per-head K/V caches
+(sparse_attention.py:241-261) and its per-step re-pooling of the whole latent
+cache (:206): HCA means are kept and extended by one mean per completed block.
+``LatentCache`` additionally offers a preallocated latent cache for serving loops
+(``decode_step``), avoiding the O(L) ``torch.cat`` that the reference's
+``forward(x, past_c_kv)`` interface implies.
+
+Prefill (several tokens) follows the reference streams with dense torch code:
+causal sliding window + sinks (:95-105), per-query gathered blocks (:145-171),
+HCA over complete-block means with the early running-mean rule (:173-219), then
+``stream_superposition``.  A prefill-side fused kernel is future work.
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from maba_sparse.kernels.dispatcher import (dispatch_hca_pool, dispatch_maba_sa_decode,
+                                            dispatch_stream_superposition)
+from maba_sparse.layers.indexer import DGIndexer, _Growing
+
+
+class LatentCache:
+    """Preallocated decode state of one layer: latent rows ``[B, capacity, d_c]`` and
+    the means of their complete ``pool``-token blocks."""
+
+    def __init__(self, batch: int, capacity: int, d_c: int, pool: int = 64,
+                 device=None, dtype: torch.dtype = torch.float32) -> None:
+        self.c = torch.empty(batch, capacity, d_c, device=device, dtype=dtype)
+        self.hca = torch.empty(batch, max(1, capacity // pool), d_c, device=device, dtype=dtype)
+        self.pool = pool
+        self.n = 0       # latent rows held
+        self.nh = 0      # complete-block means held
+
+    def append(self, c_new: torch.Tensor) -> None:
+        m = c_new.shape[1]
+        if self.n + m > self.c.shape[1]:
+            raise ValueError(f"LatentCache full: {self.n} + {m} > {self.c.shape[1]}")
+        self.c[:, self.n: self.n + m] = c_new.to(self.c.dtype)
+        self.n += m
+        full = self.n // self.pool
+        if full > self.nh:
+            lo, hi = self.nh * self.pool, full * self.pool
+            self.hca[:, self.nh: full] = dispatch_hca_pool(self.c[:, lo:hi], pool=self.pool)
+            self.nh = full
+
+
+class MabaSparseAttention(nn.Module):
+    def __init__(self, config: Optional[Any] = None, dim: int = 640, n_heads: int = 10, d_head: int = 64,
+                 d_c: int = 128, window_size: int = 128, block_size: int = 64, top_k: int = 32,
+                 hca_pool_size: int = 64, dist_lambda: float = 0.5, d_idx: int = 64,
+                 ablation_mode: str = "full") -> None:
+        super().__init__()
+        g = (lambda n, alt, d: getattr(config, n, getattr(config, alt, d)) if alt else getattr(config, n, d)) \
+            if config is not None else (lambda n, alt, d: d)
+        self.dim = g("dim", "d_model", dim)
+        self.n_heads = g("n_heads", "num_heads", n_heads)
+        self.d_head = g("d_head", None, d_head)
+        self.d_c = g("d_c", None, d_c)
+        self.window_size = g("window_size", None, window_size)
+        self.block_size = g("block_size", None, block_size)
+        self.top_k = g("top_k", None, top_k)
+        self.hca_pool_size = g("hca_pool_size", None, hca_pool_size)
+        self.dist_lambda = g("dist_lambda", None, dist_lambda)
+        self.n_sink_tokens = g("n_sink_tokens", None, 4)
+        d_idx = g("d_idx", None, d_idx)
+        self.ablation_mode = ablation_mode if ablation_mode is not None else g("ablation_mode", None, "full")
+        self.scale = 1.0 / math.sqrt(self.d_head)
+        H, dh = self.n_heads, self.d_head
+        self.q_proj = nn.Linear(self.dim, H * dh, bias=False)
+        self.kv_down_proj = nn.Linear(self.dim, self.d_c, bias=False)
+        self.k_up_proj = nn.Linear(self.d_c, H * dh, bias=False)
+        self.v_up_proj = nn.Linear(self.d_c, H * dh, bias=False)
+        self.o_proj = nn.Linear(H * dh, self.dim, bias=False)
+        self.stream_gate = nn.Linear(self.dim, 3, bias=True)
+        self.indexer = DGIndexer(dim=self.dim, d_idx=d_idx, block_size=self.block_size, top_k=self.top_k,
+                                 dist_lambda=self.dist_lambda)
+        self._hca_means: Optional[_Growing] = None
+
+    def reset_cache(self) -> None:
+        self.indexer.reset_cache()
+        self._hca_means = None
+
+    def get_gate_weights(self, x: torch.Tensor) -> torch.Tensor:
+        return F.softmax(self.stream_gate(x), dim=-1)
+
+    # ------------------------------------------------------------ decode (fused)
+    def _absorbed_query(self, x: torch.Tensor) -> torch.Tensor:
+        """``W_k,h^T q_h`` for the single token of ``x [B, 1, dim]`` -> ``[B, H, d_c]`` fp32."""
+        B = x.shape[0]
+        q = self.q_proj(x).view(B, self.n_heads, self.d_head).float()
+        Wk = self.k_up_proj.weight.float().view(self.n_heads, self.d_head, self.d_c)
+        return torch.einsum("bhd,hdc->bhc", q, Wk)
+
+    def _heads_out(self, z: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """``W_v,h z_h`` then ``o_proj``; ``z [B, H, d_c]`` -> ``[B, 1, dim]``."""
+        B = z.shape[0]
+        Wv = self.v_up_proj.weight.float().view(self.n_heads, self.d_head, self.d_c)
+        o = torch.einsum("bhc,hdc->bhd", z.float(), Wv).reshape(B, 1, self.n_heads * self.d_head)
+        return self.o_proj(o.to(dtype))
+
+    def _hca_for(self, c_full: torch.Tensor) -> torch.Tensor:
+        """Complete-block means of ``c_full``, extended incrementally across decode steps."""
+        L, r = c_full.shape[1], self.hca_pool_size
+        full = L // r
+        h = self._hca_means
+        if h is not None and h.shape[0] == c_full.shape[0] and full - 1 <= h.n <= full:
+            if h.n == full - 1:
+                h.append(dispatch_hca_pool(c_full[:, (full - 1) * r: full * r], pool=r))
+        else:
+            self._hca_means = _Growing(dispatch_hca_pool(c_full, pool=r)) if full > 0 else None
+        if self._hca_means is None:
+            return c_full.new_zeros(c_full.shape[0], 1, self.d_c)
+        return self._hca_means.view()
+
+    def _decode(self, x: torch.Tensor, c_all: torch.Tensor, L: int, hca: torch.Tensor,
+                idx: torch.Tensor) -> torch.Tensor:
+        z = dispatch_maba_sa_decode(self._absorbed_query(x), c_all, hca, idx, self.stream_gate(x).view(-1, 3),
+                                    L=L, scale=self.scale, window=self.window_size, n_sink=self.n_sink_tokens,
+                                    block_size=self.block_size, pool=self.hca_pool_size)
+        return self._heads_out(z, x.dtype)
+
+    def decode_step(self, x: torch.Tensor, cache: LatentCache,
+                    past_centroids: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One decode token over a preallocated ``LatentCache`` (appends this token's latent)."""
+        if x.shape[1] != 1:
+            raise ValueError("decode_step takes one token")
+        cache.append(self.kv_down_proj(x))
+        idx, _ = self.indexer(x, return_scores=False, past_centroids=past_centroids)
+        hca = cache.hca[:, : max(cache.nh, 1)]
+        return self._decode(x, cache.c, cache.n, hca, idx)
+
+    # ------------------------------------------------------------ prefill (dense)
+    def _dense_streams(self, x, q, c_full, idx):
+        b, h, lq, dh = q.shape
+        lkv = c_full.shape[1]
+        k = self.k_up_proj(c_full).view(b, lkv, h, dh).transpose(1, 2)
+        v = self.v_up_proj(c_full).view(b, lkv, h, dh).transpose(1, 2)
+        pos = (lkv - lq) + torch.arange(lq, device=x.device)          # absolute query positions
+        j = torch.arange(lkv, device=x.device)
+
+        def masked_attend(scores, mask, vals):
+            p = torch.nan_to_num(F.softmax(scores.masked_fill(~mask, float("-inf")), dim=-1), nan=0.0)
+            return p @ vals
+
+        # local: causal, within the window or one of the sinks
+        keep = (j[None] <= pos[:, None]) & (((pos[:, None] - j[None]) < self.window_size) |
+                                             (j[None] < min(self.n_sink_tokens, lkv)))
+        ol = masked_attend((q @ k.transpose(-1, -2)) * self.scale, keep[None, None], v)
+
+        # sparse: per query, the tokens of its selected blocks that are < L and <= its position
+        bs = self.block_size
+        nb = (lkv + bs - 1) // bs
+        ak = idx.shape[-1]
+        pad = nb * bs - lkv
+        kb = F.pad(k, (0, 0, 0, pad)).view(b, h, nb, bs, dh)
+        vb = F.pad(v, (0, 0, 0, pad)).view(b, h, nb, bs, dh)
+        os_ = torch.zeros_like(ol)
+        for t0 in range(0, lq, 128):
+            t1 = min(t0 + 128, lq)
+            bi = idx[:, t0:t1] if idx.shape[1] == lq else idx[:, :1].expand(b, t1 - t0, ak)
+            sel = bi.reshape(b, 1, -1, 1, 1).expand(b, h, (t1 - t0) * ak, bs, dh)
+            ks = torch.gather(kb, 2, sel).view(b, h, t1 - t0, ak * bs, dh)
+            vs = torch.gather(vb, 2, sel).view(b, h, t1 - t0, ak * bs, dh)
+            tok = (bi[..., None] * bs + torch.arange(bs, device=x.device)).reshape(b, t1 - t0, ak * bs)
+            ok = (tok < lkv) & (tok <= pos[t0:t1, None])
+            s = (q[:, :, t0:t1, None, :] @ ks.transpose(-1, -2)).squeeze(-2) * self.scale
+            p = torch.nan_to_num(F.softmax(s.masked_fill(~ok[:, None], float("-inf")), dim=-1), nan=0.0)
+            os_[:, :, t0:t1] = (p[..., None, :] @ vs).squeeze(-2)
+
+        # HCA: complete-block means whose last token is <= the query; running mean before that
+        r = self.hca_pool_size
+        oh = torch.zeros_like(ol)
+        if self.ablation_mode != "no_hca":
+            early = pos < (r - 1)
+            if early.any():
+                cm = torch.cumsum(c_full[:, : int(pos[early].max()) + 1], dim=1)
+                cm = cm / torch.arange(1, cm.shape[1] + 1, device=x.device).view(1, -1, 1)
+                oh[:, :, early] = self.v_up_proj(cm[:, pos[early]]).view(b, -1, h, dh).transpose(1, 2)
+            nc = lkv // r
+            if (~early).any() and nc > 0:
+                means = c_full[:, : nc * r].reshape(b, nc, r, self.d_c).mean(dim=2)
+                kh = self.k_up_proj(means).view(b, nc, h, dh).transpose(1, 2)
+                vh = self.v_up_proj(means).view(b, nc, h, dh).transpose(1, 2)
+                ends = (torch.arange(nc, device=x.device) + 1) * r - 1
+                late = ~early
+                ok = ends[None] <= pos[late][:, None]
+                oh[:, :, late] = masked_attend((q[:, :, late] @ kh.transpose(-1, -2)) * self.scale,
+                                               ok[None, None], vh)
+        return ol, os_, oh
+
+    def forward(self, x: torch.Tensor, past_c_kv: Optional[torch.Tensor] = None,
+                past_centroids: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        b, l, _ = x.shape
+        ic = self.indexer._cached_k_idx
+        if past_c_kv is None or (ic is not None and ic.shape[1] != past_c_kv.shape[1]):
+            self.reset_cache()
+        c_kv = self.kv_down_proj(x)
+        c_full = torch.cat([past_c_kv, c_kv], dim=1) if past_c_kv is not None else c_kv
+        idx, _ = self.indexer(x, return_scores=False, past_centroids=past_centroids)
+        if l == 1 and self.ablation_mode != "no_hca":
+            return self._decode(x, c_full, c_full.shape[1], self._hca_for(c_full), idx), c_full
+        q = self.q_proj(x).view(b, l, self.n_heads, self.d_head).transpose(1, 2)
+        ol, os_, oh = self._dense_streams(x, q, c_full, idx)
+        if l > 1 and not self.training and self.ablation_mode != "no_hca":
+            self._hca_for(c_full)       # seed the incremental means for the decode steps
+        o = dispatch_stream_superposition(ol, os_, oh, gate_logits=self.stream_gate(x))
+        o = o.transpose(1, 2).reshape(b, l, self.n_heads * self.d_head).to(q.dtype)
+        return self.o_proj(o), c_full
+
+
+MABASALayer = MabaSparseAttention

@@ -1,0 +1,92 @@
+"""The callers on the GPU: each layer on cuda:0 (HIP ops) against the same layer on
+the CPU (torch reference ops), over prefill + decode steps that cross 64-token
+block boundaries.
+
+Tolerances: fp32 modules 2e-3 (the north-star DGDA / sparse-attention bar);
+indexer picks must agree wherever the CPU scores separate by more than 1e-4.
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_close, topk_agrees
+from maba_sparse.layers import DGDALayer, DGIndexer, LatentCache, MabaSparseAttention
+
+pytestmark = pytest.mark.gpu
+
+
+def _x(B, T, D, seed):
+    return torch.randn(B, T, D, generator=torch.Generator().manual_seed(seed))
+
+
+def test_dgda_layer_gpu_matches_cpu(dev):
+    torch.manual_seed(0)
+    cpu = DGDALayer(dim=128, n_heads=2)
+    gpu = copy.deepcopy(cpu).to(dev)
+    x = _x(2, 150, 128, 1)
+    with torch.no_grad():
+        yc, Sc, csc = cpu(x[:, :140])
+        yg, Sg, csg = gpu(x[:, :140].to(dev))
+        assert_close(yg, yc.numpy(), 2e-3, 2e-3, "prefill out")
+        assert_close(Sg, Sc.numpy(), 2e-3, 2e-3, "prefill state")
+        for t in range(140, 150):
+            yc, Sc, csc = cpu.step(x[:, t:t + 1], state=Sc, conv_state=csc)
+            yg, Sg, csg = gpu.step(x[:, t:t + 1].to(dev), state=Sg, conv_state=csg)
+            assert_close(yg, yc.numpy(), 2e-3, 2e-3, f"step {t}")
+        assert_close(Sg, Sc.numpy(), 2e-3, 2e-3, "final state")
+
+
+def test_indexer_layer_decode_gpu_matches_cpu(dev):
+    torch.manual_seed(2)
+    cpu = DGIndexer(dim=64, d_idx=64, top_k=8, dist_lambda=0.1).eval()
+    gpu = copy.deepcopy(cpu).to(dev)
+    x = _x(2, 700, 64, 3)
+    with torch.no_grad():
+        cpu(x[:, :600])
+        gpu(x[:, :600].to(dev))
+        checked = 0
+        for t in range(600, 700):
+            ic, cc, sc = cpu(x[:, t:t + 1], return_scores=True)
+            ig, cg, _ = gpu(x[:, t:t + 1].to(dev), return_scores=True)
+            assert_close(cg, cc.numpy(), 1e-5, 1e-5, f"centroids {t}")
+            checked += topk_agrees(ig.cpu().numpy(), sc.double().numpy(), 8)
+        assert checked > 150
+
+
+@pytest.mark.parametrize("L0", [100, 1000])
+def test_maba_sa_layer_decode_gpu_matches_cpu(dev, L0):
+    torch.manual_seed(4)
+    cpu = MabaSparseAttention(dim=128, n_heads=4, d_head=32, d_c=128, top_k=4).eval()
+    gpu = copy.deepcopy(cpu).to(dev)
+    x = _x(2, L0 + 70, 128, 5)
+    with torch.no_grad():
+        _, cc = cpu(x[:, :L0])
+        _, cg = gpu(x[:, :L0].to(dev))
+        for t in range(L0, L0 + 70):
+            yc, cc = cpu(x[:, t:t + 1], past_c_kv=cc)
+            yg, cg = gpu(x[:, t:t + 1].to(dev), past_c_kv=cg)
+            assert_close(yg, yc.numpy(), 2e-3, 2e-3, f"decode {t}")
+
+
+def test_maba_sa_layer_bf16_latent_cache(dev):
+    """bf16 module on the GPU (MFMA decode path) with a preallocated LatentCache, against
+    the fp32 CPU module: agreement to bf16 precision."""
+    torch.manual_seed(6)
+    cpu = MabaSparseAttention(dim=128, n_heads=10, d_head=64, d_c=128, top_k=4).eval()
+    gpu = copy.deepcopy(cpu).to(dev, torch.bfloat16)
+    for p_c, p_g in zip(cpu.parameters(), gpu.parameters()):
+        p_c.data.copy_(p_g.data.float().cpu())        # both see the same bf16-rounded weights
+    x = _x(1, 400, 128, 7).bfloat16().float()
+    with torch.no_grad():
+        _, cc = cpu(x[:, :300])
+        gpu(x[:, :300].to(dev, torch.bfloat16))
+        cache = LatentCache(1, 512, 128, pool=64, device=dev, dtype=torch.bfloat16)
+        cache.append(gpu.kv_down_proj(x[:, :300].to(dev, torch.bfloat16)))
+        for t in range(300, 400):
+            yc, cc = cpu(x[:, t:t + 1], past_c_kv=cc)
+            yg = gpu.decode_step(x[:, t:t + 1].to(dev, torch.bfloat16), cache)
+            ref = yc.numpy()
+            err = np.abs(yg.float().cpu().numpy() - ref).max() / max(np.abs(ref).max(), 1e-6)
+            assert err < 5e-2, (t, err)
