@@ -72,9 +72,10 @@ def test_maba_sa_layer_decode_gpu_matches_cpu(dev, L0):
 
 def test_maba_sa_layer_bf16_latent_cache(dev):
     """bf16 module on the GPU (MFMA decode path) with a preallocated LatentCache, against
-    the fp32 CPU module: agreement to bf16 precision."""
+    the fp32 CPU module: agreement to bf16 precision.  top_k exceeds the block count so
+    the bf16 and fp32 indexers cannot pick different blocks."""
     torch.manual_seed(6)
-    cpu = MabaSparseAttention(dim=128, n_heads=10, d_head=64, d_c=128, top_k=4).eval()
+    cpu = MabaSparseAttention(dim=128, n_heads=10, d_head=64, d_c=128, top_k=8).eval()
     gpu = copy.deepcopy(cpu).to(dev, torch.bfloat16)
     for p_c, p_g in zip(cpu.parameters(), gpu.parameters()):
         p_c.data.copy_(p_g.data.float().cpu())        # both see the same bf16-rounded weights
