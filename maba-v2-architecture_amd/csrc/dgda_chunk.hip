@@ -106,6 +106,21 @@ __device__ __forceinline__ i16x8 lds4x2(const short* base, int row, int c0, int 
   return cat8(lds4(base, row, c0, pitch), lds4(base, row, c0 + 16, pitch));
 }
 
+// Transposed operand read (ds_read_b64_tr_b16).  Within each 16-lane group the
+// instruction returns to lane i the elements src[4r + i/4][i%4] (r = 0..3), where
+// src[j] are the four bf16 at lane j's address.  Addressing lane j of group g at
+// row r0 + 4g + j/4, column c0 + 4(j%4) of a row-major matrix M therefore gives
+// lane (c16, g) the column fragment M[r0 + 4g + r][c0 + c16], r = 0..3 -- the
+// A (or B) operand fragment of M^T for a K-slice of 4 rows.
+__device__ __forceinline__ i16x4 ldsT4(const short* base, int r0, int c0, int c16, int g, int pitch) {
+  const short* p = base + (r0 + 4 * g + (c16 >> 2)) * pitch + c0 + 4 * (c16 & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p);
+}
+// Permuted-K operand of M^T: rows r0 + 4g..+3 and r0 + 16 + 4g..+3 of column c0 + c16.
+__device__ __forceinline__ i16x8 ldsT4x2(const short* base, int r0, int c0, int c16, int g) {
+  return cat8(ldsT4(base, r0, c0, c16, g, PITCH), ldsT4(base, r0 + 16, c0, c16, g, PITCH));
+}
+
 // Lower-triangular 64x64 matrices are stored as their 10 lower 16x16 tiles
 // (tile (I,J), J <= I, at index I(I+1)/2 + J), rows padded to TPITCH.
 __device__ __forceinline__ int tri_tile(int I, int J) { return I * (I + 1) / 2 + J; }
@@ -159,7 +174,6 @@ __device__ __forceinline__ void diag_block_inverse(const short* nh, const short*
 template <bool AGG>
 struct ChunkSmem {
   short K[CH * PITCH];        // k rows (token-major)
-  short KT[DK * PITCH];       // k^T (channel-major)
   short V[CH * PITCH];        // v rows
   short Q[AGG ? 1 : CH * PITCH];
   short LH[10 * TILE_ELEMS], LL[10 * TILE_ELEMS];                      // L hi/lo, strictly lower
@@ -273,8 +287,6 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
       *(i16x8*)(sm.K + t * PITCH + c8) = pk[it];
       *(i16x8*)(sm.V + t * PITCH + c8) = pv[it];
       if (!AGG) *(i16x8*)(sm.Q + t * PITCH + c8) = pq[it];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sm.KT[(c8 + j) * PITCH + t] = pk[it][j];
     }
     if (tid < CH) {
       float la = a.use_log ? pla : __logf(fmaxf(pla, 1e-20f));
@@ -471,7 +483,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
       f32x4 acc = Sr[kt] * gdec;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const i16x8 av = lds4x2(sm.KT, 16 * kt + c16, 32 * p + 4 * g, PITCH);
+        const i16x8 av = ldsT4x2(sm.K, 32 * p, 16 * kt, c16, g);
         acc = mma32(acc, av, cat8(wh[2 * p], wh[2 * p + 1]));
         acc = mma32(acc, av, cat8(wl[2 * p], wl[2 * p + 1]));
       }

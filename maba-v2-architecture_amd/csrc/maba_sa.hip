@@ -248,12 +248,21 @@ __global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a, int p1, 
 // and the workgroup writes one partial (max, sum, weighted latent sum) per head.
 //   scores  D[key][head] = C Q^T   (A: key rows straight from global memory,
 //                                   B: the queries, bf16 hi + lo, in registers)
-//   values  Z[dim][head] += C^T P  (A: the tile transposed into per-wave LDS,
+//   values  Z[dim][head] += C^T P  (A: C^T fragments read with ds_read_b64_tr_b16
+//                                   from the tile kept row-major in per-wave LDS,
 //                                   B: the probabilities, bf16 hi + lo, used in
 //                                   place from the score accumulators)
 typedef __attribute__((ext_vector_type(8))) short s16x8;
 typedef __attribute__((ext_vector_type(4))) short s16x4;
-constexpr int SA_CTP = 68;  // row pitch (bf16) of the transposed tile: 34 words, so rows 8 apart start 16 banks apart
+
+// Transposed read: within each 16-lane group, lane i receives src[4r + i/4][i%4]
+// (r = 0..3) where src[j] are the four bf16 at lane j's address.  Lane j of group g
+// addressing row r0 + 4g + j/4, column c0 + 4(j%4) of a row-major tile gets the
+// column fragment tile[r0 + 4g + r][c0 + c16], r = 0..3.
+__device__ __forceinline__ s16x4 sa_ldsT4(const short* tile, int pitch, int r0, int c0, int c16, int g) {
+  const short* p = tile + (r0 + 4 * g + (c16 >> 2)) * pitch + c0 + 4 * (c16 & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+}
 
 struct SaSeg {
   int stream, head_only;
@@ -327,7 +336,8 @@ __device__ __forceinline__ void sa_load_tile(const SaArgs& a, const SaSeg& sg, i
 template <int NP>  // d_c = 32 * NP
 __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg, int s_sp1, int tpw) {
   constexpr int DC = 32 * NP;
-  __shared__ __attribute__((aligned(16))) short s_ct[4][DC * SA_CTP];
+  constexpr int TP = DC + 8;  // row pitch (bf16) of the per-wave key tile: 16-B aligned, rows shift 4 banks
+  __shared__ __attribute__((aligned(16))) short s_tile[4][64 * TP];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 4, c16 = lane & 15;
   const int sid = blockIdx.x;
@@ -336,7 +346,7 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
   const SaSeg sg = sa_segment(a, sid, s_sp1, 4 * tpw);
   const int64_t t0 = sg.t_begin + (int64_t)wave * tpw;
   const int64_t t1 = min(sg.t_end, t0 + tpw);
-  short* ct = s_ct[wave];
+  short* tile = s_tile[wave];
 
   // queries (B operand of the scores): head c16, dims 32p + 8g .. +7, split hi/lo
   s16x8 qh[NP], ql[NP];
@@ -375,9 +385,8 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        // transposed copy for the value product: ct[dim][key]
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) ct[(32 * p + 8 * g + jj) * SA_CTP + 16 * rb + c16] = cv[rb][p][jj];
+        // row-major copy for the value product (read back transposed)
+        *(s16x8*)(tile + (16 * rb + c16) * TP + 32 * p + 8 * g) = cv[rb][p];
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
                                                       __builtin_bit_cast(bf16x8, qh[p]), acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
@@ -430,8 +439,8 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
       f32x4 acc = z[dt] * corr;
 #pragma unroll
       for (int p2 = 0; p2 < 2; ++p2) {
-        const s16x4 a0 = *(const s16x4*)(ct + (16 * dt + c16) * SA_CTP + 32 * p2 + 4 * g);
-        const s16x4 a1 = *(const s16x4*)(ct + (16 * dt + c16) * SA_CTP + 32 * p2 + 16 + 4 * g);
+        const s16x4 a0 = sa_ldsT4(tile, TP, 32 * p2, 16 * dt, c16, g);
+        const s16x4 a1 = sa_ldsT4(tile, TP, 32 * p2 + 16, 16 * dt, c16, g);
         const s16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
         const s16x8 bh = {ph[2 * p2][0], ph[2 * p2][1], ph[2 * p2][2], ph[2 * p2][3],
                           ph[2 * p2 + 1][0], ph[2 * p2 + 1][1], ph[2 * p2 + 1][2], ph[2 * p2 + 1][3]};
@@ -453,7 +462,7 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
   }
   // merge the four wave partials: s_z[wave][head][dim], s_m / s_l[wave][head]
   __syncthreads();
-  float* s_z = (float*)&s_ct[0][0];
+  float* s_z = (float*)&s_tile[0][0];
   float* s_m = s_z + 4 * 16 * DC;
   float* s_l = s_m + 64;
 #pragma unroll
