@@ -264,6 +264,11 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
     }
   };
   prefetch(c_begin);
+  // Pass 1, M waves: once the wave's 64x16 slab of M is exactly zero it stays zero
+  // (k M = 0, so v_e = 0, u = 0 and the update adds nothing), and the wave skips its
+  // products for the rest of the segment while still joining every barrier.  With
+  // fast decay e^{Lam_63} underflows within a chunk or two.
+  bool idle = false;
 
   for (int c = c_begin; c < c_end; ++c) {
     const int t0 = c * CH;
@@ -373,6 +378,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
       }
     }
     f32x4 u[4];
+    if (!idle) {
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -393,10 +399,12 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
         u[tt][i] = y - sm.beta[tl] * sm.elam[tl] * acc[i];
       }
     }
+    }
     lds_barrier();
 
     // ---- blocked forward substitution, u_I = T_II (v_e_I - sum_{J<I} L_IJ u_J)
     i16x4 uh[4], ul[4];
+    if (!idle) {
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4 rhs = u[I];
@@ -429,6 +437,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
       x = mma16(x, tl, rh);
       u[I] = x;
       split4(x, uh[I], ul[I]);
+    }
     }
 
     // ---- outputs: o = diag(e^Lam) (q S) + A u
@@ -469,6 +478,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
     }
 
     // ---- state update: S = e^{Lam_63} S + k^T diag(e^{Lam_63 - Lam}) u
+    if (idle) continue;
     i16x4 wh[4], wl[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
@@ -488,6 +498,14 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
         acc = mma32(acc, av, cat8(wl[2 * p], wl[2 * p + 1]));
       }
       Sr[kt] = acc;
+    }
+    if (AGG && is_m) {
+      bool nz = false;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) nz |= Sr[kt][i] != 0.f;
+      idle = __ballot(nz) == 0ull;
     }
   }
 
