@@ -24,8 +24,8 @@
 //
 // Workgroup layout: wave w owns 16 columns of the carried state (pass 1: 8 waves
 // over the 128 columns of [N | M]; pass 3: 4 waves over the 64 columns of S).
-// Per chunk the workgroup stages k (and k^T, q) in LDS, builds L, A and the 16x16
-// diagonal-block inverses T_II = (I + L_II)^-1 cooperatively, then each wave runs
+// Per chunk the workgroup stages k (and q) in LDS, builds L, A and the 16x16
+// diagonal-block inverses T_II = (I + L_II)^-1 (one wave), then each wave runs
 // its columns through v_e, the blocked triangular solve, the output and the state
 // update with register-resident accumulator tiles.
 //
@@ -136,50 +136,61 @@ __device__ __forceinline__ i16x8 tri4x2(const short* base, int I, int J, int r, 
 }
 
 
-// T = (I + N)^-1 for the strictly lower 16x16 block N = nh + nl (bf16 hi/lo, row
-// pitch TPITCH), by forward substitution on one wave: lane c16 owns column j, and
-// the four lane groups g split each row's sum over the column range m in
-// [4g, 4g+4) (one 8-byte read per plane), combined with two shuffles.  Every lane
-// ends with the whole column; group g writes rows 4g..4g+3.
-__device__ __forceinline__ void diag_block_inverse(const short* nh, const short* nl, short* th, short* tl,
-                                                   int j, int g) {
-  float xg[4] = {0.f, 0.f, 0.f, 0.f};  // x[4g + r] of this lane's column, filled as rows complete
+// T_b = (I + N_b)^-1 for all four 16x16 diagonal blocks N_b = L_bb (strictly lower,
+// bf16 hi/lo, row pitch TPITCH) on one wave: lane 16b + j owns column j of block b
+// and runs its forward substitution in registers, x_i = [i == j] - sum_{m<i} N_im x_m,
+// with no cross-lane traffic (the 16 lanes of a block read the same rows of N).
+// The result is stored transposed -- row j of TT_b is column j of T_b -- so that the
+// solve reads T_b as an operand with the transposed LDS read.
+__device__ __forceinline__ void diag_inverses(const short* LH, const short* LL, short* TH, short* TL, int lane) {
+  const int b = lane >> 4, j = lane & 15;
+  const short* nh = LH + tri_tile(b, b) * TILE_ELEMS;
+  const short* nl = LL + tri_tile(b, b) * TILE_ELEMS;
+  float x[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    float part = 0.f;
-    if (4 * g < i) {
-      const i16x4 h = *(const i16x4*)(nh + i * TPITCH + 4 * g);
-      const i16x4 l = *(const i16x4*)(nl + i * TPITCH + 4 * g);
+    float acc = (i == j) ? 1.f : 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float n = (4 * g + r < i) ? bf16_val(h[r]) + bf16_val(l[r]) : 0.f;  // N is strictly lower
-        part = fmaf(n, xg[r], part);
+    for (int q = 0; q < 4; ++q) {
+      if (4 * q < i) {
+        const i16x4 h = *(const i16x4*)(nh + i * TPITCH + 4 * q);
+        const i16x4 l = *(const i16x4*)(nl + i * TPITCH + 4 * q);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (4 * q + r < i) acc = fmaf(-(bf16_val(h[r]) + bf16_val(l[r])), x[4 * q + r], acc);
       }
     }
-    part += __shfl_xor(part, 16);
-    part += __shfl_xor(part, 32);
-    const float xi = ((i == j) ? 1.f : 0.f) - part;
-    xg[i & 3] = ((i >> 2) == g) ? xi : xg[i & 3];
+    x[i] = acc;
   }
+  short* th = TH + b * TILE_ELEMS + j * TPITCH;
+  short* tl = TL + b * TILE_ELEMS + j * TPITCH;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const short h = bf16_rn(xg[r]);
-    th[(4 * g + r) * TPITCH + j] = h;
-    tl[(4 * g + r) * TPITCH + j] = bf16_rn(xg[r] - bf16_val(h));
+  for (int q = 0; q < 4; ++q) {
+    i16x4 hh, ll;
+    split4(f32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]}, hh, ll);
+    *(i16x4*)(th + 4 * q) = hh;
+    *(i16x4*)(tl + 4 * q) = ll;
   }
 }
 
 // ------------------------------------------------------------------ shared memory
 
+// Every member starts on a 16-byte boundary: the 8- and 16-byte LDS accesses and
+// the transposed reads need naturally aligned addresses.
+#define SM_ALIGN __attribute__((aligned(16)))
 template <bool AGG>
 struct ChunkSmem {
-  short K[CH * PITCH];        // k rows (token-major)
-  short V[CH * PITCH];        // v rows
-  short Q[AGG ? 1 : CH * PITCH];
-  short LH[10 * TILE_ELEMS], LL[10 * TILE_ELEMS];                      // L hi/lo, strictly lower
-  short AH[AGG ? 1 : 10 * TILE_ELEMS], AL[AGG ? 1 : 10 * TILE_ELEMS];  // A hi/lo, lower incl. diagonal
-  short TH[4 * TILE_ELEMS], TL[4 * TILE_ELEMS];                        // (I + L_II)^-1 hi/lo
-  float lam[CH], elam[CH], eend[CH], beta[CH], wtok[CH];
+  SM_ALIGN short K[CH * PITCH];        // k rows (token-major)
+  SM_ALIGN short V[CH * PITCH];        // v rows
+  SM_ALIGN short Q[AGG ? 8 : CH * PITCH];
+  SM_ALIGN short LH[10 * TILE_ELEMS];  // L hi/lo, strictly lower
+  SM_ALIGN short LL[10 * TILE_ELEMS];
+  SM_ALIGN short AH[AGG ? 8 : 10 * TILE_ELEMS];  // A hi/lo, lower incl. diagonal
+  SM_ALIGN short AL[AGG ? 8 : 10 * TILE_ELEMS];
+  SM_ALIGN short TH[4 * TILE_ELEMS];   // (I + L_II)^-1 hi/lo, stored transposed
+  SM_ALIGN short TL[4 * TILE_ELEMS];
+  SM_ALIGN float lam[CH];
+  float elam[CH], eend[CH], beta[CH], wtok[CH];
 };
 
 // ------------------------------------------------------------------ the chunk kernel
@@ -354,12 +365,10 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
     }
     lds_barrier();
 
-    // ---- T_II = (I + L_II)^-1 (waves 0..3, block I = wave), overlapped with the
+    // ---- T_II = (I + L_II)^-1 (the last wave, all four blocks), overlapped with the
     // state-dependent products that do not need it: v_e = w*v - diag(beta e^Lam)(k S)
     // and q S.
-    if (wave < 4)
-      diag_block_inverse(sm.LH + tri_tile(wave, wave) * TILE_ELEMS, sm.LL + tri_tile(wave, wave) * TILE_ELEMS,
-                         sm.TH + wave * TILE_ELEMS, sm.TL + wave * TILE_ELEMS, c16, g);
+    if (wave == NW - 1) diag_inverses(sm.LH, sm.LL, sm.TH, sm.TL, lane);
     i16x4 Sh[4], Sl[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
@@ -429,8 +438,8 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
       }
       i16x4 rh, rl;
       split4(rhs, rh, rl);
-      const i16x4 th = lds4(sm.TH + I * TILE_ELEMS, c16, 4 * g, TPITCH);
-      const i16x4 tl = lds4(sm.TL + I * TILE_ELEMS, c16, 4 * g, TPITCH);
+      const i16x4 th = ldsT4(sm.TH + I * TILE_ELEMS, 0, 0, c16, g, TPITCH);   // T_I[c16][4g..4g+3]
+      const i16x4 tl = ldsT4(sm.TL + I * TILE_ELEMS, 0, 0, c16, g, TPITCH);
       f32x4 x = {0.f, 0.f, 0.f, 0.f};
       x = mma16(x, th, rh);
       x = mma16(x, th, rl);
