@@ -136,31 +136,34 @@ __device__ __forceinline__ i16x8 tri4x2(const short* base, int I, int J, int r, 
 }
 
 
+// fp32 copies of the four diagonal 16x16 blocks of L (row pitch DPITCH floats).
+constexpr int DPITCH = 20;
+constexpr int DTILE_ELEMS = 16 * DPITCH;
+
 // T_b = (I + N_b)^-1 for all four 16x16 diagonal blocks N_b = L_bb (strictly lower,
-// bf16 hi/lo, row pitch TPITCH) on one wave: lane 16b + j owns column j of block b
+// fp32 copies, row pitch DPITCH) on one wave: lane 16b + j owns column j of block b
 // and runs its forward substitution in registers, x_i = [i == j] - sum_{m<i} N_im x_m,
 // with no cross-lane traffic (the 16 lanes of a block read the same rows of N).
 // The result is stored transposed -- row j of TT_b is column j of T_b -- so that the
 // solve reads T_b as an operand with the transposed LDS read.
-__device__ __forceinline__ void diag_inverses(const short* LH, const short* LL, short* TH, short* TL, int lane) {
+__device__ __forceinline__ void diag_inverses(const float* LD, short* TH, short* TL, int lane) {
   const int b = lane >> 4, j = lane & 15;
-  const short* nh = LH + tri_tile(b, b) * TILE_ELEMS;
-  const short* nl = LL + tri_tile(b, b) * TILE_ELEMS;
+  const float* n = LD + b * DTILE_ELEMS;
   float x[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    float acc = (i == j) ? 1.f : 0.f;
+    // four independent partial sums (one per column residue) keep the chain short
+    float acc[4] = {(i == j) ? 1.f : 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if (4 * q < i) {
-        const i16x4 h = *(const i16x4*)(nh + i * TPITCH + 4 * q);
-        const i16x4 l = *(const i16x4*)(nl + i * TPITCH + 4 * q);
+        const f32x4 v = *(const f32x4*)(n + i * DPITCH + 4 * q);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (4 * q + r < i) acc = fmaf(-(bf16_val(h[r]) + bf16_val(l[r])), x[4 * q + r], acc);
+          if (4 * q + r < i) acc[r] = fmaf(-v[r], x[4 * q + r], acc[r]);
       }
     }
-    x[i] = acc;
+    x[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   }
   short* th = TH + b * TILE_ELEMS + j * TPITCH;
   short* tl = TL + b * TILE_ELEMS + j * TPITCH;
@@ -189,6 +192,7 @@ struct ChunkSmem {
   SM_ALIGN short AL[AGG ? 8 : 10 * TILE_ELEMS];
   SM_ALIGN short TH[4 * TILE_ELEMS];   // (I + L_II)^-1 hi/lo, stored transposed
   SM_ALIGN short TL[4 * TILE_ELEMS];
+  SM_ALIGN float LD[4 * DTILE_ELEMS];  // L_II in fp32 for the inverses
   SM_ALIGN float lam[CH];
   float elam[CH], eend[CH], beta[CH], wtok[CH];
 };
@@ -349,26 +353,46 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
         const float x = acc[r] * __expf(fminf(li - sm.lam[j], 0.f));
         val[r] = isA ? ((j <= i) ? x : 0.f) : ((j < i) ? x * be : 0.f);
       }
+      if (!isA && I == J) *(f32x4*)(sm.LD + I * DTILE_ELEMS + c16 * DPITCH + 4 * g) = val;
       i16x4 h, l;
       split4(val, h, l);
       const int off = tri_tile(I, J) * TILE_ELEMS + c16 * TPITCH + 4 * g;
       *(i16x4*)((isA ? sm.AH : sm.LH) + off) = h;
       *(i16x4*)((isA ? sm.AL : sm.LL) + off) = l;
     };
-    {
-      constexpr int NTILE = AGG ? 10 : 20;
+    // Output pass: the last wave builds the four diagonal L tiles (triangular indices
+    // 0, 2, 5, 9) and inverts them at once -- its own LDS writes, read back in order --
+    // while the other waves build the off-diagonal L tiles (1, 3, 4, 6, 7, 8) and the
+    // ten A tiles.  Aggregate pass: the eight waves share the ten L tiles and the
+    // inverse runs after the barrier on wave 7, whose M slab is idle once it is zero.
+    if (AGG) {
 #pragma unroll
-      for (int k = 0; k < (NTILE + NW - 1) / NW; ++k) {
+      for (int k = 0; k < (10 + NW - 1) / NW; ++k) {
         const int tix = wave + k * NW;
-        if (tix < NTILE) build_tile(tix % 10, tix >= 10);
+        if (tix < 10) build_tile(tix, false);
+      }
+    } else if (wave == NW - 1) {
+      build_tile(0, false);
+      build_tile(2, false);
+      build_tile(5, false);
+      build_tile(9, false);
+      diag_inverses(sm.LD, sm.TH, sm.TL, lane);
+    } else {
+      constexpr int NREM = AGG ? 6 : 16;
+#pragma unroll
+      for (int k = 0; k < (NREM + NW - 2) / (NW - 1); ++k) {
+        const int r = wave + k * (NW - 1);
+        if (r < NREM) {
+          if (r < 6) build_tile(r + 1 + (r >= 1) + (r >= 3), false);  // 1, 3, 4, 6, 7, 8
+          else build_tile(r - 6, true);
+        }
       }
     }
     lds_barrier();
 
-    // ---- T_II = (I + L_II)^-1 (the last wave, all four blocks), overlapped with the
-    // state-dependent products that do not need it: v_e = w*v - diag(beta e^Lam)(k S)
-    // and q S.
-    if (wave == NW - 1) diag_inverses(sm.LH, sm.LL, sm.TH, sm.TL, lane);
+    // ---- state-dependent products: v_e = w*v - diag(beta e^Lam)(k S) and q S
+    // (aggregate pass: overlapped with the inverses on wave 7)
+    if (AGG && wave == NW - 1) diag_inverses(sm.LD, sm.TH, sm.TL, lane);
     i16x4 Sh[4], Sl[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
