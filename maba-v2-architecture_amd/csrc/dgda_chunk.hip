@@ -246,10 +246,9 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
   const float* bb = a.bp + bi * a.bs0 + hi * a.bs1;
   const float* wb = a.wp + bi * a.ws0 + hi * a.ws1 + (WTOK ? 0 : (int64_t)col * a.ws3);
   // output: this lane's column and rows 4g..4g+3 of a 16-row block, advanced per block
-  const int64_t obase = bi * a.os0 + hi * a.os1 + (int64_t)col * a.os3;
-  int64_t orow[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) orow[i] = (int64_t)(4 * g + i) * a.os2;
+  // output (unit column stride): this lane writes token row c16 of each 16-row block,
+  // columns col0 + 4g .. +3, as one 8- or 16-byte store
+  const int64_t obase = bi * a.os0 + hi * a.os1 + (int64_t)c16 * a.os2 + col0 + 4 * g;
 
   // ---- register prefetch of one chunk's k, v, q rows and per-token gates
   i16x8 pk[IPT], pv[IPT], pq[IPT];
@@ -403,9 +402,10 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
         f32x4 qs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-          const i16x8 av = lds4x2(sm.Q, 16 * I + c16, 32 * p + 4 * g, PITCH);
-          qs = mma32(qs, av, cat8(Sh[2 * p], Sh[2 * p + 1]));
-          qs = mma32(qs, av, cat8(Sl[2 * p], Sl[2 * p + 1]));
+          // operands swapped: lane (c16, g) gets (q S)[token 16I + c16][col0 + 4g .. +3]
+          const i16x8 bv = lds4x2(sm.Q, 16 * I + c16, 32 * p + 4 * g, PITCH);
+          qs = mma32(qs, cat8(Sh[2 * p], Sh[2 * p + 1]), bv);
+          qs = mma32(qs, cat8(Sl[2 * p], Sl[2 * p + 1]), bv);
         }
         qsr[I] = qs;
       }
@@ -473,7 +473,9 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
     }
     }
 
-    // ---- outputs: o = diag(e^Lam) (q S) + A u
+    // ---- outputs: o = diag(e^Lam) (q S) + A u, computed transposed (u as the A
+    // operand, the A tiles as the B operand) so that lane (c16, g) holds token
+    // 16I + c16, columns col0 + 4g .. +3
     if (!AGG) {
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
@@ -484,28 +486,25 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
           if (2 * P + 1 <= I) {
             const i16x8 ah = tri4x2(sm.AH, I, 2 * P, c16, g), al = tri4x2(sm.AL, I, 2 * P, c16, g);
             const i16x8 bh8 = cat8(uh[2 * P], uh[2 * P + 1]), bl8 = cat8(ul[2 * P], ul[2 * P + 1]);
-            au = mma32(au, ah, bh8);
-            au = mma32(au, ah, bl8);
-            au = mma32(au, al, bh8);
+            au = mma32(au, bh8, ah);
+            au = mma32(au, bl8, ah);
+            au = mma32(au, bh8, al);
           }
         }
         f32x4 au16 = {0.f, 0.f, 0.f, 0.f};  // separate K=16 accumulator (see the solve)
         if ((I & 1) == 0) {  // single J = I
           const i16x4 ah = tri4(sm.AH, I, I, c16, g), al = tri4(sm.AL, I, I, c16, g);
-          au16 = mma16(au16, ah, uh[I]);
-          au16 = mma16(au16, ah, ul[I]);
-          au16 = mma16(au16, al, uh[I]);
+          au16 = mma16(au16, uh[I], ah);
+          au16 = mma16(au16, ul[I], ah);
+          au16 = mma16(au16, uh[I], al);
         }
         au = au + au16;
-        const int64_t oblk = obase + (int64_t)(t0 + 16 * I) * a.os2;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tl = 16 * I + 4 * g + i;
-          if (t0 + tl < a.L) {
-            const float ov = sm.elam[tl] * qs[i] + au[i];
-            if (OBF) ((short*)a.op)[oblk + orow[i]] = bf16_rn(ov);
-            else ((float*)a.op)[oblk + orow[i]] = ov;
-          }
+        const int tl = 16 * I + c16;
+        if (t0 + tl < a.L) {
+          const f32x4 ov = sm.elam[tl] * qs + au;
+          const int64_t off = obase + (int64_t)(t0 + 16 * I) * a.os2;
+          if (OBF) *(bf16x4*)((short*)a.op + off) = __builtin_convertvector(ov, bf16x4);
+          else *(f32x4*)((float*)a.op + off) = ov;
         }
       }
     }

@@ -148,8 +148,11 @@ extern "C" int maba_hip_dgda_prefill(const maba_tensor* q, const maba_tensor* k,
   if (dk < 1 || dv < 1) return fail(MABA_ERR_INVALID, "dgda_prefill: empty head dims");
   if (B * H == 0) return MABA_OK;
   hipStream_t s = (hipStream_t)stream;
+  // the chunked kernels store 4 consecutive output channels per lane (8 or 16 bytes)
+  const bool out_vec = out->stride[3] == 1 && (uintptr_t)out->data % 16 == 0 && out->stride[0] % 4 == 0 &&
+                       out->stride[1] % 4 == 0 && out->stride[2] % 4 == 0;
   if (dgda_chunk_supported(q, k, v, gate, b) && w->dtype == MABA_F32 &&
-      (out->dtype == MABA_BF16 || out->dtype == MABA_F32)) {
+      (out->dtype == MABA_BF16 || out->dtype == MABA_F32) && out_vec) {
     const size_t need = dgda_chunk_workspace(B * H, L);
     if (!workspace || workspace_bytes < need)
       return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace of %zu bytes required", need);
