@@ -48,6 +48,18 @@ constexpr int PITCH = 72;     // bf16 row pitch of LDS matrices (144 B: 16-B ali
 constexpr int TPITCH = 20;    // bf16 row pitch of the 16x16 inverse blocks
 constexpr int CPS = 16;       // chunks per segment
 
+// Output-kernel modes.  OUT_FULL runs every segment from its scanned start state
+// (single-segment sequences).  For several segments, pass 1 records zc[s], the
+// number of chunks after which segment s's transition M is exactly zero in fp32
+// (-1 if it never is); from there on the segment's state, and so its outputs, no
+// longer depend on its start state.  OUT_ZERO then runs every such segment from a
+// zero start (segment 0 from the true initial state) and writes all its outputs
+// and its final state N_s; the scan sets S_{s+1} = N_s where zc[s] >= 0; OUT_FIX
+// re-runs the first zc[s] chunks of those segments from the true start state, and
+// every segment whose M never vanished in full.  With fast decay zc[s] is 1 or 2,
+// so the aggregate and fix-up passes shrink to a chunk or two per segment.
+constexpr int OUT_FULL = 0, OUT_ZERO = 1, OUT_FIX = 2;
+
 struct ChunkArgs {
   const uint16_t* q; int64_t qs0, qs1, qs2;   // bf16 [B,H,L,64], channel stride 1
   const uint16_t* k; int64_t ks0, ks1, ks2;
@@ -61,7 +73,9 @@ struct ChunkArgs {
   MView4 sf;
   float* agg;      // [BH, nseg, 64, 128]
   float* sstart;   // [BH, nseg, 64, 64]
+  int* zc;         // [BH, nseg]: chunks after which the segment's transition M is exactly zero, -1 if never
   int H, L, nseg, nchunks, use_log, has_s0;
+  int mode;        // output kernel: OUT_FULL, OUT_ZERO or OUT_FIX
 };
 
 // ------------------------------------------------------------------ MFMA helpers
@@ -213,7 +227,16 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
   const int seg = blockIdx.x % a.nseg;
   const int bh = blockIdx.x / a.nseg;
   const int bi = bh / a.H, hi = bh % a.H;
-  if (AGG && seg == a.nseg - 1) return;  // the last segment's aggregate is never needed
+  const int64_t sidx = (int64_t)bh * a.nseg + seg;
+  int c_begin = seg * CPS;
+  int c_end = min(a.nchunks, c_begin + CPS);
+  if (!AGG && a.mode == OUT_ZERO && a.zc[sidx] < 0) return;  // M never vanished: OUT_FIX runs it in full
+  if (!AGG && a.mode == OUT_FIX && a.zc[sidx] >= 0) {
+    if (seg == 0) return;                                     // OUT_ZERO ran it from the true start
+    c_end = c_begin + a.zc[sidx];                             // only the chunks that see the start state
+  }
+  // OUT_FIX: when the predecessor's M vanished its final state N_{s-1} is this segment's start
+  const bool pred_zero = !AGG && a.mode == OUT_FIX && seg > 0 && a.zc[sidx - 1] >= 0;
 
   // Carried state slab: S[16kt + 4g + i][col0 + c16] in Sr[kt][i].
   f32x4 Sr[4];
@@ -230,15 +253,17 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
         x = (is_m && r == col) ? 1.f : 0.f;
       } else if (seg == 0) {
         x = a.has_s0 ? a.s0.at(bi, hi, r, col) : 0.f;
+      } else if (a.mode == OUT_ZERO) {
+        x = 0.f;
+      } else if (pred_zero) {
+        x = a.agg[((sidx - 1) * 64 + r) * 128 + col];   // S_s = N_{s-1} when M_{s-1} = 0
       } else {
-        x = a.sstart[(((int64_t)bh * a.nseg + seg) * 64 + r) * 64 + col];
+        x = a.sstart[(sidx * 64 + r) * 64 + col];
       }
       Sr[kt][i] = x;
     }
   }
 
-  const int c_begin = seg * CPS;
-  const int c_end = min(a.nchunks, c_begin + CPS);
   const uint16_t* qb = a.q + bi * a.qs0 + hi * a.qs1;
   const uint16_t* kb = a.k + bi * a.ks0 + hi * a.ks1;
   const uint16_t* vb = a.vp + bi * a.vs0 + hi * a.vs1;
@@ -283,6 +308,9 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
   // products for the rest of the segment while still joining every barrier.  With
   // fast decay e^{Lam_63} underflows within a chunk or two.
   bool idle = false;
+  __shared__ int s_mzero[4];  // pass 1: M slab w of the workgroup is exactly zero
+  if (AGG && tid < 4) s_mzero[tid] = 0;
+  int c_stop = -1;            // pass 1: chunk at which M was found to be zero
 
   for (int c = c_begin; c < c_end; ++c) {
     const int t0 = c * CH;
@@ -298,6 +326,10 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
         }
     }
     lds_barrier();  // previous chunk is done with the shared buffers
+    if (AGG && s_mzero[0] && s_mzero[1] && s_mzero[2] && s_mzero[3]) {  // workgroup-uniform
+      c_stop = c;
+      break;
+    }
     // ---- stage the prefetched rows (k, v, q, k^T) and gates, then prefetch the next chunk
 #pragma unroll
     for (int it = 0; it < IPT; ++it) {
@@ -538,18 +570,28 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
 #pragma unroll
         for (int i = 0; i < 4; ++i) nz |= Sr[kt][i] != 0.f;
       idle = __ballot(nz) == 0ull;
+      if (lane == 0) s_mzero[wave - 4] = idle;   // read after the next loop-top barrier
     }
   }
 
   // ---- segment results
   if (AGG) {
-    float* dst = a.agg + ((int64_t)bh * a.nseg + seg) * 64 * 128;
-    const int cc = (is_m ? 64 : 0) + col;
+    if (tid == 0) a.zc[sidx] = c_stop >= 0 ? c_stop - c_begin : -1;
+    if (c_stop < 0) {  // M never vanished: [N | M] for the scan
+      float* dst = a.agg + sidx * 64 * 128;
+      const int cc = (is_m ? 64 : 0) + col;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 128 + cc] = Sr[kt][i];
+    }
+  } else if (a.mode == OUT_ZERO && seg < a.nseg - 1) {  // N_s for the scan and the fix-up pass
+    float* dst = a.agg + sidx * 64 * 128;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 128 + cc] = Sr[kt][i];
-  } else if (seg == a.nseg - 1) {
+      for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 128 + col] = Sr[kt][i];
+  } else if (seg == a.nseg - 1 && !(a.mode == OUT_FIX && a.zc[sidx] >= 0)) {
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -559,12 +601,19 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
 
 // ------------------------------------------------------------------ pass 2: segment scan
 // One wave per (b,h, 16-column slab): S_{s+1} = M_s S_s + N_s with fp32 accuracy
-// (M and S both split into bf16 hi/lo).  Writes the start state of segments 1..nseg-1.
+// (M and S both split into bf16 hi/lo), or S_{s+1} = N_s where M_s is exactly zero
+// (zc[s] >= 0).  Writes the start state of segments 1..nseg-1; the fix-up pass only
+// reads it after a segment whose M did not vanish, so if every M vanished there is
+// nothing to do.
 __global__ __launch_bounds__(64) void dgda_segment_scan_kernel(ChunkArgs a) {
   const int bh = blockIdx.x >> 2;
   const int col0 = (blockIdx.x & 3) * 16;
   const int bi = bh / a.H, hi = bh % a.H;
   const int lane = threadIdx.x, g = lane >> 4, c16 = lane & 15;
+  const int* zc = a.zc + (int64_t)bh * a.nseg;
+  bool any_full = false;
+  for (int s = lane; s + 1 < a.nseg; s += 64) any_full |= zc[s] < 0;
+  if (__ballot(any_full) == 0ull) return;
   f32x4 Sr[4];
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt)
@@ -573,6 +622,18 @@ __global__ __launch_bounds__(64) void dgda_segment_scan_kernel(ChunkArgs a) {
       Sr[kt][i] = a.has_s0 ? a.s0.at(bi, hi, 16 * kt + 4 * g + i, col0 + c16) : 0.f;
   for (int s = 0; s + 1 < a.nseg; ++s) {
     const float* X = a.agg + ((int64_t)bh * a.nseg + s) * 64 * 128;
+    if (zc[s] >= 0) {  // M_s = 0: S_{s+1} = N_s
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Sr[kt][i] = X[(16 * kt + 4 * g + i) * 128 + col0 + c16];
+      float* dst = a.sstart + ((int64_t)bh * a.nseg + s + 1) * 64 * 64;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 64 + col0 + c16] = Sr[kt][i];
+      continue;
+    }
     i16x4 Sh[4], Sl[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
@@ -636,7 +697,7 @@ static int nseg_for(int64_t L) {
 size_t dgda_chunk_workspace(int64_t BH, int64_t L) {
   const int64_t nseg = nseg_for(L);
   if (nseg <= 1) return 16;
-  return (size_t)(BH * nseg * 64 * (128 + 64)) * sizeof(float);
+  return (size_t)(BH * nseg * 64 * (128 + 64)) * sizeof(float) + (size_t)(BH * nseg) * sizeof(int);
 }
 
 int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
@@ -665,22 +726,30 @@ int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_ten
   if (ws_bytes < need) return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace too small");
   a.agg = (float*)ws;
   a.sstart = a.agg + BH * a.nseg * 64 * 128;
+  a.zc = (int*)(a.sstart + BH * a.nseg * 64 * 64);
   const dim3 grid((unsigned)(BH * a.nseg));
-  if (a.nseg > 1) {
-    if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<true, true, true>), grid, dim3(512), 0, stream, a);
-    else hipLaunchKernelGGL((dgda_chunk_kernel<true, false, true>), grid, dim3(512), 0, stream, a);
-    int rc = check_launch("dgda_prefill/aggregate");
-    if (rc) return rc;
-    hipLaunchKernelGGL(dgda_segment_scan_kernel, dim3((unsigned)(BH * 4)), dim3(64), 0, stream, a);
-    rc = check_launch("dgda_prefill/scan");
-    if (rc) return rc;
-  }
   const bool obf = out->dtype == MABA_BF16;
-  if (a.w_tok && obf) hipLaunchKernelGGL((dgda_chunk_kernel<false, true, true>), grid, dim3(256), 0, stream, a);
-  else if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<false, true, false>), grid, dim3(256), 0, stream, a);
-  else if (obf) hipLaunchKernelGGL((dgda_chunk_kernel<false, false, true>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((dgda_chunk_kernel<false, false, false>), grid, dim3(256), 0, stream, a);
-  return check_launch("dgda_prefill/output");
+  auto launch_out = [&](int mode) {
+    a.mode = mode;
+    if (a.w_tok && obf) hipLaunchKernelGGL((dgda_chunk_kernel<false, true, true>), grid, dim3(256), 0, stream, a);
+    else if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<false, true, false>), grid, dim3(256), 0, stream, a);
+    else if (obf) hipLaunchKernelGGL((dgda_chunk_kernel<false, false, true>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((dgda_chunk_kernel<false, false, false>), grid, dim3(256), 0, stream, a);
+    return check_launch("dgda_prefill/output");
+  };
+  if (a.nseg == 1) {
+    a.zc = nullptr;
+    return launch_out(OUT_FULL);
+  }
+  a.mode = OUT_FULL;
+  if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<true, true, true>), grid, dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((dgda_chunk_kernel<true, false, true>), grid, dim3(512), 0, stream, a);
+  int rc = check_launch("dgda_prefill/aggregate");
+  if (rc) return rc;
+  if ((rc = launch_out(OUT_ZERO))) return rc;
+  hipLaunchKernelGGL(dgda_segment_scan_kernel, dim3((unsigned)(BH * 4)), dim3(64), 0, stream, a);
+  if ((rc = check_launch("dgda_prefill/scan"))) return rc;
+  return launch_out(OUT_FIX);
 }
 
 }  // namespace maba

@@ -88,13 +88,13 @@ def test_prefill_shape_mismatch(lib):
 
 def test_prefill_workspace_size_at_baseline_shape(lib):
     """B=4, H=10, T=32768: 32 segments of 1024 tokens per head, each carrying a
-    [64, 128] fp32 aggregate plus a [64, 64] fp32 start state."""
+    [64, 128] fp32 aggregate, a [64, 64] fp32 start state and an int32 chunk count."""
     B, H, T, d = 4, 10, 32768, 64
     q = _t([B, H, T, d])
     gate = _t([B, H, T, d], N.MABA_F32, strides=[H * T, T, 1, 0])   # per-token, stride-0 channels
     n = lib.maba_hip_dgda_prefill_workspace_size(q, q, gate, gate)
     nseg = T // 1024
-    assert n == B * H * nseg * 64 * (128 + 64) * 4
+    assert n == B * H * nseg * (64 * (128 + 64) * 4 + 4)   # + one chunk count per segment
     per_channel = _t([B, H, T, d], N.MABA_F32)
     assert lib.maba_hip_dgda_prefill_workspace_size(q, q, per_channel, gate) == 0   # sequential path
 

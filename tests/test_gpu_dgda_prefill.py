@@ -121,3 +121,21 @@ def test_baseline_shape_split_chaining(dev):
     o2, S2 = _run(second)
     assert_close(torch.cat([o1, o2], dim=2), to_np(o), 2e-3, 2e-3, "chained out")
     assert_close(S2, to_np(S), 2e-3, 2e-3, "chained state")
+
+
+def test_chunk_mixed_decay_segments(dev):
+    """Decay that is slow for the first 2600 tokens and fast afterwards, in one head, and
+    the reverse in the other: segments whose transition vanishes after one or several
+    chunks sit next to segments where it never does (zero-start, fix-up and full paths)."""
+    L = 9000
+    inp = dgda_inputs(1, 2, L, seed=77, device=dev, with_state=True)
+    la = inp["log_alpha"][..., :1].clone()
+    t = torch.arange(L, device=dev)
+    slow = la * 0.005
+    la[0, 0, :, 0] = torch.where(t < 2600, slow[0, 0, :, 0], la[0, 0, :, 0])
+    la[0, 1, :, 0] = torch.where(t >= 6200, slow[0, 1, :, 0], la[0, 1, :, 0])
+    inp["log_alpha"] = la.expand(1, 2, L, 64)
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, "out")
+    assert_close(S, eS, 2e-3, 2e-3, "state")
