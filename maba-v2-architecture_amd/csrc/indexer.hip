@@ -13,6 +13,7 @@
 // results go to a workspace and a second kernel merges the splits.
 #include "maba_common.h"
 #include "topk_wave.h"
+#include <type_traits>
 
 namespace maba {
 
@@ -110,16 +111,20 @@ __global__ __launch_bounds__(64) void index_decode_merge_kernel(const key64* ws,
 //   the queries, heads padded to 16, in registers).  bf16 x bf16 products are
 //   exact and accumulate in fp32.  Writes every score to a workspace row per
 //   (b, head) and the tile's best key per head.
-// index_decode_select_kernel -- one workgroup per (b, head).  tau = the K-th
-//   largest of the tile maxima bounds the K-th largest key from below (K tiles
-//   each hold a key >= tau), so the top K are among the keys >= tau: collect
-//   those (typically a few dozen), rank them by counting, write ranks < K.  If
-//   more than SEL_CAP keys pass (heavily tied scores), the workgroup falls back
-//   to wave top-k merges over the whole row.
+// index_decode_select_kernel -- one 1024-thread workgroup per (b, head).  The tile
+//   maxima are folded into 64 groups; tau = the K-th largest group maximum bounds
+//   the K-th largest key from below (K groups each hold a key >= tau), so the top
+//   K are among the keys >= tau: collect those (typically a few dozen), rank them
+//   by counting, write ranks < K.  If one wave's share of the row passes more than
+//   SEL_CAP / 16 keys (heavily tied scores), the workgroup falls back to wave
+//   top-k merges over the whole row.
 typedef __attribute__((ext_vector_type(8))) short i16x8_t;
 constexpr int SEL_CAP = 1024;     // candidate slots of the select kernel
-constexpr int SEL_GROUPS = 64;    // tile maxima are folded into at most this many groups (<= 256)
-constexpr int SEL_V = 16;         // float4 score loads in flight per thread in the select kernel
+constexpr int SEL_GROUPS = 64;    // tile maxima are folded into this many groups
+constexpr int SEL_T = 1024;       // threads of the select kernel (16 waves)
+constexpr int SEL_W = SEL_T / 64;
+constexpr int SEL_V = 4;          // float4 score loads in flight per thread in the select kernel
+constexpr int SEL_PASS = SEL_T * SEL_V * 4;   // scores per pass
 
 struct DecTileArgs {
   const uint16_t* q; int64_t qsb, qsh;   // [B, Hq, d] bf16, channel stride 1
@@ -212,92 +217,176 @@ struct DecSelArgs {
   int64_t* out; int64_t osb, osh, osk;
 };
 
-__global__ __launch_bounds__(256) void index_decode_select_kernel(DecSelArgs a) {
-  __shared__ __attribute__((aligned(16))) key64 s_c[SEL_CAP + 8];
+__device__ __forceinline__ key64 readlane64(key64 x, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane);
+  return ((key64)hi << 32) | lo;
+}
+
+// Number of keys in s[0, 16) greater than k (s 16-byte aligned; broadcast reads, unrolled).
+__device__ __forceinline__ int count_greater16(const key64* s, key64 k) {
+  typedef __attribute__((ext_vector_type(2))) unsigned long long u64x2;
+  int r = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const u64x2 x = *(const u64x2*)(s + i);
+    r += (x.x > k) + (x.y > k);
+  }
+  return r;
+}
+
+__device__ __forceinline__ int lane_rank(unsigned long long m) {   // set bits of m below this lane
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a) {
+  __shared__ __attribute__((aligned(16))) key64 s_c[SEL_CAP + 8];   // candidates, one region per wave
+  __shared__ __attribute__((aligned(16))) key64 s_k[SEL_CAP + 8];   // the compacted candidate list
   __shared__ __attribute__((aligned(16))) key64 s_g[SEL_GROUPS];
+  __shared__ key64 s_part[SEL_T];
+  __shared__ int s_rank[4][64];
+  __shared__ int s_wcnt[SEL_W];
   __shared__ key64 s_tau;
-  __shared__ int s_cnt;
   const int64_t row = blockIdx.x;  // b * Hq + h
   const int64_t bi = row / a.Hq;
   const int h = (int)(row % a.Hq);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const key64* tm = a.tmax + row * a.ntiles;
   const float* sc = a.sc + row * (int64_t)a.ntiles * 64;
-  const int G = a.ntiles < SEL_GROUPS ? a.ntiles : SEL_GROUPS;
-  const int G8 = (G + 7) & ~7;
-  // first pass of score loads, issued before the tile maxima so that both are in flight together
+  // first pass of score loads, issued before the tile maxima so that both are in flight
+  // together.  Vectors past the row's end read as -inf, like the row's padding.
   f32x4 v[SEL_V];
 #pragma unroll
   for (int j = 0; j < SEL_V; ++j) {
-    const int64_t n = 1024 * j + 4 * tid;
-    f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    if (n < a.nb) z = *(const f32x4*)(sc + n);   // rows are padded to whole tiles
+    const int64_t n = 4 * (SEL_T * j + tid);
+    f32x4 z = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    if (n < a.nb) z = *(const f32x4*)(sc + n);
     v[j] = z;
   }
-  if (tid == 0) { s_cnt = 0; s_tau = KEY_NONE; }
-  if (tid < G8) {   // group j = tiles [j*ntiles/G, (j+1)*ntiles/G); padding slots hold KEY_NONE
-    key64 m = KEY_NONE;
-    if (tid < G) {
-      const int t0 = (int)((int64_t)tid * a.ntiles / G), t1 = (int)((int64_t)(tid + 1) * a.ntiles / G);
-      for (int t = t0; t < t1; ++t) m = kmax(m, tm[t]);
-    }
-    s_g[tid] = m;
+  if (tid < 64) s_k[tid] = KEY_NONE;   // list slots the final rank reads past cnt
+  // tile maxima: thread t folds tiles t, t + SEL_T, ...; group j < 64 is the tiles
+  // t = j (mod 64), i.e. lane j of every wave (any partition of the tiles gives a valid bound)
+  key64 m = KEY_NONE;
+  for (int t = tid; t < a.ntiles; t += SEL_T) m = kmax(m, tm[t]);
+  s_part[tid] = m;
+  __syncthreads();
+  // tau = K-th largest group maximum (keys are distinct; empty groups hold KEY_NONE):
+  // wave w < 4 counts the group maxima in slots [16 w, 16 w + 16) above group `lane`'s
+  if (wave == 0) {
+    key64 gm = s_part[lane];
+#pragma unroll
+    for (int w = 1; w < SEL_W; ++w) gm = kmax(gm, s_part[64 * w + lane]);
+    s_g[lane] = gm;
   }
   __syncthreads();
-  if (G >= a.K && tid < G) {  // tau = K-th largest group maximum (keys are distinct)
-    if (count_greater(s_g, G8, s_g[tid]) == a.K - 1) s_tau = s_g[tid];
+  const key64 gm = s_g[lane];
+  if (wave < 4) s_rank[wave][lane] = count_greater16(s_g + 16 * wave, gm);
+  __syncthreads();
+  if (wave == 0) {
+    const int G = a.ntiles < SEL_GROUPS ? a.ntiles : SEL_GROUPS;   // groups j < G hold a tile
+    key64 tau = KEY_NONE;
+    if (G >= a.K) {
+      const int rank = s_rank[0][lane] + s_rank[1][lane] + s_rank[2][lane] + s_rank[3][lane];
+      const unsigned long long bal = __ballot(lane < G && rank == a.K - 1);
+      tau = readlane64(gm, __builtin_ctzll(bal));
+    }
+    if (lane == 0) s_tau = tau;
   }
   __syncthreads();
   const key64 tau = s_tau;
-  // keys >= tau have scores >= tau's score: a branch-free float prefilter marks the
-  // survivors of each pass in a bit mask, and only those take the exact key test
-  const float tau_s = tau == KEY_NONE ? -INFINITY : key_score(tau);
-  for (int64_t base = 0; base < a.nb; base += 1024 * SEL_V) {
-    if (base > 0) {
+  // Candidates: keys whose score is not below tau's score.  They include every key >= tau
+  // (key order is score order first); the extra ones (equal score, larger index) rank
+  // below all K keys >= tau and are never written.  With fewer groups than K
+  // (tau = KEY_NONE) every key n < nb is a candidate.  Each wave appends to its own
+  // region of SEL_CAP / SEL_W slots at a wave-uniform running offset: a vector no lane of the
+  // wave takes costs one max and one compare, an element no lane takes one compare.
+  const bool all = tau == KEY_NONE;
+  const float tau_s = key_score(tau);
+  constexpr int WCAP = SEL_CAP / SEL_W;
+  key64* reg = s_c + wave * WCAP;
+  int run = 0;   // wave-uniform
+  auto scan = [&](auto all_c) {
+    constexpr bool ALL = decltype(all_c)::value;
+    for (int64_t base = 0; base < a.nb; base += SEL_PASS) {
+      if (base > 0) {
+#pragma unroll
+        for (int j = 0; j < SEL_V; ++j) {
+          const int64_t n = base + 4 * (SEL_T * j + tid);
+          f32x4 z = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+          if (n < a.nb) z = *(const f32x4*)(sc + n);
+          v[j] = z;
+        }
+      }
+      const int64_t n0 = base + 4 * tid;
 #pragma unroll
       for (int j = 0; j < SEL_V; ++j) {
-        const int64_t n = base + 1024 * j + 4 * tid;
-        f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        if (n < a.nb) z = *(const f32x4*)(sc + n);
-        v[j] = z;
+        const f32x4 x = v[j];
+        if (ALL) {
+          if (__ballot(n0 + 4 * SEL_T * j < a.nb) == 0ull) continue;
+        } else {
+          const float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+          if (__ballot(!(mx < tau_s)) == 0ull) continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t n = n0 + 4 * SEL_T * j + i;
+          const bool t = ALL ? n < a.nb : !(x[i] < tau_s);
+          const unsigned long long b = __ballot(t);
+          if (b == 0ull) continue;
+          const int p = run + lane_rank(b);
+          if (t && p < WCAP) reg[p] = make_key(x[i], (uint32_t)n);
+          run += __builtin_popcountll(b);
+        }
       }
     }
-    unsigned long long mask = 0ull;
+  };
+  if (all) scan(std::true_type{}); else scan(std::false_type{});
+  if (lane == 0) s_wcnt[wave] = run;
+  __syncthreads();
+  // region counts: lane l < SEL_W holds wave l's; cnt and this wave's offset are sums
+  // over lanes, taken bit plane by bit plane (exact when every count is <= WCAP = 64,
+  // the only case that uses them)
+  const int cw = lane < SEL_W ? s_wcnt[lane] : 0;
+  int cnt = 0, off = 0;
+  const bool fits = __ballot(cw > WCAP) == 0ull;
+  {
+    static_assert(WCAP < 128, "seven bit planes");
 #pragma unroll
-    for (int j = 0; j < SEL_V; ++j) {
-      const int64_t n = base + 1024 * j + 4 * tid;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        mask |= (unsigned long long)(n + i < a.nb && v[j][i] >= tau_s) << (4 * j + i);
-    }
-    while (mask) {
-      const int bit = __builtin_ctzll(mask);
-      mask &= mask - 1ull;
-      const int64_t n = base + 1024 * (bit >> 2) + 4 * tid + (bit & 3);
-      const key64 key = make_key(sc[n], (uint32_t)n);
-      if (key >= tau) {
-        const int pos = atomicAdd(&s_cnt, 1);
-        if (pos < SEL_CAP) s_c[pos] = key;
-      }
+    for (int b = 0; b < 7; ++b) {
+      const unsigned long long bits = __ballot((cw >> b) & 1);
+      cnt += __builtin_popcountll(bits) << b;
+      off += __builtin_popcountll(bits & ((1ull << wave) - 1ull)) << b;
     }
   }
-  __syncthreads();
-  const int cnt = s_cnt;
   int64_t* orow = a.out + bi * a.osb + h * a.osh;
-  if (cnt <= SEL_CAP) {
-    const int c8 = (cnt + 7) & ~7;
-    if (tid < c8 - cnt) s_c[cnt + tid] = KEY_NONE;   // pad to whole groups of 8
+  if (fits && cnt >= a.ak) {
+    // compact the regions into s_k[0, cnt)
+    if (lane < run) s_k[off + lane] = reg[lane];
     __syncthreads();
-    for (int j = tid; j < cnt; j += 256) {
-      const key64 kj = s_c[j];
-      const int rank = count_greater(s_c, c8, kj);
+    if (cnt <= 64) {  // rank across the four waves; slots past cnt hold KEY_NONE
+      const key64 kj = s_k[lane];
+      if (wave < 4) s_rank[wave][lane] = count_greater16(s_k + 16 * wave, kj);
+      __syncthreads();
+      if (wave == 0) {
+        const int rank = s_rank[0][lane] + s_rank[1][lane] + s_rank[2][lane] + s_rank[3][lane];
+        if (lane < cnt && rank < a.ak) orow[rank * a.osk] = (int64_t)key_index(kj);
+      }
+      return;
+    }
+    const int c8 = (cnt + 7) & ~7;
+    if (tid < c8 - cnt) s_k[cnt + tid] = KEY_NONE;   // pad to whole groups of 8
+    __syncthreads();
+    for (int j = tid; j < cnt; j += SEL_T) {
+      const key64 kj = s_k[j];
+      const int rank = count_greater(s_k, c8, kj);
       if (rank < a.ak) orow[rank * a.osk] = (int64_t)key_index(kj);
     }
     return;
   }
-  // fallback: each wave merges a quarter of the row, then wave 0 merges the four lists
+  // fallback: each wave merges every SEL_W-th 64-key slice of the row, then wave 0
+  // merges the SEL_W lists
   key64 list = KEY_NONE;
-  for (int64_t base = (int64_t)wave * 64; base < a.nb; base += 256) {
+  for (int64_t base = (int64_t)wave * 64; base < a.nb; base += 64 * SEL_W) {
     const int64_t n = base + lane;
     const key64 key = n < a.nb ? make_key(sc[n], (uint32_t)n) : KEY_NONE;
     list = wave_merge_topk(list, key >= tau ? key : KEY_NONE, a.K);
@@ -307,7 +396,7 @@ __global__ __launch_bounds__(256) void index_decode_select_kernel(DecSelArgs a) 
   __syncthreads();
   if (wave == 0) {
     key64 m = s_c[lane];
-    for (int w = 1; w < 4; ++w) m = wave_merge_topk(m, s_c[w * 64 + lane], a.K);
+    for (int w = 1; w < SEL_W; ++w) m = wave_merge_topk(m, s_c[w * 64 + lane], a.K);
     if (lane < a.ak) orow[lane * a.osk] = (int64_t)key_index(m);
   }
 }
@@ -437,7 +526,7 @@ extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tenso
     e.sc = m.sc; e.tmax = m.tmax; e.nb = nb; e.ntiles = m.ntiles; e.Hq = (int)Hq; e.K = top_k; e.ak = (int)ak;
     e.out = (int64_t*)out_idx->data; e.osb = out_idx->stride[0]; e.osh = out_idx->stride[1];
     e.osk = out_idx->stride[2];
-    hipLaunchKernelGGL(index_decode_select_kernel, dim3((unsigned)(B * Hq)), dim3(256), 0, s, e);
+    hipLaunchKernelGGL(index_decode_select_kernel, dim3((unsigned)(B * Hq)), dim3(SEL_T), 0, s, e);
     return check_launch("index_topk_decode/select");
   }
   DecArgs a;

@@ -30,6 +30,7 @@ constexpr int SA_MAXDC = 256;
 
 struct SaArgs {
   const void* q; int qdt; int64_t qsb, qsh, qsd;
+  int qvec;  // q is fp32 with unit channel stride and 16-byte aligned rows
   const void* c; int cdt; int64_t csb, csl, csd;
   const void* hca; int hdt; int64_t hsb, hsn, hsd;
   const int64_t* idx; int64_t isb, ish, isk;
@@ -350,11 +351,34 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
 
   // queries (B operand of the scores): head c16, dims 32p + 8g .. +7, split hi/lo
   s16x8 qh[NP], ql[NP];
+  float qv[NP][8];
+  if (a.qvec) {  // fp32 rows, 16-byte aligned: all of the lane's query loads in flight at once
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
+      if (c16 < a.H) {
+        const float* qp = (const float*)a.q + b * a.qsb + c16 * a.qsh + 32 * p + 8 * g;
+        x0 = *(const f32x4*)qp;
+        x1 = *(const f32x4*)(qp + 4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qv[p][j] = x0[j];
+        qv[p][4 + j] = x1[j];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        qv[p][j] = (c16 < a.H) ? load_elem(a.q, a.qdt, b * a.qsb + c16 * a.qsh + (32 * p + 8 * g + j) * a.qsd) : 0.f;
+  }
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float x = (c16 < a.H) ? load_elem(a.q, a.qdt, b * a.qsb + c16 * a.qsh + (32 * p + 8 * g + j) * a.qsd) : 0.f;
+      const float x = qv[p][j];
       const short h = __builtin_bit_cast(short, (__bf16)x);
       qh[p][j] = h;
       ql[p][j] = __builtin_bit_cast(short, (__bf16)(x - bf16_bits_to_f32((uint16_t)h)));
@@ -502,6 +526,19 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
   }
 }
 
+// Compute units of the current device (queried once per device).
+static int sa_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 static void sa_geometry(SaArgs& a, int64_t L, int window, int n_sink, int pool, int Hi, int K) {
   const int64_t ns = L < n_sink ? L : n_sink;
   const int64_t st = (L - window) > ns ? (L - window) : ns;
@@ -558,6 +595,8 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
   if (B * H == 0) return MABA_OK;
   SaArgs a;
   a.q = q_lat->data; a.qdt = q_lat->dtype; a.qsb = q_lat->stride[0]; a.qsh = q_lat->stride[1]; a.qsd = q_lat->stride[2];
+  a.qvec = q_lat->dtype == MABA_F32 && q_lat->stride[2] == 1 && (uintptr_t)q_lat->data % 16 == 0 &&
+           q_lat->stride[0] % 4 == 0 && q_lat->stride[1] % 4 == 0;
   a.c = c_kv->data; a.cdt = c_kv->dtype; a.csb = c_kv->stride[0]; a.csl = c_kv->stride[1]; a.csd = c_kv->stride[2];
   a.hca = hca->data; a.hdt = hca->dtype; a.hsb = hca->stride[0]; a.hsn = hca->stride[1]; a.hsd = hca->stride[2];
   a.idx = (const int64_t*)idx->data; a.isb = idx->stride[0]; a.ish = idx->stride[1]; a.isk = idx->stride[2];
@@ -577,14 +616,18 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
                        (uintptr_t)hca->data % 16 == 0 && c_kv->stride[0] % 8 == 0 && c_kv->stride[1] % 8 == 0 &&
                        hca->stride[0] % 8 == 0 && hca->stride[1] % 8 == 0 && block_size <= 64;
   if (mfma_ok) {
-    // tiles per wave: enough segments to cover the machine about twice, at most 8
-    const int64_t tiles = B * (a.t_loc + (int64_t)a.Hi * a.K + a.t_hca);
-    const int tpw = (int)std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(tiles, 2048)));
-    const int span = 4 * tpw;
-    const int s_sp1 = (int)ceil_div(a.K, span);
-    const int s_sp = a.Hi == 1 ? s_sp1 : (int)H * s_sp1;
-    const int s_hca = (int)ceil_div(a.t_hca, span);
-    const int nseg = 1 + s_sp + s_hca;
+    // tiles per wave: the fewest that still fit one workgroup per CU (every workgroup
+    // pays a fixed start-up, and one round of workgroups covers the machine), at most 8
+    const int ncu = sa_cu_count();
+    int tpw = 1, span = 4, s_sp1 = 0, s_sp = 0, s_hca = 0, nseg = 0;
+    for (tpw = 1; tpw <= 8; ++tpw) {
+      span = 4 * tpw;
+      s_sp1 = (int)ceil_div(a.K, span);
+      s_sp = a.Hi == 1 ? s_sp1 : (int)H * s_sp1;
+      s_hca = (int)ceil_div(a.t_hca, span);
+      nseg = 1 + s_sp + s_hca;
+      if (B * nseg <= ncu || tpw == 8) break;
+    }
     a.ntiles = nseg;  // partial slots are segments
     const dim3 grid((unsigned)nseg, (unsigned)B);
     switch (dc / 32) {

@@ -195,6 +195,24 @@ def test_index_topk_decode_ties(dev, nb, lam):
     assert torch.equal(idx.cpu(), exp.expand(2, 10, 32))
 
 
+def test_index_topk_decode_tied_plateau(dev):
+    """300 planted blocks share the top score (positive queries, identical centroids),
+    every other centroid is zero and lam = 0: the top 32 are the 32 lowest planted
+    indices.  The tied plateau spreads over the whole row, so the select kernel ranks a
+    few hundred candidates by counting (neither the register rank nor the merge fallback)."""
+    g = torch.Generator().manual_seed(12)
+    B, Hq, nb, d = 2, 10, 15625, 128
+    q = torch.randn(B, Hq, d, generator=g).abs().bfloat16()
+    c = torch.zeros(B, nb, d, dtype=torch.bfloat16)
+    exp = []
+    for b in range(B):
+        blocks = torch.randperm(nb, generator=g)[:300]
+        c[b, blocks] = 0.5
+        exp.append(torch.sort(blocks).values[:32])
+    idx = _hip().hip_index_topk_decode(q.to(dev), c.to(dev), lambda_dist=0.0, top_k=32)
+    assert torch.equal(idx.cpu(), torch.stack(exp)[:, None, :].expand(B, Hq, 32))
+
+
 def test_index_topk_decode_baseline_needle(dev):
     """BASELINE config 3 shape for one batch element pair: 15,625 bf16 centroids with a
     planted block; the needle block is selected first for every head aligned with it and
