@@ -37,6 +37,7 @@
 // are exact MFMA operands; fp32 operands (S, u, L, A, T) are split into bf16
 // hi + lo parts (two or three MFMAs) so products carry ~16 mantissa bits.
 #include "maba_common.h"
+#include <type_traits>
 
 namespace maba {
 
@@ -207,11 +208,32 @@ struct ChunkSmem {
   SM_ALIGN short TH[4 * TILE_ELEMS];   // (I + L_II)^-1 hi/lo, stored transposed
   SM_ALIGN short TL[4 * TILE_ELEMS];
   SM_ALIGN float LD[4 * DTILE_ELEMS];  // L_II in fp32 for the inverses
-  SM_ALIGN float lam[CH];
-  float elam[CH], eend[CH], beta[CH], wtok[CH];
+  SM_ALIGN float lam2[CH];   // inclusive cumulative log-decay, in log2 units
+  SM_ALIGN float elam[CH];   // e^Lam
+  SM_ALIGN float eend[CH];   // e^{Lam_63 - Lam}
+  SM_ALIGN float beta[CH];
+  SM_ALIGN float bel[CH];    // beta e^Lam
+  SM_ALIGN float wtok[CH];
 };
 
 // ------------------------------------------------------------------ the chunk kernel
+
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves: shifts by 1, 2, 4, 8
+// within each 16-lane row, then the row broadcasts of lanes 15 and 31.
+__device__ __forceinline__ float wave_incl_scan(float x) {
+  auto dpp = [](float v, auto ctrl_c, auto rmask_c, auto bound_c) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl_c)::value,
+                                                      decltype(rmask_c)::value, 0xf, decltype(bound_c)::value));
+  };
+  using std::integral_constant;
+  x += dpp(x, integral_constant<int, 0x111>{}, integral_constant<int, 0xf>{}, std::true_type{});  // row_shr:1
+  x += dpp(x, integral_constant<int, 0x112>{}, integral_constant<int, 0xf>{}, std::true_type{});  // row_shr:2
+  x += dpp(x, integral_constant<int, 0x114>{}, integral_constant<int, 0xf>{}, std::true_type{});  // row_shr:4
+  x += dpp(x, integral_constant<int, 0x118>{}, integral_constant<int, 0xf>{}, std::true_type{});  // row_shr:8
+  x += dpp(x, integral_constant<int, 0x142>{}, integral_constant<int, 0xa>{}, std::false_type{}); // row_bcast:15
+  x += dpp(x, integral_constant<int, 0x143>{}, integral_constant<int, 0xc>{}, std::false_type{}); // row_bcast:31
+  return x;
+}
 
 // LDS-only barrier: waits for this wave's LDS operations, not for its outstanding
 // global loads (the next chunk's prefetch stays in flight across it).
@@ -342,18 +364,15 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
     if (tid < CH) {
       float la = a.use_log ? pla : __logf(fmaxf(pla, 1e-20f));
       la = (t0 + tid < a.L) ? fminf(la, 0.f) : 0.f;
-      // inclusive prefix sum of the log decay across the wave
-      float s = la;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float o = __shfl_up(s, off);
-        if (tid >= off) s += o;
-      }
-      const float last = __shfl(s, 63);
-      sm.lam[tid] = s;
-      sm.elam[tid] = __expf(s);
+      // inclusive prefix sum of the log decay across wave 0 (tid < CH is that wave)
+      const float s = wave_incl_scan(la);
+      const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
+      const float el = __expf(s);
+      sm.lam2[tid] = s * 1.4426950408889634f;
+      sm.elam[tid] = el;
       sm.eend[tid] = __expf(last - s);
       sm.beta[tid] = pbe;
+      sm.bel[tid] = pbe * el;
       sm.wtok[tid] = pwt;
     }
     if (c + 1 < c_end) prefetch(c + 1);
@@ -361,13 +380,18 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
 
     // ---- L = beta_i (k k^T) decay (strict lower) and A = (q k^T) decay (lower)
     // Tile (I,J) is computed as D = k_J x k_I^T (or k_J x q_I^T) so each lane holds
-    // row 16I + c16 and columns 16J + 4g..+3: one 8-byte store into the tile.
-    auto build_tile = [&](int tix, bool isA) {
-      int tt = tix, I = 0;
-      while (tt > I) { tt -= I + 1; ++I; }
-      const int J = tt;  // J <= I
+    // row 16I + c16 and columns 16J + 4g..+3: one 8-byte store into the tile.  Tile
+    // index and kind are compile-time constants, so each wave's tile list is
+    // straight-line code whose loads, products and exponentials interleave.
+    // e^{Lam_i - Lam_j} = 2^{lam2_i - lam2_j}; off-diagonal tiles (I > J) hold only
+    // i > j, diagonal tiles select j < i (L) or j <= i (A).
+    auto build_tile = [&](auto tix_c, auto isa_c) {
+      constexpr int TIX = decltype(tix_c)::value;
+      constexpr bool ISA = decltype(isa_c)::value;
+      constexpr int I = TIX < 1 ? 0 : TIX < 3 ? 1 : TIX < 6 ? 2 : 3;
+      constexpr int J = TIX - I * (I + 1) / 2;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const short* Bsrc = isA ? sm.Q : sm.K;
+      const short* Bsrc = ISA ? sm.Q : sm.K;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const i16x8 av = lds8(sm.K, 16 * J + c16, 32 * p + 8 * g, PITCH);
@@ -375,50 +399,56 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
         acc = mma32(acc, av, bv);
       }
       const int i = 16 * I + c16;
-      const float li = sm.lam[i];
-      const float be = sm.beta[i];
+      const float li = sm.lam2[i];
+      const f32x4 lj = *(const f32x4*)(sm.lam2 + 16 * J + 4 * g);
       f32x4 val;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * J + 4 * g + r;
-        const float x = acc[r] * __expf(fminf(li - sm.lam[j], 0.f));
-        val[r] = isA ? ((j <= i) ? x : 0.f) : ((j < i) ? x * be : 0.f);
+        const float x = acc[r] * __builtin_amdgcn_exp2f(li - lj[r]);
+        if (I > J) val[r] = x;
+        else val[r] = (ISA ? j <= i : j < i) ? x : 0.f;
       }
-      if (!isA && I == J) *(f32x4*)(sm.LD + I * DTILE_ELEMS + c16 * DPITCH + 4 * g) = val;
+      if (!ISA) val = val * sm.beta[i];
+      if (!ISA && I == J) *(f32x4*)(sm.LD + I * DTILE_ELEMS + c16 * DPITCH + 4 * g) = val;
       i16x4 h, l;
       split4(val, h, l);
-      const int off = tri_tile(I, J) * TILE_ELEMS + c16 * TPITCH + 4 * g;
-      *(i16x4*)((isA ? sm.AH : sm.LH) + off) = h;
-      *(i16x4*)((isA ? sm.AL : sm.LL) + off) = l;
+      const int off = (I * (I + 1) / 2 + J) * TILE_ELEMS + c16 * TPITCH + 4 * g;
+      *(i16x4*)((ISA ? sm.AH : sm.LH) + off) = h;
+      *(i16x4*)((ISA ? sm.AL : sm.LL) + off) = l;
     };
+    using std::integral_constant;
+#define DGDA_TL(n) build_tile(integral_constant<int, n>{}, std::false_type{})
+#define DGDA_TA(n) build_tile(integral_constant<int, n>{}, std::true_type{})
     // Output pass: the last wave builds the four diagonal L tiles (triangular indices
     // 0, 2, 5, 9) and inverts them at once -- its own LDS writes, read back in order --
     // while the other waves build the off-diagonal L tiles (1, 3, 4, 6, 7, 8) and the
     // ten A tiles.  Aggregate pass: the eight waves share the ten L tiles and the
     // inverse runs after the barrier on wave 7, whose M slab is idle once it is zero.
-    if (AGG) {
-#pragma unroll
-      for (int k = 0; k < (10 + NW - 1) / NW; ++k) {
-        const int tix = wave + k * NW;
-        if (tix < 10) build_tile(tix, false);
+    if constexpr (AGG) {
+      switch (wave) {
+        case 0: DGDA_TL(0); DGDA_TL(8); break;
+        case 1: DGDA_TL(1); DGDA_TL(9); break;
+        case 2: DGDA_TL(2); break;
+        case 3: DGDA_TL(3); break;
+        case 4: DGDA_TL(4); break;
+        case 5: DGDA_TL(5); break;
+        case 6: DGDA_TL(6); break;
+        default: DGDA_TL(7); break;
       }
-    } else if (wave == NW - 1) {
-      build_tile(0, false);
-      build_tile(2, false);
-      build_tile(5, false);
-      build_tile(9, false);
-      diag_inverses(sm.LD, sm.TH, sm.TL, lane);
     } else {
-      constexpr int NREM = AGG ? 6 : 16;
-#pragma unroll
-      for (int k = 0; k < (NREM + NW - 2) / (NW - 1); ++k) {
-        const int r = wave + k * (NW - 1);
-        if (r < NREM) {
-          if (r < 6) build_tile(r + 1 + (r >= 1) + (r >= 3), false);  // 1, 3, 4, 6, 7, 8
-          else build_tile(r - 6, true);
-        }
+      switch (wave) {
+        case 0: DGDA_TL(1); DGDA_TL(6); DGDA_TA(0); DGDA_TA(3); DGDA_TA(6); DGDA_TA(9); break;
+        case 1: DGDA_TL(3); DGDA_TL(7); DGDA_TA(1); DGDA_TA(4); DGDA_TA(7); break;
+        case 2: DGDA_TL(4); DGDA_TL(8); DGDA_TA(2); DGDA_TA(5); DGDA_TA(8); break;
+        default:
+          DGDA_TL(0); DGDA_TL(2); DGDA_TL(5); DGDA_TL(9);
+          diag_inverses(sm.LD, sm.TH, sm.TL, lane);
+          break;
       }
     }
+#undef DGDA_TL
+#undef DGDA_TA
     lds_barrier();
 
     // ---- state-dependent products: v_e = w*v - diag(beta e^Lam)(k S) and q S
@@ -453,16 +483,17 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
         acc = mma32(acc, av, cat8(Sh[2 * p], Sh[2 * p + 1]));
         acc = mma32(acc, av, cat8(Sl[2 * p], Sl[2 * p + 1]));
       }
+      // tokens 16tt + 4g .. +3 of this lane's column: gate products as one 16-byte read,
+      // the v column fragment as one transposed read
+      const f32x4 bel = *(const f32x4*)(sm.bel + 16 * tt + 4 * g);
+      f32x4 y = {0.f, 0.f, 0.f, 0.f};
+      if (!is_m) {
+        const i16x4 vc = ldsT4(sm.V, 16 * tt, col0, c16, g, PITCH);
+        const f32x4 wv = WTOK ? *(const f32x4*)(sm.wtok + 16 * tt + 4 * g) : wreg[tt];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tl = 16 * tt + 4 * g + i;
-        float y = 0.f;
-        if (!is_m) {
-          const float wv = WTOK ? sm.wtok[tl] : wreg[tt][i];
-          y = wv * bf16_val(sm.V[tl * PITCH + col]);
-        }
-        u[tt][i] = y - sm.beta[tl] * sm.elam[tl] * acc[i];
+        for (int i = 0; i < 4; ++i) y[i] = wv[i] * bf16_val(vc[i]);
       }
+      u[tt] = y - bel * acc;
     }
     }
     lds_barrier();
@@ -546,9 +577,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
     i16x4 wh[4], wl[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      f32x4 x;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = u[tt][i] * sm.eend[16 * tt + 4 * g + i];
+      const f32x4 x = u[tt] * *(const f32x4*)(sm.eend + 16 * tt + 4 * g);
       split4(x, wh[tt], wl[tt]);
     }
     const float gdec = sm.elam[CH - 1];
