@@ -30,6 +30,18 @@ int check_launch(const char* what) {
   return MABA_OK;
 }
 
+int device_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 bool expect_shape(const maba_tensor* t, const char* name, int ndim, const int64_t* shape) {
   if (!t || !t->data) {
     set_error("%s: missing tensor", name);

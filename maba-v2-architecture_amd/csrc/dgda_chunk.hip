@@ -12,11 +12,14 @@
 // All decay factors are <= 1, so nothing overflows for any gate values.
 //
 // Sequence parallelism (only B*H = 40 recurrences at the BASELINE shape, but
-// 256 CUs): the sequence of each (b,h) is cut into segments of CPS chunks.
-//   pass 1 (dgda_chunk_kernel<AGG>) runs every segment but the last from a zero
-//          state, carrying X = [N | M] (64 x 128): N is the segment's state from
-//          S0 = 0, M its state transition (X starts as [0 | I], the M half gets
-//          no input), so S_end = M S_start + N.
+// 256 CUs): the (b,h)-major sequence of all B*H*nchunks chunks is cut into slots
+// of U chunks, U = max(CPS, ceil(total / (2 * CUs))), so that the output pass runs
+// exactly one wave of workgroups (two per CU) of equal length.  A segment is the
+// part of one (b,h) sequence inside one slot; each (b,h) has up to nseg_max.
+//   pass 1 (dgda_chunk_kernel<AGG>) runs every segment but the first of each (b,h)
+//          from a zero state, carrying X = [N | M] (64 x 128): N is the segment's
+//          state from S0 = 0, M its state transition (X starts as [0 | I], the M
+//          half gets no input), so S_end = M S_start + N.
 //   pass 2 (dgda_segment_scan_kernel) walks the segments of each (b,h):
 //          S_{s+1} = M_s S_s + N_s, writing every segment's start state.
 //   pass 3 (dgda_chunk_kernel<OUT>) re-runs each segment from its start state and
@@ -49,35 +52,51 @@ constexpr int PITCH = 72;     // bf16 row pitch of LDS matrices (144 B: 16-B ali
 constexpr int TPITCH = 20;    // bf16 row pitch of the 16x16 inverse blocks
 constexpr int CPS = 16;       // chunks per segment
 
-// Output-kernel modes.  OUT_FULL runs every segment from its scanned start state
-// (single-segment sequences).  For several segments, pass 1 records zc[s], the
-// number of chunks after which segment s's transition M is exactly zero in fp32
-// (-1 if it never is); from there on the segment's state, and so its outputs, no
-// longer depend on its start state.  OUT_ZERO then runs every such segment from a
-// zero start (segment 0 from the true initial state) and writes all its outputs
-// and its final state N_s; the scan sets S_{s+1} = N_s where zc[s] >= 0; OUT_FIX
-// re-runs the first zc[s] chunks of those segments from the true start state, and
-// every segment whose M never vanished in full.  With fast decay zc[s] is 1 or 2,
-// so the aggregate and fix-up passes shrink to a chunk or two per segment.
-constexpr int OUT_FULL = 0, OUT_ZERO = 1, OUT_FIX = 2;
+// Output-kernel modes.  Pass 1 records zc[s] for every segment s >= 1 of a (b,h):
+// the number of chunks after which its transition M is exactly zero in fp32 (-1 if
+// it never is); from there on the segment's state, and so its outputs, no longer
+// depend on its start state.  OUT_ZERO (one workgroup per slot) runs segment 0 from
+// the true initial state and every segment with zc[s] >= 0 from a zero start,
+// writing all their outputs and their final states N_s (the true final state for
+// segment 0); the scan sets S_{s+1} = N_s where s = 0 or zc[s] >= 0; OUT_FIX (one
+// workgroup per segment s >= 1) re-runs the first zc[s] chunks of those segments
+// from the true start state, and every segment whose M never vanished in full.
+// With fast decay zc[s] is 1 or 2, so the aggregate and fix-up passes shrink to a
+// chunk or two per segment.  With one segment per (b,h) only OUT_ZERO runs.
+constexpr int OUT_ZERO = 1, OUT_FIX = 2;
 
+// Element strides are 32-bit (the host checks that they fit): the kernel arguments
+// live in scalar registers for the whole kernel.
 struct ChunkArgs {
-  const uint16_t* q; int64_t qs0, qs1, qs2;   // bf16 [B,H,L,64], channel stride 1
-  const uint16_t* k; int64_t ks0, ks1, ks2;
-  const uint16_t* vp; int64_t vs0, vs1, vs2;
-  const float* gp; int64_t gs0, gs1, gs2;    // log_alpha (use_log) or alpha, fp32, per token
-  const float* bp; int64_t bs0, bs1, bs2;     // erase gate b, fp32, per token
-  const float* wp; int64_t ws0, ws1, ws2, ws3;  // write gate w, fp32 (per token when ws3 == 0)
+  const uint16_t* q; int qs0, qs1, qs2;       // bf16 [B,H,L,64], channel stride 1
+  const uint16_t* k; int ks0, ks1, ks2;
+  const uint16_t* vp; int vs0, vs1, vs2;
+  const float* gp; int gs0, gs1, gs2;         // log_alpha (use_log) or alpha, fp32, per token
+  const float* bp; int bs0, bs1, bs2;         // erase gate b, fp32, per token
+  const float* wp; int ws0, ws1, ws2, ws3;    // write gate w, fp32 (per token when ws3 == 0)
   View4 s0;
   int w_tok;                                  // write gate is per token (stride-0 channels)
-  void* op; int64_t os0, os1, os2, os3;       // output (bf16 or fp32, see OBF)
+  void* op; int os0, os1, os2, os3;           // output (bf16 or fp32, see OBF)
   MView4 sf;
-  float* agg;      // [BH, nseg, 64, 128]
-  float* sstart;   // [BH, nseg, 64, 64]
-  int* zc;         // [BH, nseg]: chunks after which the segment's transition M is exactly zero, -1 if never
-  int H, L, nseg, nchunks, use_log, has_s0;
-  int mode;        // output kernel: OUT_FULL, OUT_ZERO or OUT_FIX
+  float* agg;      // [BH, nseg_max, 64, 128]
+  float* sstart;   // [BH, nseg_max, 64, 64]
+  int* zc;         // [BH, nseg_max]: chunks after which the segment's transition M is exactly zero, -1 if never
+  int64_t U;       // chunks per slot
+  int H, L, BH, nseg_max, nchunks, use_log, has_s0;
+  int mode;        // output kernel: OUT_ZERO or OUT_FIX
 };
+
+// Segments of sequence bh: the pieces of [bh * nchunks, (bh + 1) * nchunks) between
+// multiples of U.
+__device__ __forceinline__ int seg_count(const ChunkArgs& a, int bh) {
+  const int64_t s = (int64_t)bh * a.nchunks;
+  return (int)((s + a.nchunks - 1) / a.U - s / a.U + 1);
+}
+__device__ __forceinline__ void seg_range(const ChunkArgs& a, int bh, int k, int n, int& c0, int& c1) {
+  const int64_t s = (int64_t)bh * a.nchunks, f = s / a.U;
+  c0 = k == 0 ? 0 : (int)(a.U * (f + k) - s);
+  c1 = k == n - 1 ? a.nchunks : (int)(a.U * (f + k + 1) - s);
+}
 
 // ------------------------------------------------------------------ MFMA helpers
 
@@ -95,9 +114,17 @@ __device__ __forceinline__ float bf16_val(short h) { return bf16_bits_to_f32((ui
 
 // Split four fp32 values into bf16 hi and lo parts (x ~= hi + lo), using the
 // hardware round-to-nearest-even conversion (v_cvt_pk_bf16_f32).
+// hi's fp32 values are unpacked from the two packed dwords (element 2m in the low
+// half of dword m) rather than converted back one by one.
 __device__ __forceinline__ void split4(f32x4 x, i16x4& hi, i16x4& lo) {
+  typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
   const bf16x4 h = __builtin_convertvector(x, bf16x4);
-  const f32x4 hf = __builtin_convertvector(h, f32x4);
+  const u32x2 hb = __builtin_bit_cast(u32x2, h);
+  f32x4 hf;
+  hf[0] = __uint_as_float(hb[0] << 16);
+  hf[1] = __uint_as_float(hb[0] & 0xffff0000u);
+  hf[2] = __uint_as_float(hb[1] << 16);
+  hf[3] = __uint_as_float(hb[1] & 0xffff0000u);
   const bf16x4 l = __builtin_convertvector(x - hf, bf16x4);
   hi = __builtin_bit_cast(i16x4, h);
   lo = __builtin_bit_cast(i16x4, l);
@@ -239,63 +266,65 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
 // global loads (the next chunk's prefetch stays in flight across it).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// The kernel's arguments read in place from the kernarg segment (see dgda_chunk_kernel).
+typedef const __attribute__((address_space(4))) ChunkArgs KArgs;
+
+// One segment: chunks [c_begin, c_end) of sequence bh, segment k of n.
 template <bool AGG, bool WTOK, bool OBF>
-__global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kernel(ChunkArgs a) {
+__device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int* s_mzero, int tid,
+                                              int bh, int k, int n, int c_begin, int c_end) {
   constexpr int NW = AGG ? 8 : 4;
   constexpr int IPT = (CH * 8) / (NW * 64);  // 16-byte staging items per thread
-  __shared__ ChunkSmem<AGG> sm;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int seg = blockIdx.x % a.nseg;
-  const int bh = blockIdx.x / a.nseg;
   const int bi = bh / a.H, hi = bh % a.H;
-  const int64_t sidx = (int64_t)bh * a.nseg + seg;
-  int c_begin = seg * CPS;
-  int c_end = min(a.nchunks, c_begin + CPS);
-  if (!AGG && a.mode == OUT_ZERO && a.zc[sidx] < 0) return;  // M never vanished: OUT_FIX runs it in full
-  if (!AGG && a.mode == OUT_FIX && a.zc[sidx] >= 0) {
-    if (seg == 0) return;                                     // OUT_ZERO ran it from the true start
-    c_end = c_begin + a.zc[sidx];                             // only the chunks that see the start state
-  }
-  // OUT_FIX: when the predecessor's M vanished its final state N_{s-1} is this segment's start
-  const bool pred_zero = !AGG && a.mode == OUT_FIX && seg > 0 && a.zc[sidx - 1] >= 0;
+  const int64_t sidx = (int64_t)bh * a.nseg_max + k;
+  const bool last = k == n - 1;
+  if (!AGG && a.mode == OUT_ZERO && k > 0 && a.zc[sidx] < 0) return;  // M never vanished: OUT_FIX runs it in full
+  if (!AGG && a.mode == OUT_FIX && a.zc[sidx] >= 0)
+    c_end = c_begin + a.zc[sidx];                                     // only the chunks that see the start state
+  // OUT_FIX (k >= 1): the start state is N_{k-1} when that is final (k - 1 = 0, or its M vanished)
+  const bool pred_final = !AGG && a.mode == OUT_FIX && (k == 1 || a.zc[sidx - 1] >= 0);
 
-  // Carried state slab: S[16kt + 4g + i][col0 + c16] in Sr[kt][i].
+  // Carried state slab: S[16kt + 4g + i][col0 + c16] in Sr[kt][i].  The source is
+  // chosen once (uniform branches), so the slab's 16 loads issue back to back.
   f32x4 Sr[4];
   const int col0 = (wave & 3) * 16;
   const int col = col0 + c16;
   const bool is_m = AGG && wave >= 4;  // pass 1: M half of [N | M]
+  auto fill = [&](auto load) {
 #pragma unroll
-  for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * kt + 4 * g + i;
-      float x = 0.f;
-      if (AGG) {
-        x = (is_m && r == col) ? 1.f : 0.f;
-      } else if (seg == 0) {
-        x = a.has_s0 ? a.s0.at(bi, hi, r, col) : 0.f;
-      } else if (a.mode == OUT_ZERO) {
-        x = 0.f;
-      } else if (pred_zero) {
-        x = a.agg[((sidx - 1) * 64 + r) * 128 + col];   // S_s = N_{s-1} when M_{s-1} = 0
-      } else {
-        x = a.sstart[(sidx * 64 + r) * 64 + col];
-      }
-      Sr[kt][i] = x;
-    }
+      for (int i = 0; i < 4; ++i) Sr[kt][i] = load(16 * kt + 4 * g + i);
+  };
+  if (AGG) {
+    fill([&](int r) { return (is_m && r == col) ? 1.f : 0.f; });
+  } else if (k == 0 && a.has_s0) {
+    const int64_t o = bi * a.s0.s0 + hi * a.s0.s1 + col * a.s0.s3, rs = a.s0.s2;
+    if (a.s0.dt == MABA_F32) fill([&](int r) { return ((const float*)a.s0.p)[o + r * rs]; });
+    else if (a.s0.dt == MABA_BF16) fill([&](int r) { return bf16_bits_to_f32(((const uint16_t*)a.s0.p)[o + r * rs]); });
+    else fill([&](int r) { return __half2float(((const __half*)a.s0.p)[o + r * rs]); });
+  } else if (k == 0 || a.mode == OUT_ZERO) {
+    fill([&](int) { return 0.f; });
+  } else if (pred_final) {
+    const float* src = a.agg + (sidx - 1) * 64 * 128 + col;   // S_k = N_{k-1}
+    fill([&](int r) { return src[r * 128]; });
+  } else {
+    const float* src = a.sstart + sidx * 64 * 64 + col;
+    fill([&](int r) { return src[r * 64]; });
   }
 
-  const uint16_t* qb = a.q + bi * a.qs0 + hi * a.qs1;
-  const uint16_t* kb = a.k + bi * a.ks0 + hi * a.ks1;
-  const uint16_t* vb = a.vp + bi * a.vs0 + hi * a.vs1;
-  const float* gb = a.gp + bi * a.gs0 + hi * a.gs1;
-  const float* bb = a.bp + bi * a.bs0 + hi * a.bs1;
-  const float* wb = a.wp + bi * a.ws0 + hi * a.ws1 + (WTOK ? 0 : (int64_t)col * a.ws3);
+  const uint16_t* qb = a.q + (int64_t)bi * a.qs0 + (int64_t)hi * a.qs1;
+  const uint16_t* kb = a.k + (int64_t)bi * a.ks0 + (int64_t)hi * a.ks1;
+  const uint16_t* vb = a.vp + (int64_t)bi * a.vs0 + (int64_t)hi * a.vs1;
+  const float* gb = a.gp + (int64_t)bi * a.gs0 + (int64_t)hi * a.gs1;
+  const float* bb = a.bp + (int64_t)bi * a.bs0 + (int64_t)hi * a.bs1;
+  const float* wb = a.wp + (int64_t)bi * a.ws0 + (int64_t)hi * a.ws1 + (WTOK ? 0 : (int64_t)col * a.ws3);
   // output: this lane's column and rows 4g..4g+3 of a 16-row block, advanced per block
   // output (unit column stride): this lane writes token row c16 of each 16-row block,
   // columns col0 + 4g .. +3, as one 8- or 16-byte store
-  const int64_t obase = bi * a.os0 + hi * a.os1 + (int64_t)c16 * a.os2 + col0 + 4 * g;
+  const int64_t obase = (int64_t)bi * a.os0 + (int64_t)hi * a.os1 + (int64_t)c16 * a.os2 + col0 + 4 * g;
 
   // ---- register prefetch of one chunk's k, v, q rows and per-token gates
   i16x8 pk[IPT], pv[IPT], pq[IPT];
@@ -330,12 +359,20 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
   // products for the rest of the segment while still joining every barrier.  With
   // fast decay e^{Lam_63} underflows within a chunk or two.
   bool idle = false;
-  __shared__ int s_mzero[4];  // pass 1: M slab w of the workgroup is exactly zero
-  if (AGG && tid < 4) s_mzero[tid] = 0;
+  if (AGG && tid < 4) s_mzero[tid] = 0;   // pass 1: M slab w of the workgroup is exactly zero
   int c_stop = -1;            // pass 1: chunk at which M was found to be zero
 
+  // Output pass: the hardware fills each CU with one workgroup from the first half of
+  // the grid and then one from the second, and among equal priorities the older waves
+  // issue first, so the two workgroups of a CU would finish far apart.  They take turns
+  // at the higher wave priority from chunk to chunk instead.
+  const int prio_phase = (!AGG && a.mode == OUT_ZERO && blockIdx.x >= gridDim.x / 2) ? 1 : 0;
   for (int c = c_begin; c < c_end; ++c) {
     const int t0 = c * CH;
+    if (!AGG && a.mode == OUT_ZERO) {
+      if ((c + prio_phase) & 1) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     // per-channel write gate: this wave's 16 values, fetched before the staging barrier
     f32x4 wreg[4];
     if (!WTOK && !is_m) {
@@ -614,82 +651,121 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 128 + cc] = Sr[kt][i];
     }
-  } else if (a.mode == OUT_ZERO && seg < a.nseg - 1) {  // N_s for the scan and the fix-up pass
+  } else if (a.mode == OUT_ZERO && !last) {  // N_k for the scan and the fix-up pass
     float* dst = a.agg + sidx * 64 * 128;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 128 + col] = Sr[kt][i];
-  } else if (seg == a.nseg - 1 && !(a.mode == OUT_FIX && a.zc[sidx] >= 0)) {
+  } else if (last && !(a.mode == OUT_FIX && a.zc[sidx] >= 0)) {
+    const int64_t o = bi * a.sf.s0 + hi * a.sf.s1 + col * a.sf.s3, rs = a.sf.s2;
+    auto drain = [&](auto put) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a.sf.put(bi, hi, 16 * kt + 4 * g + i, col, Sr[kt][i]);
+        for (int i = 0; i < 4; ++i) put(o + (16 * kt + 4 * g + i) * rs, Sr[kt][i]);
+    };
+    if (a.sf.dt == MABA_F32) drain([&](int64_t e, float v) { ((float*)a.sf.p)[e] = v; });
+    else if (a.sf.dt == MABA_BF16) drain([&](int64_t e, float v) { ((uint16_t*)a.sf.p)[e] = f32_to_bf16_bits(v); });
+    else drain([&](int64_t e, float v) { ((__half*)a.sf.p)[e] = __float2half(v); });
+  }
+}
+
+template <bool AGG, bool WTOK, bool OBF>
+__global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kernel(ChunkArgs a) {
+  __shared__ ChunkSmem<AGG> sm;
+  __shared__ int s_mzero[4];
+  // Pass 1 and OUT_FIX: one workgroup per segment k >= 1.  OUT_ZERO: slot w covers
+  // the chunks [U w, U w + U) of the (b,h)-major order, one segment per sequence it
+  // touches.  Both walk the same loop so the segment body is inlined once.
+  const bool per_segment = AGG || a.mode == OUT_FIX;
+  const int64_t total = (int64_t)a.BH * a.nchunks;
+  int64_t G = per_segment ? 0 : (int64_t)blockIdx.x * a.U;
+  const int64_t Gend = per_segment ? 1 : min(G + a.U, total);
+  while (G < Gend) {
+    int bh, k, n, c0, c1;
+    if (per_segment) {
+      const int per = a.nseg_max - 1;
+      bh = blockIdx.x / per;
+      k = blockIdx.x % per + 1;
+      n = seg_count(a, bh);
+      if (k >= n) return;
+      seg_range(a, bh, k, n, c0, c1);
+      G = Gend;
+    } else {
+      bh = (int)(G / a.nchunks);
+      const int64_t s = (int64_t)bh * a.nchunks;
+      c0 = (int)(G - s);
+      c1 = (int)(min(Gend, s + a.nchunks) - s);
+      k = c0 == 0 ? 0 : (int)(blockIdx.x - s / a.U);
+      n = seg_count(a, bh);
+      G = s + c1;
+    }
+    // The thread index and the argument pointer pass through empty asm statements so
+    // that nothing derived from them is hoisted out of this loop and held across the
+    // segments: the segment body reads its arguments where it uses them (scalar loads
+    // from the kernarg segment, where the single ChunkArgs argument sits at offset 0).
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    KArgs* ap = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    chunk_segment<AGG, WTOK, OBF>(*ap, sm, s_mzero, tid, bh, k, n, c0, c1);
   }
 }
 
 // ------------------------------------------------------------------ pass 2: segment scan
 // One wave per (b,h, 16-column slab): S_{s+1} = M_s S_s + N_s with fp32 accuracy
-// (M and S both split into bf16 hi/lo), or S_{s+1} = N_s where M_s is exactly zero
-// (zc[s] >= 0).  Writes the start state of segments 1..nseg-1; the fix-up pass only
-// reads it after a segment whose M did not vanish, so if every M vanished there is
-// nothing to do.
+// (M and S both split into bf16 hi/lo), or S_{s+1} = N_s where N_s is final
+// (s = 0, which the output pass ran from the true initial state, or M_s exactly zero,
+// zc[s] >= 0).  Writes the start state of segments 1..n-1; the fix-up pass only
+// reads it after a segment s >= 1 whose M did not vanish, so if there is none there
+// is nothing to do.
 __global__ __launch_bounds__(64) void dgda_segment_scan_kernel(ChunkArgs a) {
   const int bh = blockIdx.x >> 2;
   const int col0 = (blockIdx.x & 3) * 16;
-  const int bi = bh / a.H, hi = bh % a.H;
   const int lane = threadIdx.x, g = lane >> 4, c16 = lane & 15;
-  const int* zc = a.zc + (int64_t)bh * a.nseg;
+  const int n = seg_count(a, bh);
+  const int* zc = a.zc + (int64_t)bh * a.nseg_max;
   bool any_full = false;
-  for (int s = lane; s + 1 < a.nseg; s += 64) any_full |= zc[s] < 0;
+  for (int s = 1 + lane; s + 1 < n; s += 64) any_full |= zc[s] < 0;
   if (__ballot(any_full) == 0ull) return;
   f32x4 Sr[4];
-#pragma unroll
-  for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      Sr[kt][i] = a.has_s0 ? a.s0.at(bi, hi, 16 * kt + 4 * g + i, col0 + c16) : 0.f;
-  for (int s = 0; s + 1 < a.nseg; ++s) {
-    const float* X = a.agg + ((int64_t)bh * a.nseg + s) * 64 * 128;
-    if (zc[s] >= 0) {  // M_s = 0: S_{s+1} = N_s
+  for (int s = 0; s + 1 < n; ++s) {
+    const float* X = a.agg + ((int64_t)bh * a.nseg_max + s) * 64 * 128;
+    float* dst = a.sstart + ((int64_t)bh * a.nseg_max + s + 1) * 64 * 64;
+    if (s == 0 || zc[s] >= 0) {  // S_{s+1} = N_s
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) Sr[kt][i] = X[(16 * kt + 4 * g + i) * 128 + col0 + c16];
-      float* dst = a.sstart + ((int64_t)bh * a.nseg + s + 1) * 64 * 64;
+    } else {
+      i16x4 Sh[4], Sl[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 64 + col0 + c16] = Sr[kt][i];
-      continue;
-    }
-    i16x4 Sh[4], Sl[4];
+      for (int mt = 0; mt < 4; ++mt) {
+        f32x4 acc;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
+        for (int i = 0; i < 4; ++i) acc[i] = X[(16 * mt + 4 * g + i) * 128 + col0 + c16];  // N_s
+        const int row = 16 * mt + c16;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      f32x4 acc;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = X[(16 * mt + 4 * g + i) * 128 + col0 + c16];  // N_s
-      const int row = 16 * mt + c16;
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        // A operand: M_s[row][32p + 4g..+3] and [32p + 16 + 4g..+3]  (M lives in columns 64..127)
-        const float4 m0 = *(const float4*)(X + row * 128 + 64 + 32 * p + 4 * g);
-        const float4 m1 = *(const float4*)(X + row * 128 + 64 + 32 * p + 16 + 4 * g);
-        f32x4 mlo = {m0.x, m0.y, m0.z, m0.w}, mhi = {m1.x, m1.y, m1.z, m1.w};
-        i16x4 h0, l0, h1, l1;
-        split4(mlo, h0, l0);
-        split4(mhi, h1, l1);
-        const i16x8 ah = cat8(h0, h1), al = cat8(l0, l1);
-        const i16x8 bh8 = cat8(Sh[2 * p], Sh[2 * p + 1]), bl8 = cat8(Sl[2 * p], Sl[2 * p + 1]);
-        acc = mma32(acc, ah, bh8);
-        acc = mma32(acc, ah, bl8);
-        acc = mma32(acc, al, bh8);
+        for (int p = 0; p < 2; ++p) {
+          // A operand: M_s[row][32p + 4g..+3] and [32p + 16 + 4g..+3]  (M lives in columns 64..127)
+          const float4 m0 = *(const float4*)(X + row * 128 + 64 + 32 * p + 4 * g);
+          const float4 m1 = *(const float4*)(X + row * 128 + 64 + 32 * p + 16 + 4 * g);
+          f32x4 mlo = {m0.x, m0.y, m0.z, m0.w}, mhi = {m1.x, m1.y, m1.z, m1.w};
+          i16x4 h0, l0, h1, l1;
+          split4(mlo, h0, l0);
+          split4(mhi, h1, l1);
+          const i16x8 ah = cat8(h0, h1), al = cat8(l0, l1);
+          const i16x8 bh8 = cat8(Sh[2 * p], Sh[2 * p + 1]), bl8 = cat8(Sl[2 * p], Sl[2 * p + 1]);
+          acc = mma32(acc, ah, bh8);
+          acc = mma32(acc, ah, bl8);
+          acc = mma32(acc, al, bh8);
+        }
+        Sr[mt] = acc;
       }
-      Sr[mt] = acc;
     }
-    float* dst = a.sstart + ((int64_t)bh * a.nseg + s + 1) * 64 * 64;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -700,6 +776,12 @@ __global__ __launch_bounds__(64) void dgda_segment_scan_kernel(ChunkArgs a) {
 // ------------------------------------------------------------------ host side
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool dgda_chunk_strides_fit(const maba_tensor* t) {
+  for (int d = 0; d < t->ndim; ++d)
+    if (t->stride[d] < 0 || t->stride[d] > INT32_MAX) return false;
+  return true;
+}
 
 bool dgda_chunk_supported(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                           const maba_tensor* gate, const maba_tensor* b) {
@@ -715,17 +797,35 @@ bool dgda_chunk_supported(const maba_tensor* q, const maba_tensor* k, const maba
     for (int d = 0; d < 3; ++d)
       if (t->shape[d] > 1 && (t->stride[d] % 8) != 0) return false;
   }
+  for (const maba_tensor* t : {q, k, v, gate, b})
+    if (!dgda_chunk_strides_fit(t)) return false;
   return true;
 }
 
-static int nseg_for(int64_t L) {
-  const int64_t nch = ceil_div(L, CH);
-  return (int)ceil_div(nch > 0 ? nch : 1, CPS);
+// Slot geometry: U chunks per slot, at most nseg_max segments per sequence (1 when
+// every sequence fits one slot and the slots are aligned to sequences).
+struct ChunkGeom { int64_t U; int nseg_max; };
+
+static ChunkGeom chunk_geom(int64_t BH, int64_t L) {
+  const int64_t nch = ceil_div(L, CH) > 0 ? ceil_div(L, CH) : 1;
+  const int64_t slots = 2 * (int64_t)device_cu_count();   // two output workgroups per CU
+  int64_t U = ceil_div(BH * nch, slots);
+  if (U < CPS) U = CPS;
+  ChunkGeom gm;
+  if (nch <= U) {   // one sequence per slot: no cuts inside a sequence
+    gm.U = nch;
+    gm.nseg_max = 1;
+  } else {
+    gm.U = U;
+    gm.nseg_max = (int)(ceil_div(nch - 1, U) + 1);
+  }
+  return gm;
 }
 
 size_t dgda_chunk_workspace(int64_t BH, int64_t L) {
-  const int64_t nseg = nseg_for(L);
-  if (nseg <= 1) return 16;
+  const ChunkGeom gm = chunk_geom(BH, L);
+  if (gm.nseg_max <= 1) return 16;
+  const int64_t nseg = gm.nseg_max;
   return (size_t)(BH * nseg * 64 * (128 + 64)) * sizeof(float) + (size_t)(BH * nseg) * sizeof(int);
 }
 
@@ -736,43 +836,50 @@ int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_ten
   const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2];
   const int64_t BH = B * H;
   ChunkArgs a;
-  a.q = (const uint16_t*)q->data; a.qs0 = q->stride[0]; a.qs1 = q->stride[1]; a.qs2 = q->stride[2];
-  a.k = (const uint16_t*)k->data; a.ks0 = k->stride[0]; a.ks1 = k->stride[1]; a.ks2 = k->stride[2];
-  a.vp = (const uint16_t*)v->data; a.vs0 = v->stride[0]; a.vs1 = v->stride[1]; a.vs2 = v->stride[2];
-  a.gp = (const float*)gate->data; a.gs0 = gate->stride[0]; a.gs1 = gate->stride[1]; a.gs2 = gate->stride[2];
-  a.bp = (const float*)b->data; a.bs0 = b->stride[0]; a.bs1 = b->stride[1]; a.bs2 = b->stride[2];
-  a.wp = (const float*)w->data; a.ws0 = w->stride[0]; a.ws1 = w->stride[1]; a.ws2 = w->stride[2];
-  a.ws3 = w->stride[3];
+  // strides fit in int32 (dgda_chunk_supported and the caller check every operand)
+  a.q = (const uint16_t*)q->data; a.qs0 = (int)q->stride[0]; a.qs1 = (int)q->stride[1]; a.qs2 = (int)q->stride[2];
+  a.k = (const uint16_t*)k->data; a.ks0 = (int)k->stride[0]; a.ks1 = (int)k->stride[1]; a.ks2 = (int)k->stride[2];
+  a.vp = (const uint16_t*)v->data; a.vs0 = (int)v->stride[0]; a.vs1 = (int)v->stride[1]; a.vs2 = (int)v->stride[2];
+  a.gp = (const float*)gate->data; a.gs0 = (int)gate->stride[0]; a.gs1 = (int)gate->stride[1];
+  a.gs2 = (int)gate->stride[2];
+  a.bp = (const float*)b->data; a.bs0 = (int)b->stride[0]; a.bs1 = (int)b->stride[1]; a.bs2 = (int)b->stride[2];
+  a.wp = (const float*)w->data; a.ws0 = (int)w->stride[0]; a.ws1 = (int)w->stride[1]; a.ws2 = (int)w->stride[2];
+  a.ws3 = (int)w->stride[3];
   a.s0 = view4(s0);
   a.w_tok = w->stride[3] == 0;
-  a.op = out->data; a.os0 = out->stride[0]; a.os1 = out->stride[1]; a.os2 = out->stride[2]; a.os3 = out->stride[3];
+  a.op = out->data; a.os0 = (int)out->stride[0]; a.os1 = (int)out->stride[1]; a.os2 = (int)out->stride[2];
+  a.os3 = (int)out->stride[3];
   a.sf = mview4(sf);
-  a.H = (int)H; a.L = (int)L;
-  a.nchunks = (int)ceil_div(L, CH);
-  a.nseg = nseg_for(L);
+  a.H = (int)H; a.L = (int)L; a.BH = (int)BH;
+  a.nchunks = (int)(ceil_div(L, CH) > 0 ? ceil_div(L, CH) : 1);
+  const ChunkGeom gm = chunk_geom(BH, L);
+  a.U = gm.U;
+  a.nseg_max = gm.nseg_max;
   a.use_log = use_log; a.has_s0 = s0 != nullptr;
   const size_t need = dgda_chunk_workspace(BH, L);
   if (ws_bytes < need) return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace too small");
+  const int64_t nsegs = BH * a.nseg_max;
   a.agg = (float*)ws;
-  a.sstart = a.agg + BH * a.nseg * 64 * 128;
-  a.zc = (int*)(a.sstart + BH * a.nseg * 64 * 64);
-  const dim3 grid((unsigned)(BH * a.nseg));
+  a.sstart = a.agg + nsegs * 64 * 128;
+  a.zc = (int*)(a.sstart + nsegs * 64 * 64);
   const bool obf = out->dtype == MABA_BF16;
   auto launch_out = [&](int mode) {
     a.mode = mode;
+    const dim3 grid(mode == OUT_ZERO ? (unsigned)ceil_div(BH * a.nchunks, a.U) : (unsigned)(BH * (a.nseg_max - 1)));
     if (a.w_tok && obf) hipLaunchKernelGGL((dgda_chunk_kernel<false, true, true>), grid, dim3(256), 0, stream, a);
     else if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<false, true, false>), grid, dim3(256), 0, stream, a);
     else if (obf) hipLaunchKernelGGL((dgda_chunk_kernel<false, false, true>), grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((dgda_chunk_kernel<false, false, false>), grid, dim3(256), 0, stream, a);
     return check_launch("dgda_prefill/output");
   };
-  if (a.nseg == 1) {
+  if (a.nseg_max == 1) {
     a.zc = nullptr;
-    return launch_out(OUT_FULL);
+    return launch_out(OUT_ZERO);
   }
-  a.mode = OUT_FULL;
-  if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<true, true, true>), grid, dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((dgda_chunk_kernel<true, false, true>), grid, dim3(512), 0, stream, a);
+  a.mode = OUT_ZERO;
+  const dim3 agrid((unsigned)(BH * (a.nseg_max - 1)));
+  if (a.w_tok) hipLaunchKernelGGL((dgda_chunk_kernel<true, true, true>), agrid, dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((dgda_chunk_kernel<true, false, true>), agrid, dim3(512), 0, stream, a);
   int rc = check_launch("dgda_prefill/aggregate");
   if (rc) return rc;
   if ((rc = launch_out(OUT_ZERO))) return rc;

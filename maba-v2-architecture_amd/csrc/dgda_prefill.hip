@@ -103,6 +103,7 @@ int launch_dgda_seq(const maba_tensor* q, const maba_tensor* k, const maba_tenso
 }
 
 // Chunked MFMA path (dgda_chunk.hip).
+bool dgda_chunk_strides_fit(const maba_tensor* t);
 bool dgda_chunk_supported(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                           const maba_tensor* gate, const maba_tensor* b);
 size_t dgda_chunk_workspace(int64_t BH, int64_t L);
@@ -152,7 +153,8 @@ extern "C" int maba_hip_dgda_prefill(const maba_tensor* q, const maba_tensor* k,
   const bool out_vec = out->stride[3] == 1 && (uintptr_t)out->data % 16 == 0 && out->stride[0] % 4 == 0 &&
                        out->stride[1] % 4 == 0 && out->stride[2] % 4 == 0;
   if (dgda_chunk_supported(q, k, v, gate, b) && w->dtype == MABA_F32 &&
-      (out->dtype == MABA_BF16 || out->dtype == MABA_F32) && out_vec) {
+      (out->dtype == MABA_BF16 || out->dtype == MABA_F32) && out_vec && dgda_chunk_strides_fit(w) &&
+      dgda_chunk_strides_fit(out)) {
     const size_t need = dgda_chunk_workspace(B * H, L);
     if (!workspace || workspace_bytes < need)
       return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace of %zu bytes required", need);

@@ -14,6 +14,8 @@ namespace maba {
 void set_error(const char* fmt, ...);
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Compute units of the current device (cached per device; 256 when it cannot be queried).
+int device_cu_count();
 
 // ---------------------------------------------------------------- scalar types
 typedef __attribute__((ext_vector_type(4))) float f32x4;

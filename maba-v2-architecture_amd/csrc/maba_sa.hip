@@ -527,18 +527,6 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
 }
 
 // Compute units of the current device (queried once per device).
-static int sa_cu_count() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 static void sa_geometry(SaArgs& a, int64_t L, int window, int n_sink, int pool, int Hi, int K) {
   const int64_t ns = L < n_sink ? L : n_sink;
   const int64_t st = (L - window) > ns ? (L - window) : ns;
@@ -618,7 +606,7 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
   if (mfma_ok) {
     // tiles per wave: the fewest that still fit one workgroup per CU (every workgroup
     // pays a fixed start-up, and one round of workgroups covers the machine), at most 8
-    const int ncu = sa_cu_count();
+    const int ncu = device_cu_count();
     int tpw = 1, span = 4, s_sp1 = 0, s_sp = 0, s_hca = 0, nseg = 0;
     for (tpw = 1; tpw <= 8; ++tpw) {
       span = 4 * tpw;

@@ -86,15 +86,30 @@ def test_prefill_shape_mismatch(lib):
     assert rc == N.MABA_ERR_INVALID
 
 
+def _slot_geometry(BH, nch, cus=256):
+    """Chunks per slot U and segments per sequence: the B*H*nch chunks in (b,h)-major
+    order are cut into slots of U = max(16, ceil(total / (2 * CUs))) chunks; a
+    sequence that fits one slot is never cut."""
+    U = max(16, -(-BH * nch // (2 * cus)))
+    if nch <= U:
+        return nch, 1
+    return U, -(-(nch - 1) // U) + 1
+
+
 def test_prefill_workspace_size_at_baseline_shape(lib):
-    """B=4, H=10, T=32768: 32 segments of 1024 tokens per head, each carrying a
-    [64, 128] fp32 aggregate, a [64, 64] fp32 start state and an int32 chunk count."""
+    """B=4, H=10, T=32768 (512 chunks per head): slots of 40 chunks, so up to 14
+    segments per head, each carrying a [64, 128] fp32 aggregate, a [64, 64] fp32 start
+    state and an int32 chunk count.  No GPU here: the library assumes 256 CUs."""
     B, H, T, d = 4, 10, 32768, 64
     q = _t([B, H, T, d])
     gate = _t([B, H, T, d], N.MABA_F32, strides=[H * T, T, 1, 0])   # per-token, stride-0 channels
     n = lib.maba_hip_dgda_prefill_workspace_size(q, q, gate, gate)
-    nseg = T // 1024
+    U, nseg = _slot_geometry(B * H, T // 64)
+    assert (U, nseg) == (40, 14)
     assert n == B * H * nseg * (64 * (128 + 64) * 4 + 4)   # + one chunk count per segment
+    short = _t([B, H, 1024, d])                               # 16 chunks: one slot per head, no workspace
+    sgate = _t([B, H, 1024, d], N.MABA_F32, strides=[H * 1024, 1024, 1, 0])
+    assert lib.maba_hip_dgda_prefill_workspace_size(short, short, sgate, sgate) == 16
     per_channel = _t([B, H, T, d], N.MABA_F32)
     assert lib.maba_hip_dgda_prefill_workspace_size(q, q, per_channel, gate) == 0   # sequential path
 

@@ -139,3 +139,28 @@ def test_chunk_mixed_decay_segments(dev):
     eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
     assert_close(o, eo, 2e-3, 2e-3, "out")
     assert_close(S, eS, 2e-3, 2e-3, "state")
+
+
+@pytest.mark.parametrize("decay", ["baseline", "slow"])
+def test_chunk_slot_boundaries_multi_head(dev, decay):
+    """Six heads of 65 chunks: the output pass's 16-chunk slots start inside sequences
+    and span two sequences, so segments of every length meet at the cuts."""
+    inp = dgda_inputs(2, 3, 4100, seed=21, decay=decay, device=dev, with_state=True)
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, f"out {decay}")
+    assert_close(S, eS, 2e-3, 2e-3, f"state {decay}")
+
+
+def test_chunk_wide_slots_vs_c_oracle(dev):
+    """36 heads of 256 chunks exceed 16 chunks per slot on 256 CUs (U = 18), so the cuts
+    fall at sequence offsets that move from head to head; four heads are checked
+    against the C chunked oracle."""
+    inp = dgda_inputs(1, 36, 16384, seed=5, device=dev)
+    o, S = _run(inp)
+    heads = [0, 1, 17, 35]
+    f = lambda t: to_np(t[:, heads]).astype(np.float32)  # noqa: E731
+    eo, eS = dgda_c.dgda_prefill_chunked_c(f(inp["q"]), f(inp["k"]), f(inp["v"]), f(inp["log_alpha"][..., :1]),
+                                           f(inp["b"][..., :1]), f(inp["w"][..., :1]), chunk_size=64)
+    assert_close(o[:, heads], eo, 2e-3, 2e-3, "out")
+    assert_close(S[:, heads], eS, 2e-3, 2e-3, "state")
