@@ -5,6 +5,8 @@
 
 #include "maba_common.h"
 
+#include <atomic>
+
 namespace maba {
 
 static thread_local char g_last_error[1024] = "";
@@ -31,15 +33,15 @@ int check_launch(const char* what) {
 }
 
 int device_cu_count() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];   // zero-initialised (static storage); 0 = not queried yet
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 bool expect_shape(const maba_tensor* t, const char* name, int ndim, const int64_t* shape) {
