@@ -114,20 +114,37 @@ __device__ __forceinline__ float bf16_val(short h) { return bf16_bits_to_f32((ui
 
 // Split four fp32 values into bf16 hi and lo parts (x ~= hi + lo), using the
 // hardware round-to-nearest-even conversion (v_cvt_pk_bf16_f32).
-// hi's fp32 values are unpacked from the two packed dwords (element 2m in the low
-// half of dword m) rather than converted back one by one.
+// Two fp32 values to packed bf16 (round to nearest even), the first in the low half:
+// one v_cvt_pk_bf16_f32.  Converting pairs (not 4-vectors) keeps the compiler on the
+// packed form instead of re-deriving it from single conversions and byte permutes.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// hi's fp32 values are unpacked from the two packed dwords (element 2m in the low half
+// of dword m).
 __device__ __forceinline__ void split4(f32x4 x, i16x4& hi, i16x4& lo) {
   typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
-  const bf16x4 h = __builtin_convertvector(x, bf16x4);
-  const u32x2 hb = __builtin_bit_cast(u32x2, h);
+  const uint32_t h01 = cvt_pk_bf16(x[0], x[1]), h23 = cvt_pk_bf16(x[2], x[3]);
   f32x4 hf;
-  hf[0] = __uint_as_float(hb[0] << 16);
-  hf[1] = __uint_as_float(hb[0] & 0xffff0000u);
-  hf[2] = __uint_as_float(hb[1] << 16);
-  hf[3] = __uint_as_float(hb[1] & 0xffff0000u);
-  const bf16x4 l = __builtin_convertvector(x - hf, bf16x4);
-  hi = __builtin_bit_cast(i16x4, h);
-  lo = __builtin_bit_cast(i16x4, l);
+  hf[0] = __uint_as_float(h01 << 16);
+  hf[1] = __uint_as_float(h01 & 0xffff0000u);
+  hf[2] = __uint_as_float(h23 << 16);
+  hf[3] = __uint_as_float(h23 & 0xffff0000u);
+  const f32x4 r = x - hf;
+  const u32x2 hv = {h01, h23}, lv = {cvt_pk_bf16(r[0], r[1]), cvt_pk_bf16(r[2], r[3])};
+  hi = __builtin_bit_cast(i16x4, hv);
+  lo = __builtin_bit_cast(i16x4, lv);
+}
+
+// Four fp32 values to bf16, packed.
+__device__ __forceinline__ bf16x4 to_bf16x4(f32x4 x) {
+  typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+  const u32x2 v = {cvt_pk_bf16(x[0], x[1]), cvt_pk_bf16(x[2], x[3])};
+  return __builtin_bit_cast(bf16x4, v);
 }
 
 __device__ __forceinline__ i16x8 cat8(i16x4 a, i16x4 b) {
@@ -447,7 +464,10 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
         else val[r] = (ISA ? j <= i : j < i) ? x : 0.f;
       }
       if (!ISA) val = val * sm.beta[i];
-      if (!ISA && I == J) *(f32x4*)(sm.LD + I * DTILE_ELEMS + c16 * DPITCH + 4 * g) = val;
+      if (!ISA && I == J) {   // diagonal L tiles only feed the inverses, in fp32
+        *(f32x4*)(sm.LD + I * DTILE_ELEMS + c16 * DPITCH + 4 * g) = val;
+        return;
+      }
       i16x4 h, l;
       split4(val, h, l);
       const int off = (I * (I + 1) / 2 + J) * TILE_ELEMS + c16 * TPITCH + 4 * g;
@@ -603,7 +623,7 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
         if (t0 + tl < a.L) {
           const f32x4 ov = sm.elam[tl] * qs + au;
           const int64_t off = obase + (int64_t)(t0 + 16 * I) * a.os2;
-          if (OBF) *(bf16x4*)((short*)a.op + off) = __builtin_convertvector(ov, bf16x4);
+          if (OBF) *(bf16x4*)((short*)a.op + off) = to_bf16x4(ov);
           else *(f32x4*)((float*)a.op + off) = ov;
         }
       }
