@@ -343,6 +343,14 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
   // columns col0 + 4g .. +3, as one 8- or 16-byte store
   const int64_t obase = (int64_t)bi * a.os0 + (int64_t)hi * a.os1 + (int64_t)c16 * a.os2 + col0 + 4 * g;
 
+  // Output pass: wave roles rotate by two in the second half of the grid.  The two
+  // workgroups of a CU place wave w on the same SIMD, so this pairs the diagonal-
+  // inverse wave of one with a five-tile wave of the other, and the six-tile wave with
+  // the wave that also forms the gates.
+  const int rot = (!AGG && a.mode == OUT_ZERO && blockIdx.x >= gridDim.x / 2) ? 2 : 0;
+  const int role = (wave + rot) & 3;
+  const bool gate_wave = AGG ? wave == 0 : role == 2;   // forms the per-token gate arrays
+
   // ---- register prefetch of one chunk's k, v, q rows and per-token gates
   i16x8 pk[IPT], pv[IPT], pq[IPT];
   float pla = 0.f, pbe = 0.f, pwt = 0.f;
@@ -360,8 +368,8 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
         if (!AGG) pq[it] = *(const i16x8*)(qb + (int64_t)(t0 + t) * a.qs2 + c8);
       }
     }
-    if (tid < CH) {
-      const int t = t0 + tid;
+    if (gate_wave) {
+      const int t = t0 + lane;
       pla = 0.f; pbe = 0.f; pwt = 0.f;
       if (t < a.L) {
         pla = gb[(int64_t)t * a.gs2];
@@ -415,19 +423,18 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
       *(i16x8*)(sm.V + t * PITCH + c8) = pv[it];
       if (!AGG) *(i16x8*)(sm.Q + t * PITCH + c8) = pq[it];
     }
-    if (tid < CH) {
+    if (gate_wave) {   // one wave, lane = token
       float la = a.use_log ? pla : __logf(fmaxf(pla, 1e-20f));
-      la = (t0 + tid < a.L) ? fminf(la, 0.f) : 0.f;
-      // inclusive prefix sum of the log decay across wave 0 (tid < CH is that wave)
-      const float s = wave_incl_scan(la);
+      la = (t0 + lane < a.L) ? fminf(la, 0.f) : 0.f;
+      const float s = wave_incl_scan(la);   // inclusive prefix sum of the log decay
       const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
       const float el = __expf(s);
-      sm.lam2[tid] = s * 1.4426950408889634f;
-      sm.elam[tid] = el;
-      sm.eend[tid] = __expf(last - s);
-      sm.beta[tid] = pbe;
-      sm.bel[tid] = pbe * el;
-      sm.wtok[tid] = pwt;
+      sm.lam2[lane] = s * 1.4426950408889634f;
+      sm.elam[lane] = el;
+      sm.eend[lane] = __expf(last - s);
+      sm.beta[lane] = pbe;
+      sm.bel[lane] = pbe * el;
+      sm.wtok[lane] = pwt;
     }
     if (c + 1 < c_end) prefetch(c + 1);
     lds_barrier();
@@ -477,10 +484,10 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
     using std::integral_constant;
 #define DGDA_TL(n) build_tile(integral_constant<int, n>{}, std::false_type{})
 #define DGDA_TA(n) build_tile(integral_constant<int, n>{}, std::true_type{})
-    // Output pass: the last wave builds the four diagonal L tiles (triangular indices
-    // 0, 2, 5, 9) and inverts them at once -- its own LDS writes, read back in order --
-    // while the other waves build the off-diagonal L tiles (1, 3, 4, 6, 7, 8) and the
-    // ten A tiles.  Aggregate pass: the eight waves share the ten L tiles and the
+    // Output pass: the wave of role 3 builds the four diagonal L tiles (triangular
+    // indices 0, 2, 5, 9) and inverts them at once -- its own LDS writes, read back in
+    // order -- while the other roles build the off-diagonal L tiles (1, 3, 4, 6, 7, 8)
+    // and the ten A tiles.  Aggregate pass: the eight waves share the ten L tiles and the
     // inverse runs after the barrier on wave 7, whose M slab is idle once it is zero.
     if constexpr (AGG) {
       switch (wave) {
@@ -494,7 +501,7 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
         default: DGDA_TL(7); break;
       }
     } else {
-      switch (wave) {
+      switch (role) {
         case 0: DGDA_TL(1); DGDA_TL(6); DGDA_TA(0); DGDA_TA(3); DGDA_TA(6); DGDA_TA(9); break;
         case 1: DGDA_TL(3); DGDA_TL(7); DGDA_TA(1); DGDA_TA(4); DGDA_TA(7); break;
         case 2: DGDA_TL(4); DGDA_TL(8); DGDA_TA(2); DGDA_TA(5); DGDA_TA(8); break;
