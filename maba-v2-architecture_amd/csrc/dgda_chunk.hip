@@ -20,10 +20,10 @@
 //          from a zero state, carrying X = [N | M] (64 x 128): N is the segment's
 //          state from S0 = 0, M its state transition (X starts as [0 | I], the M
 //          half gets no input), so S_end = M S_start + N.
-//   pass 2 (dgda_segment_scan_kernel) walks the segments of each (b,h):
-//          S_{s+1} = M_s S_s + N_s, writing every segment's start state.
-//   pass 3 (dgda_chunk_kernel<OUT>) re-runs each segment from its start state and
-//          writes the outputs (and the final state from the last segment).
+//   passes 2 and 3 (dgda_chunk_kernel<OUT>) run the segments for the outputs (and
+//          the final state from the last segment), see the modes below.  A segment's
+//          true start state is S_{s+1} = M_s S_s + N_s, and simply N_s wherever N_s
+//          is already exact.
 //
 // Workgroup layout: wave w owns 16 columns of the carried state (pass 1: 8 waves
 // over the 128 columns of [N | M]; pass 3: 4 waves over the 64 columns of S).
@@ -58,9 +58,11 @@ constexpr int CPS = 16;       // chunks per segment
 // depend on its start state.  OUT_ZERO (one workgroup per slot) runs segment 0 from
 // the true initial state and every segment with zc[s] >= 0 from a zero start,
 // writing all their outputs and their final states N_s (the true final state for
-// segment 0); the scan sets S_{s+1} = N_s where s = 0 or zc[s] >= 0; OUT_FIX (one
+// segment 0); N_s is then exact wherever s = 0 or zc[s] >= 0.  OUT_FIX (one
 // workgroup per segment s >= 1) re-runs the first zc[s] chunks of those segments
-// from the true start state, and every segment whose M never vanished in full.
+// from the true start state, and every segment whose M never vanished in full; it
+// forms its start state itself from the last exact N_j and the maps (M, N) of the
+// segments between.
 // With fast decay zc[s] is 1 or 2, so the aggregate and fix-up passes shrink to a
 // chunk or two per segment.  With one segment per (b,h) only OUT_ZERO runs.
 constexpr int OUT_ZERO = 1, OUT_FIX = 2;
@@ -79,7 +81,6 @@ struct ChunkArgs {
   void* op; int os0, os1, os2, os3;           // output (bf16 or fp32, see OBF)
   MView4 sf;
   float* agg;      // [BH, nseg_max, 64, 128]
-  float* sstart;   // [BH, nseg_max, 64, 64]
   int* zc;         // [BH, nseg_max]: chunks after which the segment's transition M is exactly zero, -1 if never
   int64_t U;       // chunks per slot
   int H, L, BH, nseg_max, nchunks, use_log, has_s0;
@@ -283,6 +284,37 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
 // global loads (the next chunk's prefetch stays in flight across it).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// S <- M S + N for a segment map X = [N | M] (64 x 128 fp32, row-major) on the slab
+// Sr[kt][i] = S[16kt + 4g + i][col0 + c16] of one wave, with fp32 accuracy (M and S
+// both split into bf16 hi/lo, three products).
+__device__ __forceinline__ void apply_segment_map(const float* X, f32x4 (&Sr)[4], int col0, int c16, int g) {
+  i16x4 Sh[4], Sl[4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    f32x4 acc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = X[(16 * mt + 4 * g + i) * 128 + col0 + c16];  // N
+    const int row = 16 * mt + c16;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      // A operand: M[row][32p + 4g..+3] and [32p + 16 + 4g..+3]  (M lives in columns 64..127)
+      const f32x4 m0 = *(const f32x4*)(X + row * 128 + 64 + 32 * p + 4 * g);
+      const f32x4 m1 = *(const f32x4*)(X + row * 128 + 64 + 32 * p + 16 + 4 * g);
+      i16x4 h0, l0, h1, l1;
+      split4(m0, h0, l0);
+      split4(m1, h1, l1);
+      const i16x8 ah = cat8(h0, h1), al = cat8(l0, l1);
+      const i16x8 bh8 = cat8(Sh[2 * p], Sh[2 * p + 1]), bl8 = cat8(Sl[2 * p], Sl[2 * p + 1]);
+      acc = mma32(acc, ah, bh8);
+      acc = mma32(acc, ah, bl8);
+      acc = mma32(acc, al, bh8);
+    }
+    Sr[mt] = acc;
+  }
+}
+
 // The kernel's arguments read in place from the kernarg segment (see dgda_chunk_kernel).
 typedef const __attribute__((address_space(4))) ChunkArgs KArgs;
 
@@ -328,8 +360,15 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
     const float* src = a.agg + (sidx - 1) * 64 * 128 + col;   // S_k = N_{k-1}
     fill([&](int r) { return src[r * 128]; });
   } else {
-    const float* src = a.sstart + sidx * 64 * 64 + col;
-    fill([&](int r) { return src[r * 64]; });
+    // the predecessor's M did not vanish: start from the last exact final state N_j
+    // (segment 0, or one whose M vanished) and apply the maps of the segments between
+    const int* zc = a.zc + (int64_t)bh * a.nseg_max;
+    int j = k - 1;
+    while (j > 0 && zc[j] < 0) --j;
+    const float* agg = a.agg + (int64_t)bh * a.nseg_max * 64 * 128;
+    const float* src = agg + (int64_t)j * 64 * 128 + col;
+    fill([&](int r) { return src[r * 128]; });
+    for (int m = j + 1; m < k; ++m) apply_segment_map(agg + (int64_t)m * 64 * 128, Sr, col0, c16, g);
   }
 
   const uint16_t* qb = a.q + (int64_t)bi * a.qs0 + (int64_t)hi * a.qs1;
@@ -670,7 +709,7 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
   // ---- segment results
   if (AGG) {
     if (tid == 0) a.zc[sidx] = c_stop >= 0 ? c_stop - c_begin : -1;
-    if (c_stop < 0) {  // M never vanished: [N | M] for the scan
+    if (c_stop < 0) {  // M never vanished: [N | M] for the fix-up pass
       float* dst = a.agg + sidx * 64 * 128;
       const int cc = (is_m ? 64 : 0) + col;
 #pragma unroll
@@ -678,7 +717,7 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 128 + cc] = Sr[kt][i];
     }
-  } else if (a.mode == OUT_ZERO && !last) {  // N_k for the scan and the fix-up pass
+  } else if (a.mode == OUT_ZERO && !last) {  // N_k for the fix-up pass
     float* dst = a.agg + sidx * 64 * 128;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
@@ -740,66 +779,6 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kerne
   }
 }
 
-// ------------------------------------------------------------------ pass 2: segment scan
-// One wave per (b,h, 16-column slab): S_{s+1} = M_s S_s + N_s with fp32 accuracy
-// (M and S both split into bf16 hi/lo), or S_{s+1} = N_s where N_s is final
-// (s = 0, which the output pass ran from the true initial state, or M_s exactly zero,
-// zc[s] >= 0).  Writes the start state of segments 1..n-1; the fix-up pass only
-// reads it after a segment s >= 1 whose M did not vanish, so if there is none there
-// is nothing to do.
-__global__ __launch_bounds__(64) void dgda_segment_scan_kernel(ChunkArgs a) {
-  const int bh = blockIdx.x >> 2;
-  const int col0 = (blockIdx.x & 3) * 16;
-  const int lane = threadIdx.x, g = lane >> 4, c16 = lane & 15;
-  const int n = seg_count(a, bh);
-  const int* zc = a.zc + (int64_t)bh * a.nseg_max;
-  bool any_full = false;
-  for (int s = 1 + lane; s + 1 < n; s += 64) any_full |= zc[s] < 0;
-  if (__ballot(any_full) == 0ull) return;
-  f32x4 Sr[4];
-  for (int s = 0; s + 1 < n; ++s) {
-    const float* X = a.agg + ((int64_t)bh * a.nseg_max + s) * 64 * 128;
-    float* dst = a.sstart + ((int64_t)bh * a.nseg_max + s + 1) * 64 * 64;
-    if (s == 0 || zc[s] >= 0) {  // S_{s+1} = N_s
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Sr[kt][i] = X[(16 * kt + 4 * g + i) * 128 + col0 + c16];
-    } else {
-      i16x4 Sh[4], Sl[4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        f32x4 acc;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = X[(16 * mt + 4 * g + i) * 128 + col0 + c16];  // N_s
-        const int row = 16 * mt + c16;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          // A operand: M_s[row][32p + 4g..+3] and [32p + 16 + 4g..+3]  (M lives in columns 64..127)
-          const float4 m0 = *(const float4*)(X + row * 128 + 64 + 32 * p + 4 * g);
-          const float4 m1 = *(const float4*)(X + row * 128 + 64 + 32 * p + 16 + 4 * g);
-          f32x4 mlo = {m0.x, m0.y, m0.z, m0.w}, mhi = {m1.x, m1.y, m1.z, m1.w};
-          i16x4 h0, l0, h1, l1;
-          split4(mlo, h0, l0);
-          split4(mhi, h1, l1);
-          const i16x8 ah = cat8(h0, h1), al = cat8(l0, l1);
-          const i16x8 bh8 = cat8(Sh[2 * p], Sh[2 * p + 1]), bl8 = cat8(Sl[2 * p], Sl[2 * p + 1]);
-          acc = mma32(acc, ah, bh8);
-          acc = mma32(acc, ah, bl8);
-          acc = mma32(acc, al, bh8);
-        }
-        Sr[mt] = acc;
-      }
-    }
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 64 + col0 + c16] = Sr[kt][i];
-  }
-}
-
 // ------------------------------------------------------------------ host side
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -853,7 +832,7 @@ size_t dgda_chunk_workspace(int64_t BH, int64_t L) {
   const ChunkGeom gm = chunk_geom(BH, L);
   if (gm.nseg_max <= 1) return 16;
   const int64_t nseg = gm.nseg_max;
-  return (size_t)(BH * nseg * 64 * (128 + 64)) * sizeof(float) + (size_t)(BH * nseg) * sizeof(int);
+  return (size_t)(BH * nseg * 64 * 128) * sizeof(float) + (size_t)(BH * nseg) * sizeof(int);
 }
 
 int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
@@ -887,8 +866,7 @@ int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_ten
   if (ws_bytes < need) return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace too small");
   const int64_t nsegs = BH * a.nseg_max;
   a.agg = (float*)ws;
-  a.sstart = a.agg + nsegs * 64 * 128;
-  a.zc = (int*)(a.sstart + nsegs * 64 * 64);
+  a.zc = (int*)(a.agg + nsegs * 64 * 128);
   const bool obf = out->dtype == MABA_BF16;
   auto launch_out = [&](int mode) {
     a.mode = mode;
@@ -910,8 +888,6 @@ int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_ten
   int rc = check_launch("dgda_prefill/aggregate");
   if (rc) return rc;
   if ((rc = launch_out(OUT_ZERO))) return rc;
-  hipLaunchKernelGGL(dgda_segment_scan_kernel, dim3((unsigned)(BH * 4)), dim3(64), 0, stream, a);
-  if ((rc = check_launch("dgda_prefill/scan"))) return rc;
   return launch_out(OUT_FIX);
 }
 

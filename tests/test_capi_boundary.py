@@ -98,15 +98,15 @@ def _slot_geometry(BH, nch, cus=256):
 
 def test_prefill_workspace_size_at_baseline_shape(lib):
     """B=4, H=10, T=32768 (512 chunks per head): slots of 40 chunks, so up to 14
-    segments per head, each carrying a [64, 128] fp32 aggregate, a [64, 64] fp32 start
-    state and an int32 chunk count.  No GPU here: the library assumes 256 CUs."""
+    segments per head, each carrying a [64, 128] fp32 aggregate and an int32 chunk
+    count.  No GPU here: the library assumes 256 CUs."""
     B, H, T, d = 4, 10, 32768, 64
     q = _t([B, H, T, d])
     gate = _t([B, H, T, d], N.MABA_F32, strides=[H * T, T, 1, 0])   # per-token, stride-0 channels
     n = lib.maba_hip_dgda_prefill_workspace_size(q, q, gate, gate)
     U, nseg = _slot_geometry(B * H, T // 64)
     assert (U, nseg) == (40, 14)
-    assert n == B * H * nseg * (64 * (128 + 64) * 4 + 4)   # + one chunk count per segment
+    assert n == B * H * nseg * (64 * 128 * 4 + 4)   # + one chunk count per segment
     short = _t([B, H, 1024, d])                               # 16 chunks: one slot per head, no workspace
     sgate = _t([B, H, 1024, d], N.MABA_F32, strides=[H * 1024, 1024, 1, 0])
     assert lib.maba_hip_dgda_prefill_workspace_size(short, short, sgate, sgate) == 16
