@@ -509,7 +509,8 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
         if (I > J) val[r] = x;
         else val[r] = (ISA ? j <= i : j < i) ? x : 0.f;
       }
-      if (!ISA) val = val * sm.beta[i];
+      // off-diagonal L tiles are stored negated: the solve accumulates -L_IJ u_J onto v_e_I
+      if (!ISA) val = val * (I == J ? sm.beta[i] : -sm.beta[i]);
       if (!ISA && I == J) {   // diagonal L tiles only feed the inverses, in fp32
         *(f32x4*)(sm.LD + I * DTILE_ELEMS + c16 * DPITCH + 4 * g) = val;
         return;
@@ -599,32 +600,31 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
       u[tt] = y - bel * acc;
     }
     }
-    lds_barrier();
+    if (AGG) lds_barrier();   // the inverses run after the tile barrier only in the aggregate pass
 
-    // ---- blocked forward substitution, u_I = T_II (v_e_I - sum_{J<I} L_IJ u_J)
+    // ---- blocked forward substitution, u_I = T_II (v_e_I - sum_{J<I} L_IJ u_J): the
+    // negated L tiles accumulate onto v_e_I itself; K=16 products never accumulate onto
+    // a K=32 result, so I = 3 sums its two parts on the VALU
     i16x4 uh[4], ul[4];
     if (!idle) {
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4 rhs = u[I];
-      if (I >= 1) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        if (I >= 2) {  // J = 0,1 as one K = 32 step
-          const i16x8 ah = tri4x2(sm.LH, I, 0, c16, g), al = tri4x2(sm.LL, I, 0, c16, g);
-          const i16x8 bh8 = cat8(uh[0], uh[1]), bl8 = cat8(ul[0], ul[1]);
-          acc = mma32(acc, ah, bh8);
-          acc = mma32(acc, ah, bl8);
-          acc = mma32(acc, al, bh8);
-        }
-        f32x4 acc16 = {0.f, 0.f, 0.f, 0.f};  // K=16 products never accumulate onto a K=32 result
-        if (I == 1 || I == 3) {  // the remaining 16-wide step J = I-1
-          const int J = I - 1;
-          const i16x4 ah = tri4(sm.LH, I, J, c16, g), al = tri4(sm.LL, I, J, c16, g);
-          acc16 = mma16(acc16, ah, uh[J]);
-          acc16 = mma16(acc16, ah, ul[J]);
-          acc16 = mma16(acc16, al, uh[J]);
-        }
-        rhs = rhs - acc - acc16;
+      if (I >= 2) {  // J = 0,1 as one K = 32 step
+        const i16x8 ah = tri4x2(sm.LH, I, 0, c16, g), al = tri4x2(sm.LL, I, 0, c16, g);
+        const i16x8 bh8 = cat8(uh[0], uh[1]), bl8 = cat8(ul[0], ul[1]);
+        rhs = mma32(rhs, ah, bh8);
+        rhs = mma32(rhs, ah, bl8);
+        rhs = mma32(rhs, al, bh8);
+      }
+      if (I == 1 || I == 3) {  // the remaining 16-wide step J = I-1
+        const int J = I - 1;
+        const i16x4 ah = tri4(sm.LH, I, J, c16, g), al = tri4(sm.LL, I, J, c16, g);
+        f32x4 acc16 = I == 1 ? rhs : f32x4{0.f, 0.f, 0.f, 0.f};
+        acc16 = mma16(acc16, ah, uh[J]);
+        acc16 = mma16(acc16, ah, ul[J]);
+        acc16 = mma16(acc16, al, uh[J]);
+        rhs = I == 1 ? acc16 : rhs + acc16;
       }
       i16x4 rh, rl;
       split4(rhs, rh, rl);
@@ -645,29 +645,29 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
     if (!AGG) {
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
-        const f32x4 qs = qsr[I];
-        f32x4 au = {0.f, 0.f, 0.f, 0.f};
+        const int tl = 16 * I + c16;
+        // the products accumulate onto e^Lam (q S); with a K=16 product after K=32 ones
+        // (I = 2) the two parts are summed on the VALU (see the solve)
+        f32x4 ov = sm.elam[tl] * qsr[I];
 #pragma unroll
         for (int P = 0; P < 2; ++P) {  // J pairs (0,1), (2,3)
           if (2 * P + 1 <= I) {
             const i16x8 ah = tri4x2(sm.AH, I, 2 * P, c16, g), al = tri4x2(sm.AL, I, 2 * P, c16, g);
             const i16x8 bh8 = cat8(uh[2 * P], uh[2 * P + 1]), bl8 = cat8(ul[2 * P], ul[2 * P + 1]);
-            au = mma32(au, bh8, ah);
-            au = mma32(au, bl8, ah);
-            au = mma32(au, bh8, al);
+            ov = mma32(ov, bh8, ah);
+            ov = mma32(ov, bl8, ah);
+            ov = mma32(ov, bh8, al);
           }
         }
-        f32x4 au16 = {0.f, 0.f, 0.f, 0.f};  // separate K=16 accumulator (see the solve)
         if ((I & 1) == 0) {  // single J = I
           const i16x4 ah = tri4(sm.AH, I, I, c16, g), al = tri4(sm.AL, I, I, c16, g);
+          f32x4 au16 = I == 0 ? ov : f32x4{0.f, 0.f, 0.f, 0.f};
           au16 = mma16(au16, uh[I], ah);
           au16 = mma16(au16, ul[I], ah);
           au16 = mma16(au16, uh[I], al);
+          ov = I == 0 ? au16 : ov + au16;
         }
-        au = au + au16;
-        const int tl = 16 * I + c16;
         if (t0 + tl < a.L) {
-          const f32x4 ov = sm.elam[tl] * qs + au;
           const int64_t off = obase + (int64_t)(t0 + 16 * I) * a.os2;
           if (OBF) *(bf16x4*)((short*)a.op + off) = to_bf16x4(ov);
           else *(f32x4*)((float*)a.op + off) = ov;
