@@ -273,6 +273,50 @@ def decode_benches(dev, steps: int):
     return out
 
 
+def row_benches(dev):
+    """Secondary lines for hot-path rows outside the headline: DGDA prefill with
+    per-channel gates (the layer's gate layout, config-2 shape) and the causal prefill
+    index_topk."""
+    import torch
+    import torch.nn.functional as F
+    from maba_sparse.kernels import hip_backend as hb
+    out = {}
+    B, H, T, d = 4, 10, 32768, 64
+    g = torch.Generator(device="cpu").manual_seed(5)
+    q = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1).to(dev, torch.bfloat16)
+    k = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1).to(dev, torch.bfloat16)
+    v = torch.randn(B, H, T, d, generator=g).to(dev, torch.bfloat16)
+    la = (-F.softplus(torch.randn(B, H, T, d, generator=g) + 2.0)).to(dev)
+    beta = torch.sigmoid(torch.randn(B, H, T, d, generator=g)).to(dev)
+    wg = torch.sigmoid(torch.randn(B, H, T, d, generator=g)).to(dev)
+
+    def pc_step():
+        return hb.hip_dgda_prefill(q, k, v, log_alpha=la, b=beta, w=wg, chunk_size=64, out_dtype=torch.bfloat16,
+                                   state_dtype=torch.float32, allow_mixed_dtypes=True)
+
+    ms, _ = time_op(pc_step, 3, 1)
+    nbytes = B * H * T * (3 * d * 2 + 3 * d * 4 + d * 2) + B * H * d * d * 4
+    out["dgda_prefill_per_channel_gates"] = {
+        "ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3), "gbs": nbytes / (ms * 1e-3) / 1e9,
+        "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes,
+        "config": "B=4 H=10 T=32768 d=64, bf16 q/k/v, fp32 [B,H,T,64] decay/erase/write gates, bf16 out"}
+    log(f"dgda_prefill per-channel gates: {ms:.3f} ms/step")
+    del q, k, v, la, beta, wg
+    # causal prefill index_topk: one sequence of 32,768 queries over 512 block centroids
+    Bq, L, di, K = 1, 32768, 128, 32
+    qi = torch.randn(Bq, L, di, device=dev, dtype=torch.bfloat16)
+    cent = torch.randn(Bq, L // 64, di, device=dev, dtype=torch.bfloat16)
+
+    def topk_prefill():
+        return hb.hip_index_topk(qi, cent, lambda_dist=0.5, top_k=K, block_size=64)
+
+    ms, _ = time_op(topk_prefill, 5, 1)
+    out["index_topk_prefill"] = {"ms_per_call": ms, "queries_per_s": Bq * L / (ms * 1e-3),
+                                 "config": "B=1 L=32768 d=128 bf16, 512 centroids, top-32, causal"}
+    log(f"index_topk prefill 32k x 512: {ms:.3f} ms")
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -329,13 +373,14 @@ def main():
                    "state": "fp32", "out": "bf16", "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "dgda_prefill op (aggregate + scan + output launches)",
+                     "kernel": "dgda_prefill op (aggregate + zero-start + fix-up launches)",
                      "algorithmic_bytes": nbytes},
         "mfma": {"achieved": flops / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                  "frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "algorithmic_flops": flops},
     }
     if not args.only_prefill and not args.skip_decode:
         res["decode"] = decode_benches(dev, args.steps)
+        res["rows"] = row_benches(dev)
     if not args.only_prefill and not args.skip_cpu:
         log("timing the CPU baseline")
         res["cpu_baseline"] = cpu_baseline()
