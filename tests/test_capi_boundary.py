@@ -86,11 +86,11 @@ def test_prefill_shape_mismatch(lib):
     assert rc == N.MABA_ERR_INVALID
 
 
-def _slot_geometry(BH, nch, cus=256):
+def _slot_geometry(BH, nch, cus=256, min_u=16):
     """Chunks per slot U and segments per sequence: the B*H*nch chunks in (b,h)-major
-    order are cut into slots of U = max(16, ceil(total / (2 * CUs))) chunks; a
+    order are cut into slots of U = max(min_u, ceil(total / (2 * CUs))) chunks; a
     sequence that fits one slot is never cut."""
-    U = max(16, -(-BH * nch // (2 * cus)))
+    U = max(min_u, -(-BH * nch // (2 * cus)))
     if nch <= U:
         return nch, 1
     return U, -(-(nch - 1) // U) + 1
@@ -110,8 +110,15 @@ def test_prefill_workspace_size_at_baseline_shape(lib):
     short = _t([B, H, 1024, d])                               # 16 chunks: one slot per head, no workspace
     sgate = _t([B, H, 1024, d], N.MABA_F32, strides=[H * 1024, 1024, 1, 0])
     assert lib.maba_hip_dgda_prefill_workspace_size(short, short, sgate, sgate) == 16
+    # per-channel gates: the token path, slots of U staging chunks of 32 tokens (80 at this shape)
     per_channel = _t([B, H, T, d], N.MABA_F32)
-    assert lib.maba_hip_dgda_prefill_workspace_size(q, q, per_channel, gate) == 0   # sequential path
+    U, nseg = _slot_geometry(B * H, T // 32, min_u=32)
+    assert (U, nseg) == (80, 14)
+    assert lib.maba_hip_dgda_prefill_workspace_size(q, q, per_channel, gate) == B * H * nseg * (64 * 128 * 4 + 4)
+    # other head sizes take the sequential kernel, which needs no workspace
+    q32 = _t([B, H, T, 32])
+    pc32 = _t([B, H, T, 32], N.MABA_F32)
+    assert lib.maba_hip_dgda_prefill_workspace_size(q32, q32, pc32, pc32) == 0
 
 
 def test_index_topk_decode_validation(lib):

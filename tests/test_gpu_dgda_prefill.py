@@ -34,11 +34,15 @@ def test_chunk_path_is_selected(dev):
     lib = N.load()
     n = lib.maba_hip_dgda_prefill_workspace_size(N.desc(inp["q"]), N.desc(inp["v"]), N.desc(inp["log_alpha"]),
                                                  N.desc(inp["b"]))
-    assert n > 16          # multi-segment chunked path needs aggregate/scan workspace
-    inp["b"] = inp["b"].contiguous()   # per-channel erase gate -> sequential path
+    assert n > 16          # multi-segment chunked path needs aggregate workspace
+    inp["b"] = inp["b"].contiguous()   # per-channel erase gate -> token path, also segmented
     n2 = lib.maba_hip_dgda_prefill_workspace_size(N.desc(inp["q"]), N.desc(inp["v"]), N.desc(inp["log_alpha"]),
                                                   N.desc(inp["b"]))
-    assert n2 == 0
+    assert n2 > 16
+    small = dgda_inputs(1, 2, 4096, dk=32, dv=32, seed=0, device=dev)   # other head sizes -> sequential kernel
+    n3 = lib.maba_hip_dgda_prefill_workspace_size(N.desc(small["q"]), N.desc(small["v"]),
+                                                  N.desc(small["log_alpha"]), N.desc(small["b"]))
+    assert n3 == 0
 
 
 @pytest.mark.parametrize("decay", ["baseline", "slow", "none"])
@@ -164,3 +168,73 @@ def test_chunk_wide_slots_vs_c_oracle(dev):
                                            f(inp["b"][..., :1]), f(inp["w"][..., :1]), chunk_size=64)
     assert_close(o[:, heads], eo, 2e-3, 2e-3, "out")
     assert_close(S[:, heads], eS, 2e-3, 2e-3, "state")
+
+
+# ----------------------------------------------------------------------------- token path
+# Per-channel gates (the DGDA layer's layout) take the sequence-parallel token path:
+# exact token recurrence, segments chained through aggregate and fix-up passes.
+
+@pytest.mark.parametrize("qkv", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("decay", ["baseline", "slow", "none"])
+@pytest.mark.parametrize("L", [1, 31, 33, 1000, 4100])
+def test_token_path_per_channel_gates(dev, qkv, decay, L):
+    inp = dgda_inputs(2, 3, L, seed=L + 7, decay=decay, gates="channel", qkv_dtype=qkv, device=dev,
+                      with_state=(L % 2 == 1))
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, f"out L={L} {decay} {qkv}")
+    assert_close(S, eS, 2e-3, 2e-3, f"state L={L} {decay} {qkv}")
+
+
+def test_token_path_alpha_strong_decay_and_bf16_output(dev):
+    """alpha instead of log_alpha, per-channel decays down to e^-30 per token, bf16 output:
+    the token recurrence has no chunk algebra to overflow, and bf16 outputs round the
+    fp32 results."""
+    L = 3000
+    inp = dgda_inputs(1, 4, L, seed=31, gates="channel", device=dev, with_state=True)
+    la = inp.pop("log_alpha")
+    la = torch.where(torch.rand(la.shape, generator=torch.Generator().manual_seed(1)).to(dev) < 0.1, la * 15, la)
+    inp["alpha"] = torch.exp(la)
+    o32, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args({**inp, "log_alpha": la}))
+    assert_close(o32, eo, 2e-3, 2e-3, "out")
+    assert_close(S, eS, 2e-3, 2e-3, "state")
+    o16, _ = _run(inp, out_dtype=torch.bfloat16)
+    assert torch.equal(o16, o32.to(torch.bfloat16))
+
+
+def test_token_path_growing_gates_never_vanish(dev):
+    """log_alpha > 0 on some channels: the segment transitions never vanish, so every
+    segment after the first runs in the fix-up pass from a scanned start state."""
+    L = 6000
+    inp = dgda_inputs(1, 2, L, seed=41, decay="slow", gates="channel", device=dev)
+    la = inp["log_alpha"].clone()
+    la[..., :4] = 0.0005            # four channels that grow slowly
+    inp["log_alpha"] = la
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, "out")
+    assert_close(S, eS, 2e-3, 2e-3, "state")
+
+
+def test_token_path_config2_shape_split_chaining(dev):
+    """Config-2 shape with per-channel gates (B=4, H=10, T=32768): prefill(T) equals
+    prefill(T/2) chained into prefill(T/2, initial_state), and two heads match the
+    token-loop oracle over the first 4096 tokens."""
+    B, H, T = 4, 10, 32768
+    inp = dgda_inputs(B, H, T, seed=9, gates="channel", device=dev)
+    o, S = _run(inp)
+    assert torch.isfinite(o).all() and torch.isfinite(S).all()
+    h = T // 2
+    part = lambda sl: {k: (v[:, :, sl] if (v is not None and v.dim() == 4 and k != "initial_state") else v)  # noqa: E731
+                       for k, v in inp.items()}
+    o1, S1 = _run(part(slice(0, h)))
+    second = part(slice(h, T))
+    second["initial_state"] = S1
+    o2, S2 = _run(second)
+    assert_close(torch.cat([o1, o2], dim=2), to_np(o), 2e-3, 2e-3, "chained out")
+    assert_close(S2, to_np(S), 2e-3, 2e-3, "chained state")
+    few = {k: (v[:1, :2, :4096] if (v is not None and v.dim() == 4 and k != "initial_state") else v)
+           for k, v in inp.items()}
+    eo, _ = odgda.dgda_prefill_seq(**oracle_dgda_args(few))
+    assert_close(o[:1, :2, :4096], eo, 2e-3, 2e-3, "oracle heads")
