@@ -213,23 +213,26 @@ __device__ __forceinline__ void tok_segment(KTokArgs& a, TokSmem<AGG>& sm, int* 
       }
       v.W = is_m ? 0.f : sm.WV[t][col];
     };
+    // dot products of the slab with a row vector as two fma chains (even and odd rows)
+    auto dot16 = [&](const f32x4 (&x)[4]) {
+      float e = Sr[0][0] * x[0][0], o = Sr[0][1] * x[0][1];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = (kt == 0 ? 2 : 0); i < 4; i += 2) {
+          e = fmaf(Sr[kt][i], x[kt][i], e);
+          o = fmaf(Sr[kt][i + 1], x[kt][i + 1], o);
+        }
+      return e + o;
+    };
     auto token = [&](int t, const TokVec& v) {
-      float p[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        Sr[kt] = Sr[kt] * v.A[kt];
-        p[kt] = (Sr[kt][0] * v.B[kt][0] + Sr[kt][1] * v.B[kt][1]) + (Sr[kt][2] * v.B[kt][2] + Sr[kt][3] * v.B[kt][3]);
-      }
-      const float delta = v.W - sum4_groups((p[0] + p[1]) + (p[2] + p[3]));
-      float qo[4];
+      for (int kt = 0; kt < 4; ++kt) Sr[kt] = Sr[kt] * v.A[kt];
+      const float delta = v.W - sum4_groups(dot16(v.B));
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        Sr[kt] = Sr[kt] + v.K[kt] * delta;
-        if (!AGG)
-          qo[kt] = (Sr[kt][0] * v.Q[kt][0] + Sr[kt][1] * v.Q[kt][1]) + (Sr[kt][2] * v.Q[kt][2] + Sr[kt][3] * v.Q[kt][3]);
-      }
+      for (int kt = 0; kt < 4; ++kt) Sr[kt] = Sr[kt] + v.K[kt] * delta;
       if (!AGG) {
-        const float o = sum4_groups((qo[0] + qo[1]) + (qo[2] + qo[3]));
+        const float o = sum4_groups(dot16(v.Q));
         if ((t & 3) == g) { myo = o; myt = t0 + t; }
         if ((t & 3) == 3 || t == nt - 1) {   // every lane group has its token of the last four
           if (myt >= 0) {
