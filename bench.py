@@ -54,6 +54,8 @@ def parse():
     ap.add_argument("--skip-decode", action="store_true", help="do not run the decode benchmarks")
     ap.add_argument("--only-prefill", action="store_true", help="time only the DGDA prefill step (for profiling)")
     ap.add_argument("--only-decode", action="store_true", help="run only the decode benchmarks (for profiling)")
+    ap.add_argument("--only-rows", action="store_true",
+                    help="run only the secondary row benchmarks: per-channel-gate prefill, prefill top-k (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 256 MiB device-to-device copy (calibrates FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
@@ -336,6 +338,9 @@ def main():
         return
     if args.only_decode:
         print(json.dumps({"decode": decode_benches(dev, args.steps)}), flush=True)
+        return
+    if args.only_rows:
+        print(json.dumps({"rows": row_benches(dev)}), flush=True)
         return
     B, H, T, d = 4, 10, 32768, 64
     inp = dgda_prefill_case(dev, B, H, T, d)
