@@ -401,6 +401,92 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   }
 }
 
+// Prefill on MFMA (bf16 q and centroids, d = 32 NP, unit channel stride, no score
+// output): one workgroup per 16 consecutive query rows of one sequence.  Wave w
+// scores 64-centroid tiles for all 16 rows with v_mfma_f32_16x16x32_bf16 (A: the
+// centroid rows from global memory, B: the 16 query rows in registers), round by
+// round, newest tiles first, and the scores pass through LDS to the owners of the
+// per-row top-K lists: wave w keeps rows 4w..4w+3 (one key per lane each) and merges
+// each tile into them with wave_merge_topk, whose early exit skips tiles that cannot
+// beat the K-th key.  Scores and causal mask as index_prefill_kernel.
+struct PreMfmaArgs {
+  const uint16_t* q; int64_t qsb, qsl;    // [B, L, d] bf16, channel stride 1
+  const uint16_t* c; int64_t csb, csn;    // [B, nb, d] bf16, channel stride 1
+  int64_t L, nb;
+  int K, ak, bs;
+  float scale, lam;
+  int64_t* out; int64_t osb, osl, osk;
+};
+
+template <int NP>
+__global__ __launch_bounds__(256) void index_prefill_mfma_kernel(PreMfmaArgs a) {
+  constexpr int SP = 68;                                   // float pitch of a tile row in LDS
+  __shared__ __attribute__((aligned(16))) float s_sc[4][16][SP];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t bi = blockIdx.y;
+  const int64_t t0 = (int64_t)blockIdx.x * 16;
+  const uint16_t* cb = a.c + bi * a.csb;
+  // query rows t0 + c16 as the B operand (rows past L read as zero)
+  i16x8_t qb[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    i16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (t0 + c16 < a.L) z = *(const i16x8_t*)(a.q + bi * a.qsb + (t0 + c16) * a.qsl + 32 * p + 8 * g);
+    qb[p] = z;
+  }
+  // causal limits: row t sees blocks n < nvalid(t) = min(t / bs + 1, nb)
+  auto nvalid = [&](int64_t t) { const int64_t v = t / a.bs + 1; return v < a.nb ? v : a.nb; };
+  const int64_t tlast = (t0 + 15 < a.L ? t0 + 15 : a.L - 1);
+  const int ntiles = (int)((nvalid(tlast) + 63) / 64);
+  key64 list[4] = {KEY_NONE, KEY_NONE, KEY_NONE, KEY_NONE};   // rows 4 wave + r
+  for (int r0 = ntiles - 1; r0 >= 0; r0 -= 4) {                // tiles r0, r0-1, r0-2, r0-3
+    const int tile = r0 - wave;
+    if (tile >= 0) {
+      const int64_t n0 = (int64_t)tile * 64;
+      f32x4 acc[4];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        const int64_t n = n0 + 16 * rb + c16;
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          i16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+          if (n < a.nb) z = *(const i16x8_t*)(cb + n * a.csn + 32 * p + 8 * g);
+          s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, z), __builtin_bit_cast(bf16x8, qb[p]),
+                                                       s, 0, 0, 0);
+        }
+        acc[rb] = s;
+      }
+      // lane holds D[centroid n0 + 16 rb + 4 g + i][row t0 + c16]
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) *(f32x4*)&s_sc[wave][c16][16 * rb + 4 * g] = acc[rb] * a.scale;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t t = t0 + 4 * wave + r;
+      const int64_t nv = nvalid(t < a.L ? t : a.L - 1);
+      const int64_t qblk = (t < a.L ? t : a.L - 1) / a.bs;
+      for (int j = 0; j < 4 && r0 - j >= 0; ++j) {
+        const int64_t n = (int64_t)(r0 - j) * 64 + lane;
+        key64 key = KEY_NONE;
+        if (n < nv) key = make_key(s_sc[j][4 * wave + r][lane] - a.lam * log1pf((float)(qblk - n)), (uint32_t)n);
+        list[r] = wave_merge_topk(list[r], key, a.K);
+      }
+    }
+    __syncthreads();   // the next round overwrites the score tiles
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t t = t0 + 4 * wave + r;
+    if (t >= a.L) break;
+    // fewer valid blocks than ak: the remaining slots hold -inf blocks, lowest index first
+    const int64_t nv = nvalid(t);
+    if (lane < a.ak) a.out[bi * a.osb + t * a.osl + lane * a.osk] = lane < nv ? (int64_t)key_index(list[r]) : lane;
+  }
+}
+
 // Prefill: one wave per query row; lane = centroid within a 64-wide tile.
 struct PreArgs {
   const void* q; int qdt; int64_t qsb, qsl, qsd;
@@ -575,6 +661,35 @@ extern "C" int maba_hip_index_topk(const maba_tensor* q_idx, const maba_tensor* 
     if (!expect_float(out_scores, "out_scores")) return MABA_ERR_DTYPE;
   }
   if (B * L == 0 || nb == 0) return MABA_OK;
+  // MFMA path: bf16 rows with unit channel stride, 16-byte aligned, d a multiple of 32
+  const bool mfma = !out_scores && q_idx->dtype == MABA_BF16 && centroids->dtype == MABA_BF16 && d % 32 == 0 &&
+                    q_idx->stride[2] == 1 && centroids->stride[2] == 1 && (uintptr_t)q_idx->data % 16 == 0 &&
+                    (uintptr_t)centroids->data % 16 == 0 && q_idx->stride[0] % 8 == 0 && q_idx->stride[1] % 8 == 0 &&
+                    centroids->stride[0] % 8 == 0 && centroids->stride[1] % 8 == 0 && nb < ((int64_t)1 << 31);
+  if (mfma) {
+    PreMfmaArgs m;
+    m.q = (const uint16_t*)q_idx->data; m.qsb = q_idx->stride[0]; m.qsl = q_idx->stride[1];
+    m.c = (const uint16_t*)centroids->data; m.csb = centroids->stride[0]; m.csn = centroids->stride[1];
+    m.L = L; m.nb = nb;
+    m.K = (int)(top_k < 64 ? top_k : 64); m.ak = (int)ak; m.bs = block_size;
+    m.scale = 1.0f / sqrtf((float)d);
+    m.lam = lambda_dist;
+    m.out = (int64_t*)out_idx->data; m.osb = out_idx->stride[0]; m.osl = out_idx->stride[1];
+    m.osk = out_idx->stride[2];
+    const dim3 grid((unsigned)ceil_div(L, 16), (unsigned)B);
+    hipStream_t st = (hipStream_t)stream;
+    switch (d / 32) {
+      case 1: hipLaunchKernelGGL(index_prefill_mfma_kernel<1>, grid, dim3(256), 0, st, m); break;
+      case 2: hipLaunchKernelGGL(index_prefill_mfma_kernel<2>, grid, dim3(256), 0, st, m); break;
+      case 3: hipLaunchKernelGGL(index_prefill_mfma_kernel<3>, grid, dim3(256), 0, st, m); break;
+      case 4: hipLaunchKernelGGL(index_prefill_mfma_kernel<4>, grid, dim3(256), 0, st, m); break;
+      case 5: hipLaunchKernelGGL(index_prefill_mfma_kernel<5>, grid, dim3(256), 0, st, m); break;
+      case 6: hipLaunchKernelGGL(index_prefill_mfma_kernel<6>, grid, dim3(256), 0, st, m); break;
+      case 7: hipLaunchKernelGGL(index_prefill_mfma_kernel<7>, grid, dim3(256), 0, st, m); break;
+      default: hipLaunchKernelGGL(index_prefill_mfma_kernel<8>, grid, dim3(256), 0, st, m); break;
+    }
+    return check_launch("index_topk");
+  }
   PreArgs a;
   a.q = q_idx->data; a.qdt = q_idx->dtype; a.qsb = q_idx->stride[0]; a.qsl = q_idx->stride[1]; a.qsd = q_idx->stride[2];
   a.c = centroids->data; a.cdt = centroids->dtype;

@@ -251,6 +251,34 @@ def test_index_topk_prefill(dev, B, L, nb_blocks, k, lam):
         assert (ii[:, t, :avail] <= t // 64).all()
 
 
+@pytest.mark.parametrize("B,L,nb,d,k,lam,bs", [(2, 1000, 16, 128, 8, 0.5, 64), (1, 4096, 64, 64, 32, 0.1, 64),
+                                                (3, 333, 11, 96, 4, 1.0, 32), (1, 50, 1, 32, 8, 0.5, 64),
+                                                (2, 700, 24, 128, 32, 0.0, 32)])
+def test_index_topk_prefill_bf16_mfma(dev, B, L, nb, d, k, lam, bs):
+    """bf16 queries and centroids without score output take the MFMA prefill kernel
+    (16 query rows per workgroup): picks agree with the float64 oracle wherever its
+    scores separate, equal the fp32 kernel's on the same values, and rows that see
+    fewer blocks than k end with the masked blocks in index order."""
+    g = torch.Generator().manual_seed(L + d)
+    q = torch.randn(B, L, d, generator=g).bfloat16()
+    cent = torch.randn(B, nb, d, generator=g).bfloat16()
+    idx = _hip().hip_index_topk(q.to(dev), cent.to(dev), lambda_dist=lam, top_k=k, block_size=bs)
+    ak = min(k, nb)
+    assert idx.shape == (B, L, ak) and idx.dtype == torch.long
+    ref = oidx.prefill_scores(to_np(q), to_np(cent), lam, bs)
+    assert topk_agrees(idx.cpu().numpy(), ref, k) > 0
+    ii = idx.cpu().numpy()
+    for t in range(L):
+        avail = min(t // bs + 1, nb)
+        if avail < ak:
+            assert (np.sort(ii[:, t, :avail], axis=-1) == np.arange(avail)).all()
+            assert (ii[:, t, avail:] == np.arange(avail, ak)).all()
+    idx32, _ = _hip().hip_index_topk(q.float().to(dev), cent.float().to(dev), lambda_dist=lam, top_k=k, block_size=bs,
+                                     return_scores=True)
+    same = (idx32.cpu().numpy() == ii).all(axis=-1).mean()
+    assert same > 0.99, same
+
+
 def test_index_topk_penalty_order(dev):
     q = torch.ones(1, 256, 64, device=dev) / 8.0
     c = torch.ones(1, 4, 64, device=dev) / 8.0
