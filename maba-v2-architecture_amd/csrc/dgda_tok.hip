@@ -11,11 +11,12 @@
 // re-runs the first zc chunks of each segment from its true start state.
 //
 // Workgroup: wave w owns state columns 16(w&3)..+15 (aggregate pass: waves 4-7 carry
-// M); lane (c16, g) holds rows 16kt + 4g + i, kt, i = 0..3, of column 16(w&3) + c16.
-// Per token a wave does 64 VALU products on its slab and two 4-lane reductions
-// (rows are spread over the lane groups g), with v_permlane32_swap and
-// v_permlane16_swap.  The per-token gate vectors a, b*k, k, q and w*v are staged in
-// LDS for TCH tokens at a time.
+// M); lane (rg, cg) = (lane & 7, lane >> 3) holds rows 8 rg .. 8 rg + 7 of two adjacent
+// columns.  Per token a wave does 64 VALU products on its slab and reduces the two
+// dot products over the eight lanes of each column pair with three DPP steps.  The
+// per-token vectors a, b*k, k, q and w*v are staged in LDS for TCH tokens at a time;
+// a lane reads 8 rows of each (two 16-byte reads) and its two w*v entries, so the
+// broadcast LDS reads per token stay at nine.
 #include "dgda_common.h"
 
 namespace maba {
@@ -53,14 +54,17 @@ struct TokSmem {
   SM_ALIGN_TOK float WV[TCH][64];   // w_t * v_t
 };
 
-// Sum over the four lanes l, l^16, l^32, l^48 (the lane groups g of one column):
-// each swap with equal operands returns the value and its partner across the two
-// results (the partner half in one, the own half in the other).
-__device__ __forceinline__ float sum4_groups(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);          // x[l] + x[l ^ 32]
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);                   // + the l ^ 16 partner
+// Sum over the eight lanes of a half-row (lanes 8m .. 8m+7): quad swaps of 1 and 2,
+// then the half-row mirror, which pairs the two quads.
+__device__ __forceinline__ float sum8_lanes(float x) {
+  auto dpp = [](float v, auto ctrl_c) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl_c)::value, 0xf, 0xf, false));
+  };
+  using std::integral_constant;
+  x += dpp(x, integral_constant<int, 0xB1>{});    // quad_perm [1,0,3,2]
+  x += dpp(x, integral_constant<int, 0x4E>{});    // quad_perm [2,3,0,1]
+  x += dpp(x, integral_constant<int, 0x141>{});   // row_half_mirror
+  return x;
 }
 
 // Eight consecutive elements of a bf16 or fp32 row (16-byte aligned), as fp32.
@@ -91,11 +95,12 @@ __device__ __forceinline__ void gate8(const float* row, int cs, int c0, float (&
 }
 
 // One segment: staging chunks [c_begin, c_end) of sequence bh, segment k of n.
+// Lane (rg, cg) = (lane & 7, lane >> 3) holds S[8 rg + i][col0 + 2 cg + j], i < 8, j < 2.
 template <bool AGG, bool F32IN, bool OBF>
 __device__ __forceinline__ void tok_segment(KTokArgs& a, TokSmem<AGG>& sm, int* s_mzero, int tid,
                                             int bh, int k, int n, int c_begin, int c_end) {
   const int wave = tid >> 6, lane = tid & 63;
-  const int g = lane >> 4, c16 = lane & 15;
+  const int rg = lane & 7, cg = lane >> 3;
   const int bi = bh / a.H, hi = bh % a.H;
   const int64_t sidx = (int64_t)bh * a.nseg_max + k;
   const bool last = k == n - 1;
@@ -104,36 +109,53 @@ __device__ __forceinline__ void tok_segment(KTokArgs& a, TokSmem<AGG>& sm, int* 
   const bool pred_final = !AGG && a.mode == TOK_FIX && (k == 1 || a.zc[sidx - 1] >= 0);
 
   // ---- start state of the slab
-  f32x4 Sr[4];
+  float S[8][2];
   const int col0 = (wave & 3) * 16;
-  const int col = col0 + c16;
+  const int cA = col0 + 2 * cg;            // this lane's columns cA, cA + 1
   const bool is_m = AGG && wave >= 4;
   auto fill = [&](auto load) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Sr[kt][i] = load(16 * kt + 4 * g + i);
+      for (int j = 0; j < 2; ++j) S[i][j] = load(8 * rg + i, cA + j);
   };
   if (AGG) {
-    fill([&](int r) { return (is_m && r == col) ? 1.f : 0.f; });
+    fill([&](int r, int c) { return (is_m && r == c) ? 1.f : 0.f; });
   } else if (k == 0 && a.has_s0) {
-    const int64_t o = bi * a.s0.s0 + hi * a.s0.s1 + col * a.s0.s3, rs = a.s0.s2;
-    if (a.s0.dt == MABA_F32) fill([&](int r) { return ((const float*)a.s0.p)[o + r * rs]; });
-    else if (a.s0.dt == MABA_BF16) fill([&](int r) { return bf16_bits_to_f32(((const uint16_t*)a.s0.p)[o + r * rs]); });
-    else fill([&](int r) { return __half2float(((const __half*)a.s0.p)[o + r * rs]); });
+    const int64_t o = bi * a.s0.s0 + hi * a.s0.s1, rs = a.s0.s2, cs = a.s0.s3;
+    if (a.s0.dt == MABA_F32) fill([&](int r, int c) { return ((const float*)a.s0.p)[o + r * rs + c * cs]; });
+    else if (a.s0.dt == MABA_BF16)
+      fill([&](int r, int c) { return bf16_bits_to_f32(((const uint16_t*)a.s0.p)[o + r * rs + c * cs]); });
+    else fill([&](int r, int c) { return __half2float(((const __half*)a.s0.p)[o + r * rs + c * cs]); });
   } else if (k == 0 || a.mode == TOK_ZERO) {
-    fill([&](int) { return 0.f; });
+    fill([&](int, int) { return 0.f; });
   } else if (pred_final) {
-    const float* src = a.agg + (sidx - 1) * 64 * 128 + col;   // S_k = N_{k-1}
-    fill([&](int r) { return src[r * 128]; });
+    const float* src = a.agg + (sidx - 1) * 64 * 128;   // S_k = N_{k-1}
+    fill([&](int r, int c) { return src[r * 128 + c]; });
   } else {
+    // the predecessor's M did not vanish: from the last exact N_j apply the maps of the
+    // segments between on MFMA (accumulator-tile layout: lane (c16, g4) holds rows
+    // 16 kt + 4 g4 + i of column col0 + c16), then move the slab to this layout through
+    // a wave-private LDS region (the fix-up pass uses no LDS before its first chunk)
+    const int c16 = lane & 15, g4 = lane >> 4;
     const int* zc = a.zc + (int64_t)bh * a.nseg_max;
     int j = k - 1;
     while (j > 0 && zc[j] < 0) --j;
     const float* agg = a.agg + (int64_t)bh * a.nseg_max * 64 * 128;
-    const float* src = agg + (int64_t)j * 64 * 128 + col;
-    fill([&](int r) { return src[r * 128]; });
-    for (int m = j + 1; m < k; ++m) apply_segment_map(agg + (int64_t)m * 64 * 128, Sr, col0, c16, g);
+    f32x4 Sr[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Sr[kt][i] = agg[(int64_t)j * 64 * 128 + (16 * kt + 4 * g4 + i) * 128 + col0 + c16];
+    for (int m = j + 1; m < k; ++m) apply_segment_map(agg + (int64_t)m * 64 * 128, Sr, col0, c16, g4);
+    static_assert(offsetof(TokSmem<AGG>, BK) == sizeof(sm.A) && 4 * 64 * 16 <= 2 * TCH * 64,
+                  "the four output waves' [64][16] regions span A and BK");
+    float* cv = &sm.A[0][0] + wave * 64 * 16;   // [64 rows][16 columns], inside A and BK
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cv[(16 * kt + 4 * g4 + i) * 16 + c16] = Sr[kt][i];
+    fill([&](int r, int c) { return cv[r * 16 + (c - col0)]; });
   }
 
   const int64_t qb = (int64_t)bi * a.qs0 + (int64_t)hi * a.qs1;
@@ -146,20 +168,20 @@ __device__ __forceinline__ void tok_segment(KTokArgs& a, TokSmem<AGG>& sm, int* 
   bool idle = false;                       // aggregate pass, M waves: the slab is exactly zero
   if (AGG && tid < 4) s_mzero[tid] = 0;
   int c_stop = -1;
-  float myo = 0.f;                         // output of the token this lane stores (tokens t = g mod 4)
+  float myo0 = 0.f, myo1 = 0.f;            // outputs of the token this lane stores (tokens t = rg mod 8)
   int myt = -1;
 
   // ---- register prefetch of one chunk's raw rows and gates: item (token t, 8-channel group)
   const int st = tid >> 3, sc8 = (tid & 7) * 8;   // this thread's staging item (threads < TCH * 8)
   const bool stager = tid < TCH * 8;
-  float rk[8], rv[8], rq[8], rg[8], rb[8], rw[8];
+  float rk[8], rv[8], rq[8], rgt[8], rb[8], rw[8];
   auto prefetch = [&](int cc) {
     const int tok = cc * TCH + st;
     if (!stager || tok >= a.L) return;
     load8<F32IN>(a.k, kb + (int64_t)tok * a.ks2 + sc8, rk);
     load8<F32IN>(a.vp, vb + (int64_t)tok * a.vs2 + sc8, rv);
     if (!AGG) load8<F32IN>(a.q, qb + (int64_t)tok * a.qs2 + sc8, rq);
-    gate8(gb + (int64_t)tok * a.gs2, a.gs3, sc8, rg);
+    gate8(gb + (int64_t)tok * a.gs2, a.gs3, sc8, rgt);
     gate8(bb + (int64_t)tok * a.bs2, a.bs3, sc8, rb);
     gate8(wb + (int64_t)tok * a.ws2, a.ws3, sc8, rw);
   };
@@ -179,7 +201,7 @@ __device__ __forceinline__ void tok_segment(KTokArgs& a, TokSmem<AGG>& sm, int* 
       float av[8], bkv[8], wvv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        av[i] = a.use_log ? __expf(rg[i]) : rg[i];
+        av[i] = a.use_log ? __expf(rgt[i]) : rgt[i];
         bkv[i] = rb[i] * rk[i];
         wvv[i] = rw[i] * rv[i];
       }
@@ -202,43 +224,54 @@ __device__ __forceinline__ void tok_segment(KTokArgs& a, TokSmem<AGG>& sm, int* 
 
     // ---- tokens in sequence, two at a time: each token's vectors are read while the
     // previous one computes, alternating two register sets
-    struct TokVec { f32x4 A[4], B[4], K[4], Q[4]; float W; };
+    struct TokVec { f32x4 A[2], B[2], K[2], Q[2]; float W0, W1; };
     auto fetch = [&](int t, TokVec& v) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        v.A[kt] = *(const f32x4*)&sm.A[t][16 * kt + 4 * g];
-        v.B[kt] = *(const f32x4*)&sm.BK[t][16 * kt + 4 * g];
-        v.K[kt] = *(const f32x4*)&sm.K[t][16 * kt + 4 * g];
-        if (!AGG) v.Q[kt] = *(const f32x4*)&sm.Q[t][16 * kt + 4 * g];
+      for (int h = 0; h < 2; ++h) {
+        v.A[h] = *(const f32x4*)&sm.A[t][8 * rg + 4 * h];
+        v.B[h] = *(const f32x4*)&sm.BK[t][8 * rg + 4 * h];
+        v.K[h] = *(const f32x4*)&sm.K[t][8 * rg + 4 * h];
+        if (!AGG) v.Q[h] = *(const f32x4*)&sm.Q[t][8 * rg + 4 * h];
       }
-      v.W = is_m ? 0.f : sm.WV[t][col];
-    };
-    // dot products of the slab with a row vector as two fma chains (even and odd rows)
-    auto dot16 = [&](const f32x4 (&x)[4]) {
-      float e = Sr[0][0] * x[0][0], o = Sr[0][1] * x[0][1];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = (kt == 0 ? 2 : 0); i < 4; i += 2) {
-          e = fmaf(Sr[kt][i], x[kt][i], e);
-          o = fmaf(Sr[kt][i + 1], x[kt][i + 1], o);
-        }
-      return e + o;
+      if (is_m) {
+        v.W0 = 0.f; v.W1 = 0.f;
+      } else {
+        const float2 w2 = *(const float2*)&sm.WV[t][cA];
+        v.W0 = w2.x; v.W1 = w2.y;
+      }
     };
     auto token = [&](int t, const TokVec& v) {
+      float p0 = 0.f, p1 = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) Sr[kt] = Sr[kt] * v.A[kt];
-      const float delta = v.W - sum4_groups(dot16(v.B));
+      for (int i = 0; i < 8; ++i) {
+        const float ai = v.A[i >> 2][i & 3], bi_ = v.B[i >> 2][i & 3];
+        S[i][0] *= ai;
+        S[i][1] *= ai;
+        p0 = fmaf(S[i][0], bi_, p0);
+        p1 = fmaf(S[i][1], bi_, p1);
+      }
+      const float d0 = v.W0 - sum8_lanes(p0), d1 = v.W1 - sum8_lanes(p1);
+      float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) Sr[kt] = Sr[kt] + v.K[kt] * delta;
+      for (int i = 0; i < 8; ++i) {
+        const float ki = v.K[i >> 2][i & 3];
+        S[i][0] = fmaf(ki, d0, S[i][0]);
+        S[i][1] = fmaf(ki, d1, S[i][1]);
+        if (!AGG) {
+          const float qi = v.Q[i >> 2][i & 3];
+          o0 = fmaf(S[i][0], qi, o0);
+          o1 = fmaf(S[i][1], qi, o1);
+        }
+      }
       if (!AGG) {
-        const float o = sum4_groups(dot16(v.Q));
-        if ((t & 3) == g) { myo = o; myt = t0 + t; }
-        if ((t & 3) == 3 || t == nt - 1) {   // every lane group has its token of the last four
+        o0 = sum8_lanes(o0);
+        o1 = sum8_lanes(o1);
+        if ((t & 7) == rg) { myo0 = o0; myo1 = o1; myt = t0 + t; }
+        if ((t & 7) == 7 || t == nt - 1) {   // every lane of a column pair has its token of the last eight
           if (myt >= 0) {
-            const int64_t off = (int64_t)bi * a.os0 + (int64_t)hi * a.os1 + (int64_t)myt * a.os2 + col;
-            if (OBF) ((uint16_t*)a.op)[off] = f32_to_bf16_bits(myo);
-            else ((float*)a.op)[off] = myo;
+            const int64_t off = (int64_t)bi * a.os0 + (int64_t)hi * a.os1 + (int64_t)myt * a.os2 + cA;
+            if (OBF) *(uint32_t*)((uint16_t*)a.op + off) = cvt_pk_bf16(myo0, myo1);
+            else *(float2*)((float*)a.op + off) = make_float2(myo0, myo1);
           }
           myt = -1;
         }
@@ -257,42 +290,34 @@ __device__ __forceinline__ void tok_segment(KTokArgs& a, TokSmem<AGG>& sm, int* 
     if (AGG && is_m) {
       bool nz = false;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) nz |= Sr[kt][i] != 0.f;
+      for (int i = 0; i < 8; ++i) nz |= (S[i][0] != 0.f) | (S[i][1] != 0.f);
       idle = __ballot(nz) == 0ull;
       if (lane == 0) s_mzero[wave - 4] = idle;   // read after the next loop-top barrier
     }
   }
 
   // ---- segment results
+  auto drain = [&](auto put) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) put(8 * rg + i, cA + j, S[i][j]);
+  };
   if (AGG) {
     if (tid == 0) a.zc[sidx] = c_stop >= 0 ? c_stop - c_begin : -1;
     if (c_stop < 0) {  // M never vanished: [N | M] for the fix-up pass
-      float* dst = a.agg + sidx * 64 * 128;
-      const int cc = (is_m ? 64 : 0) + col;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 128 + cc] = Sr[kt][i];
+      float* dst = a.agg + sidx * 64 * 128 + (is_m ? 64 : 0);
+      drain([&](int r, int cc, float v) { dst[r * 128 + cc] = v; });
     }
   } else if (a.mode == TOK_ZERO && !last) {  // N_k for the fix-up pass
     float* dst = a.agg + sidx * 64 * 128;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dst[(16 * kt + 4 * g + i) * 128 + col] = Sr[kt][i];
+    drain([&](int r, int cc, float v) { dst[r * 128 + cc] = v; });
   } else if (last && !(a.mode == TOK_FIX && a.zc[sidx] >= 0)) {
-    const int64_t o = bi * a.sf.s0 + hi * a.sf.s1 + col * a.sf.s3, rs = a.sf.s2;
-    auto drain = [&](auto put) {
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) put(o + (16 * kt + 4 * g + i) * rs, Sr[kt][i]);
-    };
-    if (a.sf.dt == MABA_F32) drain([&](int64_t e, float v) { ((float*)a.sf.p)[e] = v; });
-    else if (a.sf.dt == MABA_BF16) drain([&](int64_t e, float v) { ((uint16_t*)a.sf.p)[e] = f32_to_bf16_bits(v); });
-    else drain([&](int64_t e, float v) { ((__half*)a.sf.p)[e] = __float2half(v); });
+    const int64_t o = bi * a.sf.s0 + hi * a.sf.s1, rs = a.sf.s2, cs = a.sf.s3;
+    if (a.sf.dt == MABA_F32) drain([&](int r, int cc, float v) { ((float*)a.sf.p)[o + r * rs + cc * cs] = v; });
+    else if (a.sf.dt == MABA_BF16)
+      drain([&](int r, int cc, float v) { ((uint16_t*)a.sf.p)[o + r * rs + cc * cs] = f32_to_bf16_bits(v); });
+    else drain([&](int r, int cc, float v) { ((__half*)a.sf.p)[o + r * rs + cc * cs] = __float2half(v); });
   }
 }
 
@@ -369,7 +394,10 @@ bool dgda_tok_supported(const maba_tensor* q, const maba_tensor* k, const maba_t
   }
   if (!gate_ok(gate) || !gate_ok(b)) return false;
   if (w && !gate_ok(w)) return false;
-  if (out && (out->stride[3] != 1 || !fits32(out) || (out->dtype != MABA_BF16 && out->dtype != MABA_F32)))
+  // outputs go out as column pairs (4- or 8-byte stores)
+  if (out && (out->stride[3] != 1 || !fits32(out) || (out->dtype != MABA_BF16 && out->dtype != MABA_F32) ||
+              (uintptr_t)out->data % 8 != 0 || out->stride[0] % 2 != 0 || out->stride[1] % 2 != 0 ||
+              out->stride[2] % 2 != 0))
     return false;
   return q->shape[2] <= ((int64_t)1 << 30);
 }
