@@ -14,11 +14,11 @@
 // of q_lat[b,h] against latent rows c_j with the latent rows as values, and the
 // kernel returns z[b,h] = sum_s g_s z_s (fp32, [B,H,dc]).
 //
-// Kernel 1 splits every stream of every batch element into 64-key tiles (one
-// workgroup per tile) and writes a flash-decoding partial (max, sum, weighted
-// latent sum) per head.  Kernel 2 merges the partials of each (b, h, stream),
-// applies the gate softmax and writes z.  Traffic is one read of the selected
-// latent rows (bf16) plus small partials: HBM-bound.
+// Each stream of each batch element is cut into segments; a workgroup writes one
+// flash-decoding partial (max, sum, weighted latent sum) per head for its segment,
+// and a merge of the partials of each (b, h) applies the gate softmax and writes z.
+// Traffic is one read of the selected latent rows (bf16) plus small partials:
+// HBM-bound.
 #include <algorithm>
 
 #include "maba_common.h"
@@ -36,18 +36,29 @@ struct SaArgs {
   const int64_t* idx; int64_t isb, ish, isk;
   const void* gate; int gdt; int64_t gsb, gsh, gsm;  // gsh = 0 for [B,3]
   float* out; int64_t osb, osh, osd;
-  float* ws;
-  int64_t L;
+  float* ws;    // partials, slot-major: [slot][b][h][dc + 2]
+  int64_t L, B;
   int H, dc, Hi, K, window, n_sink, bs, pool;
   int ns, loc_start, nloc, nc;           // local / hca geometry
   int t_loc, t_sp, t_hca, ntiles;        // tile counts per batch element
+  // segment path: tiles per wave and the segment counts; partial slots [0, s_loc)
+  // local, [s_loc, s_loc + s_hca) HCA, then the sparse ones (s_sp1 per index row)
+  int tpw, s_loc, s_hca, s_sp1, s_sp;
   float scale;
 };
 
-__device__ __forceinline__ int64_t sa_part_off(const SaArgs& a, int64_t b, int tile, int h) {
-  return (((b * a.ntiles + tile) * a.H) + h) * (int64_t)(a.dc + 2);
+__device__ __forceinline__ int64_t sa_part_off(const SaArgs& a, int64_t b, int slot, int h) {
+  return (((int64_t)slot * a.B + b) * a.H + h) * (int64_t)(a.dc + 2);
 }
 
+// Partials merged for one (b, h): n virtual partials t = 0 .. n-1 at slots t (t < na)
+// and sp0 + sp_step * h + (t - na) (t >= na).  Virtual partials [0, e1) belong to stream
+// st0, [e1, e2) to st1 and [e2, n) to st2 (streams: 0 local, 1 sparse, 2 HCA).
+struct SaMerge {
+  int n, na, sp0, sp_step, e1, e2, st0, st1, st2;
+};
+
+// Generic path: one workgroup per 64-key tile, one partial slot per tile.
 __global__ __launch_bounds__(256) void maba_sa_tile_kernel(SaArgs a) {
   __shared__ float s_c[64][SA_MAXDC + 1];
   __shared__ float s_q[SA_MAXH][SA_MAXDC];
@@ -151,36 +162,42 @@ __global__ __launch_bounds__(256) void maba_sa_tile_kernel(SaArgs a) {
   }
 }
 
-// One workgroup per (b, h): merge the partials of each stream, apply the gate.
-// Partials [0, p1) are the local stream, [p1, p2) sparse, [p2, p3) HCA.  Waves
-// 0-2 reduce the (max, sum) pairs of one stream each; then, in chunks of 256
-// partials, every partial's weight g_s exp(m - M_s) / L_s goes to LDS and the
-// threads (dim d, sub-slice) accumulate the weighted latent sums.
-__global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a, int p1, int p2, int p3) {
-  __shared__ float s_w[256];
-  __shared__ float s_M[3], s_S[3];
-  __shared__ float s_acc[256];
-  const int64_t b = blockIdx.x / a.H;
-  const int h = blockIdx.x % a.H;
+// Merge of the n virtual partials of (b, h) (streams as in SaMerge), NT threads.
+// src.m(t), src.l(t) and src.z(t, d) read partial t's max, sum and latent sum.
+// Thread (dim d, sub-slice) issues the loads of its latent sums of the first SA_PRE
+// partials together with the partial headers, so that the merge waits on one round of
+// loads; waves 0-2 then reduce the (max, sum) pairs of one stream each, every
+// partial's weight g_s exp(m - M_s) / L_s goes to LDS and the threads accumulate their
+// weighted sums.  lds holds at least 2 NT + 8 floats.
+constexpr int SA_PRE = 16;   // partials per thread whose latent sums are loaded up front
+template <int NT, class Src>
+__device__ void sa_merge(const SaArgs& a, const SaMerge& mg, int64_t b, int h, float* lds, const Src& src) {
+  float* s_w = lds;
+  float* s_acc = lds + NT;
+  float* s_M = lds + 2 * NT;
+  float* s_S = lds + 2 * NT + 4;
   const int dc = a.dc;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n = mg.n;
+  const int nsub = NT / dc;  // threads per latent dim
+  const int d = tid % dc, sub = tid / dc;
+  const bool active = sub < nsub;
+  float zpre[SA_PRE];
+#pragma unroll
+  for (int i = 0; i < SA_PRE; ++i) {
+    const int t = sub + i * nsub;
+    zpre[i] = (active && t < n) ? src.z(t, d) : 0.f;
+  }
+  const float m_first = tid < n ? src.m(tid) : -INFINITY;
   const int64_t gb = b * a.gsb + h * a.gsh;
   float z0 = load_elem(a.gate, a.gdt, gb), z1 = load_elem(a.gate, a.gdt, gb + a.gsm),
         z2 = load_elem(a.gate, a.gdt, gb + 2 * a.gsm);
-  const float gm = fmaxf(z0, fmaxf(z1, z2));
-  z0 = __expf(z0 - gm); z1 = __expf(z1 - gm); z2 = __expf(z2 - gm);
-  const float gi = 1.f / (z0 + z1 + z2);
-  const float gate[3] = {z0 * gi, z1 * gi, z2 * gi};
-  const int t_begin[3] = {0, p1, p2};
-  const int t_end[3] = {p1, p2, p3};
-  // partial headers of the first chunk, loaded alongside the stream reductions
-  float m_first = -INFINITY;
-  if (tid < p3) m_first = a.ws[sa_part_off(a, b, tid, h)];
-  if (wave < 3) {  // online (max, sum) over the stream's partials, one pass
+  if (wave < 3) {  // online (max, sum) over one stream's partials, one pass
+    const int t0 = wave == 0 ? 0 : (wave == 1 ? mg.e1 : mg.e2);
+    const int t1 = wave == 0 ? mg.e1 : (wave == 1 ? mg.e2 : n);
     float M = -INFINITY, S = 0.f;
-    for (int t = t_begin[wave] + lane; t < t_end[wave]; t += 64) {
-      const int64_t o = sa_part_off(a, b, t, h);
-      const float m = a.ws[o], l = a.ws[o + 1];
+    for (int t = t0 + lane; t < t1; t += 64) {
+      const float m = src.m(t), l = src.l(t);
       if (m != -INFINITY) {
         if (m > M) {
           S = S * __expf(M - m) + l;
@@ -202,42 +219,80 @@ __global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a, int p1, 
       s_S[wave] = S;
     }
   }
+  const float gm = fmaxf(z0, fmaxf(z1, z2));
+  z0 = __expf(z0 - gm); z1 = __expf(z1 - gm); z2 = __expf(z2 - gm);
+  const float gi = 1.f / (z0 + z1 + z2);
+  auto gate_of = [&](int st) { return (st == 0 ? z0 : (st == 1 ? z1 : z2)) * gi; };
+  const float g0 = gate_of(mg.st0), g1 = gate_of(mg.st1), g2 = gate_of(mg.st2);
   __syncthreads();
-  const int nsub = 256 / dc;  // threads per latent dim
-  const int d = tid % dc, sub = tid / dc;
-  const bool active = sub < nsub;
   float acc = 0.f;
-  for (int c0 = 0; c0 < p3; c0 += 256) {
+  for (int c0 = 0; c0 < n; c0 += NT) {
     const int t = c0 + tid;
     float w = 0.f;
-    if (t < p3) {
-      const int st = t < p1 ? 0 : (t < p2 ? 1 : 2);
-      const float m = c0 == 0 ? m_first : a.ws[sa_part_off(a, b, t, h)];
-      if (m != -INFINITY && s_S[st] > 0.f) w = gate[st] * __expf(m - s_M[st]) / s_S[st];
+    if (t < n) {
+      const int k = t < mg.e1 ? 0 : (t < mg.e2 ? 1 : 2);
+      const float m = c0 == 0 ? m_first : src.m(t);
+      const float Sk = s_S[k];
+      if (m != -INFINITY && Sk > 0.f) w = (k == 0 ? g0 : (k == 1 ? g1 : g2)) * __expf(m - s_M[k]) / Sk;
     }
     s_w[tid] = w;
     __syncthreads();
-    const int cn = (p3 - c0) < 256 ? (p3 - c0) : 256;
-    // every partial slot is written by the segment kernel, so the loads need no guard
+    const int cn = (n - c0) < NT ? (n - c0) : NT;
     if (active) {
-#pragma unroll 8
-      for (int j = sub; j < cn; j += nsub) acc = fmaf(s_w[j], a.ws[sa_part_off(a, b, c0 + j, h) + 2 + d], acc);
+      int j = sub;
+      if (c0 == 0) {
+#pragma unroll
+        for (int i = 0; i < SA_PRE; ++i)
+          if (sub + i * nsub < cn) acc = fmaf(s_w[sub + i * nsub], zpre[i], acc);
+        j = sub + SA_PRE * nsub;
+      }
+#pragma unroll 4
+      for (; j < cn; j += nsub) acc = fmaf(s_w[j], src.z(c0 + j, d), acc);
     }
     __syncthreads();
   }
   s_acc[tid] = active ? acc : 0.f;
   __syncthreads();
   if (tid < dc) {
-    float r = 0.f;
-    for (int k = 0; k < nsub; ++k) r += s_acc[k * dc + tid];
+    float res = 0.f;
+    for (int k = 0; k < nsub; ++k) res += s_acc[k * dc + tid];
     if (a.L - 1 < a.pool - 1) {
       // early HCA: running mean of c[0..L-1] (sparse_attention.py:189-199)
       float zs = 0.f;
       for (int64_t t = 0; t < a.L; ++t) zs += load_elem(a.c, a.cdt, b * a.csb + t * a.csl + tid * a.csd);
-      r = fmaf(gate[2], zs / (float)a.L, r);
+      res = fmaf(gate_of(2), zs / (float)a.L, res);
     }
-    a.out[b * a.osb + h * a.osh + tid * a.osd] = r;
+    a.out[b * a.osb + h * a.osh + tid * a.osd] = res;
   }
+}
+
+// Partials of (b, h) in the workspace: virtual partial t at slot t (t < na), else at
+// slot sp0 + sp_step * h + (t - na).  Every slot read is written by a segment kernel.
+struct SaWsSrc {
+  const float* base;   // partial (slot 0, b, h)
+  int64_t row;         // floats per slot
+  int na, spb;
+  __device__ const float* p(int t) const { return base + (int64_t)(t < na ? t : spb + t) * row; }
+  __device__ float m(int t) const { return p(t)[0]; }
+  __device__ float l(int t) const { return p(t)[1]; }
+  __device__ float z(int t, int d) const { return p(t)[2 + d]; }
+};
+
+__device__ __forceinline__ SaWsSrc sa_ws_src(const SaArgs& a, const SaMerge& mg, int64_t b, int h) {
+  SaWsSrc s;
+  s.base = a.ws + (b * a.H + h) * (int64_t)(a.dc + 2);
+  s.row = (int64_t)a.B * a.H * (a.dc + 2);
+  s.na = mg.na;
+  s.spb = mg.sp0 + mg.sp_step * h - mg.na;
+  return s;
+}
+
+// One workgroup per (b, h) over the per-tile partials of the generic path.
+__global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a, SaMerge mg) {
+  __shared__ float lds[2 * 256 + 8];
+  const int64_t b = blockIdx.x / a.H;
+  const int h = blockIdx.x % a.H;
+  sa_merge<256>(a, mg, b, h, lds, sa_ws_src(a, mg, b, h));
 }
 
 // ------------------------------------------------------------------ MFMA path
@@ -271,35 +326,41 @@ struct SaSeg {
   int hs;                  // sparse index row
 };
 
-__device__ __forceinline__ SaSeg sa_segment(const SaArgs& a, int sid, int s_sp1, int span) {
+// Segment of partial slot sid (segment path): up to 4 tpw tiles (sparse: index slots
+// of one index row).
+__device__ __forceinline__ SaSeg sa_segment(const SaArgs& a, int sid) {
   SaSeg g;
   g.head_only = -1;
   g.hs = 0;
-  const int s_sp = (a.Hi == 1) ? s_sp1 : a.H * s_sp1;
-  if (sid == 0) {
-    g.stream = 0; g.t_begin = 0; g.t_end = a.t_loc;
-  } else if (sid < 1 + s_sp) {
-    const int r = sid - 1;
+  const int span = 4 * a.tpw;
+  if (sid < a.s_loc) {
+    g.stream = 0;
+    g.t_begin = (int64_t)sid * span;
+    g.t_end = min((int64_t)a.t_loc, g.t_begin + span);
+  } else if (sid < a.s_loc + a.s_hca) {
+    g.stream = 2;
+    g.t_begin = (int64_t)(sid - a.s_loc) * span;
+    g.t_end = min((int64_t)a.t_hca, g.t_begin + span);
+  } else {
+    const int r = sid - a.s_loc - a.s_hca;
     g.stream = 1;
-    g.hs = (a.Hi == 1) ? 0 : r / s_sp1;
-    const int rr = (a.Hi == 1) ? r : r % s_sp1;
+    g.hs = (a.Hi == 1) ? 0 : r / a.s_sp1;
+    const int rr = (a.Hi == 1) ? r : r % a.s_sp1;
     if (a.Hi > 1) g.head_only = g.hs;
     g.t_begin = (int64_t)rr * span;
     g.t_end = min((int64_t)a.K, g.t_begin + span);
-  } else {
-    const int r = sid - 1 - s_sp;
-    g.stream = 2;
-    g.t_begin = (int64_t)r * span;
-    g.t_end = min((int64_t)a.t_hca, g.t_begin + span);
   }
   return g;
 }
 
-// Key rows 16 rb + c16 of tile tix of a segment, dims 32 p + 8 g .. +7; invalid rows read as zeros.
-// blk is the tile's block index for the sparse stream.
+// Key rows 16 rb + c16 of tile tix of a segment, dims 32 p + 8 g .. +7.  Invalid rows
+// read row 0 of the stream (in bounds: L >= 1, and the HCA stream is only walked when it
+// has entries); their scores are masked to -inf, so they get zero weight.  blk is the
+// tile's block index for the sparse stream.  Bit 4 rb + i of okb says whether
+// key row 16 rb + 4 g + i (a row of this lane's score accumulators) is valid.
 template <int NP>
 __device__ __forceinline__ void sa_load_tile(const SaArgs& a, const SaSeg& sg, int64_t b, int64_t tix, int64_t blk,
-                                             int c16, int g, s16x8 (&cv)[4][NP], bool (&ok)[4]) {
+                                             int c16, int g, s16x8 (&cv)[4][NP], uint32_t& okb) {
   const uint16_t* base;
   int64_t rstride;
   if (sg.stream == 2) {
@@ -310,46 +371,48 @@ __device__ __forceinline__ void sa_load_tile(const SaArgs& a, const SaSeg& sg, i
     rstride = a.csl;
   }
   const int64_t nblk = (a.L + a.bs - 1) / a.bs;
+  okb = 0;
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
     const int j = 16 * rb + c16;
     int64_t pos;
+    bool ok;
     if (sg.stream == 0) {
       const int64_t li = tix * 64 + j;
-      ok[rb] = li < a.nloc;
+      ok = li < a.nloc;
       pos = li < a.ns ? li : a.loc_start + (li - a.ns);
     } else if (sg.stream == 1) {
       pos = blk * a.bs + j;
-      ok[rb] = blk >= 0 && blk < nblk && j < a.bs && pos < a.L;
+      ok = blk >= 0 && blk < nblk && j < a.bs && pos < a.L;
     } else {
       pos = tix * 64 + j;
-      ok[rb] = pos < a.nc;
+      ok = pos < a.nc;
     }
+    const uint16_t* row = base + (ok ? pos : 0) * rstride + 8 * g;
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (ok[rb]) v = *(const s16x8*)(base + pos * rstride + 32 * p + 8 * g);
-      cv[rb][p] = v;
-    }
+    for (int p = 0; p < NP; ++p) cv[rb][p] = *(const s16x8*)(row + 32 * p);
+    // lanes 0-15 load rows 16 rb + c16: bits 4g .. 4g+3 of their ballot are this lane's rows
+    okb |= (uint32_t)((__ballot(ok) >> (4 * g)) & 0xfu) << (4 * rb);
   }
 }
 
 template <int NP>  // d_c = 32 * NP
-__global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg, int s_sp1, int tpw) {
+__global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a) {
   constexpr int DC = 32 * NP;
   constexpr int TP = DC + 8;  // row pitch (bf16) of the per-wave key tile: 16-B aligned, rows shift 4 banks
   __shared__ __attribute__((aligned(16))) short s_tile[4][64 * TP];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane >> 4, c16 = lane & 15;
-  const int sid = blockIdx.x;
+  const int sid = (int)blockIdx.x;
   const int64_t b = blockIdx.y;
-  if (sid >= nseg) return;  // uniform per workgroup
-  const SaSeg sg = sa_segment(a, sid, s_sp1, 4 * tpw);
+  const SaSeg sg = sa_segment(a, sid);
+  const int tpw = a.tpw;
   const int64_t t0 = sg.t_begin + (int64_t)wave * tpw;
   const int64_t t1 = min(sg.t_end, t0 + tpw);
   short* tile = s_tile[wave];
 
-  // queries (B operand of the scores): head c16, dims 32p + 8g .. +7, split hi/lo
+  // queries times the score scale (B operand of the scores): head c16, dims 32p + 8g .. +7,
+  // split hi/lo
   s16x8 qh[NP], ql[NP];
   float qv[NP][8];
   if (a.qvec) {  // fp32 rows, 16-byte aligned: all of the lane's query loads in flight at once
@@ -378,7 +441,7 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
   for (int p = 0; p < NP; ++p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float x = qv[p][j];
+      const float x = qv[p][j] * a.scale;   // scores come out scaled
       const short h = __builtin_bit_cast(short, (__bf16)x);
       qh[p][j] = h;
       ql[p][j] = __builtin_bit_cast(short, (__bf16)(x - bf16_bits_to_f32((uint16_t)h)));
@@ -394,22 +457,22 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
   // the tile loads do not wait on a dependent index load
   int64_t blk_l = 0;
   if (sg.stream == 1 && lane < t1 - t0) blk_l = a.idx[b * a.isb + sg.hs * a.ish + (t0 + lane) * a.isk];
-  s16x8 cv[4][NP];
-  bool ok[4];
-  if (t0 < t1) sa_load_tile<NP>(a, sg, b, t0, __shfl(blk_l, 0), c16, g, cv, ok);
-  for (int64_t tix = t0; tix < t1; ++tix) {
-    // prefetch the next tile (the current one is re-read when there is none: in bounds, unused)
-    s16x8 nv[4][NP];
-    bool nok[4];
-    const int64_t tn = tix + 1 < t1 ? tix + 1 : tix;
-    sa_load_tile<NP>(a, sg, b, tn, __shfl(blk_l, (int)(tn - t0)), c16, g, nv, nok);
+  auto blk_of = [&](int64_t tix) {   // wave-uniform lane index
+    const int src = (int)(tix - t0);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)blk_l, src);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)blk_l >> 32), src);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+  // One tile: scores, online softmax, values.  The key rows arrive in registers (cv,
+  // with their row validity ok) and are copied row-major into the wave's LDS tile for
+  // the transposed reads of the value product.
+  auto tile_step = [&](const s16x8 (&cv)[4][NP], uint32_t okb) {
     f32x4 sc[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        // row-major copy for the value product (read back transposed)
         *(s16x8*)(tile + (16 * rb + c16) * TP + 32 * p + 8 * g) = cv[rb][p];
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
                                                       __builtin_bit_cast(bf16x8, qh[p]), acc, 0, 0, 0);
@@ -424,9 +487,8 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
     for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        // key row 16 rb + 4g + i is valid iff the loading lane c16' = 4g + i had ok[rb]
-        const bool kv = __shfl(ok[rb] ? 1 : 0, 4 * g + i) != 0;
-        const float x = (kv && head_on) ? sc[rb][i] * a.scale : -INFINITY;
+        const bool kv = (okb >> (4 * rb + i)) & 1u;
+        const float x = (kv && head_on) ? sc[rb][i] : -INFINITY;
         sc[rb][i] = x;
         tmax = fmaxf(tmax, x);
       }
@@ -435,6 +497,7 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float m_new = fmaxf(m_run, tmax);
     const float corr = (m_new == -INFINITY) ? 1.f : __expf(m_run - m_new);
+    const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;   // exp(-inf - m_sub) = 0 for masked keys
     float psum = 0.f;
     s16x4 ph[4], pl[4];
 #pragma unroll
@@ -442,15 +505,15 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
       f32x4 pv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float pe = (sc[rb][i] == -INFINITY) ? 0.f : __expf(sc[rb][i] - m_new);
+        const float pe = __expf(sc[rb][i] - m_sub);
         pv[i] = pe;
         psum += pe;
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const short h = __builtin_bit_cast(short, (__bf16)pv[i]);
-        ph[rb][i] = h;
-        pl[rb][i] = __builtin_bit_cast(short, (__bf16)(pv[i] - bf16_bits_to_f32((uint16_t)h)));
+        const short hb = __builtin_bit_cast(short, (__bf16)pv[i]);
+        ph[rb][i] = hb;
+        pl[rb][i] = __builtin_bit_cast(short, (__bf16)(pv[i] - bf16_bits_to_f32((uint16_t)hb)));
       }
     }
     psum += __shfl_xor(psum, 16);
@@ -477,12 +540,22 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
       }
       z[dt] = acc;
     }
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      ok[rb] = nok[rb];
-#pragma unroll
-      for (int p = 0; p < NP; ++p) cv[rb][p] = nv[rb][p];
-    }
+  };
+  // two register sets in turn: the next tile's loads are in flight while a tile computes,
+  // and no set is copied into the other (a copy would wait for the loads)
+  s16x8 cvA[4][NP], cvB[4][NP];
+  uint32_t okA = 0, okB = 0;
+  if (t0 < t1) sa_load_tile<NP>(a, sg, b, t0, blk_of(t0), c16, g, cvA, okA);
+  for (int64_t tix = t0; tix < t1; tix += 2) {
+    // loads past the wave's last tile re-read that tile (in bounds, unused); unconditional
+    // loads keep the register pressure of the two sets at that of straight-line code
+    const int64_t n1 = tix + 1 < t1 ? tix + 1 : tix;
+    sa_load_tile<NP>(a, sg, b, n1, blk_of(n1), c16, g, cvB, okB);
+    tile_step(cvA, okA);
+    if (tix + 1 >= t1) break;
+    const int64_t n2 = tix + 2 < t1 ? tix + 2 : tix + 1;
+    sa_load_tile<NP>(a, sg, b, n2, blk_of(n2), c16, g, cvA, okA);
+    tile_step(cvB, okB);
   }
   // merge the four wave partials: s_z[wave][head][dim], s_m / s_l[wave][head]
   __syncthreads();
@@ -510,7 +583,7 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
       e[w] = (m == -INFINITY) ? 0.f : __expf(m - M);
       Ls = fmaf(e[w], s_l[w * 16 + h], Ls);
     }
-    const int64_t o = (((b * a.ntiles) + sid) * a.H + h) * (int64_t)(a.dc + 2);
+    const int64_t o = sa_part_off(a, b, sid, h);
     if (part == 0) {
       a.ws[o] = M;
       a.ws[o + 1] = Ls;
@@ -526,7 +599,7 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a, int nseg
   }
 }
 
-// Compute units of the current device (queried once per device).
+// Tile geometry of the three streams (per batch element).
 static void sa_geometry(SaArgs& a, int64_t L, int window, int n_sink, int pool, int Hi, int K) {
   const int64_t ns = L < n_sink ? L : n_sink;
   const int64_t st = (L - window) > ns ? (L - window) : ns;
@@ -540,22 +613,29 @@ static void sa_geometry(SaArgs& a, int64_t L, int window, int n_sink, int pool, 
   a.ntiles = a.t_loc + a.t_sp + a.t_hca;
 }
 
-}  // namespace maba
-
-using namespace maba;
-
-extern "C" size_t maba_hip_maba_sa_decode_workspace_size(int64_t B, int64_t H, int64_t dc, int64_t L,
-                                                         int64_t K, int window, int n_sink, int pool) {
-  SaArgs a;
-  sa_geometry(a, L, window, n_sink, pool > 0 ? pool : 64, (int)H, (int)K);  // upper bound: Hi = H
-  return (size_t)(B * (int64_t)(a.ntiles > 0 ? a.ntiles : 1) * H * (dc + 2)) * sizeof(float);
+// Segment path geometry: the fewest tiles per wave (at most 8) for which the segments
+// of all streams fit one workgroup per compute unit (every workgroup pays a fixed
+// start-up; one round of workgroups covers the machine).
+static void sa_segments(SaArgs& a, int ncu) {
+  for (a.tpw = 1;; ++a.tpw) {
+    const int span = 4 * a.tpw;
+    a.s_loc = (int)ceil_div(a.t_loc, span);
+    a.s_hca = (int)ceil_div(a.t_hca, span);
+    a.s_sp1 = (int)ceil_div(a.K, span);
+    a.s_sp = a.Hi == 1 ? a.s_sp1 : a.H * a.s_sp1;
+    if (a.B * (a.s_loc + a.s_hca + a.s_sp) <= ncu || a.tpw == 8) break;
+  }
 }
 
-extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tensor* c_kv,
-                                       const maba_tensor* hca, const maba_tensor* idx,
-                                       const maba_tensor* gate, int64_t L, float scale, int window,
-                                       int n_sink, int block_size, int pool, maba_tensor* out_lat,
-                                       void* workspace, size_t workspace_bytes, void* stream) {
+static size_t sa_part_bytes(int64_t slots, int64_t B, int64_t H, int64_t dc) {
+  return (size_t)((slots > 0 ? slots : 1) * B * H * (dc + 2)) * sizeof(float);
+}
+
+// Validation and argument set-up.
+static int sa_setup(const maba_tensor* q_lat, const maba_tensor* c_kv, const maba_tensor* hca,
+                    const maba_tensor* idx, const maba_tensor* gate, const maba_tensor* out_lat, int64_t L,
+                    float scale, int window, int n_sink, int block_size, int pool, void* workspace,
+                    size_t workspace_bytes, SaArgs& a, bool& seg, bool& empty) {
   if (!q_lat || q_lat->ndim != 3) return fail(MABA_ERR_INVALID, "maba_sa_decode: q_lat must be [B,H,dc]");
   const int64_t B = q_lat->shape[0], H = q_lat->shape[1], dc = q_lat->shape[2];
   if (!c_kv || c_kv->ndim != 3 || c_kv->shape[0] != B || c_kv->shape[2] != dc)
@@ -580,8 +660,9 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
   if (H > SA_MAXH || dc > SA_MAXDC || block_size > 64)
     return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode: H <= %d, dc <= %d, block_size <= 64 required",
                 SA_MAXH, SA_MAXDC);
-  if (B * H == 0) return MABA_OK;
-  SaArgs a;
+  empty = B * H == 0;
+  if (empty) return MABA_OK;
+  a = SaArgs{};
   a.q = q_lat->data; a.qdt = q_lat->dtype; a.qsb = q_lat->stride[0]; a.qsh = q_lat->stride[1]; a.qsd = q_lat->stride[2];
   a.qvec = q_lat->dtype == MABA_F32 && q_lat->stride[2] == 1 && (uintptr_t)q_lat->data % 16 == 0 &&
            q_lat->stride[0] % 4 == 0 && q_lat->stride[1] % 4 == 0;
@@ -591,50 +672,76 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
   a.gate = gate->data; a.gdt = gate->dtype; a.gsb = gate->stride[0];
   if (gate->ndim == 2) { a.gsh = 0; a.gsm = gate->stride[1]; } else { a.gsh = gate->stride[1]; a.gsm = gate->stride[2]; }
   a.out = (float*)out_lat->data; a.osb = out_lat->stride[0]; a.osh = out_lat->stride[1]; a.osd = out_lat->stride[2];
-  a.ws = (float*)workspace;
-  a.L = L; a.H = (int)H; a.dc = (int)dc; a.Hi = (int)idx->shape[1]; a.K = (int)idx->shape[2];
+  a.L = L; a.B = B; a.H = (int)H; a.dc = (int)dc; a.Hi = (int)idx->shape[1]; a.K = (int)idx->shape[2];
   a.window = window; a.n_sink = n_sink; a.bs = block_size; a.pool = pool; a.scale = scale;
   sa_geometry(a, L, window, n_sink, pool, a.Hi, a.K);
-  const size_t need = (size_t)(B * (int64_t)(a.ntiles > 0 ? a.ntiles : 1) * H * (dc + 2)) * sizeof(float);
+  seg = c_kv->dtype == MABA_BF16 && hca->dtype == MABA_BF16 && c_kv->stride[2] == 1 && hca->stride[2] == 1 &&
+        dc % 32 == 0 && dc <= 128 && (uintptr_t)c_kv->data % 16 == 0 && (uintptr_t)hca->data % 16 == 0 &&
+        c_kv->stride[0] % 8 == 0 && c_kv->stride[1] % 8 == 0 && hca->stride[0] % 8 == 0 && hca->stride[1] % 8 == 0;
+  int64_t slots = a.ntiles;
+  if (seg) {
+    sa_segments(a, device_cu_count());
+    slots = a.s_loc + a.s_hca + a.s_sp;
+  }
+  const size_t need = sa_part_bytes(slots, B, H, dc);
   if (!workspace || workspace_bytes < need)
     return fail(MABA_ERR_WORKSPACE, "maba_sa_decode: workspace of %zu bytes required", need);
-  hipStream_t s = (hipStream_t)stream;
-  const bool mfma_ok = c_kv->dtype == MABA_BF16 && hca->dtype == MABA_BF16 && c_kv->stride[2] == 1 &&
-                       hca->stride[2] == 1 && dc % 32 == 0 && dc <= 128 && (uintptr_t)c_kv->data % 16 == 0 &&
-                       (uintptr_t)hca->data % 16 == 0 && c_kv->stride[0] % 8 == 0 && c_kv->stride[1] % 8 == 0 &&
-                       hca->stride[0] % 8 == 0 && hca->stride[1] % 8 == 0 && block_size <= 64;
-  if (mfma_ok) {
-    // tiles per wave: the fewest that still fit one workgroup per CU (every workgroup
-    // pays a fixed start-up, and one round of workgroups covers the machine), at most 8
-    const int ncu = device_cu_count();
-    int tpw = 1, span = 4, s_sp1 = 0, s_sp = 0, s_hca = 0, nseg = 0;
-    for (tpw = 1; tpw <= 8; ++tpw) {
-      span = 4 * tpw;
-      s_sp1 = (int)ceil_div(a.K, span);
-      s_sp = a.Hi == 1 ? s_sp1 : (int)H * s_sp1;
-      s_hca = (int)ceil_div(a.t_hca, span);
-      nseg = 1 + s_sp + s_hca;
-      if (B * nseg <= ncu || tpw == 8) break;
-    }
-    a.ntiles = nseg;  // partial slots are segments
-    const dim3 grid((unsigned)nseg, (unsigned)B);
-    switch (dc / 32) {
-      case 1: hipLaunchKernelGGL(maba_sa_mfma_kernel<1>, grid, dim3(256), 0, s, a, nseg, s_sp1, tpw); break;
-      case 2: hipLaunchKernelGGL(maba_sa_mfma_kernel<2>, grid, dim3(256), 0, s, a, nseg, s_sp1, tpw); break;
-      case 3: hipLaunchKernelGGL(maba_sa_mfma_kernel<3>, grid, dim3(256), 0, s, a, nseg, s_sp1, tpw); break;
-      default: hipLaunchKernelGGL(maba_sa_mfma_kernel<4>, grid, dim3(256), 0, s, a, nseg, s_sp1, tpw); break;
-    }
-    int rc = check_launch("maba_sa_decode/segments");
-    if (rc) return rc;
-    hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(256), 0, s, a, 1, 1 + s_sp, nseg);
-    return check_launch("maba_sa_decode/combine");
+  a.ws = (float*)workspace;
+  return MABA_OK;
+}
+
+// Merge of every (b, h): one workgroup each.
+static int sa_launch_combine(const SaArgs& a, bool seg, hipStream_t s) {
+  SaMerge mg;
+  if (seg) {   // slots: local, HCA, then the sparse ones (per index row)
+    const int nsp = a.Hi == 1 ? a.s_sp : a.s_sp1;
+    mg = SaMerge{a.s_loc + a.s_hca + nsp, a.s_loc + a.s_hca, a.s_loc + a.s_hca, a.Hi == 1 ? 0 : a.s_sp1,
+                 a.s_loc, a.s_loc + a.s_hca, 0, 2, 1};
+  } else {     // per-tile slots: local, sparse, HCA
+    mg = SaMerge{a.ntiles, a.ntiles, 0, 0, a.t_loc, a.t_loc + a.t_sp, 0, 1, 2};
   }
-  if (a.ntiles > 0) {
-    hipLaunchKernelGGL(maba_sa_tile_kernel, dim3((unsigned)a.ntiles, (unsigned)B), dim3(256), 0, s, a);
-    int rc = check_launch("maba_sa_decode/tiles");
-    if (rc) return rc;
-  }
-  hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(B * H)), dim3(256), 0, s, a, a.t_loc,
-                     a.t_loc + a.t_sp, a.t_loc + a.t_sp + a.t_hca);
+  hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s, a, mg);
   return check_launch("maba_sa_decode/combine");
+}
+
+}  // namespace maba
+
+using namespace maba;
+
+extern "C" size_t maba_hip_maba_sa_decode_workspace_size(int64_t B, int64_t H, int64_t dc, int64_t L,
+                                                         int64_t K, int window, int n_sink, int pool) {
+  // upper bound over both paths and index-row counts: the generic path's per-tile slots with Hi = H
+  SaArgs a;
+  sa_geometry(a, L, window, n_sink, pool > 0 ? pool : 64, (int)H, (int)K);
+  return sa_part_bytes(a.ntiles, B, H, dc);
+}
+
+extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                       const maba_tensor* hca, const maba_tensor* idx,
+                                       const maba_tensor* gate, int64_t L, float scale, int window,
+                                       int n_sink, int block_size, int pool, maba_tensor* out_lat,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  SaArgs a;
+  bool seg = false, empty = false;
+  int rc = sa_setup(q_lat, c_kv, hca, idx, gate, out_lat, L, scale, window, n_sink, block_size, pool, workspace,
+                    workspace_bytes, a, seg, empty);
+  if (rc || empty) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned nslot = (unsigned)(seg ? a.s_loc + a.s_hca + a.s_sp : a.ntiles);
+  if (nslot > 0) {
+    const dim3 grid(nslot, (unsigned)a.B);
+    if (seg) {
+      switch (a.dc / 32) {
+        case 1: hipLaunchKernelGGL(maba_sa_mfma_kernel<1>, grid, dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(maba_sa_mfma_kernel<2>, grid, dim3(256), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(maba_sa_mfma_kernel<3>, grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(maba_sa_mfma_kernel<4>, grid, dim3(256), 0, s, a); break;
+      }
+    } else {
+      hipLaunchKernelGGL(maba_sa_tile_kernel, grid, dim3(256), 0, s, a);
+    }
+    rc = check_launch(seg ? "maba_sa_decode/segments" : "maba_sa_decode/tiles");
+    if (rc) return rc;
+  }
+  return sa_launch_combine(a, seg, s);
 }

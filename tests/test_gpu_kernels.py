@@ -317,6 +317,21 @@ def test_maba_sa_decode(dev, L, K, Hi):
     assert_close(out, exp, 2e-3, 2e-3, "maba_sa")
 
 
+@pytest.mark.parametrize("L,window,n_sink", [(5000, 1000, 4), (3000, 2999, 0), (700, 650, 16)])
+def test_maba_sa_decode_wide_window(dev, L, window, n_sink):
+    """Windows of many 64-key tiles: the local stream is cut into several segments."""
+    B, H, dh, dc, K = 2, 4, 64, 128, 16
+    c, Wk, Wv, q, idx, gate = _sa_case(B, H, dh, dc, L, K, 1, L + window, dev)
+    hca = _hip().hip_hca_pool(c.to(dev), pool=64)
+    q_lat = torch.einsum("bhd,hdc->bhc", q, Wk.view(H, dh, dc))
+    z = _hip().hip_maba_sa_decode(q_lat.to(dev), c.to(dev), hca, idx.to(dev), gate.to(dev), L=L,
+                                  scale=1.0 / math.sqrt(dh), window=window, n_sink=n_sink)
+    out = torch.einsum("bhc,hdc->bhd", z.cpu(), Wv.view(H, dh, dc))
+    exp = osa.maba_sa_decode(to_np(q), to_np(c), to_np(Wk), to_np(Wv), to_np(idx).astype(np.int64),
+                             to_np(gate), window=window, n_sink=n_sink, means=to_np(hca))
+    assert_close(out, exp, 2e-3, 2e-3, "maba_sa wide window")
+
+
 @pytest.mark.parametrize("L,K,Hi", [(8192, 64, 10), (20000, 64, 1)])
 def test_maba_sa_decode_many_segments(dev, L, K, Hi):
     """Enough tiles that every wave runs several tiles (register prefetch path) and the
