@@ -8,17 +8,23 @@ inputs resident in HBM.  ``value`` = B*T / step time (tokens/s).
 
 Also reported in the same JSON line:
   * ``roofline``   -- the DGDA prefill op (three launches: segment aggregate,
-                      segment scan, segment output) against HBM: algorithmic
+                      zero-start output, fix-up output) against HBM: algorithmic
                       bytes per step / step time (HIP events on the launch
                       stream), plus the bf16-MFMA fraction of the algorithmic
                       flops;
   * ``cpu_baseline`` -- the C/OpenMP restatement of the reference CPU chunked
-                      algorithm (oracle/dgda_chunked.c) on a bounded sample of the
-                      same workload, on the host cores;
+                      algorithm (oracle/dgda_chunked.c) on the same workload, on
+                      the host cores;
   * ``decode``     -- BASELINE configs 2b-4: the B=64 DGDA decode microbench
-                      (10,000 steps), the DG-Indexer decode scoring + top-32 at
-                      1M context and the fused MABA-SA decode step at 1M context
-                      (us/step and HBM GB/s each).
+                      (10,000 steps), centroid pooling of the 1M cache, the
+                      DG-Indexer decode scoring + top-32 at 1M context and the
+                      fused MABA-SA decode step at 1M context (us/step and HBM
+                      GB/s each);
+  * ``rows``       -- the DGDA prefill with per-channel gates (the layer's gate
+                      layout) at the config-2 shape and the causal prefill
+                      index_topk.
+Each decode / rows entry carries its own ``cpu_baseline``: the oracle timed on
+the host on a bounded sample of that workload (the sample is named).
 
 ``python bench.py --gpus N --steps K --warmup W``; only N = 1 is supported.
 """
@@ -175,6 +181,94 @@ def cpu_baseline(B=4, H=10, T=32768, d=64, min_seconds=10.0):
             "sample": f"dgda_prefill config 2 shape B={B} H={H} T={T} d={d}, fp32, chunk 64, "
                       f"{reps} timed repeats in {dt:.1f} s after 2 warm-ups, oracle/dgda_chunked.c (OpenMP over b*h)",
             "host": {"cpu_model": cpu_model, "os_cpu_count": ncpu, "omp_num_threads": omp or None}}
+
+
+def _timed(fn, min_seconds: float):
+    """(repeats, seconds) of ``fn`` after one untimed call, repeated until ``min_seconds``."""
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            return reps, dt
+
+
+def cpu_row_baselines(min_seconds: float = 2.0):
+    """The oracle timed on host cores beside each secondary row, on bounded samples of the
+    same workloads (float64 numpy for the indexer and MABA-SA restatements, the C/OpenMP
+    restatement for the per-channel DGDA prefill).  numpy's matrix products may use the
+    BLAS threads of the host; the Python loops are single-threaded."""
+    import numpy as np
+    from oracle import dgda as odg, indexer as oix, sparse_attn as osa, dgda_c
+    out = {}
+    blas = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    r = np.random.default_rng(7)
+    # DGDA decode step, B=64 H=10 d=64, fp64 numpy (oracle/dgda.py::dgda_step)
+    B, H, d = 64, 10, 64
+    q = r.standard_normal((B, H, d)); k = r.standard_normal((B, H, d)); v = r.standard_normal((B, H, d))
+    la = -np.log1p(np.exp(r.standard_normal((B, H, 1)) + 2)) * np.ones((1, 1, d))
+    be = 1 / (1 + np.exp(-r.standard_normal((B, H, 1)))) * np.ones((1, 1, d))
+    S = np.zeros((B, H, d, d))
+    reps, dt = _timed(lambda: odg.dgda_step(q, k, v, b=be, w=be, state=S, log_alpha=la), min_seconds)
+    out["dgda_step_B64"] = {"value": dt / reps * 1e6, "unit": "us/step", "cores": blas, "kind": "port",
+                            "sample": f"the full B=64 step, {reps} repeats in {dt:.1f} s, oracle/dgda.py (numpy fp64)"}
+    # DG-Indexer decode at 1M context: B=8, 10 heads, 15,625 centroids, d=128, top-32
+    B, Hq, nb, dc = 8, 10, 15625, 128
+    qi = r.standard_normal((B, Hq, dc)); cent = r.standard_normal((B, nb, dc))
+
+    def idx_step():
+        oix.topk_desc(oix.decode_scores(qi, cent, 0.1), 32)
+
+    reps, dt = _timed(idx_step, min_seconds)
+    out["index_topk_decode_1M"] = {"value": dt / reps * 1e6, "unit": "us/step", "cores": blas, "kind": "port",
+                                   "sample": f"the full config-3 step, {reps} repeats in {dt:.1f} s, "
+                                             f"oracle/indexer.py decode_scores + topk_desc (numpy fp64)"}
+    # MABA-SA decode at 1M context, one batch element of config 4 (scaled by 8): latent
+    # queries as q with identity per-head projections, per-head top-32 index rows
+    Bs, L, H = 1, 1_000_000, 10
+    c = r.standard_normal((Bs, L, dc))          # fp64 already: the oracle's conversions are no-ops
+    means = c.reshape(Bs, L // 64, 64, dc).mean(axis=2)
+    eye = np.concatenate([np.eye(dc)] * H, axis=0)            # [H*dc, dc]: W_k,h = W_v,h = I
+    qs = r.standard_normal((Bs, H, dc)) * 0.1
+    idx = np.stack([np.stack([r.permutation(L // 64)[:32] for _ in range(H)]) for _ in range(Bs)])
+    gate = r.standard_normal((Bs, 3))
+    reps, dt = _timed(lambda: osa.maba_sa_decode(qs, c, eye, eye, idx, gate, means=means), min_seconds)
+    out["maba_sa_decode_1M"] = {"value": dt / reps * 1e6 * 8, "unit": "us/step", "cores": blas, "kind": "port",
+                                "sample": f"one of the 8 batch elements of config 4 (L=1M, H=10, d_c=128, per-head "
+                                          f"top-32 rows), {reps} repeats in {dt:.1f} s, times 8; "
+                                          f"oracle/sparse_attn.py maba_sa_decode (numpy fp64)"}
+    del c, means
+    # DGDA prefill with per-channel gates: B=1 H=10 T=1024 of the config-2 shape, C/OpenMP
+    dgda_c.build()
+    B, H, T, d = 1, 10, 1024, 64
+    q = r.standard_normal((B, H, T, d), dtype=np.float32); q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k = r.standard_normal((B, H, T, d), dtype=np.float32); k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = r.standard_normal((B, H, T, d), dtype=np.float32)
+    la = (-np.log1p(np.exp(r.standard_normal((B, H, T, d), dtype=np.float32) + 2))).astype(np.float32)
+    be = (1 / (1 + np.exp(-r.standard_normal((B, H, T, d), dtype=np.float32)))).astype(np.float32)
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or 64, B * H)
+    reps, dt = _timed(lambda: dgda_c.dgda_prefill_chunked_c(q, k, v, la, be, be, chunk_size=64, nthreads=threads),
+                      min_seconds)
+    out["dgda_prefill_per_channel_gates"] = {
+        "value": reps * B * T / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": f"B=1 H=10 T=1024 d=64 of the config-2 shape with per-channel fp32 gates, {reps} repeats in "
+                  f"{dt:.1f} s, oracle/dgda_chunked.c (OpenMP over b*h)"}
+    # causal prefill index_topk: 4,096 of the 32,768 queries against 512 centroids, d=128
+    Lq, nbp = 4096, 512
+    qp = r.standard_normal((1, Lq, dc)); cp = r.standard_normal((1, nbp, dc))
+
+    def pre_step():
+        sc = oix.prefill_scores(qp, cp, 0.5)
+        oix.topk_desc(sc, 32)
+
+    reps, dt = _timed(pre_step, min_seconds)
+    out["index_topk_prefill"] = {"value": reps * Lq / dt, "unit": "queries/s", "cores": blas, "kind": "port",
+                                 "sample": f"the first 4,096 of the 32,768 query rows (512 centroids, d=128, top-32), "
+                                           f"{reps} repeats in {dt:.1f} s, oracle/indexer.py prefill_scores + "
+                                           f"topk_desc (numpy fp64)"}
+    return out
 
 
 def decode_benches(dev, steps: int):
@@ -391,6 +485,13 @@ def main():
     if not args.only_prefill and not args.skip_cpu:
         log("timing the CPU baseline")
         res["cpu_baseline"] = cpu_baseline()
+        if not args.skip_decode:
+            log("timing the CPU baselines of the secondary rows")
+            rows_cpu = cpu_row_baselines()
+            for name, cb in rows_cpu.items():
+                for section in ("decode", "rows"):
+                    if name in res.get(section, {}):
+                        res[section][name]["cpu_baseline"] = cb
     else:
         res["cpu_baseline"] = None
     print(json.dumps(res), flush=True)
