@@ -55,6 +55,13 @@ class _Growing:
     def view(self) -> torch.Tensor:
         return self.buf[:, : self.n]
 
+    def view_with(self, row: torch.Tensor) -> torch.Tensor:
+        """The rows plus ``row [B, 1, d]`` in the next slot, without appending it: the
+        next ``append`` overwrites the slot.  No copy of the held rows."""
+        self.append(row)
+        self.n -= 1
+        return self.buf[:, : self.n + 1]
+
     @property
     def shape(self) -> torch.Size:
         return torch.Size([self.buf.shape[0], self.n, self.buf.shape[2]])
@@ -110,7 +117,9 @@ class DGIndexer(nn.Module):
             tail = dispatch_compute_centroids(self._keys.view()[:, n - rem:], block_size=bs)
             if self._cents is None or self._cents.n == 0:
                 return tail
-            return torch.cat([self._cents.view(), tail], dim=1)
+            # the zero-padded tail centroid joins the complete ones for this step only
+            # (indexer.py:75-81), written into the cache's next slot instead of a concatenation
+            return self._cents.view_with(tail)
         if past_centroids is not None:
             return torch.cat([past_centroids, dispatch_compute_centroids(ki, block_size=bs)], dim=1)
         c = dispatch_compute_centroids(ki, block_size=bs)
