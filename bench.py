@@ -263,6 +263,13 @@ def cpu_row_baselines(min_seconds: float = 2.0):
         sc = oix.prefill_scores(qp, cp, 0.5)
         oix.topk_desc(sc, 32)
 
+    # gate superposition: 4,096 of the 32,768 positions of [1,10,32768,64], fp64 numpy
+    o3 = [r.standard_normal((1, 10, 4096, 64)) for _ in range(3)]
+    gz = r.standard_normal((1, 4096, 3))
+    reps_s, dt_s = _timed(lambda: osa.superposition(o3[0], o3[1], o3[2], gate_logits=gz), min_seconds)
+    out["stream_superposition"] = {"value": dt_s / reps_s * 8 * 1e6, "unit": "us/call", "cores": 1, "kind": "port",
+                                   "sample": f"4,096 of the 32,768 positions, {reps_s} repeats in {dt_s:.1f} s, times 8; "
+                                             f"oracle/sparse_attn.py superposition (numpy fp64)"}
     reps, dt = _timed(pre_step, min_seconds)
     out["index_topk_prefill"] = {"value": reps * Lq / dt, "unit": "queries/s", "cores": blas, "kind": "port",
                                  "sample": f"the first 4,096 of the 32,768 query rows (512 centroids, d=128, top-32), "
@@ -412,7 +419,71 @@ def row_benches(dev):
     out["index_topk_prefill"] = {"ms_per_call": ms, "queries_per_s": Bq * L / (ms * 1e-3),
                                  "config": "B=1 L=32768 d=128 bf16, 512 centroids, top-32, causal"}
     log(f"index_topk prefill 32k x 512: {ms:.3f} ms")
+    del qi, cent
+    # gate superposition of three prefill stream outputs [1, 10, 32768, 64] bf16 with
+    # [1, 32768, 3] logits (the layer's prefill combine, sparse_attention.py:219)
+    Bs, Hs, Ls, Ds = 1, 10, 32768, 64
+    ol, os_, oh = (torch.randn(Bs, Hs, Ls, Ds, device=dev, dtype=torch.bfloat16) for _ in range(3))
+    gl = torch.randn(Bs, Ls, 3, device=dev, dtype=torch.bfloat16)
+
+    def superpose():
+        return hb.hip_stream_superposition(ol, os_, oh, gate_logits=gl)
+
+    ms, _ = time_op(superpose, 20, 3)
+    sb = 4 * Bs * Hs * Ls * Ds * 2 + Bs * Ls * 3 * 2
+    out["stream_superposition"] = {"us_per_call": ms * 1e3, "gbs": sb / (ms * 1e-3) / 1e9,
+                                   "hbm_frac": sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": sb,
+                                   "config": "o_* [1,10,32768,64] bf16, gate logits [1,32768,3] bf16"}
+    log(f"stream superposition 1x10x32768x64: {ms * 1e3:.1f} us")
+    del ol, os_, oh, gl
+    out["maba_sa_layer_decode_1M"] = layer_decode_bench(dev)
     return out
+
+
+def layer_decode_bench(dev, B=8, L0=1_000_000 - 10, steps=20):
+    """The MABA-SA layer's decode step (layers/sparse_attention.py:221-277 orchestration):
+    latent append, indexer (projections, key/centroid cache, decode top-32), the fused
+    streams and the head projections, eager, at a 1M-token context held in synthetic
+    caches (B=8, d_model 640, 10 heads of 64, d_c 128, d_idx 64, bf16)."""
+    import torch
+    from maba_sparse.kernels import hip_backend as hb
+    from maba_sparse.layers.sparse_attention import LatentCache, MabaSparseAttention
+    from maba_sparse.layers.indexer import _Growing
+    torch.manual_seed(11)
+    layer = MabaSparseAttention(dim=640, n_heads=10, d_head=64, d_c=128, window_size=128, block_size=64,
+                                top_k=32, hca_pool_size=64, dist_lambda=0.1, d_idx=64)
+    layer = layer.to(dev, torch.bfloat16).eval()
+    cap = L0 + steps + 16
+    cache = LatentCache(B, cap, 128, pool=64, device=dev, dtype=torch.bfloat16)
+    cache.c[:, :L0].normal_()
+    cache.n = L0
+    full = L0 // 64
+    cache.hca[:, :full] = hb.hip_hca_pool(cache.c[:, : full * 64], pool=64)
+    cache.nh = full
+    keys = torch.randn(B, L0, 64, device=dev, dtype=torch.bfloat16)
+    layer.indexer._keys = _Growing(keys)
+    layer.indexer._cents = _Growing(hb.hip_compute_centroids(keys[:, : full * 64], block_size=64))
+    del keys
+    x = torch.randn(B, 1, 640, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        for _ in range(3):
+            layer.decode_step(x, cache)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            layer.decode_step(x, cache)
+        e1.record()
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    nb = cache.n // 64
+    byts = B * (nb * 64 * 2 + nb * 128 * 2 + 32 * 64 * 128 * 2 + 132 * 128 * 2)   # centroids, HCA, sparse, local
+    log(f"MABA-SA layer decode step at 1M (eager): {us:.1f} us")
+    del cache, layer
+    return {"us_per_step": us, "gbs": byts / (us * 1e-6) / 1e9, "hbm_frac": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "algorithmic_bytes": byts, "steps": steps,
+            "config": "B=8, context ~1M (synthetic latent, key and centroid caches), d_model 640, 10 heads x 64, "
+                      "d_c 128, d_idx 64, one indexer query shared by the heads, top-32, bf16, eager"}
 
 
 def main():

@@ -155,6 +155,25 @@ def test_stream_superposition(dev, gate_dim, weights):
     assert_close(out, exp, 1e-5, 1e-5, "superposition")
 
 
+@pytest.mark.parametrize("case", ["bf16_vec", "bf16_odd_d", "strided_f32", "f16_generic", "bf16_4d_gate"])
+def test_stream_superposition_layouts(dev, case):
+    """The 16-byte vector kernel (contiguous bf16 / fp32, D a multiple of the vector) and
+    the generic one (strided views, other D, fp16) against the fp64 oracle."""
+    g = torch.Generator().manual_seed(len(case))
+    B, H, L, D = 2, 3, 37, (6 if case == "bf16_odd_d" else 64)
+    dt = {"strided_f32": torch.float32, "f16_generic": torch.float16}.get(case, torch.bfloat16)
+    ol, os_, oh = (torch.randn(B, H, L, D, generator=g).to(dt) for _ in range(3))
+    z = torch.randn(*((B, H, L, 3) if case == "bf16_4d_gate" else (B, L, 3)), generator=g)
+    args = [x.to(dev) for x in (ol, os_, oh)]
+    if case == "strided_f32":   # [B, L, H, D] storage seen as [B, H, L, D]
+        args = [x.transpose(1, 2).contiguous().transpose(1, 2) for x in args]
+    out = _hip().hip_stream_superposition(*args, gate_logits=z.to(dev))
+    exp = osa.superposition(to_np(ol.float()), to_np(os_.float()), to_np(oh.float()), gate_logits=to_np(z))
+    tol = 1e-5 if dt == torch.float32 else 1e-2
+    assert out.dtype == dt
+    assert_close(out.float(), exp, tol, tol, f"superposition {case}")
+
+
 def test_superposition_partition_of_unity(dev):
     x = torch.randn(2, 4, 64, 64, device=dev)
     out = _hip().hip_stream_superposition(x, x, x, gate_logits=torch.randn(2, 64, 3, device=dev))
