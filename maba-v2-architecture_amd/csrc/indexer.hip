@@ -114,10 +114,10 @@ __global__ __launch_bounds__(64) void index_decode_merge_kernel(const key64* ws,
 // index_decode_select_kernel -- one 1024-thread workgroup per (b, head).  The tile
 //   maxima are folded into 64 groups; tau = the K-th largest group maximum bounds
 //   the K-th largest key from below (K groups each hold a key >= tau), so the top
-//   K are among the keys >= tau: collect those (typically a few dozen), rank them
-//   by counting, write ranks < K.  If one wave's share of the row passes more than
-//   SEL_CAP / 16 keys (heavily tied scores), the workgroup falls back to wave
-//   top-k merges over the whole row.
+//   K are among the keys >= tau: collect those (typically a few dozen to a few
+//   hundred) into one list, rank them by counting, write ranks < K.  With more than
+//   SEL_CAP of them (heavily tied scores) the workgroup falls back to wave top-k
+//   merges over the whole row.
 typedef __attribute__((ext_vector_type(8))) short i16x8_t;
 constexpr int SEL_CAP = 1024;     // candidate slots of the select kernel
 constexpr int SEL_GROUPS = 64;    // tile maxima are folded into this many groups
@@ -240,12 +240,12 @@ __device__ __forceinline__ int lane_rank(unsigned long long m) {   // set bits o
 }
 
 __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a) {
-  __shared__ __attribute__((aligned(16))) key64 s_c[SEL_CAP + 8];   // candidates, one region per wave
-  __shared__ __attribute__((aligned(16))) key64 s_k[SEL_CAP + 8];   // the compacted candidate list
+  __shared__ __attribute__((aligned(16))) key64 s_c[SEL_T];          // the fallback's wave lists
+  __shared__ __attribute__((aligned(16))) key64 s_k[SEL_CAP + 8];   // the candidate list
   __shared__ __attribute__((aligned(16))) key64 s_g[SEL_GROUPS];
   __shared__ key64 s_part[SEL_T];
   __shared__ int s_rank[4][64];
-  __shared__ int s_wcnt[SEL_W];
+  __shared__ int s_cnt;
   __shared__ key64 s_tau;
   const int64_t row = blockIdx.x;  // b * Hq + h
   const int64_t bi = row / a.Hq;
@@ -264,6 +264,7 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
     v[j] = z;
   }
   if (tid < 64) s_k[tid] = KEY_NONE;   // list slots the final rank reads past cnt
+  if (tid == 0) s_cnt = 0;
   // tile maxima: thread t folds tiles t, t + SEL_T, ...; group j < 64 is the tiles
   // t = j (mod 64), i.e. lane j of every wave (any partition of the tiles gives a valid bound)
   key64 m = KEY_NONE;
@@ -297,14 +298,13 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   // Candidates: keys whose score is not below tau's score.  They include every key >= tau
   // (key order is score order first); the extra ones (equal score, larger index) rank
   // below all K keys >= tau and are never written.  With fewer groups than K
-  // (tau = KEY_NONE) every key n < nb is a candidate.  Each wave appends to its own
-  // region of SEL_CAP / SEL_W slots at a wave-uniform running offset: a vector no lane of the
-  // wave takes costs one max and one compare, an element no lane takes one compare.
+  // (tau = KEY_NONE) every key n < nb is a candidate.  A wave appends a batch of taken
+  // keys to the shared list at an offset reserved with one LDS atomic (the list order
+  // does not matter: ranking is by counting), so candidates clustered in one part of the
+  // row (the distance penalty favours the newest blocks) fill the list like spread ones.
+  // A vector no lane of the wave takes costs one max and one compare.
   const bool all = tau == KEY_NONE;
   const float tau_s = key_score(tau);
-  constexpr int WCAP = SEL_CAP / SEL_W;
-  key64* reg = s_c + wave * WCAP;
-  int run = 0;   // wave-uniform
   auto scan = [&](auto all_c) {
     constexpr bool ALL = decltype(all_c)::value;
     for (int64_t base = 0; base < a.nb; base += SEL_PASS) {
@@ -333,36 +333,20 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
           const bool t = ALL ? n < a.nb : !(x[i] < tau_s);
           const unsigned long long b = __ballot(t);
           if (b == 0ull) continue;
-          const int p = run + lane_rank(b);
-          if (t && p < WCAP) reg[p] = make_key(x[i], (uint32_t)n);
-          run += __builtin_popcountll(b);
+          int at = 0;
+          if (lane == 0) at = atomicAdd(&s_cnt, __builtin_popcountll(b));
+          at = __builtin_amdgcn_readfirstlane(at);
+          const int p = at + lane_rank(b);
+          if (t && p < SEL_CAP) s_k[p] = make_key(x[i], (uint32_t)n);
         }
       }
     }
   };
   if (all) scan(std::true_type{}); else scan(std::false_type{});
-  if (lane == 0) s_wcnt[wave] = run;
   __syncthreads();
-  // region counts: lane l < SEL_W holds wave l's; cnt and this wave's offset are sums
-  // over lanes, taken bit plane by bit plane (exact when every count is <= WCAP = 64,
-  // the only case that uses them)
-  const int cw = lane < SEL_W ? s_wcnt[lane] : 0;
-  int cnt = 0, off = 0;
-  const bool fits = __ballot(cw > WCAP) == 0ull;
-  {
-    static_assert(WCAP < 128, "seven bit planes");
-#pragma unroll
-    for (int b = 0; b < 7; ++b) {
-      const unsigned long long bits = __ballot((cw >> b) & 1);
-      cnt += __builtin_popcountll(bits) << b;
-      off += __builtin_popcountll(bits & ((1ull << wave) - 1ull)) << b;
-    }
-  }
+  const int cnt = s_cnt;
   int64_t* orow = a.out + bi * a.osb + h * a.osh;
-  if (fits && cnt >= a.ak) {
-    // compact the regions into s_k[0, cnt)
-    if (lane < run) s_k[off + lane] = reg[lane];
-    __syncthreads();
+  if (cnt <= SEL_CAP && cnt >= a.ak) {
     if (cnt <= 64) {  // rank across the four waves; slots past cnt hold KEY_NONE
       const key64 kj = s_k[lane];
       if (wave < 4) s_rank[wave][lane] = count_greater16(s_k + 16 * wave, kj);
@@ -383,11 +367,14 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
     }
     return;
   }
-  // fallback: each wave merges every SEL_W-th 64-key slice of the row, then wave 0
-  // merges the SEL_W lists
+  // fallback: each wave merges every SEL_W-th 64-key slice of the row, newest slice first
+  // (the distance penalty favours recent blocks, so the list fills with its best keys at
+  // once and older slices are rejected by the merge's K-th-key test), then wave 0 merges
+  // the SEL_W lists
   key64 list = KEY_NONE;
-  for (int64_t base = (int64_t)wave * 64; base < a.nb; base += 64 * SEL_W) {
-    const int64_t n = base + lane;
+  const int64_t nsl = (a.nb + 63) / 64;
+  for (int64_t sl = nsl - 1 - wave; sl >= 0; sl -= SEL_W) {
+    const int64_t n = sl * 64 + lane;
     const key64 key = n < a.nb ? make_key(sc[n], (uint32_t)n) : KEY_NONE;
     list = wave_merge_topk(list, key >= tau ? key : KEY_NONE, a.K);
   }

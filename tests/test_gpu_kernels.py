@@ -214,6 +214,21 @@ def test_index_topk_decode_ties(dev, nb, lam):
     assert torch.equal(idx.cpu(), exp.expand(2, 10, 32))
 
 
+def test_index_topk_decode_near_equal_centroids(dev):
+    """The DGDA layer's situation: centroids 0.5 (mean + max) of random keys are nearly
+    equal, so the distance penalty orders most of the row and the group-maximum bound
+    admits thousands of candidates (the merge fallback).  One query head, d = 64."""
+    g = torch.Generator().manual_seed(21)
+    B, Hq, nb, d = 4, 1, 15625, 64
+    keys = torch.randn(B, nb * 64 // 16, d, generator=g)        # a quarter-size key sample per block
+    c = (0.5 * (keys.view(B, nb, 4, d).mean(2) + keys.view(B, nb, 4, d).amax(2))).bfloat16()
+    q = torch.randn(B, Hq, d, generator=g).bfloat16()
+    idx, sc = _hip().hip_index_topk_decode(q.to(dev), c.to(dev), lambda_dist=0.1, top_k=32, return_scores=True)
+    ref = oidx.decode_scores(to_np(q), to_np(c), 0.1)
+    assert_close(sc, ref, 1e-5, 1e-4, "decode scores")
+    assert topk_agrees(idx.cpu().numpy(), ref, 32) >= B * Hq - 1
+
+
 def test_index_topk_decode_tied_plateau(dev):
     """300 planted blocks share the top score (positive queries, identical centroids),
     every other centroid is zero and lam = 0: the top 32 are the 32 lowest planted
