@@ -1,5 +1,5 @@
 // Device helpers shared by the DGDA prefill kernels (chunked MFMA path and the
-// per-channel token path): MFMA wrappers, bf16 hi/lo splitting, LDS operand reads,
+// per-channel sub-chunk path): MFMA wrappers, bf16 hi/lo splitting, LDS operand reads,
 // wave scans, the segment map S <- M S + N and the slot geometry of the sequence-
 // parallel passes.
 #pragma once

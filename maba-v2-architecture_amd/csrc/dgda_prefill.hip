@@ -10,8 +10,9 @@
 //
 //  * the chunked MFMA path (dgda_chunk.hip) for the per-token (scalar) decay
 //    case with dk = dv = 64 and bf16 q/k/v -- the BASELINE configuration;
-//  * the sequence-parallel token path (dgda_tok.hip) for per-channel gates (the
-//    DGDA layer's layout) with dk = dv = 64 and bf16 or fp32 q/k/v.
+//  * the sub-chunk path (dgda_sub.hip) for per-channel gates (the DGDA layer's
+//    layout) with dk = dv = 64 and bf16 or fp32 q/k/v: 16-token sub-chunks with exact
+//    per-channel decay, the state products on MFMA, sequence-parallel like the above.
 #include "maba_common.h"
 
 namespace maba {
@@ -113,16 +114,15 @@ int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_ten
                       const maba_tensor* gate, int use_log, const maba_tensor* b,
                       const maba_tensor* w, const maba_tensor* s0, maba_tensor* out,
                       maba_tensor* sf, void* ws, size_t ws_bytes, hipStream_t stream);
-// Sequence-parallel token path (dgda_tok.hip).
-bool dgda_tok_supported(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
+// Sub-chunk path for per-channel gates (dgda_sub.hip).
+bool dgda_sub_supported(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                         const maba_tensor* gate, const maba_tensor* b, const maba_tensor* w,
                         const maba_tensor* out);
-size_t dgda_tok_workspace(int64_t BH, int64_t L);
-int launch_dgda_tok(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
+size_t dgda_sub_workspace(int64_t BH, int64_t L);
+int launch_dgda_sub(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                     const maba_tensor* gate, int use_log, const maba_tensor* b,
                     const maba_tensor* w, const maba_tensor* s0, maba_tensor* out,
                     maba_tensor* sf, void* ws, size_t ws_bytes, hipStream_t stream);
-
 }  // namespace maba
 
 using namespace maba;
@@ -133,8 +133,8 @@ extern "C" size_t maba_hip_dgda_prefill_workspace_size(const maba_tensor* q, con
   if (dgda_chunk_supported(q, q, v, gate, b)) return dgda_chunk_workspace(q->shape[0] * q->shape[1], q->shape[2]);
   // the write gate and output layouts are checked again at the call; the size depends
   // only on the shape
-  if (dgda_tok_supported(q, q, v, gate, b, nullptr, nullptr))
-    return dgda_tok_workspace(q->shape[0] * q->shape[1], q->shape[2]);
+  if (dgda_sub_supported(q, q, v, gate, b, nullptr, nullptr))
+    return dgda_sub_workspace(q->shape[0] * q->shape[1], q->shape[2]);
   return 0;
 }
 
@@ -175,11 +175,11 @@ extern "C" int maba_hip_dgda_prefill(const maba_tensor* q, const maba_tensor* k,
     return launch_dgda_chunk(q, k, v, gate, log_alpha != nullptr, b, w, initial_state, out, final_state,
                              workspace, workspace_bytes, s);
   }
-  if (dgda_tok_supported(q, k, v, gate, b, w, out)) {
-    const size_t need = dgda_tok_workspace(B * H, L);
+  if (dgda_sub_supported(q, k, v, gate, b, w, out)) {
+    const size_t need = dgda_sub_workspace(B * H, L);
     if (!workspace || workspace_bytes < need)
       return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace of %zu bytes required", need);
-    return launch_dgda_tok(q, k, v, gate, log_alpha != nullptr, b, w, initial_state, out, final_state,
+    return launch_dgda_sub(q, k, v, gate, log_alpha != nullptr, b, w, initial_state, out, final_state,
                            workspace, workspace_bytes, s);
   }
   return launch_dgda_seq(q, k, v, gate, log_alpha != nullptr, b, w, initial_state, out, final_state, s);

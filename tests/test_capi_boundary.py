@@ -110,10 +110,10 @@ def test_prefill_workspace_size_at_baseline_shape(lib):
     short = _t([B, H, 1024, d])                               # 16 chunks: one slot per head, no workspace
     sgate = _t([B, H, 1024, d], N.MABA_F32, strides=[H * 1024, 1024, 1, 0])
     assert lib.maba_hip_dgda_prefill_workspace_size(short, short, sgate, sgate) == 16
-    # per-channel gates: the token path, slots of U staging chunks of 32 tokens (80 at this shape)
+    # per-channel gates: the sub-chunk path, slots of U sub-chunks of 16 tokens (160 at this shape)
     per_channel = _t([B, H, T, d], N.MABA_F32)
-    U, nseg = _slot_geometry(B * H, T // 32, min_u=32)
-    assert (U, nseg) == (80, 14)
+    U, nseg = _slot_geometry(B * H, T // 16, min_u=64)
+    assert (U, nseg) == (160, 14)
     assert lib.maba_hip_dgda_prefill_workspace_size(q, q, per_channel, gate) == B * H * nseg * (64 * 128 * 4 + 4)
     # other head sizes take the sequential kernel, which needs no workspace
     q32 = _t([B, H, T, 32])

@@ -35,7 +35,7 @@ def test_chunk_path_is_selected(dev):
     n = lib.maba_hip_dgda_prefill_workspace_size(N.desc(inp["q"]), N.desc(inp["v"]), N.desc(inp["log_alpha"]),
                                                  N.desc(inp["b"]))
     assert n > 16          # multi-segment chunked path needs aggregate workspace
-    inp["b"] = inp["b"].contiguous()   # per-channel erase gate -> token path, also segmented
+    inp["b"] = inp["b"].contiguous()   # per-channel erase gate -> sub-chunk path, also segmented
     n2 = lib.maba_hip_dgda_prefill_workspace_size(N.desc(inp["q"]), N.desc(inp["v"]), N.desc(inp["log_alpha"]),
                                                   N.desc(inp["b"]))
     assert n2 > 16
@@ -170,14 +170,16 @@ def test_chunk_wide_slots_vs_c_oracle(dev):
     assert_close(S[:, heads], eS, 2e-3, 2e-3, "state")
 
 
-# ----------------------------------------------------------------------------- token path
-# Per-channel gates (the DGDA layer's layout) take the sequence-parallel token path:
-# exact token recurrence, segments chained through aggregate and fix-up passes.
+# ----------------------------------------------------------------------------- per-channel gates
+# Per-channel gates (the DGDA layer's layout) take the sub-chunk path: 16-token
+# sub-chunks with exact per-channel decay (pair-by-pair exponentials when a sub-chunk's
+# decay range is too wide for the MFMA factorisation), segments chained through
+# aggregate and fix-up passes.
 
 @pytest.mark.parametrize("qkv", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("decay", ["baseline", "slow", "none"])
 @pytest.mark.parametrize("L", [1, 31, 33, 1000, 4100])
-def test_token_path_per_channel_gates(dev, qkv, decay, L):
+def test_subchunk_path_per_channel_gates(dev, qkv, decay, L):
     inp = dgda_inputs(2, 3, L, seed=L + 7, decay=decay, gates="channel", qkv_dtype=qkv, device=dev,
                       with_state=(L % 2 == 1))
     o, S = _run(inp)
@@ -186,10 +188,10 @@ def test_token_path_per_channel_gates(dev, qkv, decay, L):
     assert_close(S, eS, 2e-3, 2e-3, f"state L={L} {decay} {qkv}")
 
 
-def test_token_path_alpha_strong_decay_and_bf16_output(dev):
-    """alpha instead of log_alpha, per-channel decays down to e^-30 per token, bf16 output:
-    the token recurrence has no chunk algebra to overflow, and bf16 outputs round the
-    fp32 results."""
+def test_subchunk_path_alpha_strong_decay_and_bf16_output(dev):
+    """alpha instead of log_alpha, per-channel decays down to e^-30 per token (sub-chunks
+    whose decay range exceeds the MFMA factorisation take the exact pair-by-pair form),
+    bf16 output: bf16 outputs round the fp32 results."""
     L = 3000
     inp = dgda_inputs(1, 4, L, seed=31, gates="channel", device=dev, with_state=True)
     la = inp.pop("log_alpha")
@@ -203,7 +205,7 @@ def test_token_path_alpha_strong_decay_and_bf16_output(dev):
     assert torch.equal(o16, o32.to(torch.bfloat16))
 
 
-def test_token_path_growing_gates_never_vanish(dev):
+def test_subchunk_path_growing_gates_never_vanish(dev):
     """log_alpha > 0 on some channels: the segment transitions never vanish, so every
     segment after the first runs in the fix-up pass from a scanned start state."""
     L = 6000
@@ -217,7 +219,7 @@ def test_token_path_growing_gates_never_vanish(dev):
     assert_close(S, eS, 2e-3, 2e-3, "state")
 
 
-def test_token_path_config2_shape_split_chaining(dev):
+def test_subchunk_path_config2_shape_split_chaining(dev):
     """Config-2 shape with per-channel gates (B=4, H=10, T=32768): prefill(T) equals
     prefill(T/2) chained into prefill(T/2, initial_state), and two heads match the
     token-loop oracle over the first 4096 tokens."""
