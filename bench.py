@@ -255,6 +255,15 @@ def cpu_row_baselines(min_seconds: float = 2.0):
         "value": reps * B * T / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
         "sample": f"B=1 H=10 T=1024 d=64 of the config-2 shape with per-channel fp32 gates, {reps} repeats in "
                   f"{dt:.1f} s, oracle/dgda_chunked.c (OpenMP over b*h)"}
+    # DGDA layer prologue: B=1, 512 of the 32,768 tokens, C=640, fp64 numpy (oracle/dgda.py::layer_prologue)
+    Tp, Cp = 512, 640
+    xs = [r.standard_normal((1, Tp, Cp)) for _ in range(6)]
+    wsp = [r.standard_normal((Cp, 4)) * 0.3 for _ in range(3)]
+    reps, dt = _timed(lambda: odg.layer_prologue(*xs, *wsp, n_heads=10), min_seconds)
+    out["dgda_layer_prologue"] = {"value": dt / reps * 1e6 * (4 * 32768 / Tp), "unit": "us/call", "cores": blas,
+                                  "kind": "port",
+                                  "sample": f"B=1, 512 of the 32,768 tokens (C=640), {reps} repeats in {dt:.1f} s, "
+                                            f"scaled by 256 to the B=4 call; oracle/dgda.py layer_prologue (numpy fp64)"}
     # causal prefill index_topk: 4,096 of the 32,768 queries against 512 centroids, d=128
     Lq, nbp = 4096, 512
     qp = r.standard_normal((1, Lq, dc)); cp = r.standard_normal((1, nbp, dc))
@@ -407,6 +416,7 @@ def row_benches(dev):
         "config": "B=4 H=10 T=32768 d=64, bf16 q/k/v, fp32 [B,H,T,64] decay/erase/write gates, bf16 out"}
     log(f"dgda_prefill per-channel gates: {ms:.3f} ms/step")
     del q, k, v, la, beta, wg
+    out.update(prologue_benches(dev))
     # causal prefill index_topk: one sequence of 32,768 queries over 512 block centroids
     Bq, L, di, K = 1, 32768, 128, 32
     qi = torch.randn(Bq, L, di, device=dev, dtype=torch.bfloat16)
@@ -437,6 +447,53 @@ def row_benches(dev):
     log(f"stream superposition 1x10x32768x64: {ms * 1e3:.1f} us")
     del ol, os_, oh, gl
     out["maba_sa_layer_decode_1M"] = layer_decode_bench(dev)
+    return out
+
+
+def prologue_benches(dev, B=4, T=32768, dim=640, H=10):
+    """The DGDA layer's prologue at the config-2 layer shape (bf16 projections -> bf16
+    q/k/v and fp32 gates, the layer's HIP path), the same math as torch reference ops on
+    the GPU, and the whole bf16 layer forward that uses it."""
+    import torch
+    from maba_sparse.kernels import common as C
+    from maba_sparse.kernels import hip_backend as hb
+    from maba_sparse.layers import DGDALayer
+    out = {}
+    Cc = 64 * H
+    g = torch.Generator(device=dev).manual_seed(11)
+    projs = torch.randn(B, T, 6 * Cc, device=dev, generator=g, dtype=torch.bfloat16).split(Cc, dim=-1)
+    ws = [torch.randn(Cc, 1, 4, device=dev, generator=g) * 0.3 for _ in range(3)]
+    hist = [torch.randn(B, Cc, 3, device=dev, generator=g, dtype=torch.bfloat16) for _ in range(3)]
+
+    def fused():
+        return hb.hip_dgda_prologue(projs, ws, hist, n_heads=H, gate_dtype=torch.float32, with_alpha=False)[0]
+
+    def torch_ref():
+        return C.ref_dgda_prologue(projs, ws, hist, n_heads=H, gate_dtype=torch.float32, with_alpha=False)[0]
+
+    ms, _ = time_op(fused, 10, 2)
+    ms_t, _ = time_op(torch_ref, 5, 1)
+    nbytes = B * T * (6 * Cc * 2 + 3 * Cc * 2 + 3 * Cc * 4)
+    out["dgda_layer_prologue"] = {
+        "us_per_call": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "algorithmic_bytes": nbytes, "torch_reference_ops_us": ms_t * 1e3,
+        "config": "B=4 T=32768 C=640 (10 heads x 64): six bf16 projections in, bf16 q/k/v + fp32 log_alpha/b/w out, "
+                  "conv history carried"}
+    log(f"dgda layer prologue: {ms * 1e3:.1f} us (torch reference ops {ms_t * 1e3:.1f} us)")
+    del projs, ws, hist
+    layer = DGDALayer(dim=dim, n_heads=H).to(dev, torch.bfloat16).eval()
+    x = torch.randn(B, T, dim, device=dev, generator=g, dtype=torch.bfloat16)
+
+    def fwd():
+        with torch.no_grad():
+            return layer(x)[0]
+
+    ms, _ = time_op(fwd, 5, 1)
+    out["dgda_layer_forward"] = {
+        "ms_per_call": ms, "tokens_per_s": B * T / (ms * 1e-3),
+        "config": "DGDALayer(dim=640, 10 heads) bf16, x [4, 32768, 640], no_grad: one 640x3840 projection GEMM, "
+                  "the HIP prologue, the per-channel-gate DGDA prefill, o_proj"}
+    log(f"dgda layer forward (bf16, B=4, T=32768): {ms:.3f} ms")
     return out
 
 

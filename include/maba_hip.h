@@ -29,6 +29,10 @@
  *                                   (local + sparse + HCA decode streams and the
  *                                   gate superposition; inline torch code in the
  *                                   reference, no dispatcher op)
+ *   maba_hip_dgda_prologue          layers/dgda.py:103-121,186-207 (the DGDA
+ *                                   layer's conv + SiLU with carried history,
+ *                                   gate activations and key normalisation;
+ *                                   inline torch code in the reference)
  */
 #ifndef MABA_HIP_H
 #define MABA_HIP_H
@@ -146,6 +150,21 @@ int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tensor* c_kv,
                             const maba_tensor* gate, int64_t L, float scale, int window,
                             int n_sink, int block_size, int pool, maba_tensor* out_lat,
                             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * DGDA layer prologue.  xs[0..5]: the q, k, v, alpha, erase and write projections
+ * [B,L,C] (C = 64*H, H <= 16; f32 or bf16, one dtype, unit channel stride).
+ * conv_w[0..2]: depthwise kernels [C,1,4] of q, k, v.  hist: NULL (zeros) or three
+ * [B,C,3] carried conv inputs, oldest first.  Outputs ys[0..6] [B,L,C]:
+ *   q = silu(conv_q([hist, x_q])), k = silu(conv_k(...)) / (||.||_head + eps),
+ *   v = silu(conv_v(...))                        (f32 or bf16, one dtype)
+ *   log_alpha = max(-softplus(x_alpha), -14), alpha = exp(log_alpha) (ys[4] may be
+ *   NULL), b = sigmoid(x_erase), w = sigmoid(x_write)    (f32 or bf16, one dtype)
+ * new_hist[0..2] [B,C,3]: the last three conv inputs of q, k, v; must not alias hist.
+ */
+int maba_hip_dgda_prologue(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
+                           const maba_tensor* const* hist, float eps, maba_tensor* const* ys,
+                           maba_tensor* const* new_hist, void* stream);
 
 #ifdef __cplusplus
 }

@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "maba_hip_hca_pool",
     "maba_hip_maba_sa_decode_workspace_size",
     "maba_hip_maba_sa_decode",
+    "maba_hip_dgda_prologue",
 )
 
 
@@ -68,6 +69,7 @@ _lock = threading.Lock()
 
 def _declare(lib) -> None:
     T = ctypes.POINTER(MabaTensor)
+    TA = ctypes.POINTER(T)   # array of descriptor pointers
     vp, i, f, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_size_t
     sig = {
         "maba_hip_last_error": ([], ctypes.c_char_p),
@@ -83,6 +85,7 @@ def _declare(lib) -> None:
         "maba_hip_hca_pool": ([T, T, i, vp], i),
         "maba_hip_maba_sa_decode_workspace_size": ([i64, i64, i64, i64, i64, i, i, i], sz),
         "maba_hip_maba_sa_decode": ([T, T, T, T, T, i64, f, i, i, i, i, T, vp, sz, vp], i),
+        "maba_hip_dgda_prologue": ([TA, TA, TA, f, TA, TA, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -132,6 +135,12 @@ def desc(t: Optional[torch.Tensor]):
         d.shape[k] = t.shape[k] if k < t.dim() else 1
         d.stride[k] = t.stride(k) if k < t.dim() else 0
     return ctypes.pointer(d)
+
+
+def desc_array(tensors: Sequence[Optional[torch.Tensor]]):
+    """A C array of descriptor pointers (``const maba_tensor* const*``); None entries are NULL."""
+    T = ctypes.POINTER(MabaTensor)
+    return (T * len(tensors))(*[desc(t) if t is not None else T() for t in tensors])
 
 
 def stream_ptr(device: torch.device) -> int:

@@ -345,6 +345,37 @@ def ref_maba_sa_decode(q_lat, c_kv, hca, idx, gate, L: int, scale: float, window
     return g[..., 0:1] * z_loc + g[..., 1:2] * z_sp + g[..., 2:3] * z_hca
 
 
+def ref_dgda_prologue(projections, conv_weights, history=None, n_heads: int = 10, eps: float = 1e-6,
+                      gate_dtype: Optional[torch.dtype] = None, with_alpha: bool = True, **kwargs: Any):
+    """DGDA layer prologue (reference layers/dgda.py:103-121, 186-207) in torch.
+
+    ``projections`` = (x_q, x_k, x_v, x_alpha, x_erase, x_write), each ``[B, L, C]``;
+    ``conv_weights`` = three depthwise ``[C, 1, K]`` kernels; ``history`` = three
+    ``[B, C, K-1]`` carried conv inputs or None.  Returns ``(q, k, v, log_alpha, alpha,
+    b, w, (hq, hk, hv))`` with q/k/v ``[B, L, C]`` in the projections' dtype and the gates in
+    ``gate_dtype`` (default: that dtype); k is normalised per ``C // n_heads``-channel head.
+    """
+    xq, xk, xv, xa, xb, xw = projections
+    B, L, C = xq.shape
+    dt = xq.dtype
+    outs, hists = [], []
+    for i, (x, wgt) in enumerate(zip((xq, xk, xv), conv_weights)):
+        kh = wgt.shape[-1] - 1
+        xt = x.transpose(1, 2)
+        hist = None if history is None else history[i]
+        seq = F.pad(xt, (kh, 0)) if hist is None else torch.cat([hist.to(dt), xt], dim=2)
+        hists.append(seq[..., seq.shape[-1] - kh:].contiguous())
+        outs.append(F.silu(F.conv1d(seq, wgt.to(dt), groups=C)).transpose(1, 2))
+    q, k, v = outs
+    dk = C // n_heads
+    kh_ = k.reshape(B, L, n_heads, dk)
+    k = (kh_ / (torch.linalg.vector_norm(kh_, dim=-1, keepdim=True) + eps)).reshape(B, L, C)
+    gdt = gate_dtype or dt
+    la = torch.clamp(-F.softplus(xa), min=-14.0)
+    alpha = torch.exp(la).to(gdt) if with_alpha else None
+    return (q, k, v, la.to(gdt), alpha, torch.sigmoid(xb).to(gdt), torch.sigmoid(xw).to(gdt), tuple(hists))
+
+
 reference_dgda_prefill = ref_dgda_prefill
 reference_dgda_step = ref_dgda_step
 reference_dgda_sequential = ref_dgda_sequential

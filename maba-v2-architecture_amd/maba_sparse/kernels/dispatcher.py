@@ -15,10 +15,11 @@ Differences, all deliberate:
   the reference's tests require.
 * A missing HIP library is never papered over: ``HipLibraryMissing`` propagates
   instead of falling back, so a GPU run cannot silently take a non-HIP path.
-* Three ops the reference only has as inline torch code get dispatcher entries:
+* Four ops the reference only has as inline torch code get dispatcher entries:
   ``index_topk_decode`` (layers/indexer.py:101-112), ``hca_pool``
-  (layers/sparse_attention.py:206) and ``maba_sa_decode``
-  (layers/sparse_attention.py:79-219,263-275).
+  (layers/sparse_attention.py:206), ``maba_sa_decode``
+  (layers/sparse_attention.py:79-219,263-275) and ``dgda_prologue`` (the DGDA
+  layer's conv, gates and key normalisation, layers/dgda.py:103-121,186-207).
 * ``allow_mixed_dtypes=True`` (keyword) lets ``dgda_prefill``/``dgda_step``
   accept bf16 q/k/v with fp32 gates and state; without it the reference's
   "dtypes must match" ``TypeError`` is kept.
@@ -47,6 +48,7 @@ _KERNEL_REGISTRY: Dict[str, Dict[str, Callable]] = {
         "index_topk_decode": _c.ref_index_topk_decode,
         "hca_pool": _c.ref_hca_pool,
         "maba_sa_decode": _c.ref_maba_sa_decode,
+        "dgda_prologue": _c.ref_dgda_prologue,
     },
     # CPU tensors run the same torch code; no separate CPU kernels are built here.
     "cpu": {
@@ -58,6 +60,7 @@ _KERNEL_REGISTRY: Dict[str, Dict[str, Callable]] = {
         "index_topk_decode": _c.ref_index_topk_decode,
         "hca_pool": _c.ref_hca_pool,
         "maba_sa_decode": _c.ref_maba_sa_decode,
+        "dgda_prologue": _c.ref_dgda_prologue,
     },
     "hip": {},
     "xla": {},
@@ -303,6 +306,25 @@ def dispatch_maba_sa_decode(q_lat, c_kv, hca, idx, gate, L: int, scale: float, w
                                                      block_size=block_size, pool=pool, **kwargs))
 
 
+def dispatch_dgda_prologue(projections, conv_weights, history=None, n_heads: int = 10, eps: float = 1e-6,
+                           gate_dtype: Optional[torch.dtype] = None, with_alpha: bool = True, **kwargs: Any):
+    """The DGDA layer's op inputs from its six projections (see ``common.ref_dgda_prologue``)."""
+    if len(projections) != 6 or len(conv_weights) != 3 or (history is not None and len(history) != 3):
+        raise ValueError("dgda_prologue takes six projections, three conv weights and three histories or None")
+    dev = projections[0].device
+    for t in (*projections, *conv_weights, *(history or ())):
+        if t.device != dev:
+            raise RuntimeError(f"Expected all tensors to be on the same device, but got {dev} and {t.device}")
+    shape = projections[0].shape
+    if len(shape) != 3 or any(p.shape != shape for p in projections):
+        raise ValueError(f"projections must share one [B, L, C] shape, got {[list(p.shape) for p in projections]}")
+    if shape[2] % n_heads != 0:
+        raise ValueError(f"C={shape[2]} is not a multiple of n_heads={n_heads}")
+    return _run("dgda_prologue", dev, dict(projections=projections, conv_weights=conv_weights, history=history,
+                                           n_heads=n_heads, eps=eps, gate_dtype=gate_dtype, with_alpha=with_alpha,
+                                           **kwargs))
+
+
 dgda_prefill = dispatch_dgda_prefill
 dgda_step = dispatch_dgda_step
 compute_centroids = dispatch_compute_centroids
@@ -311,6 +333,7 @@ stream_superposition = dispatch_stream_superposition
 index_topk_decode = dispatch_index_topk_decode
 hca_pool = dispatch_hca_pool
 maba_sa_decode = dispatch_maba_sa_decode
+dgda_prologue = dispatch_dgda_prologue
 ref_dgda_prefill = _c.ref_dgda_prefill
 ref_dgda_step = _c.ref_dgda_step
 ref_centroids = _c.ref_centroids

@@ -234,3 +234,32 @@ def hip_maba_sa_decode(q_lat, c_kv, hca, idx, gate, L: int, scale: float, window
                                      N.desc(out), ws.data_ptr(), ws.numel(), N.stream_ptr(dev))
     N.check(rc, "maba_sa_decode")
     return out
+
+
+@register_kernel("hip", "dgda_prologue")
+def hip_dgda_prologue(projections, conv_weights, history=None, n_heads: int = 10, eps: float = 1e-6,
+                      gate_dtype: Optional[torch.dtype] = None, with_alpha: bool = True, **kwargs: Any):
+    """DGDA layer prologue in one pass (layers/dgda.py:103-121, 186-207): causal depthwise
+    conv (kernel 4) + SiLU of q/k/v with the carried history, per-head L2 norm of k, and
+    the gate activations.  Same returns as ``common.ref_dgda_prologue``."""
+    _no_grad_needed("dgda_prologue", *projections, *conv_weights, *(history or ()))
+    dev = N.require_device([*projections, *conv_weights, *(history or ())], "dgda_prologue")
+    B, L, C = projections[0].shape
+    if C != 64 * n_heads or conv_weights[0].shape[-1] != 4:
+        raise NotImplementedError("dgda_prologue: 64-channel heads and kernel 4 only")
+    dt = projections[0].dtype
+    gdt = gate_dtype or dt
+    new = lambda d: torch.empty(B, L, C, dtype=d, device=dev)  # noqa: E731
+    ys = [new(dt), new(dt), new(dt), new(gdt), new(gdt) if with_alpha else None, new(gdt), new(gdt)]
+    hdt = history[0].dtype if history is not None else dt
+    nh = [torch.empty(B, C, 3, dtype=hdt, device=dev) for _ in range(3)]
+    if L == 0:
+        for h, old in zip(nh, history or (None,) * 3):
+            h.copy_(old) if old is not None else h.zero_()
+        return (*ys, tuple(nh))
+    arr = lambda ts: N.desc_array(ts)  # noqa: E731
+    rc = N.load().maba_hip_dgda_prologue(arr(projections), arr(conv_weights),
+                                         arr(history) if history is not None else None, float(eps), arr(ys),
+                                         arr(nh), N.stream_ptr(dev))
+    N.check(rc, "dgda_prologue")
+    return (*ys, tuple(nh))

@@ -24,7 +24,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from maba_sparse.kernels.dispatcher import dispatch_dgda_prefill, dispatch_dgda_step
+from maba_sparse.kernels.dispatcher import (dispatch_dgda_prefill, dispatch_dgda_prologue, dispatch_dgda_step,
+                                            get_backend)
 
 
 class ConvState(tuple):
@@ -127,11 +128,52 @@ class DGDALayer(nn.Module):
         raise ValueError(f"Unsupported conv_state shape or type: {type(cs)}")
 
     # ---------------------------------------------------------------- inputs
+    def _prologue_fusable(self, x: torch.Tensor) -> bool:
+        """Whether the one-pass HIP prologue takes this call: the ``hip`` backend, the
+        model's head shape (64-channel heads, kernel 4), f32/bf16 and no gradients."""
+        if x.device.type != "cuda" or get_backend(x.device) != "hip":
+            return False
+        if self.kernel_size != 4 or self.d_k != 64 or self.d_v != 64 or self.n_heads > 16:
+            return False
+        if x.dtype not in (torch.float32, torch.bfloat16):
+            return False
+        return not (torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())))
+
+    def _fused_op_inputs(self, x: torch.Tensor, state, hists):
+        """One GEMM for the six projections, then the HIP prologue (conv + SiLU, gates, key
+        norm) in one pass.  Gates come out in fp32 (the chunked kernels' gate format, more
+        precise than the reference's cast to the module dtype), so the op is called with
+        ``allow_mixed_dtypes``."""
+        B, L, _ = x.shape
+        H, dk = self.n_heads, self.d_k
+        C = H * dk
+        W = torch.cat([m.weight for m in (self.q_proj, self.k_proj, self.v_proj, self.gate_alpha,
+                                          self.gate_erase, self.gate_write)], dim=0)
+        projs = F.linear(x, W.to(x.dtype)).split(C, dim=-1)   # [B, L, C] views, row stride 6C
+        kh = self.kernel_size - 1
+        hist = None
+        if hists[0] is not None:
+            fit = lambda h: F.pad(h, (kh - h.shape[-1], 0)) if h.shape[-1] < kh else h[..., h.shape[-1] - kh:]  # noqa: E731
+            hist = tuple(fit(h) for h in hists)
+        q, k, v, la, _, b, w, nh = dispatch_dgda_prologue(
+            projs, (self.conv_q.weight, self.conv_k.weight, self.conv_v.weight), hist, n_heads=H, eps=self.eps,
+            gate_dtype=torch.float32, with_alpha=False)
+        heads = lambda t: t.view(B, L, H, dk).transpose(1, 2)  # noqa: E731
+        # the op takes log_alpha when both decay forms are given (common.py:242-243 computes
+        # alpha = exp(log_alpha) when only log_alpha is given), so alpha is not materialised
+        args = dict(q=heads(q), k=heads(k), v=heads(v), alpha=None, b=heads(b), w=heads(w),
+                    log_alpha=heads(la), allow_mixed_dtypes=True)
+        if state is not None:
+            state = state.to(x.dtype)
+        return args, state, ConvState(nh)
+
     def _op_inputs(self, x: torch.Tensor, state, conv_state):
         """Projections, convs, gates and head-major views -- the op's keyword arguments."""
         B, L, _ = x.shape
         H, dk, dv = self.n_heads, self.d_k, self.d_v
         hq, hk, hv = self._split_conv_state(conv_state, B, x.device, x.dtype)
+        if self._prologue_fusable(x):
+            return self._fused_op_inputs(x, state, (hq, hk, hv))
         q, nq = self._conv_silu(self.q_proj(x), self.conv_q, hq)
         k, nk = self._conv_silu(self.k_proj(x), self.conv_k, hk)
         v, nv = self._conv_silu(self.v_proj(x), self.conv_v, hv)

@@ -31,6 +31,15 @@ Functions
                          independence, test_dgda.py:122-137) and the
                          all-ones analytic inverse (test_dgda_precision.py:
                          102-129).
+``layer_prologue``       the DGDA layer's op inputs from its projections
+                         (layers/dgda.py:103-121 conv + SiLU with carried
+                         history, :193-197 gates, :207 key norm), float64
+                         loops.  Pinned by: identity and pure-shift conv
+                         kernels (the conv reduces to SiLU of the input, or of
+                         the input three tokens back through the history),
+                         softplus/sigmoid closed forms at 0 and the -14 clamp,
+                         unit-norm keys, and prefill-then-continue equal to one
+                         pass (the history carry).
 """
 from __future__ import annotations
 
@@ -181,3 +190,38 @@ def dgda_prefill_dense(q, k, v, alpha=None, b=None, w=None, initial_state=None,
                 o[bi, hi, t] = (q[bi, hi, t].reshape(1, dk) @ S).ravel()
             Sf[bi, hi] = S
     return o, Sf
+
+
+def layer_prologue(xq, xk, xv, xa, xb, xw, wq, wk, wv, hist=None, n_heads=10, eps=1e-6):
+    """DGDA layer prologue in float64 (reference layers/dgda.py:103-121, 186-207).
+
+    x* : [B, L, C] projections; w* : [C, K] depthwise conv taps (cross-correlation, as
+    torch's conv1d: y_t = sum_j w[j] p[t + j] over p = [history, x]); hist: None or
+    three [B, C, K-1] carried inputs, oldest first.  Returns q, k, v, log_alpha, alpha,
+    b, w ([B, L, C]) and the three new histories [B, C, K-1]."""
+    def silu(z):
+        return z / (1.0 + np.exp(-z))
+
+    outs, hists = [], []
+    for i, (x, w) in enumerate(((xq, wq), (xk, wk), (xv, wv))):
+        x = np.asarray(x, np.float64)
+        w = np.asarray(w, np.float64)
+        B, L, C = x.shape
+        K = w.shape[1]
+        h = np.zeros((B, C, K - 1)) if hist is None else np.asarray(hist[i], np.float64)
+        p = np.concatenate([h, x.transpose(0, 2, 1)], axis=2)          # [B, C, K-1+L]
+        y = np.zeros((B, L, C))
+        for t in range(L):
+            for j in range(K):
+                y[:, t, :] += w[None, :, j] * p[:, :, t + j]
+        outs.append(silu(y))
+        hists.append(p[:, :, p.shape[2] - (K - 1):].copy())
+    q, k, v = outs
+    B, L, C = q.shape
+    kh = k.reshape(B, L, n_heads, C // n_heads)
+    k = (kh / (np.sqrt((kh * kh).sum(-1, keepdims=True)) + eps)).reshape(B, L, C)
+    xa = np.asarray(xa, np.float64)
+    softplus = np.where(xa > 20.0, xa, np.log1p(np.exp(np.minimum(xa, 20.0))))
+    la = np.maximum(-softplus, -14.0)
+    sig = lambda z: 1.0 / (1.0 + np.exp(-np.asarray(z, np.float64)))  # noqa: E731
+    return q, k, v, la, np.exp(la), sig(xb), sig(xw), hists

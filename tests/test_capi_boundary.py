@@ -159,6 +159,44 @@ def test_maba_sa_decode_validation(lib):
     assert rc == N.MABA_ERR_WORKSPACE
 
 
+def _arr(*descs):
+    T = ctypes.POINTER(N.MabaTensor)
+    return (T * len(descs))(*[d if d is not None else T() for d in descs])
+
+
+def _p(shape, dtype=N.MABA_BF16, data=0x10000):
+    t = N.MabaTensor()
+    t.data, t.dtype, t.ndim = data, dtype, len(shape)
+    acc = 1
+    for i in reversed(range(len(shape))):
+        t.shape[i], t.stride[i] = shape[i], acc
+        acc *= shape[i]
+    return ctypes.pointer(t)
+
+
+def test_dgda_prologue_validation(lib):
+    """Host checks of the prologue: 64-channel heads, one projection dtype, and a new
+    conv history that does not alias the old one (each call returns before any launch)."""
+    B, L, C = 2, 40, 640
+    xs = _arr(*[_p([B, L, C]) for _ in range(6)])
+    cw = _arr(*[_p([C, 1, 4], N.MABA_F32) for _ in range(3)])
+    hist = [_p([B, C, 3], N.MABA_F32, data=0x20000 + 0x1000 * i) for i in range(3)]
+    ys = _arr(*[_p([B, L, C]) for _ in range(3)], *[_p([B, L, C], N.MABA_F32) for _ in range(4)])
+    fresh = _arr(*[_p([B, C, 3], N.MABA_F32, data=0x40000 + 0x1000 * i) for i in range(3)])
+    aliased = _arr(_p([B, C, 3], N.MABA_F32, data=0x40000), hist[0], _p([B, C, 3], N.MABA_F32, data=0x48000))
+    rc = lib.maba_hip_dgda_prologue(xs, cw, _arr(*hist), 1e-6, ys, aliased, None)
+    assert rc == N.MABA_ERR_INVALID and b"must not alias" in lib.maba_hip_last_error()
+    odd = _arr(*[_p([B, L, 100]) for _ in range(6)])
+    rc = lib.maba_hip_dgda_prologue(odd, cw, None, 1e-6, ys, fresh, None)
+    assert rc == N.MABA_ERR_UNSUPPORTED and b"64 * H" in lib.maba_hip_last_error()
+    mixed = _arr(*[_p([B, L, C]) for _ in range(5)], _p([B, L, C], N.MABA_F32))
+    rc = lib.maba_hip_dgda_prologue(mixed, cw, None, 1e-6, ys, fresh, None)
+    assert rc == N.MABA_ERR_UNSUPPORTED and b"share one" in lib.maba_hip_last_error()
+    bad_w = _arr(*[_p([C, 1, 3], N.MABA_F32) for _ in range(3)])
+    rc = lib.maba_hip_dgda_prologue(xs, bad_w, None, 1e-6, ys, fresh, None)
+    assert rc == N.MABA_ERR_INVALID
+
+
 def test_check_maps_status_to_python_exceptions(lib):
     q = _t([2, 3, 4])
     rc = lib.maba_hip_dgda_prefill(q, q, q, None, q, q, q, None, q, q, 64, None, 0, None)

@@ -67,7 +67,7 @@ def test_register_kernel_creates_backend_and_op():
 
 def test_hip_backend_registers_every_op():
     for op in ("dgda_prefill", "dgda_step", "compute_centroids", "index_topk", "stream_superposition",
-               "index_topk_decode", "hca_pool", "maba_sa_decode"):
+               "index_topk_decode", "hca_pool", "maba_sa_decode", "dgda_prologue"):
         assert D.get_kernel("hip", op) is not None, op
 
 

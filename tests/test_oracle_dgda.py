@@ -149,3 +149,70 @@ def test_c_chunked_oracle_matches_sequential(gates, L, chunk):
     oc, Sc = dgda_c.dgda_prefill_chunked_c(q, k, v, g(la), g(b), g(w), initial_state=S0, chunk_size=chunk)
     np.testing.assert_allclose(oc, o, atol=2e-5, rtol=2e-5)
     np.testing.assert_allclose(Sc, S, atol=2e-5, rtol=2e-5)
+
+
+# ----------------------------------------------------------------------------- layer prologue
+
+def _pro_inputs(B=2, L=9, C=8, K=4, seed=0):
+    rng = np.random.default_rng(seed)
+    xs = [rng.standard_normal((B, L, C)) for _ in range(6)]
+    ws = [rng.standard_normal((C, K)) * 0.5 for _ in range(3)]
+    return xs, ws
+
+
+def test_prologue_identity_and_shift_kernels():
+    """Tap [0,0,0,1] is the identity (y = silu(x)); tap [1,0,0,0] reads three tokens back,
+    through the carried history for the first three tokens."""
+    xs, _ = _pro_inputs()
+    B, L, C = xs[0].shape
+    ident = np.zeros((C, 4)); ident[:, 3] = 1.0
+    shift = np.zeros((C, 4)); shift[:, 0] = 1.0
+    hist = [np.full((B, C, 3), 0.25 * (i + 1)) + np.arange(3) for i in range(3)]
+    q, k, v, *_ , nh = od.layer_prologue(*xs, ident, ident, shift, hist=hist, n_heads=2)
+    silu = lambda z: z / (1 + np.exp(-z))  # noqa: E731
+    assert np.allclose(q, silu(xs[0]))
+    exp_v = np.concatenate([hist[2].transpose(0, 2, 1), xs[2]], axis=1)[:, :L]
+    assert np.allclose(v, silu(exp_v))
+    for i in range(3):   # new history = last three conv inputs
+        assert np.allclose(nh[i], xs[i][:, L - 3:].transpose(0, 2, 1))
+
+
+def test_prologue_gate_closed_forms_and_unit_keys():
+    xs, ws = _pro_inputs()
+    xs[3][:] = 0.0
+    xs[3][0, 0, 0] = 50.0           # softplus(50) = 50 -> clamped to -14
+    xs[4][:] = 0.0
+    q, k, v, la, al, b, w, _ = od.layer_prologue(*xs, *ws, n_heads=2)
+    assert np.isclose(la[0, 0, 0], -14.0)
+    assert np.allclose(la.ravel()[1:], -np.log(2.0))
+    assert np.allclose(al, np.exp(la))
+    assert np.allclose(b, 0.5)
+    norms = np.sqrt((k.reshape(2, 9, 2, 4) ** 2).sum(-1))
+    assert np.allclose(norms, 1.0, atol=1e-5)
+
+
+def test_prologue_history_carry_equals_one_pass():
+    xs, ws = _pro_inputs(L=12)
+    full = od.layer_prologue(*xs, *ws, n_heads=2)
+    first = od.layer_prologue(*[x[:, :5] for x in xs], *ws, n_heads=2)
+    second = od.layer_prologue(*[x[:, 5:] for x in xs], *ws, hist=first[7], n_heads=2)
+    for j in range(7):
+        assert np.allclose(np.concatenate([first[j], second[j]], axis=1), full[j])
+    for i in range(3):
+        assert np.allclose(second[7][i], full[7][i])
+
+
+def test_prologue_torch_reference_matches_oracle():
+    """The dispatcher's torch prologue (the CPU path and the fallback) against the oracle."""
+    import torch
+    from maba_sparse.kernels import common as C
+    xs, ws = _pro_inputs(B=2, L=11, C=16, seed=3)
+    hist = [np.random.default_rng(i).standard_normal((2, 16, 3)) for i in range(3)]
+    T = lambda a: torch.from_numpy(np.asarray(a))  # noqa: E731
+    got = C.ref_dgda_prologue([T(x) for x in xs], [T(w).unsqueeze(1) for w in ws], [T(h) for h in hist],
+                              n_heads=4, eps=1e-6)
+    exp = od.layer_prologue(*xs, *ws, hist=hist, n_heads=4, eps=1e-6)
+    for j in range(7):
+        assert np.allclose(got[j].numpy(), exp[j], rtol=1e-10, atol=1e-12), j
+    for i in range(3):
+        assert np.allclose(got[7][i].numpy(), exp[7][i])
