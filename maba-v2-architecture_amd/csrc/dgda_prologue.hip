@@ -18,7 +18,7 @@
 
 namespace maba {
 
-constexpr int PRO_TOK = 32;   // tokens per workgroup
+constexpr int PRO_TOK = 64;   // tokens per workgroup
 constexpr int PRO_GRP = 4;    // tokens whose loads are issued together
 constexpr int PRO_KH = 3;     // conv history (kernel 4)
 
