@@ -29,6 +29,9 @@
  *                                   (local + sparse + HCA decode streams and the
  *                                   gate superposition; inline torch code in the
  *                                   reference, no dispatcher op)
+ *   maba_hip_maba_sa_prefill        layers/sparse_attention.py:95-105,145-171,
+ *                                   173-219,275 (the three prefill streams over
+ *                                   dense masks and the gate; inline torch code)
  *   maba_hip_dgda_prologue          layers/dgda.py:103-121,186-207 (the DGDA
  *                                   layer's conv + SiLU with carried history,
  *                                   gate activations and key normalisation;
@@ -150,6 +153,24 @@ int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tensor* c_kv,
                             const maba_tensor* gate, int64_t L, float scale, int window,
                             int n_sink, int block_size, int pool, maba_tensor* out_lat,
                             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * MABA-SA prefill: every query's local, sparse and HCA streams and their gate.
+ *   q [B,H,Lq,dh], k, v [B,H,Lkv,dh] (bf16, unit channel stride, 16-byte aligned rows,
+ *   dh in {32,64,128}); query t sits at position pos = Lkv - Lq + t.
+ *   kh, vh [B,H,Lkv/pool,dh] bf16: keys / values of the complete-block means (NULL when
+ *   Lkv < pool).  early [B,H,n_early,dh]: the HCA rows of the queries with pos < pool-1
+ *   (n_early of them; NULL when none).  idx int64 [B,Lq|1,K], K <= 64: each query's
+ *   64-token blocks (block_size must be 64; a block listed twice counts twice).
+ *   gate [B,Lq,3] or [B,H,Lq,3] logits.  out [B,H,Lq,dh] f32 or bf16.
+ *   local: keys j <= pos with pos - j < window or j < min(n_sink, Lkv); sparse: the listed
+ *   blocks' tokens <= pos; HCA: means e with (e+1)*pool - 1 <= pos.  Lkv <= 1,048,576.
+ */
+int maba_hip_maba_sa_prefill(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
+                             const maba_tensor* kh, const maba_tensor* vh, const maba_tensor* early,
+                             const maba_tensor* idx, const maba_tensor* gate, float scale,
+                             int window, int n_sink, int block_size, int pool, maba_tensor* out,
+                             void* stream);
 
 /*
  * DGDA layer prologue.  xs[0..5]: the q, k, v, alpha, erase and write projections

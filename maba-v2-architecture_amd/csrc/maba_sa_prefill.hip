@@ -1,0 +1,409 @@
+// MABA-SA prefill: the three attention streams for every query of a sequence and their
+// gate superposition, without the reference's dense [Lq, Lkv] masks.
+//
+// Reference semantics (maba_sparse/layers/sparse_attention.py), per batch b, head h and
+// query t at position pos = (Lkv - Lq) + t, with per-head keys/values k, v [Lkv, dh]:
+//   local  (:95-105)  keys j <= pos with pos - j < window or j < min(n_sink, Lkv)
+//   sparse (:145-171) the tokens of the blocks idx[b, t, :] that are < Lkv and <= pos
+//                     (a block listed twice counts twice, as the reference's gather does)
+//   HCA    (:173-219) pos >= pool - 1: the complete-block means e with (e+1) pool - 1 <= pos,
+//                     keys kh / values vh (up-projected means); pos < pool - 1: the caller's
+//                     running-mean row early[t]
+//   gate   (:275)     out = sum_s softmax(logits)_s o_s; a stream with no valid key gives 0
+//
+// One wave per 16 consecutive queries of one (b, h); four independent waves per workgroup
+// (no barrier).  Per 64-key tile, on bf16 MFMA with fp32 accumulation:
+//   scores  S^T[key][query] = K Q^T     (A: key rows from global memory, B: the wave's
+//                                        16 queries in registers)
+//   values  O^T[dim][query] += V^T P    (A: V^T fragments read transposed from the tile
+//                                        kept row-major in the wave's LDS, B: the
+//                                        probabilities in bf16 hi + lo)
+// with an online softmax per query and stream.  The sparse stream walks the union of the
+// 16 queries' blocks (an LDS bitmap, compacted in ascending block order) and weights each
+// key by how often the lane's query lists its block.
+#include <algorithm>
+
+#include "maba_common.h"
+
+namespace maba {
+
+constexpr int PF_MAXK = 64;          // index slots per query
+constexpr int PF_WORDS = 512;        // bitmap words per wave: blocks below 16384
+constexpr int PF_LIST = 16 * PF_MAXK;
+
+typedef __attribute__((ext_vector_type(8))) short pf16x8;
+typedef __attribute__((ext_vector_type(4))) short pf16x4;
+
+struct PfArgs {
+  const uint16_t* q; int64_t qsb, qsh, qst;       // [B,H,Lq,dh] bf16, unit channel stride
+  const uint16_t* k; int64_t ksb, ksh, kst;       // [B,H,Lkv,dh]
+  const uint16_t* v; int64_t vsb, vsh, vst;
+  const uint16_t* kh; int64_t khb, khh, khe;      // [B,H,nc,dh] (unused when nc == 0)
+  const uint16_t* vh; int64_t vhb, vhh, vhe;
+  const void* early; int edt; int64_t esb, esh, est, esd;   // [B,H,n_early,dh] or null
+  const int64_t* idx; int64_t isb, ist, isk;      // [B,Lq,K] (ist = 0 for one shared row)
+  const void* gate; int gdt; int64_t gsb, gsh, gst, gsm;    // [B,Lq,3] (gsh = 0) or [B,H,Lq,3]
+  void* out; int odt; int64_t osb, osh, ost;      // [B,H,Lq,dh], unit channel stride
+  int64_t Lq, Lkv, nc, n_early, nb;
+  int K, window, n_sink, pool;
+  float scale;
+};
+
+// Transposed LDS read: lane j of 16-lane group g addressing row r0 + 4g + j/4, column
+// c0 + 4(j%4) of a row-major tile receives the column fragment tile[r0 + 4g + r][c0 + j],
+// r = 0..3.
+__device__ __forceinline__ pf16x4 pf_ldsT4(const short* tile, int pitch, int r0, int c0, int c16, int g) {
+  const short* p = tile + (r0 + 4 * g + (c16 >> 2)) * pitch + c0 + 4 * (c16 & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) pf16x4*)p);
+}
+
+// Running softmax state of one stream for the lane's query.
+template <int NDT>
+struct PfAcc {
+  float m, l;
+  f32x4 z[NDT];   // O^T[16 dt + 4g + i][query c16]
+};
+
+template <int NP>   // dh = 32 NP
+__global__ __launch_bounds__(256) void maba_sa_prefill_kernel(PfArgs a) {
+  constexpr int DH = 32 * NP;
+  constexpr int TP = DH + 8;      // row pitch (bf16) of the wave's value tile
+  constexpr int NDT = DH / 16;
+  __shared__ __attribute__((aligned(16))) short s_v[4][64 * TP];
+  __shared__ uint32_t s_bits[4][PF_WORDS];
+  __shared__ int s_list[4][PF_LIST];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t b = blockIdx.z;
+  const int h = blockIdx.y;
+  const int64_t tq0 = (int64_t)blockIdx.x * 64 + wave * 16;   // the wave's first query
+  if (tq0 >= a.Lq) return;                                     // whole wave; no barriers below
+  const bool qvalid = tq0 + c16 < a.Lq;
+  const int64_t tq = qvalid ? tq0 + c16 : a.Lq - 1;            // extra columns repeat the last query
+  const int64_t off = a.Lkv - a.Lq;
+  const int64_t pos = off + tq;
+  const int64_t pos_lo = off + tq0;
+  const int64_t pos_hi = off + min(tq0 + 15, a.Lq - 1);
+  short* vt = s_v[wave];
+
+  pf16x8 qb[NP];   // lane (query c16, group g): dims 32 p + 8 g .. +7
+#pragma unroll
+  for (int p = 0; p < NP; ++p) qb[p] = *(const pf16x8*)(a.q + b * a.qsb + h * a.qsh + tq * a.qst + 32 * p + 8 * g);
+
+  // gate weights of the lane's query
+  const int64_t gb = b * a.gsb + h * a.gsh + tq * a.gst;
+  float g0 = load_elem(a.gate, a.gdt, gb), g1 = load_elem(a.gate, a.gdt, gb + a.gsm),
+        g2 = load_elem(a.gate, a.gdt, gb + 2 * a.gsm);
+  {
+    const float gm = fmaxf(g0, fmaxf(g1, g2));
+    g0 = __expf(g0 - gm); g1 = __expf(g1 - gm); g2 = __expf(g2 - gm);
+    const float gi = 1.f / (g0 + g1 + g2);
+    g0 *= gi; g1 *= gi; g2 *= gi;
+  }
+  f32x4 o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // One 64-key tile: krow(j) / vrow(j) give in-bounds rows for tile row j; mult(j) the
+  // weight (0 = masked) of tile row j for the lane's query.
+  auto tile = [&](PfAcc<NDT>& st, auto krow, auto vrow, auto mult) {
+    pf16x8 kv[4][NP];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const uint16_t* kr = krow(16 * rb + c16);
+      const uint16_t* vr = vrow(16 * rb + c16);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        kv[rb][p] = *(const pf16x8*)(kr + 32 * p + 8 * g);
+        *(pf16x8*)(vt + (16 * rb + c16) * TP + 32 * p + 8 * g) = *(const pf16x8*)(vr + 32 * p + 8 * g);
+      }
+    }
+    f32x4 sc[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kv[rb][p]),
+                                                      __builtin_bit_cast(bf16x8, qb[p]), acc, 0, 0, 0);
+      sc[rb] = acc;
+    }
+    // lane (query c16, g) holds the scores of keys 16 rb + 4 g + i
+    float wgt[4][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wgt[rb][i] = mult(16 * rb + 4 * g + i);
+        const float x = wgt[rb][i] > 0.f ? sc[rb][i] * a.scale : -INFINITY;
+        sc[rb][i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(st.m, tmax);
+    const float corr = (m_new == -INFINITY) ? 1.f : __expf(st.m - m_new);
+    const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;
+    float psum = 0.f;
+    pf16x4 ph[4], pl[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pe = wgt[rb][i] * __expf(sc[rb][i] - m_sub);   // exp(-inf) = 0 for masked keys
+        psum += pe;
+        const short hb = __builtin_bit_cast(short, (__bf16)pe);
+        ph[rb][i] = hb;
+        pl[rb][i] = __builtin_bit_cast(short, (__bf16)(pe - bf16_bits_to_f32((uint16_t)hb)));
+      }
+    }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    st.l = st.l * corr + psum;
+    st.m = m_new;
+    // O^T[dim][query] = corr O^T + V^T P over the 64 keys as two 32-key steps whose key order
+    // (16 rb + 4 g + i, rb in {2 p2, 2 p2 + 1}) matches the probabilities this lane holds
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      f32x4 acc = st.z[dt] * corr;
+#pragma unroll
+      for (int p2 = 0; p2 < 2; ++p2) {
+        const pf16x4 a0 = pf_ldsT4(vt, TP, 32 * p2, 16 * dt, c16, g);
+        const pf16x4 a1 = pf_ldsT4(vt, TP, 32 * p2 + 16, 16 * dt, c16, g);
+        const pf16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        const pf16x8 bh = {ph[2 * p2][0], ph[2 * p2][1], ph[2 * p2][2], ph[2 * p2][3],
+                           ph[2 * p2 + 1][0], ph[2 * p2 + 1][1], ph[2 * p2 + 1][2], ph[2 * p2 + 1][3]};
+        const pf16x8 bl = {pl[2 * p2][0], pl[2 * p2][1], pl[2 * p2][2], pl[2 * p2][3],
+                           pl[2 * p2 + 1][0], pl[2 * p2 + 1][1], pl[2 * p2 + 1][2], pl[2 * p2 + 1][3]};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bh),
+                                                      acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bl),
+                                                      acc, 0, 0, 0);
+      }
+      st.z[dt] = acc;
+    }
+  };
+  auto reset = [&](PfAcc<NDT>& st) {
+    st.m = -INFINITY;
+    st.l = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) st.z[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto fold = [&](const PfAcc<NDT>& st, float gs) {   // o += g_s z_s / l_s
+    const float w = st.l > 0.f ? gs / st.l : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] += st.z[dt] * w;
+  };
+
+  const uint16_t* kbase = a.k + b * a.ksb + h * a.ksh;
+  const uint16_t* vbase = a.v + b * a.vsb + h * a.vsh;
+  auto krow_at = [&](int64_t j) { return kbase + min(j, a.Lkv - 1) * a.kst; };
+  auto vrow_at = [&](int64_t j) { return vbase + min(j, a.Lkv - 1) * a.vst; };
+  PfAcc<NDT> st;
+
+  // ---- local stream: the sink tiles below the first window tile, then the window tiles
+  {
+    reset(st);
+    const int64_t ns = min((int64_t)a.n_sink, a.Lkv);
+    const int64_t lo = max((int64_t)0, pos_lo - a.window + 1);
+    const int64_t wt0 = (lo / 64) * 64;
+    const int64_t sink_end = min(ns, wt0);
+    for (int64_t tb = 0; tb < sink_end; tb += 64)
+      tile(st, [&](int j) { return krow_at(tb + j); }, [&](int j) { return vrow_at(tb + j); },
+           [&](int j) { const int64_t kj = tb + j; return (kj < sink_end && kj <= pos) ? 1.f : 0.f; });
+    for (int64_t tb = wt0; tb <= pos_hi; tb += 64)
+      tile(st, [&](int j) { return krow_at(tb + j); }, [&](int j) { return vrow_at(tb + j); },
+           [&](int j) {
+             const int64_t kj = tb + j;
+             return (kj <= pos && (pos - kj < a.window || kj < ns)) ? 1.f : 0.f;
+           });
+    fold(st, g0);
+  }
+
+  // ---- sparse stream: union of the 16 queries' blocks, ascending
+  {
+    reset(st);
+    // this lane's share of its query's index slots: k = g, g + 4, ...
+    int64_t myblk[PF_MAXK / 4];
+#pragma unroll
+    for (int r = 0; r < PF_MAXK / 4; ++r) {
+      const int kk = g + 4 * r;
+      myblk[r] = kk < a.K ? a.idx[b * a.isb + tq * a.ist + kk * a.isk] : -1;
+    }
+    const int64_t nbl = min(a.nb, pos_hi / 64 + 1);   // blocks that hold a key <= pos_hi
+    const int nwords = (int)((nbl + 31) / 32);
+    uint32_t* bits = s_bits[wave];
+    int* list = s_list[wave];
+    for (int wd = lane; wd < nwords; wd += 64) bits[wd] = 0u;
+    if (qvalid) {
+#pragma unroll
+      for (int r = 0; r < PF_MAXK / 4; ++r) {
+        const int64_t bk = myblk[r];
+        if (bk >= 0 && bk < nbl) atomicOr(&bits[bk >> 5], 1u << (bk & 31));
+      }
+    }
+    // compaction in ascending block order: word wd's set bits at base + (bits before it)
+    int nlist = 0;
+    for (int w0 = 0; w0 < nwords; w0 += 64) {
+      const int wd = w0 + lane;
+      const uint32_t word = wd < nwords ? bits[wd] : 0u;
+      const int cnt = __popc(word);
+      int incl = cnt;
+#pragma unroll
+      for (int o2 = 1; o2 < 64; o2 <<= 1) {
+        const int y = __shfl_up(incl, o2);
+        if (lane >= o2) incl += y;
+      }
+      int at = nlist + incl - cnt;
+      uint32_t rest = word;
+      while (rest) {
+        const int bit = __ffs(rest) - 1;
+        list[at++] = wd * 32 + bit;
+        rest &= rest - 1;
+      }
+      nlist += __shfl(incl, 63);
+    }
+    for (int u = 0; u < nlist; ++u) {
+      const int64_t blk = list[u];           // wave-uniform
+      int cnt = 0;                           // times the lane's query lists blk
+#pragma unroll
+      for (int r = 0; r < PF_MAXK / 4; ++r) cnt += myblk[r] == blk;
+      cnt += __shfl_xor(cnt, 16);
+      cnt += __shfl_xor(cnt, 32);
+      const float fc = qvalid ? (float)cnt : 0.f;
+      const int64_t tb = blk * 64;
+      tile(st, [&](int j) { return krow_at(tb + j); }, [&](int j) { return vrow_at(tb + j); },
+           [&](int j) { return (tb + j <= pos) ? fc : 0.f; });
+    }
+    fold(st, g1);
+  }
+
+  // ---- HCA stream: means e with (e + 1) pool - 1 <= pos; early queries take their row
+  {
+    reset(st);
+    const int64_t e_hi = min(a.nc - 1, (pos_hi + 1) / a.pool - 1);
+    if (e_hi >= 0) {
+      const uint16_t* khb = a.kh + b * a.khb + h * a.khh;
+      const uint16_t* vhb = a.vh + b * a.vhb + h * a.vhh;
+      for (int64_t eb = 0; eb <= e_hi; eb += 64)
+        tile(st, [&](int j) { return khb + min(eb + j, a.nc - 1) * a.khe; },
+             [&](int j) { return vhb + min(eb + j, a.nc - 1) * a.vhe; },
+             [&](int j) { const int64_t e = eb + j; return (e < a.nc && (e + 1) * a.pool - 1 <= pos) ? 1.f : 0.f; });
+    }
+    if (pos < a.pool - 1) {   // running mean of c[0..pos] through W_v (the caller's row)
+      const bool have = a.early && tq < a.n_early;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 16 * dt + 4 * g + i;
+          const float x = have ? load_elem(a.early, a.edt, b * a.esb + h * a.esh + tq * a.est + d * a.esd) : 0.f;
+          o[dt][i] += g2 * x;
+        }
+    } else {
+      fold(st, g2);
+    }
+  }
+
+  if (!qvalid) return;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    const int64_t oo = b * a.osb + h * a.osh + tq * a.ost + 16 * dt + 4 * g;
+    if (a.odt == MABA_F32) {
+      *(f32x4*)((float*)a.out + oo) = o[dt];
+    } else {
+      uint2 u;
+      u.x = (uint32_t)f32_to_bf16_bits(o[dt][0]) | ((uint32_t)f32_to_bf16_bits(o[dt][1]) << 16);
+      u.y = (uint32_t)f32_to_bf16_bits(o[dt][2]) | ((uint32_t)f32_to_bf16_bits(o[dt][3]) << 16);
+      *(uint2*)((uint16_t*)a.out + oo) = u;
+    }
+  }
+}
+
+static bool pf_rows_ok(const maba_tensor* t, int64_t B, int64_t H, int64_t n, int64_t dh) {
+  if (!t || t->ndim != 4 || t->dtype != MABA_BF16) return false;
+  if (t->shape[0] != B || t->shape[1] != H || t->shape[2] != n || t->shape[3] != dh) return false;
+  if (t->stride[3] != 1 || (uintptr_t)t->data % 16 != 0) return false;
+  for (int d = 0; d < 3; ++d)
+    if (t->shape[d] > 1 && t->stride[d] % 8 != 0) return false;
+  return true;
+}
+
+}  // namespace maba
+
+using namespace maba;
+
+extern "C" int maba_hip_maba_sa_prefill(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
+                                        const maba_tensor* kh, const maba_tensor* vh,
+                                        const maba_tensor* early, const maba_tensor* idx,
+                                        const maba_tensor* gate, float scale, int window, int n_sink,
+                                        int block_size, int pool, maba_tensor* out, void* stream) {
+  if (!q || q->ndim != 4) return fail(MABA_ERR_INVALID, "maba_sa_prefill: q must be [B,H,Lq,dh]");
+  const int64_t B = q->shape[0], H = q->shape[1], Lq = q->shape[2], dh = q->shape[3];
+  if (!k || k->ndim != 4 || !v || v->ndim != 4)
+    return fail(MABA_ERR_INVALID, "maba_sa_prefill: k and v must be [B,H,Lkv,dh]");
+  const int64_t Lkv = k->shape[2];
+  if (Lq > Lkv) return fail(MABA_ERR_INVALID, "maba_sa_prefill: more queries than keys");
+  if (window < 0 || n_sink < 0 || pool <= 0) return fail(MABA_ERR_INVALID, "maba_sa_prefill: bad window/sink/pool");
+  if (block_size != 64) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill: block_size 64 only");
+  if (dh != 32 && dh != 64 && dh != 128) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill: dh in {32, 64, 128}");
+  if (!pf_rows_ok(q, B, H, Lq, dh) || !pf_rows_ok(k, B, H, Lkv, dh) || !pf_rows_ok(v, B, H, Lkv, dh))
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill: q, k, v must be bf16 with unit channel stride and "
+                "16-byte aligned rows");
+  const int64_t nc = Lkv / pool;
+  if (nc > 0 && (!pf_rows_ok(kh, B, H, nc, dh) || !pf_rows_ok(vh, B, H, nc, dh)))
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill: kh, vh must be bf16 [B,H,Lkv/pool,dh], unit channel stride");
+  const int64_t off = Lkv - Lq;
+  const int64_t n_early = off < pool - 1 ? std::min(Lq, (int64_t)(pool - 1) - off) : 0;
+  if (n_early > 0) {
+    const int64_t se[4] = {B, H, n_early, dh};
+    if (!expect_shape(early, "early", 4, se) || !expect_float(early, "early")) return MABA_ERR_INVALID;
+  }
+  if (!idx || idx->ndim != 3 || idx->shape[0] != B || (idx->shape[1] != Lq && idx->shape[1] != 1))
+    return fail(MABA_ERR_INVALID, "maba_sa_prefill: idx must be [B,Lq|1,K]");
+  if (idx->dtype != MABA_I64) return fail(MABA_ERR_DTYPE, "maba_sa_prefill: idx must be int64");
+  const int64_t K = idx->shape[2];
+  if (K > PF_MAXK) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill: at most %d index slots", PF_MAXK);
+  const int64_t nb = (Lkv + 63) / 64;
+  if (nb > (int64_t)PF_WORDS * 32) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill: Lkv up to %d", PF_WORDS * 32 * 64);
+  if (!gate || !((gate->ndim == 3 && gate->shape[0] == B && gate->shape[1] == Lq && gate->shape[2] == 3) ||
+                 (gate->ndim == 4 && gate->shape[0] == B && gate->shape[1] == H && gate->shape[2] == Lq &&
+                  gate->shape[3] == 3)))
+    return fail(MABA_ERR_INVALID, "maba_sa_prefill: gate must be [B,Lq,3] or [B,H,Lq,3]");
+  if (!expect_float(gate, "gate")) return MABA_ERR_DTYPE;
+  const int64_t so[4] = {B, H, Lq, dh};
+  if (!expect_shape(out, "out", 4, so)) return MABA_ERR_INVALID;
+  if ((out->dtype != MABA_F32 && out->dtype != MABA_BF16) || out->stride[3] != 1 ||
+      (uintptr_t)out->data % 16 != 0 || out->stride[0] % 4 != 0 || out->stride[1] % 4 != 0 ||
+      out->stride[2] % 4 != 0)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill: out must be f32/bf16 with unit channel stride");
+  if (B * H * Lq == 0) return MABA_OK;
+  PfArgs a;
+  a.q = (const uint16_t*)q->data; a.qsb = q->stride[0]; a.qsh = q->stride[1]; a.qst = q->stride[2];
+  a.k = (const uint16_t*)k->data; a.ksb = k->stride[0]; a.ksh = k->stride[1]; a.kst = k->stride[2];
+  a.v = (const uint16_t*)v->data; a.vsb = v->stride[0]; a.vsh = v->stride[1]; a.vst = v->stride[2];
+  a.kh = nc > 0 ? (const uint16_t*)kh->data : nullptr;
+  a.khb = nc > 0 ? kh->stride[0] : 0; a.khh = nc > 0 ? kh->stride[1] : 0; a.khe = nc > 0 ? kh->stride[2] : 0;
+  a.vh = nc > 0 ? (const uint16_t*)vh->data : nullptr;
+  a.vhb = nc > 0 ? vh->stride[0] : 0; a.vhh = nc > 0 ? vh->stride[1] : 0; a.vhe = nc > 0 ? vh->stride[2] : 0;
+  a.early = n_early > 0 ? early->data : nullptr; a.edt = n_early > 0 ? early->dtype : MABA_F32;
+  a.esb = n_early > 0 ? early->stride[0] : 0; a.esh = n_early > 0 ? early->stride[1] : 0;
+  a.est = n_early > 0 ? early->stride[2] : 0; a.esd = n_early > 0 ? early->stride[3] : 0;
+  a.idx = (const int64_t*)idx->data; a.isb = idx->stride[0];
+  a.ist = idx->shape[1] == 1 ? 0 : idx->stride[1]; a.isk = idx->stride[2];
+  a.gate = gate->data; a.gdt = gate->dtype; a.gsb = gate->stride[0];
+  if (gate->ndim == 3) { a.gsh = 0; a.gst = gate->stride[1]; a.gsm = gate->stride[2]; }
+  else { a.gsh = gate->stride[1]; a.gst = gate->stride[2]; a.gsm = gate->stride[3]; }
+  a.out = out->data; a.odt = out->dtype; a.osb = out->stride[0]; a.osh = out->stride[1]; a.ost = out->stride[2];
+  a.Lq = Lq; a.Lkv = Lkv; a.nc = nc; a.n_early = n_early; a.nb = nb;
+  a.K = (int)K; a.window = window; a.n_sink = n_sink; a.pool = pool; a.scale = scale;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)ceil_div(Lq, 64), (unsigned)H, (unsigned)B);
+  switch (dh) {
+    case 32: hipLaunchKernelGGL(maba_sa_prefill_kernel<1>, grid, dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL(maba_sa_prefill_kernel<2>, grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(maba_sa_prefill_kernel<4>, grid, dim3(256), 0, s, a); break;
+  }
+  return check_launch("maba_sa_prefill");
+}

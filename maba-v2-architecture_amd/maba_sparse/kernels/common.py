@@ -345,6 +345,58 @@ def ref_maba_sa_decode(q_lat, c_kv, hca, idx, gate, L: int, scale: float, window
     return g[..., 0:1] * z_loc + g[..., 1:2] * z_sp + g[..., 2:3] * z_hca
 
 
+def ref_maba_sa_prefill(q, k, v, kh, vh, early, idx, gate_logits, scale: float, window: int = 128,
+                        n_sink: int = 4, block_size: int = 64, pool: int = 64, out_dtype=None, **kwargs: Any):
+    """MABA-SA prefill streams and their gate (reference layers/sparse_attention.py:95-105,
+    145-171, 173-219, 275) with dense masks, in fp32.
+
+    q ``[B,H,Lq,dh]``, k/v ``[B,H,Lkv,dh]`` per-head keys and values, kh/vh ``[B,H,Lkv//pool,dh]``
+    the up-projected complete-block means, early ``[B,H,n_early,dh]`` the rows of the queries
+    before position ``pool - 1`` (or None), idx ``[B,Lq|1,K]``, gate logits ``[B,Lq,3]`` or
+    ``[B,H,Lq,3]``.  A block listed twice in a row counts twice.  Returns ``[B,H,Lq,dh]``
+    (computed in fp32, or fp64 for fp64 inputs)."""
+    B, H, Lq, dh = q.shape
+    Lkv = k.shape[2]
+    dev = q.device
+    ct = torch.promote_types(q.dtype, torch.float32)
+    qf, kf, vf = q.to(ct), k.to(ct), v.to(ct)
+    pos = (Lkv - Lq) + torch.arange(Lq, device=dev)
+    j = torch.arange(Lkv, device=dev)
+    ns = min(n_sink, Lkv)
+
+    def attend(s, w, vals):
+        s = s.masked_fill(w <= 0, float("-inf"))
+        m = s.amax(dim=-1, keepdim=True)
+        m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
+        p = w * torch.exp(s - m)
+        tot = p.sum(dim=-1, keepdim=True)
+        return torch.where(tot > 0, (p / tot.clamp_min(1e-38)) @ vals, torch.zeros((), device=dev))
+
+    s = (qf @ kf.transpose(-1, -2)) * scale                                  # [B,H,Lq,Lkv]
+    local_w = ((j[None] <= pos[:, None]) & (((pos[:, None] - j[None]) < window) | (j[None] < ns))).to(ct)
+    ol = attend(s, local_w[None, None], vf)
+    nb = (Lkv + block_size - 1) // block_size
+    rows = idx if idx.shape[1] == Lq else idx[:, :1].expand(B, Lq, idx.shape[2])
+    blk_of = (j // block_size)[None, None, None, :]                         # [1,1,1,Lkv]
+    ok = (rows >= 0) & (rows < nb)
+    cnt = ((rows[..., None] == blk_of) & ok[..., None]).sum(dim=2).to(ct)   # [B,Lq,Lkv]
+    sp_w = cnt * (j[None, None] <= pos[None, :, None]).to(ct)
+    os_ = attend(s, sp_w[:, None], vf)
+    nc = Lkv // pool
+    oh = torch.zeros_like(ol)
+    if nc > 0:
+        ends = (torch.arange(nc, device=dev) + 1) * pool - 1
+        hca_w = (ends[None] <= pos[:, None]).to(ct)
+        oh = attend((qf @ kh.to(ct).transpose(-1, -2)) * scale, hca_w[None, None], vh.to(ct))
+    n_early = int((pos < pool - 1).sum())
+    if n_early > 0:
+        oh[:, :, :n_early] = early[:, :, :n_early].to(ct)
+    g = torch.softmax(gate_logits.to(ct), dim=-1)
+    g = g[:, None] if g.dim() == 3 else g
+    out = g[..., 0:1] * ol + g[..., 1:2] * os_ + g[..., 2:3] * oh
+    return out.to(out_dtype or q.dtype)
+
+
 def ref_dgda_prologue(projections, conv_weights, history=None, n_heads: int = 10, eps: float = 1e-6,
                       gate_dtype: Optional[torch.dtype] = None, with_alpha: bool = True, **kwargs: Any):
     """DGDA layer prologue (reference layers/dgda.py:103-121, 186-207) in torch.

@@ -15,11 +15,13 @@ Differences, all deliberate:
   the reference's tests require.
 * A missing HIP library is never papered over: ``HipLibraryMissing`` propagates
   instead of falling back, so a GPU run cannot silently take a non-HIP path.
-* Four ops the reference only has as inline torch code get dispatcher entries:
+* Five ops the reference only has as inline torch code get dispatcher entries:
   ``index_topk_decode`` (layers/indexer.py:101-112), ``hca_pool``
   (layers/sparse_attention.py:206), ``maba_sa_decode``
-  (layers/sparse_attention.py:79-219,263-275) and ``dgda_prologue`` (the DGDA
-  layer's conv, gates and key normalisation, layers/dgda.py:103-121,186-207).
+  (layers/sparse_attention.py:79-219,263-275), ``maba_sa_prefill`` (the three
+  prefill streams and their gate, layers/sparse_attention.py:95-219,275) and
+  ``dgda_prologue`` (the DGDA layer's conv, gates and key normalisation,
+  layers/dgda.py:103-121,186-207).
 * ``allow_mixed_dtypes=True`` (keyword) lets ``dgda_prefill``/``dgda_step``
   accept bf16 q/k/v with fp32 gates and state; without it the reference's
   "dtypes must match" ``TypeError`` is kept.
@@ -49,6 +51,7 @@ _KERNEL_REGISTRY: Dict[str, Dict[str, Callable]] = {
         "hca_pool": _c.ref_hca_pool,
         "maba_sa_decode": _c.ref_maba_sa_decode,
         "dgda_prologue": _c.ref_dgda_prologue,
+        "maba_sa_prefill": _c.ref_maba_sa_prefill,
     },
     # CPU tensors run the same torch code; no separate CPU kernels are built here.
     "cpu": {
@@ -61,6 +64,7 @@ _KERNEL_REGISTRY: Dict[str, Dict[str, Callable]] = {
         "hca_pool": _c.ref_hca_pool,
         "maba_sa_decode": _c.ref_maba_sa_decode,
         "dgda_prologue": _c.ref_dgda_prologue,
+        "maba_sa_prefill": _c.ref_maba_sa_prefill,
     },
     "hip": {},
     "xla": {},
@@ -325,6 +329,23 @@ def dispatch_dgda_prologue(projections, conv_weights, history=None, n_heads: int
                                            **kwargs))
 
 
+def dispatch_maba_sa_prefill(q, k, v, kh, vh, early, idx, gate_logits, scale: float, window: int = 128,
+                             n_sink: int = 4, block_size: int = 64, pool: int = 64, **kwargs: Any) -> torch.Tensor:
+    """The three MABA-SA prefill streams and their gate (see ``common.ref_maba_sa_prefill``)."""
+    dev = q.device
+    for name, t in (("k", k), ("v", v), ("kh", kh), ("vh", vh), ("early", early), ("idx", idx),
+                    ("gate_logits", gate_logits)):
+        if t is not None and t.device != dev:
+            raise RuntimeError(f"Expected all tensors to be on the same device, but got {dev} and {t.device} for {name}")
+    if q.dim() != 4 or k.dim() != 4 or v.shape != k.shape or q.shape[:2] != k.shape[:2] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"q [B,H,Lq,dh] and k, v [B,H,Lkv,dh] expected, got {list(q.shape)}, {list(k.shape)}")
+    if q.shape[2] > k.shape[2]:
+        raise ValueError(f"more queries ({q.shape[2]}) than keys ({k.shape[2]})")
+    return _run("maba_sa_prefill", dev, dict(q=q, k=k, v=v, kh=kh, vh=vh, early=early, idx=idx,
+                                             gate_logits=gate_logits, scale=scale, window=window, n_sink=n_sink,
+                                             block_size=block_size, pool=pool, **kwargs))
+
+
 dgda_prefill = dispatch_dgda_prefill
 dgda_step = dispatch_dgda_step
 compute_centroids = dispatch_compute_centroids
@@ -334,6 +355,7 @@ index_topk_decode = dispatch_index_topk_decode
 hca_pool = dispatch_hca_pool
 maba_sa_decode = dispatch_maba_sa_decode
 dgda_prologue = dispatch_dgda_prologue
+maba_sa_prefill = dispatch_maba_sa_prefill
 ref_dgda_prefill = _c.ref_dgda_prefill
 ref_dgda_step = _c.ref_dgda_step
 ref_centroids = _c.ref_centroids

@@ -263,3 +263,24 @@ def hip_dgda_prologue(projections, conv_weights, history=None, n_heads: int = 10
                                          arr(nh), N.stream_ptr(dev))
     N.check(rc, "dgda_prologue")
     return (*ys, tuple(nh))
+
+
+@register_kernel("hip", "maba_sa_prefill")
+def hip_maba_sa_prefill(q, k, v, kh, vh, early, idx, gate_logits, scale: float, window: int = 128,
+                        n_sink: int = 4, block_size: int = 64, pool: int = 64, out_dtype=None,
+                        **kwargs: Any) -> torch.Tensor:
+    """The three MABA-SA prefill streams and their gate in one launch
+    (layers/sparse_attention.py:95-105, 145-171, 173-219, 275): bf16 per-head q, k, v and
+    up-projected means, 64-token blocks.  Same contract as ``common.ref_maba_sa_prefill``."""
+    _no_grad_needed("maba_sa_prefill", q, k, v, kh, vh, early, gate_logits)
+    dev = N.require_device([q, k, v, kh, vh, early, idx, gate_logits], "maba_sa_prefill")
+    B, H, Lq, dh = q.shape
+    out = torch.empty(B, H, Lq, dh, dtype=out_dtype or q.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    rc = N.load().maba_hip_maba_sa_prefill(N.desc(q), N.desc(k), N.desc(v), N.desc(kh), N.desc(vh), N.desc(early),
+                                           N.desc(idx), N.desc(gate_logits), float(scale), int(window),
+                                           int(n_sink), int(block_size), int(pool), N.desc(out),
+                                           N.stream_ptr(dev))
+    N.check(rc, "maba_sa_prefill")
+    return out

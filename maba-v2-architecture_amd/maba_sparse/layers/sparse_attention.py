@@ -27,8 +27,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from maba_sparse.kernels.dispatcher import (dispatch_hca_pool, dispatch_maba_sa_decode,
-                                            dispatch_stream_superposition)
+from maba_sparse.kernels.dispatcher import (dispatch_hca_pool, dispatch_maba_sa_decode, dispatch_maba_sa_prefill,
+                                            dispatch_stream_superposition, get_backend)
 from maba_sparse.layers.indexer import DGIndexer, _Growing
 
 
@@ -142,6 +142,44 @@ class MabaSparseAttention(nn.Module):
         hca = cache.hca[:, : max(cache.nh, 1)]
         return self._decode(x, cache.c, cache.n, hca, idx)
 
+    # ------------------------------------------------------------ prefill (HIP)
+    def _prefill_fusable(self, q: torch.Tensor, c_full: torch.Tensor, idx: torch.Tensor) -> bool:
+        """Whether the one-launch HIP prefill takes this call: the ``hip`` backend, bf16, the
+        kernel's head sizes and 64-token blocks, no gradients and the full three streams."""
+        if q.device.type != "cuda" or get_backend(q.device) != "hip" or self.ablation_mode == "no_hca":
+            return False
+        if q.dtype != torch.bfloat16 or c_full.dtype != torch.bfloat16 or self.d_head not in (32, 64, 128):
+            return False
+        if self.block_size != 64 or idx.shape[-1] > 64 or c_full.shape[1] > (1 << 20):
+            return False
+        return not (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()))
+
+    def _fused_prefill(self, x, q, c_full, idx):
+        """The streams' inputs as the dense path forms them (per-head keys and values, the
+        up-projected complete-block means, the running-mean rows before ``pool - 1``), then
+        one ``maba_sa_prefill`` launch with the gate.  Returns ``[B, H, Lq, dh]``."""
+        b, h, lq, dh = q.shape
+        lkv = c_full.shape[1]
+        heads = lambda t, n: t.view(b, n, h, dh).transpose(1, 2)  # noqa: E731
+        k = heads(self.k_up_proj(c_full), lkv)
+        v = heads(self.v_up_proj(c_full), lkv)
+        r = self.hca_pool_size
+        nc = lkv // r
+        kh = vh = None
+        if nc > 0:
+            means = c_full[:, : nc * r].reshape(b, nc, r, self.d_c).mean(dim=2)
+            kh, vh = heads(self.k_up_proj(means), nc), heads(self.v_up_proj(means), nc)
+        off = lkv - lq
+        n_early = max(0, min(lq, r - 1 - off))
+        early = None
+        if n_early > 0:
+            cm = torch.cumsum(c_full[:, : off + n_early], dim=1)
+            cm = cm / torch.arange(1, cm.shape[1] + 1, device=x.device).view(1, -1, 1)
+            early = heads(self.v_up_proj(cm[:, off: off + n_early]), n_early)
+        return dispatch_maba_sa_prefill(q, k, v, kh, vh, early, idx, self.stream_gate(x), scale=self.scale,
+                                        window=self.window_size, n_sink=self.n_sink_tokens,
+                                        block_size=self.block_size, pool=r)
+
     # ------------------------------------------------------------ prefill (dense)
     def _dense_streams(self, x, q, c_full, idx):
         b, h, lq, dh = q.shape
@@ -213,10 +251,13 @@ class MabaSparseAttention(nn.Module):
         if l == 1 and self.ablation_mode != "no_hca":
             return self._decode(x, c_full, c_full.shape[1], self._hca_for(c_full), idx), c_full
         q = self.q_proj(x).view(b, l, self.n_heads, self.d_head).transpose(1, 2)
-        ol, os_, oh = self._dense_streams(x, q, c_full, idx)
+        if self._prefill_fusable(q, c_full, idx):
+            o = self._fused_prefill(x, q, c_full, idx)
+        else:
+            ol, os_, oh = self._dense_streams(x, q, c_full, idx)
+            o = dispatch_stream_superposition(ol, os_, oh, gate_logits=self.stream_gate(x))
         if l > 1 and not self.training and self.ablation_mode != "no_hca":
             self._hca_for(c_full)       # seed the incremental means for the decode steps
-        o = dispatch_stream_superposition(ol, os_, oh, gate_logits=self.stream_gate(x))
         o = o.transpose(1, 2).reshape(b, l, self.n_heads * self.d_head).to(q.dtype)
         return self.o_proj(o), c_full
 

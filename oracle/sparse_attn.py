@@ -35,6 +35,17 @@ Functions
 ``maba_sa_decode``      the composition of the three streams and the gate
                         (sparse_attention.py:263-275), before ``o_proj``.
 
+``maba_sa_prefill_heads``  every query of a prefill (sparse_attention.py:95-105,
+                        145-171, 173-219, 275) from per-head keys and values, as
+                        explicit dense masks over [Lq, Lkv]: the local window and
+                        sinks, each query's selected blocks with multiplicity and
+                        ``token <= pos``, the complete means with
+                        ``(e+1) pool - 1 <= pos`` (or the given running-mean row
+                        before ``pool - 1``), then the gate.
+``maba_sa_prefill``     the same from the latent cache and ``W_k``/``W_v``.  Pinned
+                        against ``maba_sa_decode`` run at every prefix length
+                        ``L = pos + 1`` (a decode step is the last prefill row).
+
 Pinned by: partition of unity and extreme logits (test_triton_indexer.py:
 326-346), a single-key stream returning that key's value, uniform scores
 returning the mean value, brute-force dense masked softmax on tiny shapes and
@@ -170,3 +181,84 @@ def maba_sa_decode(q, c_kv, Wk, Wv, idx, gate_logits, L=None, window=128,
     g4 = g[:, None, None, :] if g.ndim == 2 else g[:, :, None, :]
     out = superposition(ol[:, :, None], os_[:, :, None], oh[:, :, None], gate_logits=g4)
     return out[:, :, 0]
+
+
+def maba_sa_prefill_heads(q, k, v, kh, vh, early, idx, gate_logits, window=128, n_sink=4,
+                          block_size=64, pool=64, scale=None):
+    """Prefill output ``[B, H, Lq, dh]`` from per-head q ``[B,H,Lq,dh]``, k/v ``[B,H,Lkv,dh]``,
+    kh/vh ``[B,H,Lkv//pool,dh]``, early ``[B,H,n_early,dh]`` (rows for pos < pool-1) or
+    None, idx ``[B,Lq|1,K]`` and gate logits ``[B,Lq,3]`` or ``[B,H,Lq,3]``."""
+    q, k, v = (np.asarray(x, np.float64) for x in (q, k, v))
+    B, H, Lq, dh = q.shape
+    Lkv = k.shape[2]
+    scale = 1.0 / math.sqrt(dh) if scale is None else scale
+    pos = (Lkv - Lq) + np.arange(Lq)
+    j = np.arange(Lkv)
+    ns = min(n_sink, Lkv)
+    idx = np.asarray(idx, np.int64)
+    nc = Lkv // pool
+
+    def attend(s, w, vals):      # rows of scores s with multiplicities w (0 = masked)
+        s = np.where(w > 0, s, -np.inf)
+        m = s.max(axis=-1, keepdims=True)
+        m = np.where(np.isfinite(m), m, 0.0)
+        p = w * np.exp(s - m)
+        tot = p.sum(axis=-1, keepdims=True)
+        return np.where(tot > 0, (p / np.where(tot > 0, tot, 1.0)) @ vals, 0.0)
+
+    local_w = ((j[None] <= pos[:, None]) &
+               (((pos[:, None] - j[None]) < window) | (j[None] < ns))).astype(np.float64)
+    nb = (Lkv + block_size - 1) // block_size
+    out = np.zeros((B, H, Lq, dh))
+    for b in range(B):
+        sp_w = np.zeros((Lq, Lkv))
+        for t in range(Lq):
+            row = idx[b, t] if idx.shape[1] == Lq else idx[b, 0]
+            for blk in row:
+                if 0 <= blk < nb:
+                    toks = np.arange(blk * block_size, min((blk + 1) * block_size, Lkv))
+                    toks = toks[toks <= pos[t]]
+                    sp_w[t, toks] += 1.0
+        hca_w = (((np.arange(nc) + 1) * pool - 1)[None] <= pos[:, None]).astype(np.float64)
+        for h in range(H):
+            s = q[b, h] @ k[b, h].T * scale
+            ol = attend(s, local_w, v[b, h])
+            os_ = attend(s, sp_w, v[b, h])
+            if nc > 0:
+                khb, vhb = np.asarray(kh, np.float64)[b, h], np.asarray(vh, np.float64)[b, h]
+                oh = attend(q[b, h] @ khb.T * scale, hca_w, vhb)
+            else:
+                oh = np.zeros((Lq, dh))
+            for t in range(Lq):
+                if pos[t] < pool - 1:
+                    oh[t] = np.asarray(early, np.float64)[b, h, t]
+            g = np.asarray(gate_logits, np.float64)
+            g = g[b] if g.ndim == 3 else g[b, h]
+            g = np.exp(g - g.max(axis=-1, keepdims=True))
+            g = g / g.sum(axis=-1, keepdims=True)
+            out[b, h] = g[:, 0:1] * ol + g[:, 1:2] * os_ + g[:, 2:3] * oh
+    return out
+
+
+def maba_sa_prefill(q, c_kv, Wk, Wv, idx, gate_logits, Lq=None, window=128, n_sink=4,
+                    block_size=64, pool=64):
+    """Prefill from the latent cache ``c_kv [B, Lkv, d_c]``: the last ``Lq`` positions are the
+    queries (``q [B, H, Lq, dh]``); keys, values and the complete-block means are up-projected
+    per head, and the rows before ``pool - 1`` take ``W_v`` of the running mean."""
+    q = np.asarray(q, np.float64)
+    B, H, Lq_, dh = q.shape
+    c = np.asarray(c_kv, np.float64)
+    Lkv = c.shape[1]
+    Wk_h, Wv_h = _heads(Wk, H), _heads(Wv, H)
+    k = np.einsum("bld,hed->bhle", c, Wk_h)
+    v = np.einsum("bld,hed->bhle", c, Wv_h)
+    means = hca_means(c, Lkv, pool)
+    kh = np.einsum("bnd,hed->bhne", means, Wk_h)
+    vh = np.einsum("bnd,hed->bhne", means, Wv_h)
+    off = Lkv - Lq_
+    n_early = max(0, min(Lq_, pool - 1 - off))
+    early = np.zeros((B, H, max(n_early, 1), dh))
+    for t in range(n_early):
+        cm = c[:, : off + t + 1].mean(axis=1)
+        early[:, :, t] = np.einsum("bd,hed->bhe", cm, Wv_h)
+    return maba_sa_prefill_heads(q, k, v, kh, vh, early, idx, gate_logits, window, n_sink, block_size, pool)

@@ -67,7 +67,8 @@ def test_register_kernel_creates_backend_and_op():
 
 def test_hip_backend_registers_every_op():
     for op in ("dgda_prefill", "dgda_step", "compute_centroids", "index_topk", "stream_superposition",
-               "index_topk_decode", "hca_pool", "maba_sa_decode", "dgda_prologue"):
+               "index_topk_decode", "hca_pool", "maba_sa_decode", "dgda_prologue",
+               "maba_sa_prefill"):
         assert D.get_kernel("hip", op) is not None, op
 
 
@@ -204,3 +205,23 @@ def test_maba_sa_decode_reference_matches_explicit_streams():
                 p = torch.softmax(rows @ q_lat[b, h] * 0.25, 0)
                 out += g[b, s] * (p @ rows)
             assert torch.allclose(z[b, h].double(), out, rtol=1e-5, atol=1e-5), (b, h)   # fp32 result
+
+
+def test_maba_sa_prefill_reference_matches_oracle():
+    """The dispatcher's torch prefill (the CPU path and the fallback) against the oracle's
+    dense-mask restatement, with a past (Lq < Lkv), early rows, a shared index row and a
+    repeated block."""
+    import numpy as np
+    from oracle import sparse_attn as osa
+    g = torch.Generator().manual_seed(3)
+    B, H, Lq, Lkv, dh, K = 2, 3, 90, 150, 8, 4
+    q = torch.randn(B, H, Lq, dh, generator=g, dtype=torch.float64)
+    k, v = (torch.randn(B, H, Lkv, dh, generator=g, dtype=torch.float64) for _ in range(2))
+    kh, vh = (torch.randn(B, H, Lkv // 64, dh, generator=g, dtype=torch.float64) for _ in range(2))
+    early = torch.randn(B, H, 3, dh, generator=g, dtype=torch.float64)     # pos 60..62 < 63
+    gate = torch.randn(B, Lq, 3, generator=g, dtype=torch.float64)
+    for idx in (torch.randint(0, 3, (B, Lq, K), generator=g), torch.tensor([[[0, 2, 2, 1]], [[1, 1, 0, 0]]])):
+        got = D.dispatch_maba_sa_prefill(q, k, v, kh, vh, early, idx, gate, scale=0.3, window=40, n_sink=2)
+        exp = osa.maba_sa_prefill_heads(q.numpy(), k.numpy(), v.numpy(), kh.numpy(), vh.numpy(), early.numpy(),
+                                        idx.numpy(), gate.numpy(), window=40, n_sink=2, scale=0.3)
+        assert np.allclose(got.numpy(), exp, rtol=1e-10, atol=1e-12)

@@ -1,0 +1,98 @@
+"""MABA-SA prefill streams on the GPU (``maba_hip_maba_sa_prefill``) against the float64
+oracle (``oracle.sparse_attn.maba_sa_prefill_heads``, pinned against the decode oracle at
+every prefix length) and, at a longer shape, against the torch reference op on the GPU.
+
+Tolerance: rtol = atol = 2e-3 (the north-star sparse-attention bar) on bf16 inputs with
+fp32 accumulation; the bf16 layer against its own dense torch path: 3e-2 of the output's
+largest magnitude (the dense path rounds its scores and probabilities to bf16).
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_close, to_np
+from oracle import sparse_attn as osa
+
+pytestmark = pytest.mark.gpu
+
+
+def _hip():
+    from maba_sparse.kernels import hip_backend
+    return hip_backend
+
+
+def _case(B, H, Lq, Lkv, dh, K, seed, shared=False, gate4=False, dup=False):
+    g = torch.Generator().manual_seed(seed)
+    bf = lambda *s: torch.randn(*s, generator=g).bfloat16()  # noqa: E731
+    q, k, v = bf(B, H, Lq, dh), bf(B, H, Lkv, dh), bf(B, H, Lkv, dh)
+    nc = Lkv // 64
+    kh, vh = (bf(B, H, nc, dh), bf(B, H, nc, dh)) if nc > 0 else (None, None)
+    off = Lkv - Lq
+    n_early = max(0, min(Lq, 63 - off))
+    early = bf(B, H, n_early, dh) if n_early > 0 else None
+    nb = (Lkv + 63) // 64
+    rows = 1 if shared else Lq
+    idx = torch.randint(0, nb, (B, rows, K), generator=g)
+    idx[:, :, 0] = -1 if K > 2 else idx[:, :, 0]             # an empty slot (ignored)
+    if dup and K > 2:
+        idx[:, ::3, 2] = idx[:, ::3, 1]                        # repeated blocks count twice
+    gate = torch.randn(B, H, Lq, 3, generator=g) if gate4 else torch.randn(B, Lq, 3, generator=g)
+    return q, k, v, kh, vh, early, idx, gate
+
+
+@pytest.mark.parametrize("B,H,Lq,Lkv,dh,K,window,n_sink,shared,gate4,dup", [
+    (2, 3, 150, 150, 64, 4, 128, 4, False, False, True),   # early rows, one complete mean, repeats
+    (1, 2, 77, 300, 64, 8, 40, 2, False, True, False),     # a past, per-head gates, narrow window
+    (2, 2, 64, 64, 32, 3, 16, 0, True, False, False),      # d_head 32, one index row for all queries
+    (1, 2, 40, 40, 128, 2, 128, 4, False, False, False),   # d_head 128, no complete block: all early
+    (1, 4, 1000, 1000, 64, 32, 128, 4, False, False, True),
+    (1, 2, 700, 2000, 64, 16, 300, 70, False, False, False),  # sinks wider than one tile
+])
+def test_maba_sa_prefill(dev, B, H, Lq, Lkv, dh, K, window, n_sink, shared, gate4, dup):
+    q, k, v, kh, vh, early, idx, gate = _case(B, H, Lq, Lkv, dh, K, Lq + Lkv + dh, shared, gate4, dup)
+    d = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    out = _hip().hip_maba_sa_prefill(d(q), d(k), d(v), d(kh), d(vh), d(early), d(idx), d(gate),
+                                     scale=dh ** -0.5, window=window, n_sink=n_sink, out_dtype=torch.float32)
+    exp = osa.maba_sa_prefill_heads(to_np(q), to_np(k), to_np(v), to_np(kh), to_np(vh), to_np(early), idx.numpy(),
+                                    to_np(gate), window=window, n_sink=n_sink, scale=dh ** -0.5)
+    assert_close(out, exp, 2e-3, 2e-3, "maba_sa_prefill")
+    out_bf = _hip().hip_maba_sa_prefill(d(q), d(k), d(v), d(kh), d(vh), d(early), d(idx), d(gate),
+                                        scale=dh ** -0.5, window=window, n_sink=n_sink)
+    assert out_bf.dtype == torch.bfloat16
+    assert torch.equal(out_bf, out.bfloat16())   # the bf16 output is the fp32 result rounded once
+
+
+def test_maba_sa_prefill_long_against_torch_reference(dev):
+    """4,096 queries over their own 4,096 keys with 32 causal blocks each, against the torch
+    reference op on the GPU (dense masks, fp32)."""
+    from maba_sparse.kernels import common as C
+    B, H, L, dh, K = 1, 4, 4096, 64, 32
+    q, k, v, kh, vh, early, _, gate = _case(B, H, L, L, dh, K, 5)
+    g = torch.Generator().manual_seed(6)
+    pos_blk = torch.arange(L) // 64
+    idx = (torch.rand(B, L, K, generator=g) * (pos_blk[None, :, None] + 1).float()).long()   # causal blocks
+    d = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    args = [d(t) for t in (q, k, v, kh, vh, early, idx, gate)]
+    out = _hip().hip_maba_sa_prefill(*args, scale=0.125, out_dtype=torch.float32)
+    ref = C.ref_maba_sa_prefill(*args, scale=0.125, out_dtype=torch.float32)
+    assert_close(out, to_np(ref), 2e-3, 2e-3, "maba_sa_prefill 4k")
+
+
+def test_layer_prefill_fused_matches_dense_path(dev):
+    """The bf16 MabaSparseAttention prefill through the HIP kernel against the same layer's
+    dense torch path, then decode steps continue from either."""
+    from maba_sparse.layers import MabaSparseAttention
+    torch.manual_seed(8)
+    layer = MabaSparseAttention(dim=256, n_heads=4, d_head=64, d_c=64, d_idx=32, top_k=8,
+                                dist_lambda=0.1).to(dev, torch.bfloat16).eval()
+    dense = copy.deepcopy(layer)
+    dense._prefill_fusable = lambda *a: False
+    x = torch.randn(2, 700, 256, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        yf, cf = layer(x)
+        yd, cd = dense(x)
+        assert torch.equal(cf, cd)
+        err = (yf.float() - yd.float()).abs().max().item()
+        assert err <= 3e-2 * yd.float().abs().max().item(), err

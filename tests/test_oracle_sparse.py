@@ -10,6 +10,7 @@ latent-absorption identity the HIP kernel relies on.
 import math
 
 import numpy as np
+import pytest
 
 from oracle import sparse_attn as osa
 
@@ -123,3 +124,45 @@ def test_latent_absorption_identity():
                 z += g[b, s] * (p @ rows)
             got[b, h] = Wv_h[h] @ z
     assert np.allclose(got, exp, rtol=1e-12, atol=1e-12)
+
+
+# ----------------------------------------------------------------------------- prefill streams
+
+@pytest.mark.parametrize("Lkv,Lq,window,n_sink,K", [(150, 150, 128, 4, 3), (300, 77, 40, 2, 4),
+                                                    (70, 70, 16, 0, 2), (500, 33, 128, 4, 5)])
+def test_prefill_rows_equal_decode_at_each_prefix(Lkv, Lq, window, n_sink, K):
+    """A decode step is the last row of a prefill: every prefill row equals the decode oracle
+    run on the prefix that ends at its position, with that row's blocks and gate."""
+    rng = np.random.default_rng(Lkv + Lq)
+    B, H, dh, dc = 2, 3, 8, 12
+    c = rng.standard_normal((B, Lkv, dc))
+    Wk = rng.standard_normal((H * dh, dc)) * 0.3
+    Wv = rng.standard_normal((H * dh, dc))
+    q = rng.standard_normal((B, H, Lq, dh))
+    nb = (Lkv + 63) // 64
+    idx = rng.integers(0, nb, size=(B, Lq, K))
+    idx[0, 0, 1] = idx[0, 0, 0]                     # a repeated block counts twice
+    gate = rng.standard_normal((B, Lq, 3))
+    got = osa.maba_sa_prefill(q, c, Wk, Wv, idx, gate, window=window, n_sink=n_sink)
+    off = Lkv - Lq
+    for t in range(Lq):
+        L = off + t + 1
+        exp = osa.maba_sa_decode(q[:, :, t], c[:, :L], Wk, Wv, idx[:, t:t + 1], gate[:, t], window=window,
+                                 n_sink=n_sink)
+        assert np.allclose(got[:, :, t], exp, rtol=1e-10, atol=1e-12), t
+
+
+def test_prefill_full_window_is_causal_attention():
+    """With the window covering everything, no selected blocks and the local gate saturated,
+    the prefill is plain causal softmax attention."""
+    rng = np.random.default_rng(9)
+    B, H, L, dh = 1, 2, 40, 4
+    q, k, v = (rng.standard_normal((B, H, L, dh)) for _ in range(3))
+    idx = np.full((B, L, 1), 10**6)                 # out-of-range block: empty sparse stream
+    gate = np.zeros((B, L, 3)); gate[..., 0] = 60.0
+    got = osa.maba_sa_prefill_heads(q, k, v, None, None, np.zeros((B, H, L, dh)), idx, gate, window=L)
+    s = np.einsum("bhtd,bhjd->bhtj", q, k) / 2.0
+    s = np.where(np.tril(np.ones((L, L)))[None, None] > 0, s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    exp = np.einsum("bhtj,bhjd->bhtd", p / p.sum(-1, keepdims=True), v)
+    assert np.allclose(got, exp, atol=1e-9)
