@@ -264,6 +264,19 @@ def cpu_row_baselines(min_seconds: float = 2.0):
                                   "kind": "port",
                                   "sample": f"B=1, 512 of the 32,768 tokens (C=640), {reps} repeats in {dt:.1f} s, "
                                             f"scaled by 256 to the B=4 call; oracle/dgda.py layer_prologue (numpy fp64)"}
+    # MABA-SA prefill streams: the last 128 of the 32,768 queries of one head, scaled by 256 x 10 heads
+    Lp, dhp, Kp = 32768, 64, 32
+    qp1 = r.standard_normal((1, 1, 128, dhp)); kp1 = r.standard_normal((1, 1, Lp, dhp))
+    vp1 = r.standard_normal((1, 1, Lp, dhp))
+    khp = r.standard_normal((1, 1, Lp // 64, dhp)); vhp = r.standard_normal((1, 1, Lp // 64, dhp))
+    idxp = r.integers(0, Lp // 64, size=(1, 128, Kp))
+    gp = r.standard_normal((1, 128, 3))
+    reps, dt = _timed(lambda: osa.maba_sa_prefill_heads(qp1, kp1, vp1, khp, vhp, None, idxp, gp), min_seconds)
+    out["maba_sa_prefill_32k"] = {"value": dt / reps * 1e3 * (Lp / 128) * 10, "unit": "ms/call", "cores": blas,
+                                  "kind": "port",
+                                  "sample": f"the last 128 of 32,768 queries of one head, {reps} repeats in "
+                                            f"{dt:.1f} s, scaled by 256 x 10 heads; oracle/sparse_attn.py "
+                                            f"maba_sa_prefill_heads (numpy fp64)"}
     # causal prefill index_topk: 4,096 of the 32,768 queries against 512 centroids, d=128
     Lq, nbp = 4096, 512
     qp = r.standard_normal((1, Lq, dc)); cp = r.standard_normal((1, nbp, dc))
@@ -446,8 +459,37 @@ def row_benches(dev):
                                    "config": "o_* [1,10,32768,64] bf16, gate logits [1,32768,3] bf16"}
     log(f"stream superposition 1x10x32768x64: {ms * 1e3:.1f} us")
     del ol, os_, oh, gl
+    out.update(prefill_attention_bench(dev))
     out["maba_sa_layer_decode_1M"] = layer_decode_bench(dev)
     return out
+
+
+def prefill_attention_bench(dev, B=1, H=10, L=32768, dh=64, K=32):
+    """MABA-SA prefill streams (local + sparse + HCA + gate) for a 32k-token sequence: per-head
+    bf16 q/k/v, up-projected means, and each query's top-32 blocks from the HIP causal
+    index_topk over random queries and centroids (lambda 0.5, the layer's default)."""
+    import torch
+    from maba_sparse.kernels import hip_backend as hb
+    g = torch.Generator(device=dev).manual_seed(21)
+    bf = lambda *sh: torch.randn(*sh, device=dev, generator=g, dtype=torch.bfloat16)  # noqa: E731
+    q, k, v = bf(B, H, L, dh), bf(B, H, L, dh), bf(B, H, L, dh)
+    kh, vh = bf(B, H, L // 64, dh), bf(B, H, L // 64, dh)
+    early = bf(B, H, 63, dh)
+    gate = torch.randn(B, L, 3, device=dev, generator=g)
+    idx = hb.hip_index_topk(bf(B, L, 64), bf(B, L // 64, 64), lambda_dist=0.5, top_k=K, block_size=64)
+
+    def call():
+        return hb.hip_maba_sa_prefill(q, k, v, kh, vh, early, idx, gate, scale=dh ** -0.5)
+
+    ms, _ = time_op(call, 5, 1)
+    # distinct blocks per 16-query wave: the sparse stream's tiles
+    u = idx.view(B, L // 16, 16 * K).sort(dim=-1).values
+    distinct = (u[..., 1:] != u[..., :-1]).sum(-1).float().mean().item() + 1
+    log(f"MABA-SA prefill streams 32k: {ms:.3f} ms ({distinct:.0f} distinct blocks per 16 queries)")
+    return {"maba_sa_prefill_32k": {
+        "ms_per_call": ms, "queries_per_s": B * L / (ms * 1e-3), "sparse_blocks_per_wave": distinct,
+        "config": "B=1 H=10 L=32768 d_head=64 bf16, window 128 + 4 sinks, top-32 causal blocks per query from "
+                  "index_topk (lambda 0.5), 512 HCA means, one launch with the gate"}}
 
 
 def prologue_benches(dev, B=4, T=32768, dim=640, H=10):
