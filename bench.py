@@ -62,6 +62,10 @@ def parse():
     ap.add_argument("--only-decode", action="store_true", help="run only the decode benchmarks (for profiling)")
     ap.add_argument("--only-rows", action="store_true",
                     help="run only the secondary row benchmarks: per-channel-gate prefill, prefill top-k (for profiling)")
+    ap.add_argument("--only-model", action="store_true", help="run only the config-5 full-model decode")
+    ap.add_argument("--model-batch", type=int, default=16)
+    ap.add_argument("--model-prefill", type=int, default=131072)
+    ap.add_argument("--model-steps", type=int, default=256)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 256 MiB device-to-device copy (calibrates FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
@@ -277,6 +281,22 @@ def cpu_row_baselines(min_seconds: float = 2.0):
                                   "sample": f"the last 128 of 32,768 queries of one head, {reps} repeats in "
                                             f"{dt:.1f} s, scaled by 256 x 10 heads; oracle/sparse_attn.py "
                                             f"maba_sa_prefill_heads (numpy fp64)"}
+    # config 5 on the host: the same 101M stack in fp32 through the dispatcher's torch reference
+    # ops (the reference's own CPU path), B=1, a 256-token prefill, then 8 greedy steps
+    import torch
+    from maba_sparse.model import MabaSparseForCausalLM, get_101m_config
+    torch.manual_seed(0)
+    cm = MabaSparseForCausalLM(get_101m_config()).init_normal(0.02).eval()
+    cids = torch.randint(0, 32768, (1, 256))
+    marks = []
+    t0 = time.perf_counter()
+    cm.generate_greedy(cids, 9, on_prefill_done=lambda: marks.append(time.perf_counter()))
+    t1 = time.perf_counter()
+    out["model_decode_config5"] = {"value": (t1 - marks[0]) / 8 * 1e3, "unit": "ms/token", "cores": torch.get_num_threads(),
+                                   "kind": "port",
+                                   "sample": f"B=1, 256-token prefill ({marks[0] - t0:.1f} s), then 8 greedy steps; the "
+                                             f"same stack in fp32 on the host through the torch reference ops"}
+    del cm
     # causal prefill index_topk: 4,096 of the 32,768 queries against 512 centroids, d=128
     Lq, nbp = 4096, 512
     qp = r.standard_normal((1, Lq, dc)); cp = r.standard_normal((1, nbp, dc))
@@ -461,6 +481,7 @@ def row_benches(dev):
     del ol, os_, oh, gl
     out.update(prefill_attention_bench(dev))
     out["maba_sa_layer_decode_1M"] = layer_decode_bench(dev)
+    out.update(model_decode_bench(dev))
     return out
 
 
@@ -539,6 +560,39 @@ def prologue_benches(dev, B=4, T=32768, dim=640, H=10):
     return out
 
 
+def model_decode_bench(dev, B=16, L=131072, steps=256):
+    """the 101M Maba v2 stack (20 layers, 15 DGDA + 5 MABA-SA) in bf16 with
+    N(0, 0.02) random weights, a prefill of B x L uniform random token ids, then greedy decode
+    (one token from the prefill logits, steps - 1 single-token steps over the decode caches)."""
+    import torch
+    from maba_sparse.model import MabaSparseForCausalLM, get_101m_config
+    torch.manual_seed(0)
+    model = MabaSparseForCausalLM(get_101m_config()).init_normal(0.02).to(dev, torch.bfloat16).eval()
+    ids = torch.randint(0, model.config.vocab_size, (B, L), device=dev)
+    marks = []
+
+    def mark():
+        torch.cuda.synchronize()
+        marks.append(time.perf_counter())
+
+    mark()
+    toks = model.generate_greedy(ids, steps, on_prefill_done=mark)
+    mark()
+    prefill_s, decode_s = marks[1] - marks[0], marks[2] - marks[1]
+    per_step = decode_s / max(steps - 1, 1)
+    log(f"model config 5: prefill {prefill_s:.2f} s ({B * L / prefill_s / 1e6:.2f} M tok/s), decode "
+        f"{per_step * 1e3:.2f} ms/step ({B / per_step:.0f} tok/s)")
+    out = {"model_decode_config5": {
+        "ms_per_token": per_step * 1e3, "tokens_per_s": B / per_step, "decode_steps": steps - 1,
+        "prefill_s": prefill_s, "prefill_tokens_per_s": B * L / prefill_s, "first_tokens": toks[0, :4].tolist(),
+        "config": f"101M Maba v2 (20 layers, 3:1 DGDA:MABA-SA, d_model 640, factorised 32768->128->640 "
+                  f"embedding, SwiGLU 1248, RMSNorm), bf16 weights ~N(0,0.02), B={B}, prefill {L} uniform "
+                  f"random ids, {steps} greedy tokens (one from the prefill, {steps - 1} decode steps), eager"}}
+    del model, ids
+    torch.cuda.empty_cache()
+    return out
+
+
 def layer_decode_bench(dev, B=8, L0=1_000_000 - 10, steps=20):
     """The MABA-SA layer's decode step (layers/sparse_attention.py:221-277 orchestration):
     latent append, indexer (projections, key/centroid cache, decode top-32), the fused
@@ -607,6 +661,10 @@ def main():
         return
     if args.only_rows:
         print(json.dumps({"rows": row_benches(dev)}), flush=True)
+        return
+    if args.only_model:
+        print(json.dumps({"rows": model_decode_bench(dev, args.model_batch, args.model_prefill, args.model_steps)}),
+              flush=True)
         return
     B, H, T, d = 4, 10, 32768, 64
     inp = dgda_prefill_case(dev, B, H, T, d)

@@ -1,0 +1,211 @@
+"""The Maba v2 causal LM around the hot-path layers: the full-model decode harness.
+
+Mirrors ``maba_sparse/model.py`` of the reference (``:11-313``): RMSNorm, SwiGLU FFN,
+factorised embeddings tied to the LM head, blocks in a 3:1 pattern (every fourth block
+is MABA-SA, the others DGDA) with sigmoid-gated residuals, ``forward`` (prefill, returning
+per-layer states) and ``step`` (one token).  ``generate_greedy`` is the serving loop: one
+prefill, then single-token steps in which the DGDA blocks carry their recurrent and conv
+states and the MABA-SA blocks decode over a preallocated ``LatentCache`` (incremental
+latent rows, HCA means and indexer centroids) instead of the reference's per-step
+``torch.cat`` of the whole cache (``model.py:280-313`` with ``sparse_attention.py:241-261``).
+The multi-token-prediction head and the loss are training-side and are not built here.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from maba_sparse.layers.dgda import DGDALayer
+from maba_sparse.layers.sparse_attention import LatentCache, MabaSparseAttention
+
+
+@dataclass
+class MabaConfig:
+    """The fields of the reference's ``MabaSparseConfig`` (config.py:5-38) the stack reads."""
+    dim: int = 640
+    n_layers: int = 20
+    n_heads: int = 10
+    d_head: int = 64
+    vocab_size: int = 32768
+    d_emb: int = 128
+    kernel_size: int = 4
+    chunk_size: int = 16
+    eps: float = 1e-6
+    d_c: int = 128
+    d_idx: int = 64
+    block_size: int = 64
+    window_size: int = 128
+    top_k: int = 32
+    hca_pool_size: int = 64
+    dist_lambda: float = 0.5
+    intermediate_size: int = 1248
+    rms_norm_eps: float = 1e-6
+    residual_gate_bias: float = 2.0
+
+
+def get_101m_config(**overrides: Any) -> MabaConfig:
+    """The 101M configuration (reference model.py:165-181): 20 layers, d_model 640, 10 heads,
+    factorised 32768 -> 128 -> 640 embedding, SwiGLU width 1248."""
+    return MabaConfig(**overrides)
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.dim = dim
+        self.eps = max(float(eps), 1e-6)
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.rms_norm(x, (self.dim,), self.weight, eps=self.eps)
+
+
+class SwiGLUFFN(nn.Module):
+    def __init__(self, dim: int, intermediate_size: int) -> None:
+        super().__init__()
+        self.w_gate = nn.Linear(dim, intermediate_size, bias=False)
+        self.w_up = nn.Linear(dim, intermediate_size, bias=False)
+        self.w_down = nn.Linear(intermediate_size, dim, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.w_down(F.silu(self.w_gate(x)) * self.w_up(x))
+
+
+class FactorizedEmbeddings(nn.Module):
+    def __init__(self, vocab_size: int, d_emb: int, dim: int) -> None:
+        super().__init__()
+        self.in_emb = nn.Embedding(vocab_size, d_emb)
+        self.proj = nn.Linear(d_emb, dim, bias=False)
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        return self.proj(self.in_emb(input_ids))
+
+
+class MabaBlock(nn.Module):
+    def __init__(self, config: MabaConfig, layer_idx: int) -> None:
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.is_attention = (layer_idx + 1) % 4 == 0
+        self.norm1 = RMSNorm(config.dim, eps=config.rms_norm_eps)
+        self.mixer = MabaSparseAttention(config) if self.is_attention else DGDALayer(config)
+        self.norm2 = RMSNorm(config.dim, eps=config.rms_norm_eps)
+        self.ffn = SwiGLUFFN(config.dim, config.intermediate_size)
+        self.res_gate1 = nn.Parameter(torch.full((config.dim,), config.residual_gate_bias))
+        self.res_gate2 = nn.Parameter(torch.full((config.dim,), config.residual_gate_bias))
+
+    def _residual(self, x: torch.Tensor, mo: torch.Tensor) -> torch.Tensor:
+        x = x + torch.sigmoid(self.res_gate1) * mo
+        return x + torch.sigmoid(self.res_gate2) * self.ffn(self.norm2(x))
+
+    def forward(self, x, state=None, conv_state=None, past_c_kv=None):
+        h = self.norm1(x)
+        if self.is_attention:
+            mo, nc = self.mixer(h, past_c_kv=past_c_kv)
+            return self._residual(x, mo), None, None, nc
+        mo, ns, ncv = self.mixer(h, state=state, conv_state=conv_state)
+        return self._residual(x, mo), ns, ncv, None
+
+    def step(self, x, state=None, conv_state=None, past_c_kv=None):
+        h = self.norm1(x)
+        if self.is_attention:
+            mo, nc = self.mixer(h, past_c_kv=past_c_kv)
+            return self._residual(x, mo), None, None, nc
+        mo, ns, ncv = self.mixer.step(h, state=state, conv_state=conv_state)
+        return self._residual(x, mo), ns, ncv, None
+
+    def decode(self, x, state=None, conv_state=None, cache: Optional[LatentCache] = None):
+        """One token: DGDA blocks carry (state, conv_state); MABA-SA blocks append to and
+        decode over ``cache``."""
+        h = self.norm1(x)
+        if self.is_attention:
+            return self._residual(x, self.mixer.decode_step(h, cache)), None, None
+        mo, ns, ncv = self.mixer.step(h, state=state, conv_state=conv_state)
+        return self._residual(x, mo), ns, ncv
+
+
+class MabaSparseForCausalLM(nn.Module):
+    def __init__(self, config: Optional[MabaConfig] = None) -> None:
+        super().__init__()
+        self.config = config or get_101m_config()
+        c = self.config
+        self.embeddings = FactorizedEmbeddings(c.vocab_size, c.d_emb, c.dim)
+        self.layers = nn.ModuleList([MabaBlock(c, i) for i in range(c.n_layers)])
+        self.final_norm = RMSNorm(c.dim, eps=c.rms_norm_eps)
+        self.head_proj = nn.Linear(c.dim, c.d_emb, bias=False)
+        self.lm_head = nn.Linear(c.d_emb, c.vocab_size, bias=False)
+        self.lm_head.weight = self.embeddings.in_emb.weight      # tied (model.py:205)
+
+    def init_normal(self, std: float = 0.02) -> "MabaSparseForCausalLM":
+        """Every weight matrix and embedding ~ N(0, std) (the BASELINE's random init); norms,
+        biases and residual gates keep their constructor values."""
+        with torch.no_grad():
+            for m in self.modules():
+                if isinstance(m, (nn.Linear, nn.Embedding)):
+                    m.weight.normal_(0.0, std)
+        return self
+
+    def _logits(self, x: torch.Tensor) -> torch.Tensor:
+        return self.lm_head(self.head_proj(self.final_norm(x)))
+
+    def forward(self, input_ids: torch.Tensor, past_states: Optional[List[Any]] = None):
+        """Prefill: ``(logits, past_states)`` with ``(state, conv_state, c_kv)`` per block
+        (reference model.py:207-234; the loss and MTP head are left out)."""
+        x = self.embeddings(input_ids)
+        nps = []
+        for i, layer in enumerate(self.layers):
+            st, cv, pk = past_states[i] if past_states is not None else (None, None, None)
+            x, nst, ncv, nck = layer(x, state=st, conv_state=cv, past_c_kv=pk)
+            nps.append((nst, ncv, nck))
+        return self._logits(x), nps
+
+    def step(self, input_ids: torch.Tensor, past_states: Optional[List[Any]] = None):
+        """One token with the reference's state passing (model.py:251-270)."""
+        if input_ids.shape[1] != 1:
+            raise ValueError(f"step() expects single-token input (L=1), got L={input_ids.shape[1]}")
+        x = self.embeddings(input_ids)
+        nps = []
+        for i, layer in enumerate(self.layers):
+            st, cv, pk = past_states[i] if past_states is not None else (None, None, None)
+            x, nst, ncv, nck = layer.step(x, state=st, conv_state=cv, past_c_kv=pk)
+            nps.append((nst, ncv, nck))
+        return self._logits(x), nps
+
+    @torch.no_grad()
+    def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
+                        on_prefill_done=None) -> torch.Tensor:
+        """Greedy decoding (reference model.py:272-305 at temperature 0): one prefill, then
+        ``max_new_tokens - 1`` single-token steps over per-layer decode caches.  Returns the
+        new tokens ``[B, max_new_tokens]``.  ``on_prefill_done()`` runs between the two phases
+        (a timing hook)."""
+        B, L = input_ids.shape
+        logits, states = self(input_ids)
+        caches: List[Optional[LatentCache]] = []
+        for layer, (_, _, c_kv) in zip(self.layers, states):
+            if layer.is_attention:
+                cache = LatentCache(B, L + max_new_tokens, self.config.d_c, pool=self.config.hca_pool_size,
+                                    device=input_ids.device, dtype=c_kv.dtype)
+                cache.append(c_kv)
+                caches.append(cache)
+            else:
+                caches.append(None)
+        if on_prefill_done is not None:
+            on_prefill_done()
+        tok = logits[:, -1].argmax(dim=-1, keepdim=True)
+        out = [tok]
+        for _ in range(max_new_tokens - 1):
+            x = self.embeddings(tok)
+            for i, layer in enumerate(self.layers):
+                st, cv, _ = states[i]
+                x, nst, ncv = layer.decode(x, state=st, conv_state=cv, cache=caches[i])
+                states[i] = (nst, ncv, None)
+            tok = self._logits(x)[:, -1].argmax(dim=-1, keepdim=True)
+            out.append(tok)
+        return torch.cat(out, dim=1)
+
+
+MabaSparseLM = MabaSparseForCausalLM
+MabaLM = MabaSparseForCausalLM

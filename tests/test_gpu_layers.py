@@ -91,3 +91,35 @@ def test_maba_sa_layer_bf16_latent_cache(dev):
             ref = yc.numpy()
             err = np.abs(yg.float().cpu().numpy() - ref).max() / max(np.abs(ref).max(), 1e-6)
             assert err < 5e-2, (t, err)
+
+
+def test_model_harness_gpu(dev):
+    """The full-model harness on the GPU: fp32 prefill logits against the CPU model, the
+    LatentCache serving loop against the reference-style state passing (same tokens), and a
+    bf16 run through the fused prologue, prefill-attention and decode kernels."""
+    from maba_sparse.model import MabaSparseForCausalLM, get_101m_config
+    torch.manual_seed(0)
+    cfg = get_101m_config(dim=128, n_layers=4, n_heads=2, d_head=64, vocab_size=97, d_emb=16, d_c=32, d_idx=16,
+                          intermediate_size=96, top_k=4, dist_lambda=0.1)
+    cpu = MabaSparseForCausalLM(cfg).init_normal(0.02).eval()
+    gpu = copy.deepcopy(cpu).to(dev)
+    ids = torch.randint(0, 97, (2, 300), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        lc, _ = cpu(ids)
+        lg, states = gpu(ids.to(dev))
+        scale = lc.abs().max().item()
+        assert (lg.cpu() - lc).abs().max().item() <= 2e-3 * scale
+        got = gpu.generate_greedy(ids.to(dev), 10)
+        tok = lg[:, -1].argmax(-1, keepdim=True)
+        ref = [tok]
+        for _ in range(9):
+            lg, states = gpu.step(tok, past_states=states)
+            tok = lg[:, -1].argmax(-1, keepdim=True)
+            ref.append(tok)
+        assert torch.equal(got, torch.cat(ref, dim=1))
+        bf = copy.deepcopy(cpu).to(dev, torch.bfloat16)
+        lb, _ = bf(ids.to(dev))
+        assert torch.isfinite(lb.float()).all()
+        assert (lb.float().cpu() - lc).abs().max().item() <= 0.1 * scale
+        toks = bf.generate_greedy(ids.to(dev), 6)
+        assert toks.shape == (2, 6) and int(toks.min()) >= 0 and int(toks.max()) < 97
