@@ -147,9 +147,13 @@ class DGDALayer(nn.Module):
         B, L, _ = x.shape
         H, dk = self.n_heads, self.d_k
         C = H * dk
-        W = torch.cat([m.weight for m in (self.q_proj, self.k_proj, self.v_proj, self.gate_alpha,
-                                          self.gate_erase, self.gate_write)], dim=0)
-        projs = F.linear(x, W.to(x.dtype)).split(C, dim=-1)   # [B, L, C] views, row stride 6C
+        ws = [m.weight for m in (self.q_proj, self.k_proj, self.v_proj, self.gate_alpha, self.gate_erase,
+                                 self.gate_write)]
+        tag = tuple((w.data_ptr(), w._version) for w in ws) + (x.dtype,)
+        if getattr(self, "_w6_tag", None) != tag:   # restack only after the weights change
+            self._w6 = torch.cat(ws, dim=0).to(x.dtype)
+            self._w6_tag = tag
+        projs = F.linear(x, self._w6).split(C, dim=-1)   # [B, L, C] views, row stride 6C
         kh = self.kernel_size - 1
         hist = None
         if hists[0] is not None:

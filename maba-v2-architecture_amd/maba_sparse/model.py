@@ -64,6 +64,19 @@ class RMSNorm(nn.Module):
         return F.rms_norm(x, (self.dim,), self.weight, eps=self.eps)
 
 
+def _frozen(module: nn.Module, key: str, fn, *params: torch.Tensor) -> torch.Tensor:
+    """``fn(*params)``, kept on ``module`` until a parameter changes (an in-place update bumps
+    its version counter).  For inference: under autograd the value is recomputed."""
+    if torch.is_grad_enabled() and any(p.requires_grad for p in params):
+        return fn(*params)
+    tag = tuple((p.data_ptr(), p._version, p.dtype) for p in params)
+    held = module.__dict__.get("_frozen_" + key)
+    if held is None or held[0] != tag:
+        held = (tag, fn(*params))
+        module.__dict__["_frozen_" + key] = held
+    return held[1]
+
+
 class SwiGLUFFN(nn.Module):
     def __init__(self, dim: int, intermediate_size: int) -> None:
         super().__init__()
@@ -72,7 +85,10 @@ class SwiGLUFFN(nn.Module):
         self.w_down = nn.Linear(intermediate_size, dim, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.w_down(F.silu(self.w_gate(x)) * self.w_up(x))
+        # gate and up projections as one GEMM over the stacked weights
+        w = _frozen(self, "gate_up", lambda a, b: torch.cat([a, b], dim=0), self.w_gate.weight, self.w_up.weight)
+        g, u = F.linear(x, w).chunk(2, dim=-1)
+        return self.w_down(F.silu(g) * u)
 
 
 class FactorizedEmbeddings(nn.Module):
@@ -98,8 +114,10 @@ class MabaBlock(nn.Module):
         self.res_gate2 = nn.Parameter(torch.full((config.dim,), config.residual_gate_bias))
 
     def _residual(self, x: torch.Tensor, mo: torch.Tensor) -> torch.Tensor:
-        x = x + torch.sigmoid(self.res_gate1) * mo
-        return x + torch.sigmoid(self.res_gate2) * self.ffn(self.norm2(x))
+        g1 = _frozen(self, "g1", torch.sigmoid, self.res_gate1)
+        g2 = _frozen(self, "g2", torch.sigmoid, self.res_gate2)
+        x = torch.addcmul(x, g1, mo)
+        return torch.addcmul(x, g2, self.ffn(self.norm2(x)))
 
     def forward(self, x, state=None, conv_state=None, past_c_kv=None):
         h = self.norm1(x)
