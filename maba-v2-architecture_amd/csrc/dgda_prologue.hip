@@ -50,11 +50,14 @@ template <> struct Pair<uint16_t> {   // bf16 bits
   }
 };
 
-__device__ __forceinline__ float pro_silu(float x) { return x / (1.f + expf(-x)); }
-__device__ __forceinline__ float pro_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
-// max(-softplus(x), -14) with torch's softplus (x itself above 20, where the clamp applies anyway)
+// Hardware exp2/rcp based forms (a few ulp in fp32; the outputs are then rounded to the
+// output dtype): the kernel issues seven transcendentals per channel and token.
+__device__ __forceinline__ float pro_silu(float x) { return __fdividef(x, 1.f + __expf(-x)); }
+__device__ __forceinline__ float pro_sigmoid(float x) { return __fdividef(1.f, 1.f + __expf(-x)); }
+// max(-softplus(x), -14) with torch's softplus (x itself above 20, where the clamp applies anyway);
+// log(1 + e^x) loses e^x below fp32's epsilon, an absolute error under 1.2e-7
 __device__ __forceinline__ float pro_log_decay(float x) {
-  const float sp = x > 20.f ? x : log1pf(expf(x));
+  const float sp = x > 20.f ? x : __logf(1.f + __expf(x));
   return fmaxf(-sp, -14.f);
 }
 
@@ -138,13 +141,13 @@ __global__ __launch_bounds__(512) void dgda_prologue_kernel(ProArgs a) {
       float ss = y[1][0] * y[1][0] + y[1][1] * y[1][1];
 #pragma unroll
       for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off);
-      const float kinv = 1.f / (sqrtf(ss) + a.eps);
+      const float kinv = __fdividef(1.f, sqrtf(ss) + a.eps);
       const float la0 = pro_log_decay(xv[3].x), la1 = pro_log_decay(xv[3].y);
       Pair<QT>::st(a.y[0], b * a.ysb[0] + t * a.ysl[0] + c, y[0][0], y[0][1]);
       Pair<QT>::st(a.y[1], b * a.ysb[1] + t * a.ysl[1] + c, y[1][0] * kinv, y[1][1] * kinv);
       Pair<QT>::st(a.y[2], b * a.ysb[2] + t * a.ysl[2] + c, y[2][0], y[2][1]);
       Pair<GT>::st(a.y[3], b * a.ysb[3] + t * a.ysl[3] + c, la0, la1);
-      if (a.y[4]) Pair<GT>::st(a.y[4], b * a.ysb[4] + t * a.ysl[4] + c, expf(la0), expf(la1));
+      if (a.y[4]) Pair<GT>::st(a.y[4], b * a.ysb[4] + t * a.ysl[4] + c, __expf(la0), __expf(la1));
       Pair<GT>::st(a.y[5], b * a.ysb[5] + t * a.ysl[5] + c, pro_sigmoid(xv[4].x), pro_sigmoid(xv[4].y));
       Pair<GT>::st(a.y[6], b * a.ysb[6] + t * a.ysl[6] + c, pro_sigmoid(xv[5].x), pro_sigmoid(xv[5].y));
     }
