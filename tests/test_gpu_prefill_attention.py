@@ -96,3 +96,22 @@ def test_layer_prefill_fused_matches_dense_path(dev):
         assert torch.equal(cf, cd)
         err = (yf.float() - yd.float()).abs().max().item()
         assert err <= 3e-2 * yd.float().abs().max().item(), err
+
+
+@pytest.mark.parametrize("Lq,Lkv,window,n_sink,empty_sparse", [
+    (1, 1, 128, 4, False),      # one token
+    (1, 500, 128, 4, False),    # one query over a past: a decode step
+    (50, 200, 0, 0, False),     # no local keys at all: the local stream contributes 0
+    (40, 100, 16, 200, True),   # sinks wider than the sequence; every index slot empty
+])
+def test_maba_sa_prefill_edges(dev, Lq, Lkv, window, n_sink, empty_sparse):
+    B, H, dh, K = 2, 2, 64, 4
+    q, k, v, kh, vh, early, idx, gate = _case(B, H, Lq, Lkv, dh, K, Lq * 7 + Lkv)
+    if empty_sparse:
+        idx[:] = -1
+    d = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    out = _hip().hip_maba_sa_prefill(d(q), d(k), d(v), d(kh), d(vh), d(early), d(idx), d(gate),
+                                     scale=0.125, window=window, n_sink=n_sink, out_dtype=torch.float32)
+    exp = osa.maba_sa_prefill_heads(to_np(q), to_np(k), to_np(v), to_np(kh), to_np(vh), to_np(early), idx.numpy(),
+                                    to_np(gate), window=window, n_sink=n_sink, scale=0.125)
+    assert_close(out, exp, 2e-3, 2e-3, "maba_sa_prefill edge")

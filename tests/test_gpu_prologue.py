@@ -63,3 +63,26 @@ def test_dgda_prologue_no_alpha_and_continuation(dev):
         assert torch.equal(torch.cat([a[j], b[j]], dim=1), full[j]), j
     for i in range(3):
         assert torch.equal(b[7][i], full[7][i])
+
+
+def test_dgda_prologue_empty_and_fp32_history(dev):
+    """L = 0 returns empty outputs and carries the history over unchanged; an fp32 history
+    with bf16 projections is read in its own dtype."""
+    B, H = 2, 2
+    C = 64 * H
+    g = torch.Generator().manual_seed(5)
+    ws = [(torch.randn(C, 1, 4, generator=g) * 0.4).to(dev) for _ in range(3)]
+    hist = [torch.randn(B, C, 3, generator=g).to(dev) for _ in range(3)]
+    xs0 = [torch.empty(B, 0, C, device=dev, dtype=torch.bfloat16) for _ in range(6)]
+    res = _hip().hip_dgda_prologue(xs0, ws, hist, n_heads=H)
+    assert res[0].shape == (B, 0, C)
+    for i in range(3):
+        assert torch.equal(res[7][i], hist[i])
+    xs = [torch.randn(B, 5, C, generator=g).bfloat16() for _ in range(6)]
+    res = _hip().hip_dgda_prologue([x.to(dev) for x in xs], ws, hist, n_heads=H, gate_dtype=torch.float32)
+    exp = od.layer_prologue(*[to_np(x) for x in xs], *[to_np(w[:, 0]) for w in ws], hist=[to_np(h) for h in hist],
+                            n_heads=H)
+    assert_close(res[0], exp[0], 5e-3, 1e-6, "q")
+    assert_close(res[3], exp[3], 1e-5, 1e-6, "log_alpha")
+    for i in range(3):
+        assert torch.equal(res[7][i].cpu(), torch.from_numpy(exp[7][i]).float()), i
