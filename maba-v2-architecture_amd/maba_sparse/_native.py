@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 import threading
 from typing import Optional, Sequence
 
@@ -120,29 +121,36 @@ def available() -> bool:
     return load(required=False) is not None
 
 
+_PAD_SHAPE = ((), (1,), (1, 1), (1, 1, 1), (1, 1, 1, 1))
+_PAD_STRIDE = ((), (0,), (0, 0), (0, 0, 0), (0, 0, 0, 0))
+_PACK = struct.Struct("<qii4q4q")   # maba_tensor: data, dtype, ndim, shape[4], stride[4]
+
+
+def _struct(t: torch.Tensor) -> MabaTensor:
+    """The ``maba_tensor`` of ``t`` (shape padded with 1, strides with 0, to four dims).  Packed in
+    one call and copied into the structure: it runs for every tensor of every op call, and
+    per-field ctypes assignments cost three times as much."""
+    nd = t.dim()
+    if nd > 4:
+        raise ValueError(f"descriptor supports at most 4 dims, got {nd}")
+    code = _DTYPE_CODES.get(t.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {t.dtype}")
+    return MabaTensor.from_buffer_copy(_PACK.pack(t.data_ptr() if t.numel() > 0 else 0, code, nd, *t.shape,
+                                                  *_PAD_SHAPE[4 - nd], *t.stride(), *_PAD_STRIDE[4 - nd]))
+
+
 def desc(t: Optional[torch.Tensor]):
     """Build a ``maba_tensor`` descriptor (pointer to it) for a tensor, or None."""
     if t is None:
         return None
-    if t.dim() > 4:
-        raise ValueError(f"descriptor supports at most 4 dims, got {t.dim()}")
-    code = _DTYPE_CODES.get(t.dtype)
-    if code is None:
-        raise TypeError(f"unsupported dtype {t.dtype}")
-    d = MabaTensor()
-    d.data = t.data_ptr() if t.numel() > 0 else 0
-    d.dtype = code
-    d.ndim = t.dim()
-    for k in range(4):
-        d.shape[k] = t.shape[k] if k < t.dim() else 1
-        d.stride[k] = t.stride(k) if k < t.dim() else 0
-    return ctypes.pointer(d)
+    return ctypes.byref(_struct(t))
 
 
 def desc_array(tensors: Sequence[Optional[torch.Tensor]]):
     """A C array of descriptor pointers (``const maba_tensor* const*``); None entries are NULL."""
     T = ctypes.POINTER(MabaTensor)
-    return (T * len(tensors))(*[desc(t) if t is not None else T() for t in tensors])
+    return (T * len(tensors))(*[ctypes.pointer(_struct(t)) if t is not None else T() for t in tensors])
 
 
 def stream_ptr(device: torch.device) -> int:
