@@ -403,19 +403,26 @@ def decode_benches(dev, steps: int):
     idx_bytes = B * nb * dc * 2
     nloc = 132
     sa_bytes = B * (hca.shape[1] * dc * 2 + H * K * 64 * dc * 2 + nloc * dc * 2)
-    out["index_topk_decode_1M"] = {"us_per_step": idx_ms * 1e3, "gbs": idx_bytes / (idx_ms * 1e-3) / 1e9,
-                                   "eager_us_per_step": idx_eager_ms * 1e3}
-    out["maba_sa_decode_1M"] = {"us_per_step": sa_ms * 1e3, "gbs": sa_bytes / (sa_ms * 1e-3) / 1e9,
-                                "eager_us_per_step": sa_eager_ms * 1e3, "index_sets": "per head [8,10,32]"}
+    # us_per_step: the faster of graph replay and back-to-back eager calls (events around the
+    # loop; the host enqueues ahead of the GPU, and the stream keeps steps from overlapping)
+    idx_us, sa_us = min(idx_ms, idx_eager_ms) * 1e3, min(sa_ms, sa_eager_ms) * 1e3
+    step_us = min(step_ms, step_eager_ms) * 1e3
+    timing = "the faster of HIP graph replay and back-to-back eager calls, events on the stream"
+    out["index_topk_decode_1M"] = {"us_per_step": idx_us, "gbs": idx_bytes / (idx_us * 1e-6) / 1e9,
+                                   "graph_us_per_step": idx_ms * 1e3, "eager_us_per_step": idx_eager_ms * 1e3,
+                                   "timing": timing}
+    out["maba_sa_decode_1M"] = {"us_per_step": sa_us, "gbs": sa_bytes / (sa_us * 1e-6) / 1e9,
+                                "graph_us_per_step": sa_ms * 1e3, "eager_us_per_step": sa_eager_ms * 1e3,
+                                "index_sets": "per head [8,10,32]", "timing": timing}
     tot_bytes = sa_bytes + idx_bytes
-    out["indexer_plus_maba_sa_1M"] = {"us_per_step": step_ms * 1e3, "gbs": tot_bytes / (step_ms * 1e-3) / 1e9,
-                                      "hbm_frac": tot_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                                      "algorithmic_bytes": tot_bytes,
+    out["indexer_plus_maba_sa_1M"] = {"us_per_step": step_us, "gbs": tot_bytes / (step_us * 1e-6) / 1e9,
+                                      "hbm_frac": tot_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                      "algorithmic_bytes": tot_bytes, "graph_us_per_step": step_ms * 1e3,
                                       "eager_us_per_step": step_eager_ms * 1e3,
-                                      "timing": "HIP graph replay of the two entry points, events on the stream"}
-    log(f"indexer decode 1M: {idx_ms * 1e3:.1f} us (eager {idx_eager_ms * 1e3:.1f})")
-    log(f"MABA-SA decode 1M: {sa_ms * 1e3:.1f} us (eager {sa_eager_ms * 1e3:.1f})")
-    log(f"indexer + MABA-SA decode step 1M: {step_ms * 1e3:.1f} us (eager {step_eager_ms * 1e3:.1f})")
+                                      "timing": timing + " (the two entry points per step)"}
+    log(f"indexer decode 1M: graph {idx_ms * 1e3:.1f} us, eager {idx_eager_ms * 1e3:.1f} us")
+    log(f"MABA-SA decode 1M: graph {sa_ms * 1e3:.1f} us, eager {sa_eager_ms * 1e3:.1f} us")
+    log(f"indexer + MABA-SA decode step 1M: graph {step_ms * 1e3:.1f} us, eager {step_eager_ms * 1e3:.1f} us")
     del c_kv
     return out
 
