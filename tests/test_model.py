@@ -36,3 +36,17 @@ def test_greedy_cache_loop_equals_state_passing():
             tok = logits[:, -1].argmax(-1, keepdim=True)
             ref.append(tok)
     assert torch.equal(got, torch.cat(ref, dim=1))
+
+
+def test_parameter_names_follow_reference_model():
+    """The names a reference state dict carries for these modules (model.py:62-205)."""
+    m = MabaSparseForCausalLM(get_101m_config(n_layers=4))
+    keys = set(m.state_dict())
+    for k in ("embeddings.in_emb.weight", "embeddings.proj.weight", "final_norm.weight", "head_proj.weight",
+              "lm_head.weight", "layers.0.norm1.weight", "layers.0.norm2.weight", "layers.0.res_gate1",
+              "layers.0.res_gate2", "layers.0.ffn.w_gate.weight", "layers.0.ffn.w_up.weight",
+              "layers.0.ffn.w_down.weight", "layers.0.mixer.q_proj.weight", "layers.0.mixer.conv_q.weight",
+              "layers.0.mixer.gate_alpha.weight", "layers.3.mixer.kv_down_proj.weight",
+              "layers.3.mixer.k_up_proj.weight", "layers.3.mixer.stream_gate.bias",
+              "layers.3.mixer.indexer.q_idx_proj.weight"):
+        assert k in keys, k
