@@ -650,7 +650,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); multi-GPU sharding is "
-              f"described in DESIGN.md but not launched", file=sys.stderr)
+              f"designed (per-GPU shards of (b, h) pairs, indexer blocks and decode segments) but not launched",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     from maba_sparse.kernels import hip_backend as hb
