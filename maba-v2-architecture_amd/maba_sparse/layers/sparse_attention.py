@@ -97,17 +97,29 @@ class MabaSparseAttention(nn.Module):
         return F.softmax(self.stream_gate(x), dim=-1)
 
     # ------------------------------------------------------------ decode (fused)
+    def _f32_heads(self, lin: nn.Linear, key: str) -> torch.Tensor:
+        """``lin.weight`` in fp32 as ``[H, d_head, d_c]``, converted again only after the weight
+        changes (decode calls this twice per token)."""
+        w = lin.weight
+        if torch.is_grad_enabled() and w.requires_grad:
+            return w.float().view(self.n_heads, self.d_head, self.d_c)
+        tag = (w.data_ptr(), w._version, w.dtype)
+        held = self.__dict__.get(key)
+        if held is None or held[0] != tag:
+            held = (tag, w.float().view(self.n_heads, self.d_head, self.d_c))
+            self.__dict__[key] = held
+        return held[1]
+
     def _absorbed_query(self, x: torch.Tensor) -> torch.Tensor:
         """``W_k,h^T q_h`` for the single token of ``x [B, 1, dim]`` -> ``[B, H, d_c]`` fp32."""
         B = x.shape[0]
         q = self.q_proj(x).view(B, self.n_heads, self.d_head).float()
-        Wk = self.k_up_proj.weight.float().view(self.n_heads, self.d_head, self.d_c)
-        return torch.einsum("bhd,hdc->bhc", q, Wk)
+        return torch.einsum("bhd,hdc->bhc", q, self._f32_heads(self.k_up_proj, "_wk_f32"))
 
     def _heads_out(self, z: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
         """``W_v,h z_h`` then ``o_proj``; ``z [B, H, d_c]`` -> ``[B, 1, dim]``."""
         B = z.shape[0]
-        Wv = self.v_up_proj.weight.float().view(self.n_heads, self.d_head, self.d_c)
+        Wv = self._f32_heads(self.v_up_proj, "_wv_f32")
         o = torch.einsum("bhc,hdc->bhd", z.float(), Wv).reshape(B, 1, self.n_heads * self.d_head)
         return self.o_proj(o.to(dtype))
 
