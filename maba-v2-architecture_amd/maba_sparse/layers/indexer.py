@@ -134,11 +134,18 @@ class DGIndexer(nn.Module):
     def forward(self, x: torch.Tensor, top_k: Optional[int] = None, dist_lambda: Optional[float] = None,
                 return_scores: bool = False, past_centroids: Optional[torch.Tensor] = None,
                 past_k_idx: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, ...]:
-        b, l, _ = x.shape
+        return self.forward_projected(self.q_idx_proj(x), self.k_idx_proj(x), top_k, dist_lambda, return_scores,
+                                      past_centroids, past_k_idx)
+
+    def forward_projected(self, qi: torch.Tensor, ki: torch.Tensor, top_k: Optional[int] = None,
+                          dist_lambda: Optional[float] = None, return_scores: bool = False,
+                          past_centroids: Optional[torch.Tensor] = None,
+                          past_k_idx: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, ...]:
+        """``forward`` from the query and key projections ``q_idx_proj(x)``, ``k_idx_proj(x)``
+        (a caller that projects the token once for several modules passes them in)."""
+        b, l, _ = qi.shape
         k = self.top_k if top_k is None else top_k
         lam = self.dist_lambda if dist_lambda is None else dist_lambda
-        qi = self.q_idx_proj(x)
-        ki = self.k_idx_proj(x)
         c = self._centroids(ki, past_centroids, past_k_idx)
         nb = c.shape[1]
         if l == 1 and (past_centroids is not None or past_k_idx is not None or nb > 1):

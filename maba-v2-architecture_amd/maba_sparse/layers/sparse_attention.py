@@ -138,21 +138,45 @@ class MabaSparseAttention(nn.Module):
         return self._hca_means.view()
 
     def _decode(self, x: torch.Tensor, c_all: torch.Tensor, L: int, hca: torch.Tensor,
-                idx: torch.Tensor) -> torch.Tensor:
-        z = dispatch_maba_sa_decode(self._absorbed_query(x), c_all, hca, idx, self.stream_gate(x).view(-1, 3),
+                idx: torch.Tensor, q: Optional[torch.Tensor] = None,
+                gate_logits: Optional[torch.Tensor] = None) -> torch.Tensor:
+        q_lat = self._absorbed_query(x) if q is None else torch.einsum(
+            "bhd,hdc->bhc", q.reshape(x.shape[0], self.n_heads, self.d_head).float(),
+            self._f32_heads(self.k_up_proj, "_wk_f32"))
+        gl = self.stream_gate(x) if gate_logits is None else gate_logits
+        z = dispatch_maba_sa_decode(q_lat, c_all, hca, idx, gl.view(-1, 3),
                                     L=L, scale=self.scale, window=self.window_size, n_sink=self.n_sink_tokens,
                                     block_size=self.block_size, pool=self.hca_pool_size)
         return self._heads_out(z, x.dtype)
+
+    def _token_projections(self, x: torch.Tensor):
+        """q, the new latent, the indexer's query and key and the gate logits of one token from
+        one GEMM over the stacked weights (the stack is rebuilt only after a weight changes)."""
+        mods = (self.q_proj, self.kv_down_proj, self.indexer.q_idx_proj, self.indexer.k_idx_proj, self.stream_gate)
+        ws = [m.weight for m in mods]
+        tag = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
+        if getattr(self, "_w5_tag", None) != tag:
+            self._w5 = torch.cat(ws, dim=0)
+            self._w5_tag = tag
+        sizes = [w.shape[0] for w in ws]
+        q, c_new, qi, ki, gl = F.linear(x, self._w5).split(sizes, dim=-1)
+        return q, c_new, qi, ki, gl + self.stream_gate.bias
 
     def decode_step(self, x: torch.Tensor, cache: LatentCache,
                     past_centroids: Optional[torch.Tensor] = None) -> torch.Tensor:
         """One decode token over a preallocated ``LatentCache`` (appends this token's latent)."""
         if x.shape[1] != 1:
             raise ValueError("decode_step takes one token")
-        cache.append(self.kv_down_proj(x))
-        idx, _ = self.indexer(x, return_scores=False, past_centroids=past_centroids)
+        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+            cache.append(self.kv_down_proj(x))
+            idx, _ = self.indexer(x, return_scores=False, past_centroids=past_centroids)
+            hca = cache.hca[:, : max(cache.nh, 1)]
+            return self._decode(x, cache.c, cache.n, hca, idx)
+        q, c_new, qi, ki, gl = self._token_projections(x)
+        cache.append(c_new)
+        idx, _ = self.indexer.forward_projected(qi, ki, return_scores=False, past_centroids=past_centroids)
         hca = cache.hca[:, : max(cache.nh, 1)]
-        return self._decode(x, cache.c, cache.n, hca, idx)
+        return self._decode(x, cache.c, cache.n, hca, idx, q=q, gate_logits=gl)
 
     # ------------------------------------------------------------ prefill (HIP)
     def _prefill_fusable(self, q: torch.Tensor, c_full: torch.Tensor, idx: torch.Tensor) -> bool:
