@@ -249,10 +249,12 @@ def hip_dgda_prologue(projections, conv_weights, history=None, n_heads: int = 10
         raise NotImplementedError("dgda_prologue: 64-channel heads and kernel 4 only")
     dt = projections[0].dtype
     gdt = gate_dtype or dt
-    new = lambda d: torch.empty(B, L, C, dtype=d, device=dev)  # noqa: E731
-    ys = [new(dt), new(dt), new(dt), new(gdt), new(gdt) if with_alpha else None, new(gdt), new(gdt)]
+    # three allocations, carved into the outputs (this runs once per layer and decode token)
+    qkv = torch.empty(3, B, L, C, dtype=dt, device=dev)
+    gates = torch.empty(4 if with_alpha else 3, B, L, C, dtype=gdt, device=dev)
+    ys = [qkv[0], qkv[1], qkv[2], gates[0], gates[3] if with_alpha else None, gates[1], gates[2]]
     hdt = history[0].dtype if history is not None else dt
-    nh = [torch.empty(B, C, 3, dtype=hdt, device=dev) for _ in range(3)]
+    nh = list(torch.empty(3, B, C, 3, dtype=hdt, device=dev).unbind(0))
     if L == 0:
         for h, old in zip(nh, history or (None,) * 3):
             h.copy_(old) if old is not None else h.zero_()
