@@ -13,6 +13,8 @@
 //  * the sub-chunk path (dgda_sub.hip) for per-channel gates (the DGDA layer's
 //    layout) with dk = dv = 64 and bf16 or fp32 q/k/v: 16-token sub-chunks with exact
 //    per-channel decay, the state products on MFMA, sequence-parallel like the above.
+#include <algorithm>
+
 #include "maba_common.h"
 
 namespace maba {
@@ -130,11 +132,12 @@ using namespace maba;
 extern "C" size_t maba_hip_dgda_prefill_workspace_size(const maba_tensor* q, const maba_tensor* v,
                                                       const maba_tensor* gate, const maba_tensor* b) {
   if (!q || q->ndim != 4 || !v || v->ndim != 4 || !gate || !b) return 0;
-  if (dgda_chunk_supported(q, q, v, gate, b)) return dgda_chunk_workspace(q->shape[0] * q->shape[1], q->shape[2]);
-  // the write gate and output layouts are checked again at the call; the size depends
-  // only on the shape
-  if (dgda_sub_supported(q, q, v, gate, b, nullptr, nullptr))
-    return dgda_sub_workspace(q->shape[0] * q->shape[1], q->shape[2]);
+  // The call picks its path from every operand (k, w and out included), which this query
+  // does not see.  Both workspace sizes depend only on the shape, so whenever q admits a
+  // workspace path the larger of the two is returned: the call's choice always fits.
+  const int64_t BH = q->shape[0] * q->shape[1], L = q->shape[2];
+  if (dgda_chunk_supported(q, q, v, gate, b) || dgda_sub_supported(q, q, v, gate, b, nullptr, nullptr))
+    return std::max(dgda_chunk_workspace(BH, L), dgda_sub_workspace(BH, L));
   return 0;
 }
 

@@ -567,8 +567,9 @@ extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tenso
   hipStream_t s = (hipStream_t)stream;
   const bool mfma_ok = q->dtype == MABA_BF16 && centroids->dtype == MABA_BF16 && q->stride[2] == 1 &&
                        centroids->stride[2] == 1 && d % 32 == 0 && d <= 256 && (uintptr_t)q->data % 16 == 0 &&
-                       (uintptr_t)centroids->data % 16 == 0 && q->stride[0] % 8 == 0 && q->stride[1] % 8 == 0 &&
-                       centroids->stride[0] % 8 == 0 && centroids->stride[1] % 8 == 0;
+                       (uintptr_t)centroids->data % 16 == 0 && (B == 1 || q->stride[0] % 8 == 0) &&
+                       (Hq == 1 || q->stride[1] % 8 == 0) && (B == 1 || centroids->stride[0] % 8 == 0) &&
+                       centroids->stride[1] % 8 == 0;
   if (mfma_ok) {
     DecTileArgs m;
     m.q = (const uint16_t*)q->data; m.qsb = q->stride[0]; m.qsh = q->stride[1];

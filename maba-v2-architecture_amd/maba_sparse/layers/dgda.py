@@ -24,6 +24,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from maba_sparse.layers._wcache import WeightCacheMixin, cached
 from maba_sparse.kernels.dispatcher import (dispatch_dgda_prefill, dispatch_dgda_prologue, dispatch_dgda_step,
                                             get_backend)
 
@@ -49,7 +50,7 @@ def _cfg(config: Any, names: Sequence[str], default: Any) -> Any:
     return default
 
 
-class DGDALayer(nn.Module):
+class DGDALayer(WeightCacheMixin, nn.Module):
     def __init__(self, config: Optional[Any] = None, dim: int = 640, n_heads: int = 10,
                  d_head: Optional[int] = None, kernel_size: int = 4, eps: float = 1e-6) -> None:
         super().__init__()
@@ -77,6 +78,7 @@ class DGDALayer(nn.Module):
             nn.init.xavier_uniform_(m.weight)
         for m in (self.conv_q, self.conv_k, self.conv_v):
             nn.init.normal_(m.weight, mean=0.0, std=0.02)
+        self._install_weight_cache_hooks()
 
     # reference aliases (layers/dgda.py:78-88)
     alpha_proj = property(lambda self: self.gate_alpha)
@@ -149,11 +151,9 @@ class DGDALayer(nn.Module):
         C = H * dk
         ws = [m.weight for m in (self.q_proj, self.k_proj, self.v_proj, self.gate_alpha, self.gate_erase,
                                  self.gate_write)]
-        tag = tuple((w.data_ptr(), w._version) for w in ws) + (x.dtype,)
-        if getattr(self, "_w6_tag", None) != tag:   # restack only after the weights change
-            self._w6 = torch.cat(ws, dim=0).to(x.dtype)
-            self._w6_tag = tag
-        projs = F.linear(x, self._w6).split(C, dim=-1)   # [B, L, C] views, row stride 6C
+        # restacked only after a weight changes (one stack per input dtype)
+        w6 = cached(self, f"w6_{x.dtype}", ws, lambda: torch.cat(ws, dim=0).to(x.dtype))
+        projs = F.linear(x, w6).split(C, dim=-1)   # [B, L, C] views, row stride 6C
         kh = self.kernel_size - 1
         hist = None
         if hists[0] is not None:

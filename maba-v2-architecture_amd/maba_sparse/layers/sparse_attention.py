@@ -29,6 +29,7 @@ import torch.nn.functional as F
 
 from maba_sparse.kernels.dispatcher import (dispatch_hca_pool, dispatch_maba_sa_decode, dispatch_maba_sa_prefill,
                                             dispatch_stream_superposition, get_backend)
+from maba_sparse.layers._wcache import WeightCacheMixin, cached
 from maba_sparse.layers.indexer import DGIndexer, _Growing
 
 
@@ -57,7 +58,7 @@ class LatentCache:
             self.nh = full
 
 
-class MabaSparseAttention(nn.Module):
+class MabaSparseAttention(WeightCacheMixin, nn.Module):
     def __init__(self, config: Optional[Any] = None, dim: int = 640, n_heads: int = 10, d_head: int = 64,
                  d_c: int = 128, window_size: int = 128, block_size: int = 64, top_k: int = 32,
                  hca_pool_size: int = 64, dist_lambda: float = 0.5, d_idx: int = 64,
@@ -88,6 +89,7 @@ class MabaSparseAttention(nn.Module):
         self.indexer = DGIndexer(dim=self.dim, d_idx=d_idx, block_size=self.block_size, top_k=self.top_k,
                                  dist_lambda=self.dist_lambda)
         self._hca_means: Optional[_Growing] = None
+        self._install_weight_cache_hooks()
 
     def reset_cache(self) -> None:
         self.indexer.reset_cache()
@@ -101,14 +103,7 @@ class MabaSparseAttention(nn.Module):
         """``lin.weight`` in fp32 as ``[H, d_head, d_c]``, converted again only after the weight
         changes (decode calls this twice per token)."""
         w = lin.weight
-        if torch.is_grad_enabled() and w.requires_grad:
-            return w.float().view(self.n_heads, self.d_head, self.d_c)
-        tag = (w.data_ptr(), w._version, w.dtype)
-        held = self.__dict__.get(key)
-        if held is None or held[0] != tag:
-            held = (tag, w.float().view(self.n_heads, self.d_head, self.d_c))
-            self.__dict__[key] = held
-        return held[1]
+        return cached(self, key, (w,), lambda: w.float().view(self.n_heads, self.d_head, self.d_c))
 
     def _absorbed_query(self, x: torch.Tensor) -> torch.Tensor:
         """``W_k,h^T q_h`` for the single token of ``x [B, 1, dim]`` -> ``[B, H, d_c]`` fp32."""
@@ -151,15 +146,23 @@ class MabaSparseAttention(nn.Module):
 
     def _token_projections(self, x: torch.Tensor):
         """q, the new latent, the indexer's query and key and the gate logits of one token from
-        one GEMM over the stacked weights (the stack is rebuilt only after a weight changes)."""
-        mods = (self.q_proj, self.kv_down_proj, self.indexer.q_idx_proj, self.indexer.k_idx_proj, self.stream_gate)
+        one GEMM over the stacked weights (the stack is rebuilt only after a weight changes).
+
+        The indexer query comes first and the stack is padded with zero rows to a multiple of
+        eight, so that the query view starts at the GEMM output's base with a row stride that is
+        a multiple of eight elements: the bf16 MFMA decode scoring requires 16-byte aligned query
+        rows and takes a scalar kernel otherwise."""
+        mods = (self.indexer.q_idx_proj, self.indexer.k_idx_proj, self.q_proj, self.kv_down_proj, self.stream_gate)
         ws = [m.weight for m in mods]
-        tag = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
-        if getattr(self, "_w5_tag", None) != tag:
-            self._w5 = torch.cat(ws, dim=0)
-            self._w5_tag = tag
         sizes = [w.shape[0] for w in ws]
-        q, c_new, qi, ki, gl = F.linear(x, self._w5).split(sizes, dim=-1)
+        pad = -sum(sizes) % 8
+
+        def stack():
+            st = torch.cat(ws, dim=0)
+            return torch.cat([st, st.new_zeros(pad, st.shape[1])], dim=0) if pad else st
+
+        w5 = cached(self, "w5", ws, stack)
+        qi, ki, q, c_new, gl, _ = F.linear(x, w5).split(sizes + [pad], dim=-1)
         return q, c_new, qi, ki, gl + self.stream_gate.bias
 
     def decode_step(self, x: torch.Tensor, cache: LatentCache,

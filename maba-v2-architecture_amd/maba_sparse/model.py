@@ -19,6 +19,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from maba_sparse.layers._wcache import WeightCacheMixin, cached
 from maba_sparse.layers.dgda import DGDALayer
 from maba_sparse.layers.sparse_attention import LatentCache, MabaSparseAttention
 
@@ -65,19 +66,12 @@ class RMSNorm(nn.Module):
 
 
 def _frozen(module: nn.Module, key: str, fn, *params: torch.Tensor) -> torch.Tensor:
-    """``fn(*params)``, kept on ``module`` until a parameter changes (an in-place update bumps
-    its version counter).  For inference: under autograd the value is recomputed."""
-    if torch.is_grad_enabled() and any(p.requires_grad for p in params):
-        return fn(*params)
-    tag = tuple((p.data_ptr(), p._version, p.dtype) for p in params)
-    held = module.__dict__.get("_frozen_" + key)
-    if held is None or held[0] != tag:
-        held = (tag, fn(*params))
-        module.__dict__["_frozen_" + key] = held
-    return held[1]
+    """``fn(*params)``, kept on ``module`` until a parameter changes (see ``layers/_wcache.py``).
+    For inference: under autograd the value is recomputed."""
+    return cached(module, key, params, lambda: fn(*params))
 
 
-class SwiGLUFFN(nn.Module):
+class SwiGLUFFN(WeightCacheMixin, nn.Module):
     def __init__(self, dim: int, intermediate_size: int) -> None:
         super().__init__()
         self.w_gate = nn.Linear(dim, intermediate_size, bias=False)
@@ -101,7 +95,7 @@ class FactorizedEmbeddings(nn.Module):
         return self.proj(self.in_emb(input_ids))
 
 
-class MabaBlock(nn.Module):
+class MabaBlock(WeightCacheMixin, nn.Module):
     def __init__(self, config: MabaConfig, layer_idx: int) -> None:
         super().__init__()
         self.layer_idx = layer_idx
@@ -145,7 +139,7 @@ class MabaBlock(nn.Module):
         return self._residual(x, mo), ns, ncv
 
 
-class MabaSparseForCausalLM(nn.Module):
+class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
     def __init__(self, config: Optional[MabaConfig] = None) -> None:
         super().__init__()
         self.config = config or get_101m_config()
@@ -156,6 +150,7 @@ class MabaSparseForCausalLM(nn.Module):
         self.head_proj = nn.Linear(c.dim, c.d_emb, bias=False)
         self.lm_head = nn.Linear(c.d_emb, c.vocab_size, bias=False)
         self.lm_head.weight = self.embeddings.in_emb.weight      # tied (model.py:205)
+        self._install_weight_cache_hooks()
 
     def init_normal(self, std: float = 0.02) -> "MabaSparseForCausalLM":
         """Every weight matrix and embedding ~ N(0, std) (the BASELINE's random init); norms,
@@ -194,11 +189,16 @@ class MabaSparseForCausalLM(nn.Module):
 
     @torch.no_grad()
     def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
-                        on_prefill_done=None) -> torch.Tensor:
+                        on_prefill_done=None, return_logits: bool = False):
         """Greedy decoding (reference model.py:272-305 at temperature 0): one prefill, then
         ``max_new_tokens - 1`` single-token steps over per-layer decode caches.  Returns the
         new tokens ``[B, max_new_tokens]``.  ``on_prefill_done()`` runs between the two phases
-        (a timing hook)."""
+        (a timing hook).  With ``return_logits`` the last-position logits of the prefill and
+        of every step come back too, ``[B, max_new_tokens, vocab]``.
+
+        The stacked and converted weights the decode path keeps are dropped on entry, so a
+        weight written through ``.data`` since the last call takes effect."""
+        self.clear_weight_caches()
         B, L = input_ids.shape
         logits, states = self(input_ids)
         caches: List[Optional[LatentCache]] = []
@@ -212,17 +212,23 @@ class MabaSparseForCausalLM(nn.Module):
                 caches.append(None)
         if on_prefill_done is not None:
             on_prefill_done()
-        tok = logits[:, -1].argmax(dim=-1, keepdim=True)
+        last = logits[:, -1]
+        tok = last.argmax(dim=-1, keepdim=True)
         out = [tok]
+        seen = [last] if return_logits else None
         for _ in range(max_new_tokens - 1):
             x = self.embeddings(tok)
             for i, layer in enumerate(self.layers):
                 st, cv, _ = states[i]
                 x, nst, ncv = layer.decode(x, state=st, conv_state=cv, cache=caches[i])
                 states[i] = (nst, ncv, None)
-            tok = self._logits(x)[:, -1].argmax(dim=-1, keepdim=True)
+            last = self._logits(x)[:, -1]
+            tok = last.argmax(dim=-1, keepdim=True)
             out.append(tok)
-        return torch.cat(out, dim=1)
+            if return_logits:
+                seen.append(last)
+        toks = torch.cat(out, dim=1)
+        return (toks, torch.stack(seen, dim=1)) if return_logits else toks
 
 
 MabaSparseLM = MabaSparseForCausalLM

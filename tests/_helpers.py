@@ -106,3 +106,19 @@ def topk_agrees(idx_actual, scores_ref, k, gap=1e-4):
             if lo > gap and hi > gap:
                 assert ia[r][p] == order[p], f"row {r} rank {p}: {ia[r][p]} vs {order[p]}"
     return checked
+
+
+def topk_is_valid(idx_actual, scores_ref, tol=1e-4):
+    """Every row's selection is a top-k of the reference scores up to ``tol``: no unselected
+    score exceeds a selected one by more than ``tol``, and no index repeats.  Holds for the
+    rows whose k-th gap is too small for ``topk_agrees`` to compare them."""
+    ia = np.asarray(idx_actual).reshape(-1, idx_actual.shape[-1])
+    s = np.asarray(scores_ref, np.float64).reshape(ia.shape[0], -1)
+    for r in range(ia.shape[0]):
+        sel = ia[r]
+        assert len(set(sel.tolist())) == sel.size, f"row {r}: repeated index"
+        mask = np.ones(s.shape[1], bool)
+        mask[sel] = False
+        if mask.any():
+            worst_in, best_out = s[r][sel].min(), s[r][mask].max()
+            assert best_out <= worst_in + tol, f"row {r}: unselected {best_out} above selected {worst_in}"

@@ -41,25 +41,6 @@ __global__ void k_32x32x16bf16(const short* a, const short* b, float* d) {
   for (int i = 0; i < 16; ++i) d[l * 16 + i] = acc[i];
 }
 
-// Issue-rate probe: NACC independent accumulator chains, ITERS MFMAs each.
-template <int KIND>
-__global__ void k_rate(float* out, int iters) {
-  f32x4 acc[4] = {};
-  i16x4 a4 = {1, 2, 3, 4};
-  bf16x8 a8;
-  for (int i = 0; i < 8; ++i) a8[i] = (__bf16)(float)(threadIdx.x & 7);
-  for (int it = 0; it < iters; ++it) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (KIND == 0) acc[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a4, a4, acc[j], 0, 0, 0);
-      else acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a8, a8, acc[j], 0, 0, 0);
-    }
-  }
-  float s = 0.f;
-  for (int j = 0; j < 4; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
-  out[blockIdx.x * blockDim.x + threadIdx.x] = s;
-}
-
 extern "C" int probe_mfma(int kind, const void* a, const void* b, void* d, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (kind == 0) hipLaunchKernelGGL(k_16x16x16bf16, dim3(1), dim3(64), 0, s, (const short*)a, (const short*)b, (float*)d);
@@ -68,9 +49,3 @@ extern "C" int probe_mfma(int kind, const void* a, const void* b, void* d, void*
   return (int)hipGetLastError();
 }
 
-extern "C" int probe_mfma_rate(int kind, int blocks, int iters, void* out, void* stream) {
-  hipStream_t s = (hipStream_t)stream;
-  if (kind == 0) hipLaunchKernelGGL(k_rate<0>, dim3(blocks), dim3(256), 0, s, (float*)out, iters);
-  else hipLaunchKernelGGL(k_rate<1>, dim3(blocks), dim3(256), 0, s, (float*)out, iters);
-  return (int)hipGetLastError();
-}

@@ -23,7 +23,6 @@ def lib():
         pytest.skip("needs GPU and built probe library")
     lib = ctypes.CDLL(PROBE)
     lib.probe_mfma.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
-    lib.probe_mfma_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return lib
 
 
@@ -86,25 +85,3 @@ def test_32x32x16_bf16_layout(lib):
     exp = np.array([[C[8 * (i // 4) + 4 * (l // 32) + (i % 4), l % 32] for i in range(16)] for l in range(64)])
     np.testing.assert_array_equal(d, exp)
 
-
-def test_mfma_issue_rate_report(lib):
-    """Times back-to-back MFMAs (4 independent chains per wave) and prints cycles/op."""
-    dev = torch.device("cuda:0")
-    blocks, iters = 1024, 2000
-    out = torch.empty(blocks * 256, device=dev)
-    s = torch.cuda.current_stream().cuda_stream
-    props = torch.cuda.get_device_properties(0)
-    res = {}
-    for kind, name, flops in ((0, "16x16x16bf16", 2 * 16 * 16 * 16), (1, "16x16x32bf16", 2 * 16 * 16 * 32)):
-        lib.probe_mfma_rate(kind, blocks, 10, out.data_ptr(), s)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        lib.probe_mfma_rate(kind, blocks, iters, out.data_ptr(), s)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1)
-        total = blocks * 4 * iters * 4 * flops
-        res[name] = total / (ms * 1e-3) / 1e12
-    print(f"\nMFMA rate (TFLOP/s, {props.multi_processor_count} CUs): {res}")
-    assert all(v > 0 for v in res.values())

@@ -1,0 +1,171 @@
+"""BASELINE config 5 (the 101M model, bf16 weights ~ N(0, 0.02), B = 16) on the GPU.
+
+- The ``generate_greedy`` serving loop (LatentCache, incremental centroid and HCA caches,
+  stacked projections) against the reference-style ``forward``/``step`` state passing fed
+  the same tokens, across a 64-token block boundary: in bf16, last-position logits within
+  3e-2 of the logit scale (a few ulps of the bf16 logits: the two paths round different
+  GEMMs) and equal greedy tokens wherever a step's top-2 gap exceeds twice that step's
+  logit difference; in fp32, logits within 1e-5 of the scale and equal tokens.  The
+  prefill is 2,000 (bf16) or 1,000 (fp32) tokens instead of 131,072 (the property does not
+  depend on the length; the full length runs in bench.py).
+- One DGDA block at the model's widths against the float64 oracle, in two stages: the
+  prologue kernel from the block's own bf16 projection GEMM output (q/k/v one bf16 ulp,
+  gates 1e-5), then the chunked prefill from the prologue's outputs (rtol = atol = 2e-3).
+- One MABA-SA block at the model's widths, one decode step at a 4,100-token context:
+  the indexer's picks against oracle decode scores of the centroids it saw, and the fused
+  decode against ``oracle.sparse_attn.maba_sa_decode`` with oracle-computed means
+  (rtol = atol = 2e-3).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _helpers import assert_close, to_np, topk_agrees
+from oracle import dgda as odgda
+from oracle import indexer as oidx
+from oracle import sparse_attn as osa
+
+pytestmark = pytest.mark.gpu
+
+BATCH = 16
+
+
+def _build(dtype):
+    from maba_sparse.model import MabaSparseForCausalLM, get_101m_config
+    torch.manual_seed(0)
+    return MabaSparseForCausalLM(get_101m_config()).init_normal(0.02).to(torch.device("cuda:0"), dtype).eval()
+
+
+@pytest.fixture(scope="module")
+def model():
+    import conftest
+    if not conftest.gpu_available():
+        pytest.skip("no ROCm GPU")
+    return _build(torch.bfloat16)
+
+
+def _two_loops(m, prefill, steps, seed):
+    """Last-position logits [B, steps, V] of the serving loop and of the state-passing loop
+    fed the serving loop's tokens, and those tokens."""
+    dev = next(m.parameters()).device
+    ids = torch.randint(0, m.config.vocab_size, (BATCH, prefill), generator=torch.Generator().manual_seed(seed)).to(dev)
+    print(f"\nconfig 5 serving loop: B={BATCH} prefill={prefill} steps={steps} {next(m.parameters()).dtype}", flush=True)
+    with torch.no_grad():
+        toks, lg_serve = m.generate_greedy(ids, steps, return_logits=True)
+        logits, states = m(ids)
+        ref = [logits[:, -1]]
+        for t in range(steps - 1):
+            lg, states = m.step(toks[:, t:t + 1], past_states=states)
+            ref.append(lg[:, -1])
+    return toks.cpu(), lg_serve.float().cpu(), torch.stack(ref, dim=1).float().cpu()
+
+
+def _check_tokens(toks, got, ref, min_sure):
+    err = (got - ref).abs().amax(dim=(0, 2))                    # per step
+    top2 = ref.topk(2, dim=-1).values
+    sure = (top2[..., 0] - top2[..., 1]) > 2 * err[None, :]      # argmax fixed by that step's bound
+    assert sure.float().mean() >= min_sure, f"only {sure.float().mean():.2f} of the positions separate"
+    assert torch.equal(toks[sure], ref.argmax(-1)[sure])
+
+
+def test_config5_serving_loop_matches_state_passing(model):
+    """bf16 (config 5's dtype).  The logits are themselves bf16: one ulp is about 0.4 % of their
+    scale, and the two paths' differently rounded projections move them by a few ulps from the
+    first decode step on, without growth."""
+    toks, got, ref = _two_loops(model, 2000, 60, 1)          # positions 2000..2059 cross 2048
+    scale = ref.abs().max().item()
+    err = (got - ref).abs().max().item()
+    assert err <= 3e-2 * scale, f"serving-loop logits differ by {err:.3e} (scale {scale:.3e})"
+    assert (got[:, 0] == ref[:, 0]).all()                     # the shared prefill
+    _check_tokens(toks, got, ref, 0.3)
+
+
+def test_config5_serving_loop_fp32_exact():
+    """The same property in fp32 at the model's widths: the two loops agree to 1e-5 of the
+    logit scale (bit-identical on the boxes measured) and pick the same token at every
+    position whose top-2 gap exceeds twice that."""
+    import conftest
+    if not conftest.gpu_available():
+        pytest.skip("no ROCm GPU")
+    m = _build(torch.float32)
+    toks, got, ref = _two_loops(m, 1000, 40, 2)              # positions 1000..1039 cross 1024
+    scale = ref.abs().max().item()
+    err = (got - ref).abs().max().item()
+    assert err <= 1e-5 * scale, f"fp32 serving-loop logits differ by {err:.3e} (scale {scale:.3e})"
+    _check_tokens(toks, got, ref, 0.95)
+
+
+def _block_input(model, ids, upto):
+    """The normalised input of block ``upto`` for the token ids."""
+    x = model.embeddings(ids)
+    for i in range(upto):
+        x = model.layers[i](x)[0]
+    return model.layers[upto].norm1(x)
+
+
+def test_config5_dgda_block_oracle(model):
+    dev = next(model.parameters()).device
+    layer = model.layers[0].mixer
+    ids = torch.randint(0, model.config.vocab_size, (BATCH, 256), generator=torch.Generator().manual_seed(2)).to(dev)
+    with torch.no_grad():
+        x = _block_input(model, ids, 0)
+        args, _, ncs = layer._op_inputs(x, None, None)
+        from maba_sparse.kernels.dispatcher import dispatch_dgda_prefill
+        o, S = dispatch_dgda_prefill(**args, chunk_size=64, initial_state=None)
+        ws = [m.weight for m in (layer.q_proj, layer.k_proj, layer.v_proj, layer.gate_alpha, layer.gate_erase,
+                                 layer.gate_write)]
+        projs = F.linear(x, torch.cat(ws, dim=0)).split(layer.n_heads * layer.d_k, dim=-1)
+    H, d = layer.n_heads, layer.d_k
+    taps = [to_np(c.weight)[:, 0, :] for c in (layer.conv_q, layer.conv_k, layer.conv_v)]
+    pq, pk, pv, pla, _, pb, pw, _ = odgda.layer_prologue(*[to_np(p) for p in projs], *taps, n_heads=H, eps=layer.eps)
+    heads = lambda t: np.ascontiguousarray(t.reshape(t.shape[0], t.shape[1], H, d).transpose(0, 2, 1, 3))  # noqa: E731
+    for name, got, exp in (("q", args["q"], pq), ("k", args["k"], pk), ("v", args["v"], pv)):
+        bound = (2.0 ** -8 + 1e-5) * np.abs(heads(exp)) + 1e-6      # half an ulp plus fp32 slack
+        assert (np.abs(to_np(got) - heads(exp)) <= bound).all(), f"prologue {name} beyond one bf16 ulp"
+    assert_close(args["log_alpha"], heads(pla), 1e-5, 1e-6, "prologue log_alpha")
+    assert_close(args["b"], heads(pb), 1e-5, 1e-6, "prologue erase gate")
+    assert_close(args["w"], heads(pw), 1e-5, 1e-6, "prologue write gate")
+    eo, eS = odgda.dgda_prefill_seq(to_np(args["q"]), to_np(args["k"]), to_np(args["v"]),
+                                    alpha=np.exp(to_np(args["log_alpha"])), b=to_np(args["b"]), w=to_np(args["w"]))
+    assert_close(o, eo, 2e-3, 2e-3, "DGDA block prefill output")
+    assert_close(S, eS, 2e-3, 2e-3, "DGDA block final state")
+
+
+def test_config5_maba_sa_block_oracle(model):
+    from maba_sparse.kernels.dispatcher import dispatch_maba_sa_decode
+    from maba_sparse.layers import LatentCache
+    dev = next(model.parameters()).device
+    blk = 3
+    layer = model.layers[blk].mixer
+    L0 = 4099
+    ids = torch.randint(0, model.config.vocab_size, (BATCH, L0), generator=torch.Generator().manual_seed(3)).to(dev)
+    x_tok = torch.randn(BATCH, 1, model.config.dim, generator=torch.Generator().manual_seed(4)).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        h = _block_input(model, ids, blk)
+        _, c_full = layer(h)                                   # prefill: seeds the indexer caches
+        cache = LatentCache(BATCH, L0 + 8, layer.d_c, pool=64, device=dev, dtype=torch.bfloat16)
+        cache.append(c_full)
+        q, c_new, qi, ki, gl = layer._token_projections(x_tok)
+        cache.append(c_new)
+        idx, cent = layer.indexer.forward_projected(qi, ki)
+        L = cache.n
+        hca = cache.hca[:, : cache.nh]
+        q_lat = torch.einsum("bhd,hdc->bhc", q.reshape(BATCH, layer.n_heads, layer.d_head).float(),
+                             layer._f32_heads(layer.k_up_proj, "_wk_f32"))
+        z = dispatch_maba_sa_decode(q_lat, cache.c, hca, idx, gl.view(-1, 3), L=L, scale=layer.scale,
+                                    window=layer.window_size, n_sink=layer.n_sink_tokens,
+                                    block_size=layer.block_size, pool=layer.hca_pool_size)
+        out = torch.einsum("bhc,hdc->bhd", z, layer._f32_heads(layer.v_up_proj, "_wv_f32"))
+    assert L == L0 + 1 and cent.shape[1] == (L + 63) // 64
+    ref_sc = oidx.decode_scores(to_np(qi), to_np(cent), layer.dist_lambda)
+    assert topk_agrees(idx.cpu().numpy(), ref_sc, layer.top_k) >= BATCH - 2
+    c_np = to_np(cache.c[:, :L])
+    exp = osa.maba_sa_decode(to_np(q.reshape(BATCH, layer.n_heads, layer.d_head)), c_np, to_np(layer.k_up_proj.weight),
+                             to_np(layer.v_up_proj.weight), to_np(idx).astype(np.int64), to_np(gl.view(-1, 3)), L=L,
+                             window=layer.window_size, n_sink=layer.n_sink_tokens, block_size=layer.block_size,
+                             pool=layer.hca_pool_size)
+    assert_close(out, exp, 2e-3, 2e-3, "MABA-SA block decode")
+    assert math.isfinite(float(out.abs().max()))
