@@ -155,6 +155,26 @@ int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tensor* c_kv,
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * maba_hip_maba_sa_decode without a workspace argument: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, checks and result as
+ * maba_hip_maba_sa_decode; the partial slots live in a static device array of
+ * MABA_SA_STATIC_SCRATCH_BYTES per GPU (held until the process ends), whose address is
+ * queried once per device on the first call with that device current.  A call whose
+ * partials need more (maba_hip_maba_sa_decode_workspace_size bounds it) fails with
+ * MABA_ERR_WORKSPACE before launching anything.  Calls allocate nothing.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (different streams or
+ * threads) race and must be serialised by the caller.  Nothing in the array needs to
+ * start at zero: each call writes every slot it reads.
+ */
+#define MABA_SA_STATIC_SCRATCH_BYTES ((size_t)8 << 20)
+int maba_hip_maba_sa_decode_static(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                   const maba_tensor* hca, const maba_tensor* idx,
+                                   const maba_tensor* gate, int64_t L, float scale, int window,
+                                   int n_sink, int block_size, int pool, maba_tensor* out_lat,
+                                   void* stream);
+
+/*
  * MABA-SA prefill: every query's local, sparse and HCA streams and their gate.
  *   q [B,H,Lq,dh], k, v [B,H,Lkv,dh] (bf16, unit channel stride, 16-byte aligned rows,
  *   dh in {32,64,128}); query t sits at position pos = Lkv - Lq + t.

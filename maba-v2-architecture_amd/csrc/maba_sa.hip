@@ -20,6 +20,7 @@
 // Traffic is one read of the selected latent rows (bf16) plus small partials:
 // HBM-bound.
 #include <algorithm>
+#include <mutex>
 
 #include "maba_common.h"
 
@@ -635,7 +636,7 @@ static size_t sa_part_bytes(int64_t slots, int64_t B, int64_t H, int64_t dc) {
 static int sa_setup(const maba_tensor* q_lat, const maba_tensor* c_kv, const maba_tensor* hca,
                     const maba_tensor* idx, const maba_tensor* gate, const maba_tensor* out_lat, int64_t L,
                     float scale, int window, int n_sink, int block_size, int pool, void* workspace,
-                    size_t workspace_bytes, SaArgs& a, bool& seg, bool& empty) {
+                    size_t workspace_bytes, SaArgs& a, bool& seg, bool& empty, size_t& need) {
   if (!q_lat || q_lat->ndim != 3) return fail(MABA_ERR_INVALID, "maba_sa_decode: q_lat must be [B,H,dc]");
   const int64_t B = q_lat->shape[0], H = q_lat->shape[1], dc = q_lat->shape[2];
   if (!c_kv || c_kv->ndim != 3 || c_kv->shape[0] != B || c_kv->shape[2] != dc)
@@ -683,7 +684,7 @@ static int sa_setup(const maba_tensor* q_lat, const maba_tensor* c_kv, const mab
     sa_segments(a, device_cu_count());
     slots = a.s_loc + a.s_hca + a.s_sp;
   }
-  const size_t need = sa_part_bytes(slots, B, H, dc);
+  need = sa_part_bytes(slots, B, H, dc);
   if (!workspace || workspace_bytes < need)
     return fail(MABA_ERR_WORKSPACE, "maba_sa_decode: workspace of %zu bytes required", need);
   a.ws = (float*)workspace;
@@ -702,6 +703,56 @@ static int sa_launch_combine(const SaArgs& a, bool seg, hipStream_t s) {
   }
   hipLaunchKernelGGL(maba_sa_combine_kernel, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s, a, mg);
   return check_launch("maba_sa_decode/combine");
+}
+
+// The segment (or per-tile) launch and the merge, once sa_setup has filled the arguments.
+static int sa_run(const SaArgs& a, bool seg, hipStream_t s) {
+  const unsigned nslot = (unsigned)(seg ? a.s_loc + a.s_hca + a.s_sp : a.ntiles);
+  if (nslot > 0) {
+    const dim3 grid(nslot, (unsigned)a.B);
+    if (seg) {
+      switch (a.dc / 32) {
+        case 1: hipLaunchKernelGGL(maba_sa_mfma_kernel<1>, grid, dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(maba_sa_mfma_kernel<2>, grid, dim3(256), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(maba_sa_mfma_kernel<3>, grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(maba_sa_mfma_kernel<4>, grid, dim3(256), 0, s, a); break;
+      }
+    } else {
+      hipLaunchKernelGGL(maba_sa_tile_kernel, grid, dim3(256), 0, s, a);
+    }
+    const int rc = check_launch(seg ? "maba_sa_decode/segments" : "maba_sa_decode/tiles");
+    if (rc) return rc;
+  }
+  return sa_launch_combine(a, seg, s);
+}
+
+// Scratch of maba_hip_maba_sa_decode_static: the partial slots of one decode step, held by
+// every GPU the library runs on until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device address); it passes
+// the device address hipGetSymbolAddress returns for the current device, kept per device.
+static __device__ __align__(256) float scratch[MABA_SA_STATIC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int SA_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[SA_MAX_DEVICES];
+
+// Device address of the current device's scratch, queried on the first call per device.
+static int sa_static_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MABA_ERR_HIP, "maba_sa_decode_static: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= SA_MAX_DEVICES)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_static: device %d beyond %d", dev, SA_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MABA_ERR_HIP, "maba_sa_decode_static: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MABA_OK;
 }
 
 }  // namespace maba
@@ -723,25 +774,32 @@ extern "C" int maba_hip_maba_sa_decode(const maba_tensor* q_lat, const maba_tens
                                        void* workspace, size_t workspace_bytes, void* stream) {
   SaArgs a;
   bool seg = false, empty = false;
+  size_t need = 0;
   int rc = sa_setup(q_lat, c_kv, hca, idx, gate, out_lat, L, scale, window, n_sink, block_size, pool, workspace,
-                    workspace_bytes, a, seg, empty);
+                    workspace_bytes, a, seg, empty, need);
   if (rc || empty) return rc;
-  hipStream_t s = (hipStream_t)stream;
-  const unsigned nslot = (unsigned)(seg ? a.s_loc + a.s_hca + a.s_sp : a.ntiles);
-  if (nslot > 0) {
-    const dim3 grid(nslot, (unsigned)a.B);
-    if (seg) {
-      switch (a.dc / 32) {
-        case 1: hipLaunchKernelGGL(maba_sa_mfma_kernel<1>, grid, dim3(256), 0, s, a); break;
-        case 2: hipLaunchKernelGGL(maba_sa_mfma_kernel<2>, grid, dim3(256), 0, s, a); break;
-        case 3: hipLaunchKernelGGL(maba_sa_mfma_kernel<3>, grid, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL(maba_sa_mfma_kernel<4>, grid, dim3(256), 0, s, a); break;
-      }
-    } else {
-      hipLaunchKernelGGL(maba_sa_tile_kernel, grid, dim3(256), 0, s, a);
-    }
-    rc = check_launch(seg ? "maba_sa_decode/segments" : "maba_sa_decode/tiles");
-    if (rc) return rc;
-  }
-  return sa_launch_combine(a, seg, s);
+  return sa_run(a, seg, (hipStream_t)stream);
+}
+
+extern "C" int maba_hip_maba_sa_decode_static(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                              const maba_tensor* hca, const maba_tensor* idx,
+                                              const maba_tensor* gate, int64_t L, float scale, int window,
+                                              int n_sink, int block_size, int pool, maba_tensor* out_lat,
+                                              void* stream) {
+  void* ws = nullptr;
+  int rc = sa_static_scratch(&ws);
+  if (rc) return rc;
+  SaArgs a;
+  bool seg = false, empty = false;
+  size_t need = 0;
+  rc = sa_setup(q_lat, c_kv, hca, idx, gate, out_lat, L, scale, window, n_sink, block_size, pool, ws,
+                MABA_SA_STATIC_SCRATCH_BYTES, a, seg, empty, need);
+  if (rc == MABA_ERR_WORKSPACE)
+    return fail(MABA_ERR_WORKSPACE,
+                "maba_sa_decode_static: this call needs %zu bytes of scratch; the static scratch holds %zu "
+                "(use maba_hip_maba_sa_decode with a workspace)", need, (size_t)MABA_SA_STATIC_SCRATCH_BYTES);
+  if (rc || empty) return rc;
+  // every partial slot the merge reads is written by this call's first launch, so nothing
+  // left in the scratch by an earlier call is read
+  return sa_run(a, seg, (hipStream_t)stream);
 }

@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "maba_hip_hca_pool",
     "maba_hip_maba_sa_decode_workspace_size",
     "maba_hip_maba_sa_decode",
+    "maba_hip_maba_sa_decode_static",
     "maba_hip_dgda_prologue",
     "maba_hip_maba_sa_prefill",
 )
@@ -87,6 +88,7 @@ def _declare(lib) -> None:
         "maba_hip_hca_pool": ([T, T, i, vp], i),
         "maba_hip_maba_sa_decode_workspace_size": ([i64, i64, i64, i64, i64, i, i, i], sz),
         "maba_hip_maba_sa_decode": ([T, T, T, T, T, i64, f, i, i, i, i, T, vp, sz, vp], i),
+        "maba_hip_maba_sa_decode_static": ([T, T, T, T, T, i64, f, i, i, i, i, T, vp], i),
         "maba_hip_dgda_prologue": ([TA, TA, TA, f, TA, TA, vp], i),
         "maba_hip_maba_sa_prefill": ([T, T, T, T, T, T, T, T, f, i, i, i, i, T, vp], i),
     }
