@@ -36,6 +36,16 @@
  *                                   layer's conv + SiLU with carried history,
  *                                   gate activations and key normalisation;
  *                                   inline torch code in the reference)
+ *   maba_hip_cache_append           layers/indexer.py:62-82 (key cache, complete
+ *                                   and tail centroids), layers/sparse_attention.py:
+ *                                   206, 241-251 (latent rows, HCA block means)
+ *   maba_hip_index_topk_decode_dev  layers/indexer.py:101-112 with the centroid
+ *                                   count read from device memory
+ *   maba_hip_maba_sa_decode_dev     layers/sparse_attention.py:79-219,263-275 with
+ *                                   the sequence length read from device memory
+ *   maba_hip_rmsnorm                model.py:11-22 (RMSNorm) and the gated residual
+ *                                   of MabaBlock, model.py:92-128
+ *   maba_hip_swiglu                 model.py:25-38 (SwiGLU activation)
  */
 #ifndef MABA_HIP_H
 #define MABA_HIP_H
@@ -96,7 +106,9 @@ int maba_hip_dgda_prefill(const maba_tensor* q, const maba_tensor* k, const maba
                           size_t workspace_bytes, void* stream);
 
 /* DGDA single decode step.  q,k,alpha,log_alpha,b: [B,H,dk]; v,w: [B,H,dv];
- * state / new_state: [B,H,dk,dv] (state NULL = zeros); out: [B,H,dv]. */
+ * state / new_state: [B,H,dk,dv] (state NULL = zeros); out: [B,H,dv].  With dk = dv = 64,
+ * fp32 gates and an fp32 or bf16 state with unit column stride, new_state may be state
+ * itself (the state is updated in place). */
 int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                        const maba_tensor* alpha, const maba_tensor* log_alpha,
                        const maba_tensor* b, const maba_tensor* w, const maba_tensor* state,
@@ -201,11 +213,54 @@ int maba_hip_maba_sa_prefill(const maba_tensor* q, const maba_tensor* k, const m
  *   v = silu(conv_v(...))                        (f32 or bf16, one dtype)
  *   log_alpha = max(-softplus(x_alpha), -14), alpha = exp(log_alpha) (ys[4] may be
  *   NULL), b = sigmoid(x_erase), w = sigmoid(x_write)    (f32 or bf16, one dtype)
- * new_hist[0..2] [B,C,3]: the last three conv inputs of q, k, v; must not alias hist.
+ * new_hist[0..2] [B,C,3]: the last three conv inputs of q, k, v; must not alias hist
+ * unless L == 1 (a single token reads each channel's history before writing it).
  */
 int maba_hip_dgda_prologue(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
                            const maba_tensor* const* hist, float eps, maba_tensor* const* ys,
                            maba_tensor* const* new_hist, void* stream);
+
+/*
+ * Serving path: a decode step whose position lives in device memory, so that one captured
+ * HIP graph serves every position.  `pos` / `d_len` are device pointers to one int64.
+ *
+ * Cache append (one launch per decode token and MABA-SA layer).  Writes c_new [B,dc] to row
+ * p = *pos of c_cache [B,Lmax,dc] and k_new [B,di] to row p of k_cache [B,Lmax,di]; when row
+ * p completes a pool-block, hca[b, (p+1)/pool - 1] = the block's mean; and
+ * centroids[b, p/block_size] = 0.5 (mean + max) of the block holding row p, zero-padded when
+ * incomplete (the padding counts in the mean and the max).  All bf16, unit channel strides;
+ * hca [B,>=Lmax/pool,dc], centroids [B,>=ceil(Lmax/block_size),di].  The caller advances *pos.
+ */
+int maba_hip_cache_append(const maba_tensor* c_new, const maba_tensor* k_new, const int64_t* pos,
+                          maba_tensor* c_cache, maba_tensor* k_cache, maba_tensor* hca,
+                          maba_tensor* centroids, int pool, int block_size, void* stream);
+
+/* maba_hip_index_topk_decode over the first nb = ceil(*d_len / block_size) rows of centroids
+ * [B,Ncap,d] (bf16 MFMA path; nb must reach top_k).  out_idx int64 [B,Hq,top_k]; workspace
+ * sized by maba_hip_index_topk_decode_workspace_size(B, Hq, Ncap, top_k). */
+int maba_hip_index_topk_decode_dev(const maba_tensor* q, const maba_tensor* centroids,
+                                   const int64_t* d_len, int block_size, float lambda_dist,
+                                   int top_k, maba_tensor* out_idx, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/* maba_hip_maba_sa_decode with L = *d_len <= L_cap (bf16 MFMA path); workspace sized by
+ * maba_hip_maba_sa_decode_workspace_size(..., L_cap, ...). */
+int maba_hip_maba_sa_decode_dev(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                const maba_tensor* hca, const maba_tensor* idx,
+                                const maba_tensor* gate, const int64_t* d_len, int64_t L_cap,
+                                float scale, int window, int n_sink, int block_size, int pool,
+                                maba_tensor* out_lat, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/* h = x' / sqrt(mean(x'^2) + eps) * weight over the last dim C (even, <= 2048), where
+ * x' = x + gate * mo when mo is given (gate [C]), else x; x' is written to x_out when given
+ * (may alias x).  x, mo, x_out, h: [..,C] f32 or bf16 rows; weight, gate f32 or bf16. */
+int maba_hip_rmsnorm(const maba_tensor* x, const maba_tensor* mo, const maba_tensor* gate,
+                     const maba_tensor* weight, float eps, maba_tensor* x_out, maba_tensor* h,
+                     void* stream);
+
+/* out [..,I] = silu(g) * u for gate_up [..,2I] = [g | u] (f32 or bf16, one dtype). */
+int maba_hip_swiglu(const maba_tensor* gate_up, maba_tensor* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,151 @@
+// Decode-time cache append: one launch per decode token and MABA-SA layer.
+//
+// Reference semantics:
+//   layers/indexer.py:62-82          the new indexer key joins the key cache; a completed
+//                                    block adds its centroid 0.5 (mean + max); otherwise the
+//                                    zero-padded tail block's centroid stands in for the last
+//                                    block (the padding counts in the mean and the max)
+//   layers/sparse_attention.py:206   the HCA stream attends to the means of complete
+//                                    pool-token blocks of the latent cache
+//   (the latent row itself is the reference's per-step concatenation, :241-251)
+//
+// Cache format (device memory, all bf16, rows of one sequence contiguous):
+//   c     [B, Lmax, dc]        latent rows; rows [0, n) valid
+//   keys  [B, Lmax, di]        indexer keys; rows [0, n) valid
+//   hca   [B, Lmax/pool, dc]   means of the complete pool-blocks: entries [0, n/pool) valid
+//   cent  [B, ceil(Lmax/bs), di]  centroids: entries [0, ceil(n/bs)) valid, the last one the
+//                              zero-padded tail centroid while its block is incomplete
+// The new row goes to index p = *pos (a device scalar, so that one captured launch serves
+// every position); the caller advances *pos after the step.  One workgroup per sequence:
+// it writes the two rows, then reduces the block that holds row p, taking row p from the
+// inputs and rows before it from the caches (written by earlier launches).
+#include "maba_common.h"
+
+namespace maba {
+
+constexpr int AP_T = 256;
+constexpr int AP_MAXD = 256;
+
+struct AppendArgs {
+  const uint16_t* cn; int64_t cnsb, cnsd;   // new latent rows [B, dc]
+  const uint16_t* kn; int64_t knsb, knsd;   // new keys [B, di]
+  uint16_t* c; int64_t csb, csl;            // latent cache, channel stride 1
+  uint16_t* k; int64_t ksb, ksl;            // key cache, channel stride 1
+  uint16_t* hca; int64_t hsb, hsn;          // block means, channel stride 1
+  uint16_t* cent; int64_t esb, esn;         // centroids, channel stride 1
+  const int64_t* pos;
+  int64_t Lmax, nh_max, nc_max;
+  int dc, di, pool, bs;
+};
+
+// Column reduction of rows [r0, p) of a cache plus the new row (newrow[col * nsd]): sum
+// (and max when WITH_MAX) per column; the threads split the rows in AP_T / d parts, and
+// thread `col` of the result holds column col.
+template <bool WITH_MAX>
+__device__ void ap_reduce(const uint16_t* base, int64_t rstride, int64_t r0, int64_t p, int d,
+                          const uint16_t* newrow, int64_t nsd, float* s_sum, float* s_max, float& sum, float& mx) {
+  const int tid = threadIdx.x;
+  const int parts = AP_T / d;
+  const int col = tid % d, part = tid / d;
+  float s = 0.f, m = -INFINITY;
+  if (part < parts) {
+    for (int64_t r = r0 + part; r < p; r += parts) {
+      const float x = bf16_bits_to_f32(base[r * rstride + col]);
+      s += x;
+      if (WITH_MAX) m = fmaxf(m, x);
+    }
+    if (part == parts - 1) {
+      const float xn = bf16_bits_to_f32(newrow[col * nsd]);
+      s += xn;
+      if (WITH_MAX) m = fmaxf(m, xn);
+    }
+    s_sum[part * d + col] = s;
+    if (WITH_MAX) s_max[part * d + col] = m;
+  }
+  __syncthreads();
+  sum = 0.f;
+  mx = -INFINITY;
+  if (tid < d) {
+    for (int q = 0; q < parts; ++q) {   // fixed order: deterministic
+      sum += s_sum[q * d + tid];
+      if (WITH_MAX) mx = fmaxf(mx, s_max[q * d + tid]);
+    }
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(AP_T) void cache_append_kernel(AppendArgs a) {
+  __shared__ float s_sum[AP_T], s_max[AP_T];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t p = *a.pos;
+  if (p < 0 || p >= a.Lmax) return;   // the host checks capacity; never write out of bounds
+  // the new rows
+  const uint16_t xc = tid < a.dc ? a.cn[b * a.cnsb + tid * a.cnsd] : 0;
+  const uint16_t xk = tid < a.di ? a.kn[b * a.knsb + tid * a.knsd] : 0;
+  if (tid < a.dc) a.c[b * a.csb + p * a.csl + tid] = xc;
+  if (tid < a.di) a.k[b * a.ksb + p * a.ksl + tid] = xk;
+  // HCA mean of the pool-block that row p completes
+  if ((p + 1) % a.pool == 0) {
+    const int64_t e = (p + 1) / a.pool - 1;
+    float sum, mx;
+    ap_reduce<false>(a.c + b * a.csb, a.csl, p + 1 - a.pool, p, a.dc, a.cn + b * a.cnsb, a.cnsd, s_sum, s_max,
+                     sum, mx);
+    if (tid < a.dc && e < a.nh_max) a.hca[b * a.hsb + e * a.hsn + tid] = f32_to_bf16_bits(sum * (1.0f / (float)a.pool));
+  }
+  // centroid of the block holding row p: complete, or the zero-padded tail
+  const int64_t blk = p / a.bs;
+  const int64_t r0 = blk * a.bs;
+  float sum, mx;
+  ap_reduce<true>(a.k + b * a.ksb, a.ksl, r0, p, a.di, a.kn + b * a.knsb, a.knsd, s_sum, s_max, sum, mx);
+  if (tid < a.di && blk < a.nc_max) {
+    if (p - r0 + 1 < a.bs) mx = fmaxf(mx, 0.f);   // the zero padding takes part in the max
+    const float c = 0.5f * (sum * (1.0f / (float)a.bs) + mx);
+    a.cent[b * a.esb + blk * a.esn + tid] = f32_to_bf16_bits(c);
+  }
+}
+
+}  // namespace maba
+
+using namespace maba;
+
+extern "C" int maba_hip_cache_append(const maba_tensor* c_new, const maba_tensor* k_new, const int64_t* pos,
+                                     maba_tensor* c_cache, maba_tensor* k_cache, maba_tensor* hca,
+                                     maba_tensor* centroids, int pool, int block_size, void* stream) {
+  if (!c_new || c_new->ndim != 2 || !k_new || k_new->ndim != 2)
+    return fail(MABA_ERR_INVALID, "cache_append: c_new must be [B,dc] and k_new [B,di]");
+  const int64_t B = c_new->shape[0], dc = c_new->shape[1], di = k_new->shape[1];
+  if (k_new->shape[0] != B) return fail(MABA_ERR_INVALID, "cache_append: batch mismatch");
+  if (!pos) return fail(MABA_ERR_INVALID, "cache_append: pos (device int64) required");
+  if (pool <= 0 || block_size <= 0) return fail(MABA_ERR_INVALID, "cache_append: bad pool / block size");
+  if (!c_cache || c_cache->ndim != 3 || c_cache->shape[0] != B || c_cache->shape[2] != dc)
+    return fail(MABA_ERR_INVALID, "cache_append: c_cache must be [B,Lmax,dc]");
+  const int64_t Lmax = c_cache->shape[1];
+  const int64_t sk[3] = {B, Lmax, di};
+  if (!expect_shape(k_cache, "k_cache", 3, sk)) return MABA_ERR_INVALID;
+  if (!hca || hca->ndim != 3 || hca->shape[0] != B || hca->shape[2] != dc || hca->shape[1] < Lmax / pool)
+    return fail(MABA_ERR_INVALID, "cache_append: hca must be [B,>=Lmax/pool,dc]");
+  if (!centroids || centroids->ndim != 3 || centroids->shape[0] != B || centroids->shape[2] != di ||
+      centroids->shape[1] < ceil_div(Lmax, block_size))
+    return fail(MABA_ERR_INVALID, "cache_append: centroids must be [B,>=ceil(Lmax/block),di]");
+  const maba_tensor* all[] = {c_new, k_new, c_cache, k_cache, hca, centroids};
+  for (const maba_tensor* t : all)
+    if (t->dtype != MABA_BF16) return fail(MABA_ERR_DTYPE, "cache_append: bf16 tensors only");
+  if (dc > AP_MAXD || di > AP_MAXD || dc < 1 || di < 1)
+    return fail(MABA_ERR_UNSUPPORTED, "cache_append: dc and di in [1, %d]", AP_MAXD);
+  for (const maba_tensor* t : {c_cache, k_cache, hca, centroids})
+    if (t->stride[2] != 1) return fail(MABA_ERR_UNSUPPORTED, "cache_append: caches need unit channel stride");
+  if (B == 0) return MABA_OK;
+  AppendArgs a;
+  a.cn = (const uint16_t*)c_new->data; a.cnsb = c_new->stride[0]; a.cnsd = c_new->stride[1];
+  a.kn = (const uint16_t*)k_new->data; a.knsb = k_new->stride[0]; a.knsd = k_new->stride[1];
+  a.c = (uint16_t*)c_cache->data; a.csb = c_cache->stride[0]; a.csl = c_cache->stride[1];
+  a.k = (uint16_t*)k_cache->data; a.ksb = k_cache->stride[0]; a.ksl = k_cache->stride[1];
+  a.hca = (uint16_t*)hca->data; a.hsb = hca->stride[0]; a.hsn = hca->stride[1];
+  a.cent = (uint16_t*)centroids->data; a.esb = centroids->stride[0]; a.esn = centroids->stride[1];
+  a.pos = pos;
+  a.Lmax = Lmax; a.nh_max = hca->shape[1]; a.nc_max = centroids->shape[1];
+  a.dc = (int)dc; a.di = (int)di; a.pool = pool; a.bs = block_size;
+  hipLaunchKernelGGL(cache_append_kernel, dim3((unsigned)B), dim3(AP_T), 0, (hipStream_t)stream, a);
+  return check_launch("cache_append");
+}

@@ -154,6 +154,67 @@ __global__ __launch_bounds__(512) void dgda_prologue_kernel(ProArgs a) {
   }
 }
 
+// One element of a projection / output row.
+template <class T> __device__ __forceinline__ float pro_ld1(const void* p, int64_t i);
+template <> __device__ __forceinline__ float pro_ld1<float>(const void* p, int64_t i) { return ((const float*)p)[i]; }
+template <> __device__ __forceinline__ float pro_ld1<uint16_t>(const void* p, int64_t i) {
+  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+template <class T> __device__ __forceinline__ void pro_st1(void* p, int64_t i, float x);
+template <> __device__ __forceinline__ void pro_st1<float>(void* p, int64_t i, float x) { ((float*)p)[i] = x; }
+template <> __device__ __forceinline__ void pro_st1<uint16_t>(void* p, int64_t i, float x) {
+  ((uint16_t*)p)[i] = f32_to_bf16_bits(x);
+}
+
+// One token (a decode step): one wave per (head, batch element), one lane per channel.
+// Every input, the carried history included, is read before the first store, so the new
+// history may overwrite the old one in place.  Same arithmetic as the run kernel.
+template <class XT, class QT, class GT>
+__global__ __launch_bounds__(64) void dgda_prologue_step_kernel(ProArgs a) {
+  const int lane = threadIdx.x;
+  const int c = 64 * blockIdx.x + lane;
+  const int64_t b = blockIdx.y;
+  float x[6], w[3][4], h[3][PRO_KH];
+#pragma unroll
+  for (int s = 0; s < 6; ++s) x[s] = pro_ld1<XT>(a.x[s], b * a.xsb[s] + c);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[s][j] = load_elem(a.cw[s], a.cwdt, c * a.cwsc[s] + j * a.cwst[s]);
+#pragma unroll
+    for (int j = 0; j < PRO_KH; ++j)
+      h[s][j] = a.hist[s] ? load_elem(a.hist[s], a.hdt, b * a.hsb[s] + c * a.hsc[s] + j * a.hst[s]) : 0.f;
+  }
+  float y[3];
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {
+    float acc = w[s][3] * x[s];
+    acc = fmaf(w[s][2], h[s][2], acc);
+    acc = fmaf(w[s][1], h[s][1], acc);
+    acc = fmaf(w[s][0], h[s][0], acc);
+    y[s] = pro_silu(acc);
+  }
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {   // new history: the inputs of tokens -2, -1, 0
+    const int64_t o = b * a.nhsb[s] + c * a.nhsc[s];
+    store_elem(a.nh[s], a.nhdt, o, h[s][1]);
+    store_elem(a.nh[s], a.nhdt, o + a.nhst[s], h[s][2]);
+    store_elem(a.nh[s], a.nhdt, o + 2 * a.nhst[s], x[s]);
+  }
+  float ss = y[1] * y[1];
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
+  const float kinv = __fdividef(1.f, sqrtf(ss) + a.eps);
+  const float la = pro_log_decay(x[3]);
+  pro_st1<QT>(a.y[0], b * a.ysb[0] + c, y[0]);
+  pro_st1<QT>(a.y[1], b * a.ysb[1] + c, y[1] * kinv);
+  pro_st1<QT>(a.y[2], b * a.ysb[2] + c, y[2]);
+  pro_st1<GT>(a.y[3], b * a.ysb[3] + c, la);
+  if (a.y[4]) pro_st1<GT>(a.y[4], b * a.ysb[4] + c, __expf(la));
+  pro_st1<GT>(a.y[5], b * a.ysb[5] + c, pro_sigmoid(x[4]));
+  pro_st1<GT>(a.y[6], b * a.ysb[6] + c, pro_sigmoid(x[5]));
+}
+
 static bool pro_pair_ok(const maba_tensor* t, int64_t B, int64_t L, int64_t C) {
   if (!t || t->ndim != 3 || t->shape[0] != B || t->shape[1] != L || t->shape[2] != C) return false;
   if (t->dtype != MABA_F32 && t->dtype != MABA_BF16) return false;
@@ -164,8 +225,14 @@ static bool pro_pair_ok(const maba_tensor* t, int64_t B, int64_t L, int64_t C) {
 
 template <class XT, class QT>
 static void pro_launch_g(const ProArgs& a, int gdt, dim3 grid, dim3 block, hipStream_t s) {
-  if (gdt == MABA_F32) hipLaunchKernelGGL((dgda_prologue_kernel<XT, QT, float>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((dgda_prologue_kernel<XT, QT, uint16_t>), grid, block, 0, s, a);
+  const bool step = a.L == 1;   // grid (H, B) of 64-lane waves for a single token
+  if (gdt == MABA_F32) {
+    if (step) hipLaunchKernelGGL((dgda_prologue_step_kernel<XT, QT, float>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((dgda_prologue_kernel<XT, QT, float>), grid, block, 0, s, a);
+  } else {
+    if (step) hipLaunchKernelGGL((dgda_prologue_step_kernel<XT, QT, uint16_t>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((dgda_prologue_kernel<XT, QT, uint16_t>), grid, block, 0, s, a);
+  }
 }
 
 }  // namespace maba
@@ -209,8 +276,9 @@ extern "C" int maba_hip_dgda_prologue(const maba_tensor* const* xs, const maba_t
     if (new_hist[s]->dtype != new_hist[0]->dtype)
       return fail(MABA_ERR_DTYPE, "dgda_prologue: new histories differ in dtype");
   }
-  // the new history is written while other workgroups still read the old one
-  for (int s = 0; hist && s < 3; ++s)
+  // with several tokens the new history is written while other workgroups still read the
+  // old one; a single token reads each channel's history before writing it (in place is fine)
+  for (int s = 0; hist && L > 1 && s < 3; ++s)
     for (int r = 0; r < 3; ++r)
       if (new_hist[s]->data == hist[r]->data)
         return fail(MABA_ERR_INVALID, "dgda_prologue: the new conv history must not alias the old one");
@@ -236,7 +304,8 @@ extern "C" int maba_hip_dgda_prologue(const maba_tensor* const* xs, const maba_t
   a.L = L;
   a.eps = eps;
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)ceil_div(L, PRO_TOK), (unsigned)B), block((unsigned)(C / 2));
+  const dim3 grid = L == 1 ? dim3((unsigned)(C / 64), (unsigned)B) : dim3((unsigned)ceil_div(L, PRO_TOK), (unsigned)B);
+  const dim3 block = L == 1 ? dim3(64) : dim3((unsigned)(C / 2));
   if (xdt == MABA_F32) {
     if (qdt == MABA_F32) pro_launch_g<float, float>(a, gdt, grid, block, st);
     else pro_launch_g<float, uint16_t>(a, gdt, grid, block, st);

@@ -102,8 +102,8 @@ struct StepFast {
   const float* gate; int64_t gsb, gsh, gsd;   // log_alpha (use_log) or alpha
   const float* bb; int64_t bsb, bsh, bsd;
   const float* ww; int64_t wsb, wsh, wsd;
-  const float* state; int64_t ssb, ssh, ssr;  // may be null (zero state)
-  float* nst; int64_t nsb, nsh, nsr;
+  const void* state; int64_t ssb, ssh, ssr;   // may be null (zero state); fp32 or bf16 (TS)
+  void* nst; int64_t nsb, nsh, nsr;           // same dtype as the state; may alias it
   void* out; int odt; int64_t osb, osh, osd;
   int64_t BH;
   int H, use_log;
@@ -122,7 +122,9 @@ __device__ __forceinline__ float bcast(float x, int r) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), r));
 }
 
-template <typename T>
+// T: dtype of q, k, v; TS: dtype of the state in and out (fp32 or bf16).  Every row of the
+// lane's column is loaded before the first store, so the new state may alias the old one.
+template <typename T, typename TS>
 __global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t bh = (int64_t)blockIdx.x * 4 + wave;
@@ -130,9 +132,9 @@ __global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
   const int64_t bi = bh / a.H, hi = bh % a.H;
   float s[64];
   if (a.state) {
-    const float* S = a.state + bi * a.ssb + hi * a.ssh + lane;
+    const int64_t S = bi * a.ssb + hi * a.ssh + lane;
 #pragma unroll
-    for (int r = 0; r < 64; ++r) s[r] = S[r * a.ssr];
+    for (int r = 0; r < 64; ++r) s[r] = ldf<TS>(a.state, S + r * a.ssr);
   } else {
 #pragma unroll
     for (int r = 0; r < 64; ++r) s[r] = 0.f;
@@ -154,12 +156,13 @@ __global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
   }
   const float delta = wc * vc - pred;
   float o = 0.f;
-  float* N = a.nst + bi * a.nsb + hi * a.nsh + lane;
+  const int64_t N = bi * a.nsb + hi * a.nsh + lane;
 #pragma unroll
   for (int r = 0; r < 64; ++r) {
     const float sn = fmaf(bcast(kr, r), delta, s[r]);
-    N[r * a.nsr] = sn;
-    o = fmaf(bcast(qr, r), sn, o);
+    if constexpr (sizeof(TS) == 4) ((float*)a.nst)[N + r * a.nsr] = sn;
+    else ((uint16_t*)a.nst)[N + r * a.nsr] = f32_to_bf16_bits(sn);
+    o = fmaf(bcast(qr, r), sn, o);   // the fp32 state before its rounding, as the generic kernel
   }
   store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
 }
@@ -213,9 +216,10 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
   hipStream_t s = (hipStream_t)stream;
   const maba_tensor* gate = log_alpha ? log_alpha : alpha;
   const bool qkv_same = q->dtype == k->dtype && q->dtype == v->dtype && (q->dtype == MABA_BF16 || q->dtype == MABA_F32);
+  const int sdt = new_state->dtype;
   const bool fast = dk == 64 && dv == 64 && qkv_same && gate->dtype == MABA_F32 && b->dtype == MABA_F32 &&
-                    w->dtype == MABA_F32 && new_state->dtype == MABA_F32 && new_state->stride[3] == 1 &&
-                    (!state || (state->dtype == MABA_F32 && state->stride[3] == 1));
+                    w->dtype == MABA_F32 && (sdt == MABA_F32 || sdt == MABA_BF16) && new_state->stride[3] == 1 &&
+                    (!state || (state->dtype == sdt && state->stride[3] == 1));
   if (fast) {
     StepFast f;
     f.q = q->data; f.qsb = q->stride[0]; f.qsh = q->stride[1]; f.qsd = q->stride[2];
@@ -224,15 +228,18 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
     f.gate = (const float*)gate->data; f.gsb = gate->stride[0]; f.gsh = gate->stride[1]; f.gsd = gate->stride[2];
     f.bb = (const float*)b->data; f.bsb = b->stride[0]; f.bsh = b->stride[1]; f.bsd = b->stride[2];
     f.ww = (const float*)w->data; f.wsb = w->stride[0]; f.wsh = w->stride[1]; f.wsd = w->stride[2];
-    f.state = state ? (const float*)state->data : nullptr;
+    f.state = state ? state->data : nullptr;
     f.ssb = state ? state->stride[0] : 0; f.ssh = state ? state->stride[1] : 0; f.ssr = state ? state->stride[2] : 0;
-    f.nst = (float*)new_state->data; f.nsb = new_state->stride[0]; f.nsh = new_state->stride[1];
+    f.nst = new_state->data; f.nsb = new_state->stride[0]; f.nsh = new_state->stride[1];
     f.nsr = new_state->stride[2];
     f.out = out->data; f.odt = out->dtype; f.osb = out->stride[0]; f.osh = out->stride[1]; f.osd = out->stride[2];
     f.BH = B * H; f.H = (int)H; f.use_log = log_alpha != nullptr;
     const dim3 g4((unsigned)ceil_div(B * H, 4));
-    if (q->dtype == MABA_BF16) hipLaunchKernelGGL(dgda_step_wave_kernel<uint16_t>, g4, dim3(256), 0, s, f);
-    else hipLaunchKernelGGL(dgda_step_wave_kernel<float>, g4, dim3(256), 0, s, f);
+    const bool sbf = sdt == MABA_BF16;
+    if (q->dtype == MABA_BF16 && sbf) hipLaunchKernelGGL((dgda_step_wave_kernel<uint16_t, uint16_t>), g4, dim3(256), 0, s, f);
+    else if (q->dtype == MABA_BF16) hipLaunchKernelGGL((dgda_step_wave_kernel<uint16_t, float>), g4, dim3(256), 0, s, f);
+    else if (sbf) hipLaunchKernelGGL((dgda_step_wave_kernel<float, uint16_t>), g4, dim3(256), 0, s, f);
+    else hipLaunchKernelGGL((dgda_step_wave_kernel<float, float>), g4, dim3(256), 0, s, f);
     return check_launch("dgda_step");
   }
   dim3 grid((unsigned)(B * H)), block(256);

@@ -130,7 +130,8 @@ struct DecTileArgs {
   const uint16_t* q; int64_t qsb, qsh;   // [B, Hq, d] bf16, channel stride 1
   const uint16_t* c; int64_t csb, csn;   // [B, nb, d] bf16, channel stride 1
   int64_t nb;
-  int ntiles, Hq;
+  int ntiles, Hq;                         // ntiles: the workspace rows' tile capacity
+  const int64_t* dlen; int bs;            // device sequence length: nb = ceil(*dlen / bs) (null: nb as given)
   float scale, lam;
   float* sc;                              // [B, Hq, ntiles * 64] workspace scores
   key64* tmax;                            // [B, Hq, ntiles] best key per tile
@@ -143,7 +144,9 @@ __global__ __launch_bounds__(256) void index_decode_tile_kernel(DecTileArgs a) {
   const int g = lane >> 4, c16 = lane & 15;
   const int tile = blockIdx.x * 4 + wave;
   const int64_t bi = blockIdx.y;
-  if (tile >= a.ntiles) return;  // wave-uniform; the kernel has no barrier
+  // a device length never reaches past the capacity the buffers were sized for
+  const int64_t nb = a.dlen ? min((*a.dlen + a.bs - 1) / a.bs, a.nb) : a.nb;
+  if ((int64_t)tile * 64 >= nb) return;  // wave-uniform; the kernel has no barrier
   const int64_t n0 = (int64_t)tile * 64;
   const uint16_t* cb = a.c + bi * a.csb;
   // all centroid loads of the tile first: lane (c16, g) reads row 16 rb + c16, dims 32 p + 8 g .. +7
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(256) void index_decode_tile_kernel(DecTileArgs a) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       i16x8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (n < a.nb) z = *(const i16x8_t*)(cb + n * a.csn + 32 * p + 8 * g);
+      if (n < nb) z = *(const i16x8_t*)(cb + n * a.csn + 32 * p + 8 * g);
       av[rb][p] = z;
     }
   }
@@ -181,9 +184,9 @@ __global__ __launch_bounds__(256) void index_decode_tile_kernel(DecTileArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int64_t n = n0 + 16 * rb + 4 * g + i;
       float sc = -INFINITY;
-      if (n < a.nb) {
+      if (n < nb) {
         // log1p(m) = log(1 + m) with 1 + m exact for integer block distances m < 2^24
-        sc = acc[i] * a.scale - a.lam * __logf(1.f + (float)(a.nb - 1 - n));
+        sc = acc[i] * a.scale - a.lam * __logf(1.f + (float)(nb - 1 - n));
         best = kmax(best, make_key(sc, (uint32_t)n));
         if (hv && a.scores) a.scores[bi * a.ssb + c16 * a.ssh + n * a.ssn] = sc;
       }
@@ -213,7 +216,8 @@ __device__ __forceinline__ int count_greater(const key64* s, int n8, key64 k) {
 struct DecSelArgs {
   const float* sc; const key64* tmax;
   int64_t nb;
-  int ntiles, Hq, K, ak;
+  int ntiles, Hq, K, ak;                  // ntiles: the workspace rows' tile capacity
+  const int64_t* dlen; int bs;            // as in DecTileArgs
   int64_t* out; int64_t osb, osh, osk;
 };
 
@@ -251,6 +255,9 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   const int64_t bi = row / a.Hq;
   const int h = (int)(row % a.Hq);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t nb = a.dlen ? min((*a.dlen + a.bs - 1) / a.bs, a.nb) : a.nb;   // clamped to the capacity
+  const int ntl = (int)((nb + 63) / 64);                 // tiles holding centroids
+  const int ak = (int)(a.K < nb ? a.K : nb);
   const key64* tm = a.tmax + row * a.ntiles;
   const float* sc = a.sc + row * (int64_t)a.ntiles * 64;
   // first pass of score loads, issued before the tile maxima so that both are in flight
@@ -260,7 +267,7 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   for (int j = 0; j < SEL_V; ++j) {
     const int64_t n = 4 * (SEL_T * j + tid);
     f32x4 z = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    if (n < a.nb) z = *(const f32x4*)(sc + n);
+    if (n < nb) z = *(const f32x4*)(sc + n);
     v[j] = z;
   }
   if (tid < 64) s_k[tid] = KEY_NONE;   // list slots the final rank reads past cnt
@@ -268,7 +275,7 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   // tile maxima: thread t folds tiles t, t + SEL_T, ...; group j < 64 is the tiles
   // t = j (mod 64), i.e. lane j of every wave (any partition of the tiles gives a valid bound)
   key64 m = KEY_NONE;
-  for (int t = tid; t < a.ntiles; t += SEL_T) m = kmax(m, tm[t]);
+  for (int t = tid; t < ntl; t += SEL_T) m = kmax(m, tm[t]);
   s_part[tid] = m;
   __syncthreads();
   // tau = K-th largest group maximum (keys are distinct; empty groups hold KEY_NONE):
@@ -284,7 +291,7 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   if (wave < 4) s_rank[wave][lane] = count_greater16(s_g + 16 * wave, gm);
   __syncthreads();
   if (wave == 0) {
-    const int G = a.ntiles < SEL_GROUPS ? a.ntiles : SEL_GROUPS;   // groups j < G hold a tile
+    const int G = ntl < SEL_GROUPS ? ntl : SEL_GROUPS;   // groups j < G hold a tile
     key64 tau = KEY_NONE;
     if (G >= a.K) {
       const int rank = s_rank[0][lane] + s_rank[1][lane] + s_rank[2][lane] + s_rank[3][lane];
@@ -307,13 +314,13 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   const float tau_s = key_score(tau);
   auto scan = [&](auto all_c) {
     constexpr bool ALL = decltype(all_c)::value;
-    for (int64_t base = 0; base < a.nb; base += SEL_PASS) {
+    for (int64_t base = 0; base < nb; base += SEL_PASS) {
       if (base > 0) {
 #pragma unroll
         for (int j = 0; j < SEL_V; ++j) {
           const int64_t n = base + 4 * (SEL_T * j + tid);
           f32x4 z = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-          if (n < a.nb) z = *(const f32x4*)(sc + n);
+          if (n < nb) z = *(const f32x4*)(sc + n);
           v[j] = z;
         }
       }
@@ -322,7 +329,7 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
       for (int j = 0; j < SEL_V; ++j) {
         const f32x4 x = v[j];
         if (ALL) {
-          if (__ballot(n0 + 4 * SEL_T * j < a.nb) == 0ull) continue;
+          if (__ballot(n0 + 4 * SEL_T * j < nb) == 0ull) continue;
         } else {
           const float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
           if (__ballot(!(mx < tau_s)) == 0ull) continue;
@@ -330,7 +337,7 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int64_t n = n0 + 4 * SEL_T * j + i;
-          const bool t = ALL ? n < a.nb : !(x[i] < tau_s);
+          const bool t = ALL ? n < nb : !(x[i] < tau_s);
           const unsigned long long b = __ballot(t);
           if (b == 0ull) continue;
           int at = 0;
@@ -346,14 +353,14 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   __syncthreads();
   const int cnt = s_cnt;
   int64_t* orow = a.out + bi * a.osb + h * a.osh;
-  if (cnt <= SEL_CAP && cnt >= a.ak) {
+  if (cnt <= SEL_CAP && cnt >= ak) {
     if (cnt <= 64) {  // rank across the four waves; slots past cnt hold KEY_NONE
       const key64 kj = s_k[lane];
       if (wave < 4) s_rank[wave][lane] = count_greater16(s_k + 16 * wave, kj);
       __syncthreads();
       if (wave == 0) {
         const int rank = s_rank[0][lane] + s_rank[1][lane] + s_rank[2][lane] + s_rank[3][lane];
-        if (lane < cnt && rank < a.ak) orow[rank * a.osk] = (int64_t)key_index(kj);
+        if (lane < cnt && rank < ak) orow[rank * a.osk] = (int64_t)key_index(kj);
       }
       return;
     }
@@ -363,7 +370,7 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
     for (int j = tid; j < cnt; j += SEL_T) {
       const key64 kj = s_k[j];
       const int rank = count_greater(s_k, c8, kj);
-      if (rank < a.ak) orow[rank * a.osk] = (int64_t)key_index(kj);
+      if (rank < ak) orow[rank * a.osk] = (int64_t)key_index(kj);
     }
     return;
   }
@@ -372,10 +379,10 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   // once and older slices are rejected by the merge's K-th-key test), then wave 0 merges
   // the SEL_W lists
   key64 list = KEY_NONE;
-  const int64_t nsl = (a.nb + 63) / 64;
+  const int64_t nsl = (nb + 63) / 64;
   for (int64_t sl = nsl - 1 - wave; sl >= 0; sl -= SEL_W) {
     const int64_t n = sl * 64 + lane;
-    const key64 key = n < a.nb ? make_key(sc[n], (uint32_t)n) : KEY_NONE;
+    const key64 key = n < nb ? make_key(sc[n], (uint32_t)n) : KEY_NONE;
     list = wave_merge_topk(list, key >= tau ? key : KEY_NONE, a.K);
   }
   __syncthreads();
@@ -384,7 +391,7 @@ __global__ __launch_bounds__(SEL_T) void index_decode_select_kernel(DecSelArgs a
   if (wave == 0) {
     key64 m = s_c[lane];
     for (int w = 1; w < SEL_W; ++w) m = wave_merge_topk(m, s_c[w * 64 + lane], a.K);
-    if (lane < a.ak) orow[lane * a.osk] = (int64_t)key_index(m);
+    if (lane < ak) orow[lane * a.osk] = (int64_t)key_index(m);
   }
 }
 
@@ -537,6 +544,57 @@ extern "C" size_t maba_hip_index_topk_decode_workspace_size(int64_t B, int64_t H
   return mfma > scalar ? mfma : scalar;
 }
 
+// The MFMA decode (tile + select launches).  nb_cap: centroid capacity of the workspace
+// rows; dlen (device) holds the sequence length when the centroid count is device-resident
+// (nb = ceil(*dlen / block_size), at most nb_cap), else null and nb_cap is the count.
+static int launch_decode_mfma(const maba_tensor* q, const maba_tensor* centroids, int64_t nb_cap,
+                              const int64_t* dlen, int block_size, float lambda_dist, int top_k, int ak,
+                              maba_tensor* out_idx, maba_tensor* out_scores, void* workspace, hipStream_t s) {
+  const int64_t B = q->shape[0], Hq = q->shape[1], d = q->shape[2];
+  DecTileArgs m;
+  m.q = (const uint16_t*)q->data; m.qsb = q->stride[0]; m.qsh = q->stride[1];
+  m.c = (const uint16_t*)centroids->data; m.csb = centroids->stride[0]; m.csn = centroids->stride[1];
+  m.nb = nb_cap; m.ntiles = (int)ceil_div(nb_cap, 64); m.Hq = (int)Hq;
+  m.dlen = dlen; m.bs = block_size;
+  m.scale = 1.0f / sqrtf((float)d);
+  m.lam = lambda_dist;
+  m.sc = (float*)workspace;
+  m.tmax = (key64*)((char*)workspace + decode_scores_bytes(B, Hq, nb_cap));
+  m.scores = out_scores ? (float*)out_scores->data : nullptr;
+  m.ssb = out_scores ? out_scores->stride[0] : 0;
+  m.ssh = out_scores ? out_scores->stride[1] : 0;
+  m.ssn = out_scores ? out_scores->stride[2] : 0;
+  const dim3 grid((unsigned)ceil_div(m.ntiles, 4), (unsigned)B);
+  switch (d / 32) {
+    case 1: hipLaunchKernelGGL(index_decode_tile_kernel<1>, grid, dim3(256), 0, s, m); break;
+    case 2: hipLaunchKernelGGL(index_decode_tile_kernel<2>, grid, dim3(256), 0, s, m); break;
+    case 3: hipLaunchKernelGGL(index_decode_tile_kernel<3>, grid, dim3(256), 0, s, m); break;
+    case 4: hipLaunchKernelGGL(index_decode_tile_kernel<4>, grid, dim3(256), 0, s, m); break;
+    case 5: hipLaunchKernelGGL(index_decode_tile_kernel<5>, grid, dim3(256), 0, s, m); break;
+    case 6: hipLaunchKernelGGL(index_decode_tile_kernel<6>, grid, dim3(256), 0, s, m); break;
+    case 7: hipLaunchKernelGGL(index_decode_tile_kernel<7>, grid, dim3(256), 0, s, m); break;
+    default: hipLaunchKernelGGL(index_decode_tile_kernel<8>, grid, dim3(256), 0, s, m); break;
+  }
+  int rc = check_launch("index_topk_decode/tiles");
+  if (rc) return rc;
+  DecSelArgs e;
+  e.sc = m.sc; e.tmax = m.tmax; e.nb = nb_cap; e.ntiles = m.ntiles; e.Hq = (int)Hq; e.K = top_k; e.ak = ak;
+  e.dlen = dlen; e.bs = block_size;
+  e.out = (int64_t*)out_idx->data; e.osb = out_idx->stride[0]; e.osh = out_idx->stride[1];
+  e.osk = out_idx->stride[2];
+  hipLaunchKernelGGL(index_decode_select_kernel, dim3((unsigned)(B * Hq)), dim3(SEL_T), 0, s, e);
+  return check_launch("index_topk_decode/select");
+}
+
+// Whether the MFMA decode takes q / centroids (bf16 rows, 16-byte aligned, d a multiple of 32).
+static bool decode_mfma_ok(const maba_tensor* q, const maba_tensor* centroids) {
+  const int64_t B = q->shape[0], Hq = q->shape[1], d = q->shape[2];
+  return q->dtype == MABA_BF16 && centroids->dtype == MABA_BF16 && q->stride[2] == 1 && centroids->stride[2] == 1 &&
+         d % 32 == 0 && d <= 256 && (uintptr_t)q->data % 16 == 0 && (uintptr_t)centroids->data % 16 == 0 &&
+         (B == 1 || q->stride[0] % 8 == 0) && (Hq == 1 || q->stride[1] % 8 == 0) &&
+         (B == 1 || centroids->stride[0] % 8 == 0) && centroids->stride[1] % 8 == 0;
+}
+
 extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tensor* centroids,
                                           float lambda_dist, int top_k, maba_tensor* out_idx,
                                           maba_tensor* out_scores, void* workspace,
@@ -565,44 +623,10 @@ extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tenso
   if (!workspace || workspace_bytes < need)
     return fail(MABA_ERR_WORKSPACE, "index_topk_decode: workspace of %zu bytes required", need);
   hipStream_t s = (hipStream_t)stream;
-  const bool mfma_ok = q->dtype == MABA_BF16 && centroids->dtype == MABA_BF16 && q->stride[2] == 1 &&
-                       centroids->stride[2] == 1 && d % 32 == 0 && d <= 256 && (uintptr_t)q->data % 16 == 0 &&
-                       (uintptr_t)centroids->data % 16 == 0 && (B == 1 || q->stride[0] % 8 == 0) &&
-                       (Hq == 1 || q->stride[1] % 8 == 0) && (B == 1 || centroids->stride[0] % 8 == 0) &&
-                       centroids->stride[1] % 8 == 0;
-  if (mfma_ok) {
-    DecTileArgs m;
-    m.q = (const uint16_t*)q->data; m.qsb = q->stride[0]; m.qsh = q->stride[1];
-    m.c = (const uint16_t*)centroids->data; m.csb = centroids->stride[0]; m.csn = centroids->stride[1];
-    m.nb = nb; m.ntiles = (int)ceil_div(nb, 64); m.Hq = (int)Hq;
-    m.scale = 1.0f / sqrtf((float)d);
-    m.lam = lambda_dist;
-    m.sc = (float*)workspace;
-    m.tmax = (key64*)((char*)workspace + decode_scores_bytes(B, Hq, nb));
-    m.scores = out_scores ? (float*)out_scores->data : nullptr;
-    m.ssb = out_scores ? out_scores->stride[0] : 0;
-    m.ssh = out_scores ? out_scores->stride[1] : 0;
-    m.ssn = out_scores ? out_scores->stride[2] : 0;
-    const dim3 grid((unsigned)ceil_div(m.ntiles, 4), (unsigned)B);
-    switch (d / 32) {
-      case 1: hipLaunchKernelGGL(index_decode_tile_kernel<1>, grid, dim3(256), 0, s, m); break;
-      case 2: hipLaunchKernelGGL(index_decode_tile_kernel<2>, grid, dim3(256), 0, s, m); break;
-      case 3: hipLaunchKernelGGL(index_decode_tile_kernel<3>, grid, dim3(256), 0, s, m); break;
-      case 4: hipLaunchKernelGGL(index_decode_tile_kernel<4>, grid, dim3(256), 0, s, m); break;
-      case 5: hipLaunchKernelGGL(index_decode_tile_kernel<5>, grid, dim3(256), 0, s, m); break;
-      case 6: hipLaunchKernelGGL(index_decode_tile_kernel<6>, grid, dim3(256), 0, s, m); break;
-      case 7: hipLaunchKernelGGL(index_decode_tile_kernel<7>, grid, dim3(256), 0, s, m); break;
-      default: hipLaunchKernelGGL(index_decode_tile_kernel<8>, grid, dim3(256), 0, s, m); break;
-    }
-    int rc = check_launch("index_topk_decode/tiles");
-    if (rc) return rc;
-    DecSelArgs e;
-    e.sc = m.sc; e.tmax = m.tmax; e.nb = nb; e.ntiles = m.ntiles; e.Hq = (int)Hq; e.K = top_k; e.ak = (int)ak;
-    e.out = (int64_t*)out_idx->data; e.osb = out_idx->stride[0]; e.osh = out_idx->stride[1];
-    e.osk = out_idx->stride[2];
-    hipLaunchKernelGGL(index_decode_select_kernel, dim3((unsigned)(B * Hq)), dim3(SEL_T), 0, s, e);
-    return check_launch("index_topk_decode/select");
-  }
+  const bool mfma_ok = decode_mfma_ok(q, centroids);
+  if (mfma_ok)
+    return launch_decode_mfma(q, centroids, nb, nullptr, 0, lambda_dist, top_k, (int)ak, out_idx, out_scores,
+                              workspace, s);
   DecArgs a;
   a.q = q->data; a.qdt = q->dtype; a.qsb = q->stride[0]; a.qsh = q->stride[1]; a.qsd = q->stride[2];
   a.c = centroids->data; a.cdt = centroids->dtype;
@@ -624,6 +648,34 @@ extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tenso
                      (int)Hq, top_k, (int)ak, (int64_t*)out_idx->data, out_idx->stride[0],
                      out_idx->stride[1], out_idx->stride[2]);
   return check_launch("index_topk_decode/merge");
+}
+
+extern "C" int maba_hip_index_topk_decode_dev(const maba_tensor* q, const maba_tensor* centroids,
+                                              const int64_t* d_len, int block_size, float lambda_dist,
+                                              int top_k, maba_tensor* out_idx, void* workspace,
+                                              size_t workspace_bytes, void* stream) {
+  if (!q || q->ndim != 3) return fail(MABA_ERR_INVALID, "index_topk_decode_dev: q must be [B,Hq,d]");
+  if (!centroids || centroids->ndim != 3)
+    return fail(MABA_ERR_INVALID, "index_topk_decode_dev: centroids must be [B,Ncap,d]");
+  if (!d_len) return fail(MABA_ERR_INVALID, "index_topk_decode_dev: d_len (device int64) required");
+  const int64_t B = q->shape[0], Hq = q->shape[1], d = q->shape[2], ncap = centroids->shape[1];
+  if (centroids->shape[0] != B || centroids->shape[2] != d)
+    return fail(MABA_ERR_INVALID, "index_topk_decode_dev: centroids shape mismatch");
+  if (top_k <= 0 || top_k > 64) return fail(MABA_ERR_INVALID, "index_topk_decode_dev: top_k in [1, 64]");
+  if (block_size <= 0) return fail(MABA_ERR_INVALID, "index_topk_decode_dev: block_size must be positive");
+  const int64_t so[3] = {B, Hq, top_k};
+  if (!expect_shape(out_idx, "out_idx", 3, so)) return MABA_ERR_INVALID;
+  if (out_idx->dtype != MABA_I64) return fail(MABA_ERR_DTYPE, "index_topk_decode_dev: out_idx must be int64");
+  if (Hq > IDX_MAX_HEADS) return fail(MABA_ERR_UNSUPPORTED, "index_topk_decode_dev: Hq <= %d", IDX_MAX_HEADS);
+  if (!decode_mfma_ok(q, centroids))
+    return fail(MABA_ERR_UNSUPPORTED, "index_topk_decode_dev: bf16 q and centroids, 16-byte aligned rows, d a "
+                                      "multiple of 32 up to 256");
+  if (B * Hq == 0 || ncap == 0) return MABA_OK;
+  const size_t need = maba_hip_index_topk_decode_workspace_size(B, Hq, ncap, top_k);
+  if (!workspace || workspace_bytes < need)
+    return fail(MABA_ERR_WORKSPACE, "index_topk_decode_dev: workspace of %zu bytes required", need);
+  return launch_decode_mfma(q, centroids, ncap, d_len, block_size, lambda_dist, top_k, top_k, out_idx, nullptr,
+                            workspace, (hipStream_t)stream);
 }
 
 extern "C" int maba_hip_index_topk(const maba_tensor* q_idx, const maba_tensor* centroids,

@@ -46,7 +46,35 @@ struct SaArgs {
   // local, [s_loc, s_loc + s_hca) HCA, then the sparse ones (s_sp1 per index row)
   int tpw, s_loc, s_hca, s_sp1, s_sp;
   float scale;
+  const int64_t* dlen;   // device sequence length (null: L as given); the geometry above is then re-derived
 };
+
+// Tile geometry of the three streams (per batch element).
+__host__ __device__ inline void sa_geometry(SaArgs& a, int64_t L, int window, int n_sink, int pool, int Hi, int K) {
+  const int64_t ns = L < n_sink ? L : n_sink;
+  const int64_t st = (L - window) > ns ? (L - window) : ns;
+  a.ns = (int)ns;
+  a.loc_start = (int)st;
+  a.nloc = (int)(ns + (L - st));
+  a.nc = (int)(L / pool);
+  a.t_loc = (int)((a.nloc + 63) / 64);
+  a.t_sp = Hi * K;
+  a.t_hca = (L - 1 >= pool - 1) ? (int)((a.nc + 63) / 64) : 0;
+  a.ntiles = a.t_loc + a.t_sp + a.t_hca;
+}
+
+// The arguments of a launch with a device-resident sequence length: the stream geometry
+// of the current length (the partial-slot layout stays that of the capacity the host
+// planned for, so slots past the current length hold empty partials).
+__device__ __forceinline__ SaArgs sa_live(const SaArgs& in) {
+  SaArgs a = in;
+  if (a.dlen) {   // a.L holds the capacity the buffers were checked against
+    const int64_t L = *a.dlen;
+    a.L = L < 1 ? 1 : (L < a.L ? L : a.L);
+    sa_geometry(a, a.L, a.window, a.n_sink, a.pool, a.Hi, a.K);
+  }
+  return a;
+}
 
 __device__ __forceinline__ int64_t sa_part_off(const SaArgs& a, int64_t b, int slot, int h) {
   return (((int64_t)slot * a.B + b) * a.H + h) * (int64_t)(a.dc + 2);
@@ -289,8 +317,9 @@ __device__ __forceinline__ SaWsSrc sa_ws_src(const SaArgs& a, const SaMerge& mg,
 }
 
 // One workgroup per (b, h) over the per-tile partials of the generic path.
-__global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a, SaMerge mg) {
+__global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a_in, SaMerge mg) {
   __shared__ float lds[2 * 256 + 8];
+  const SaArgs a = sa_live(a_in);
   const int64_t b = blockIdx.x / a.H;
   const int h = blockIdx.x % a.H;
   sa_merge<256>(a, mg, b, h, lds, sa_ws_src(a, mg, b, h));
@@ -398,7 +427,8 @@ __device__ __forceinline__ void sa_load_tile(const SaArgs& a, const SaSeg& sg, i
 }
 
 template <int NP>  // d_c = 32 * NP
-__global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a) {
+__global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a_in) {
+  const SaArgs a = sa_live(a_in);
   constexpr int DC = 32 * NP;
   constexpr int TP = DC + 8;  // row pitch (bf16) of the per-wave key tile: 16-B aligned, rows shift 4 banks
   __shared__ __attribute__((aligned(16))) short s_tile[4][64 * TP];
@@ -600,20 +630,6 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a) {
   }
 }
 
-// Tile geometry of the three streams (per batch element).
-static void sa_geometry(SaArgs& a, int64_t L, int window, int n_sink, int pool, int Hi, int K) {
-  const int64_t ns = L < n_sink ? L : n_sink;
-  const int64_t st = (L - window) > ns ? (L - window) : ns;
-  a.ns = (int)ns;
-  a.loc_start = (int)st;
-  a.nloc = (int)(ns + (L - st));
-  a.nc = (int)(L / pool);
-  a.t_loc = (int)ceil_div(a.nloc, 64);
-  a.t_sp = Hi * K;
-  a.t_hca = (L - 1 >= pool - 1) ? (int)ceil_div(a.nc, 64) : 0;
-  a.ntiles = a.t_loc + a.t_sp + a.t_hca;
-}
-
 // Segment path geometry: the fewest tiles per wave (at most 8) for which the segments
 // of all streams fit one workgroup per compute unit (every workgroup pays a fixed
 // start-up; one round of workgroups covers the machine).
@@ -664,6 +680,7 @@ static int sa_setup(const maba_tensor* q_lat, const maba_tensor* c_kv, const mab
   empty = B * H == 0;
   if (empty) return MABA_OK;
   a = SaArgs{};
+  a.dlen = nullptr;
   a.q = q_lat->data; a.qdt = q_lat->dtype; a.qsb = q_lat->stride[0]; a.qsh = q_lat->stride[1]; a.qsd = q_lat->stride[2];
   a.qvec = q_lat->dtype == MABA_F32 && q_lat->stride[2] == 1 && (uintptr_t)q_lat->data % 16 == 0 &&
            q_lat->stride[0] % 4 == 0 && q_lat->stride[1] % 4 == 0;
@@ -801,5 +818,26 @@ extern "C" int maba_hip_maba_sa_decode_static(const maba_tensor* q_lat, const ma
   if (rc || empty) return rc;
   // every partial slot the merge reads is written by this call's first launch, so nothing
   // left in the scratch by an earlier call is read
+  return sa_run(a, seg, (hipStream_t)stream);
+}
+
+extern "C" int maba_hip_maba_sa_decode_dev(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                           const maba_tensor* hca, const maba_tensor* idx,
+                                           const maba_tensor* gate, const int64_t* d_len, int64_t L_cap,
+                                           float scale, int window, int n_sink, int block_size, int pool,
+                                           maba_tensor* out_lat, void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+  if (!d_len) return fail(MABA_ERR_INVALID, "maba_sa_decode_dev: d_len (device int64) required");
+  SaArgs a;
+  bool seg = false, empty = false;
+  size_t need = 0;
+  int rc = sa_setup(q_lat, c_kv, hca, idx, gate, out_lat, L_cap, scale, window, n_sink, block_size, pool,
+                    workspace, workspace_bytes, a, seg, empty, need);
+  if (rc || empty) return rc;
+  if (!seg)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_dev: bf16 caches with 16-byte aligned rows and d_c a "
+                                      "multiple of 32 up to 128 required");
+  if (L_cap < pool) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_dev: L_cap must be at least pool");
+  a.dlen = d_len;
   return sa_run(a, seg, (hipStream_t)stream);
 }

@@ -1,0 +1,187 @@
+// The full-model harness's elementwise kernels (reference maba_sparse/model.py):
+//   RMSNorm                 :11-22    h = x / sqrt(mean(x^2) + eps) * w
+//   gated residual + norm   :92-128   x' = x + g * mo (MabaBlock's sigmoid-gated residual),
+//                                     then h = RMSNorm(x') for the next sub-layer
+//   SwiGLU activation       :25-38    a = silu(x W_gate^T) * (x W_up^T), from the one GEMM over
+//                                     the stacked [W_gate; W_up] ([.., 2I] -> [.., I])
+// One wave per row (token); arithmetic in fp32, each output rounded once to its dtype.
+// Bound: HBM (a few row reads and writes per token).
+#include <algorithm>
+
+#include "maba_common.h"
+
+namespace maba {
+
+constexpr int NRM_MAXP = 16;   // channel pairs per lane: C <= 2048
+
+struct NormArgs {
+  const void* x; int64_t xs;        // [R, C] rows (row stride xs, unit channel stride)
+  const void* mo; int64_t ms;       // residual input rows (null: plain RMSNorm)
+  const void* g;                    // [C] residual gate (fp32 or the row dtype)
+  int gdt;
+  const void* w; int wdt;           // [C] norm weight
+  void* xo; int64_t xos;            // x' rows (null: not written)
+  void* h; int64_t hs;              // normalised rows
+  int64_t R;
+  int C;
+  float eps;
+};
+
+template <class T> struct P2;
+template <> struct P2<float> {
+  static __device__ __forceinline__ float2 ld(const void* p, int64_t i) { return *(const float2*)((const float*)p + i); }
+  static __device__ __forceinline__ void st(void* p, int64_t i, float2 v) { *(float2*)((float*)p + i) = v; }
+};
+template <> struct P2<uint16_t> {
+  static __device__ __forceinline__ float2 ld(const void* p, int64_t i) {
+    const uint32_t u = *(const uint32_t*)((const uint16_t*)p + i);
+    return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+  }
+  static __device__ __forceinline__ void st(void* p, int64_t i, float2 v) {
+    *(uint32_t*)((uint16_t*)p + i) = (uint32_t)f32_to_bf16_bits(v.x) | ((uint32_t)f32_to_bf16_bits(v.y) << 16);
+  }
+};
+
+__device__ __forceinline__ float2 ld_any2(const void* p, int dt, int64_t i) {
+  return dt == MABA_F32 ? P2<float>::ld(p, i) : P2<uint16_t>::ld(p, i);
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.R) return;   // wave-uniform; no barriers
+  const int np = a.C / 2;
+  float2 v[NRM_MAXP];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NRM_MAXP; ++i) {
+    const int j = lane + 64 * i;
+    if (j < np) {
+      float2 x = P2<T>::ld(a.x, r * a.xs + 2 * j);
+      if (a.mo) {
+        const float2 m = P2<T>::ld(a.mo, r * a.ms + 2 * j);
+        const float2 g = ld_any2(a.g, a.gdt, 2 * j);
+        x.x = fmaf(g.x, m.x, x.x);
+        x.y = fmaf(g.y, m.y, x.y);
+        if (a.xo) {   // the residual stream is stored in the row dtype; the norm reads it as stored
+          P2<T>::st(a.xo, r * a.xos + 2 * j, x);
+          x = P2<T>::ld(a.xo, r * a.xos + 2 * j);
+        }
+      }
+      v[i] = x;
+      ss = fmaf(x.x, x.x, fmaf(x.y, x.y, ss));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  const float inv = rsqrtf(ss / (float)a.C + a.eps);
+#pragma unroll
+  for (int i = 0; i < NRM_MAXP; ++i) {
+    const int j = lane + 64 * i;
+    if (j < np) {
+      const float2 w = ld_any2(a.w, a.wdt, 2 * j);
+      P2<T>::st(a.h, r * a.hs + 2 * j, make_float2(v[i].x * inv * w.x, v[i].y * inv * w.y));
+    }
+  }
+}
+
+struct SwigluArgs {
+  const void* gu; int64_t gus;      // [R, 2I]: gate columns [0, I), up columns [I, 2I)
+  void* out; int64_t os;            // [R, I]
+  int64_t R;
+  int I;
+};
+
+template <class T>
+__global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
+  const int np = a.I / 2;
+  const int64_t total = a.R * np;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t r = e / np;
+    const int j = (int)(e - r * np);
+    const float2 g = P2<T>::ld(a.gu, r * a.gus + 2 * j);
+    const float2 u = P2<T>::ld(a.gu, r * a.gus + a.I + 2 * j);
+    const float s0 = __fdividef(g.x, 1.f + __expf(-g.x)), s1 = __fdividef(g.y, 1.f + __expf(-g.y));
+    P2<T>::st(a.out, r * a.os + 2 * j, make_float2(s0 * u.x, s1 * u.y));
+  }
+}
+
+// Rows of a [..., C] tensor: leading dims collapse into one when they are contiguous.
+static bool rows_of(const maba_tensor* t, int C, int64_t& R, int64_t& rs) {
+  if (!t || t->ndim < 1 || t->ndim > 3 || t->shape[t->ndim - 1] != C || t->stride[t->ndim - 1] != 1) return false;
+  R = 1;
+  for (int d = 0; d < t->ndim - 1; ++d) R *= t->shape[d];
+  rs = C;
+  if (t->ndim == 2) {
+    rs = t->stride[0];
+  } else if (t->ndim == 3) {
+    if (t->shape[1] == 1) rs = t->stride[0];                   // [B, 1, C]: rows over the batch
+    else if (t->shape[0] == 1) rs = t->stride[1];
+    else if (t->stride[0] == t->shape[1] * t->stride[1]) rs = t->stride[1];
+    else return false;
+  }
+  return R <= 1 || (rs % 2 == 0 && (uintptr_t)t->data % 4 == 0);
+}
+
+}  // namespace maba
+
+using namespace maba;
+
+extern "C" int maba_hip_rmsnorm(const maba_tensor* x, const maba_tensor* mo, const maba_tensor* gate,
+                                const maba_tensor* weight, float eps, maba_tensor* x_out, maba_tensor* h,
+                                void* stream) {
+  if (!x || !weight || !h) return fail(MABA_ERR_INVALID, "rmsnorm: x, weight and h required");
+  const int C = (int)x->shape[x->ndim - 1];
+  if (C % 2 != 0 || C > 2 * 64 * NRM_MAXP) return fail(MABA_ERR_UNSUPPORTED, "rmsnorm: C even and <= %d", 128 * NRM_MAXP);
+  if (x->dtype != MABA_F32 && x->dtype != MABA_BF16) return fail(MABA_ERR_DTYPE, "rmsnorm: f32 or bf16 rows");
+  NormArgs a;
+  int64_t R, R2;
+  if (!rows_of(x, C, R, a.xs)) return fail(MABA_ERR_UNSUPPORTED, "rmsnorm: x rows must be [.., C] with unit channel stride");
+  if (!rows_of(h, C, R2, a.hs) || R2 != R || h->dtype != x->dtype)
+    return fail(MABA_ERR_INVALID, "rmsnorm: h must match x");
+  if (weight->ndim != 1 || weight->shape[0] != C || weight->stride[0] != 1 ||
+      (weight->dtype != MABA_F32 && weight->dtype != MABA_BF16) || (uintptr_t)weight->data % 4)
+    return fail(MABA_ERR_INVALID, "rmsnorm: weight must be [C] f32/bf16");
+  a.mo = nullptr; a.ms = 0; a.g = nullptr; a.gdt = MABA_F32; a.xo = nullptr; a.xos = 0;
+  if (mo) {
+    if (!rows_of(mo, C, R2, a.ms) || R2 != R || mo->dtype != x->dtype)
+      return fail(MABA_ERR_INVALID, "rmsnorm: mo must match x");
+    if (!gate || gate->ndim != 1 || gate->shape[0] != C || gate->stride[0] != 1 ||
+        (gate->dtype != MABA_F32 && gate->dtype != MABA_BF16) || (uintptr_t)gate->data % 4)
+      return fail(MABA_ERR_INVALID, "rmsnorm: gate must be [C] f32/bf16");
+    a.mo = mo->data; a.g = gate->data; a.gdt = gate->dtype;
+    if (x_out) {
+      if (!rows_of(x_out, C, R2, a.xos) || R2 != R || x_out->dtype != x->dtype)
+        return fail(MABA_ERR_INVALID, "rmsnorm: x_out must match x");
+      a.xo = x_out->data;
+    }
+  }
+  a.x = x->data; a.w = weight->data; a.wdt = weight->dtype; a.h = h->data;
+  a.R = R; a.C = C; a.eps = eps;
+  if (R == 0) return MABA_OK;
+  const dim3 grid((unsigned)ceil_div(R, 4));
+  if (x->dtype == MABA_F32) hipLaunchKernelGGL(rmsnorm_kernel<float>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  else hipLaunchKernelGGL(rmsnorm_kernel<uint16_t>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch("rmsnorm");
+}
+
+extern "C" int maba_hip_swiglu(const maba_tensor* gate_up, maba_tensor* out, void* stream) {
+  if (!gate_up || !out) return fail(MABA_ERR_INVALID, "swiglu: gate_up and out required");
+  const int I = (int)out->shape[out->ndim - 1];
+  if (gate_up->shape[gate_up->ndim - 1] != 2 * (int64_t)I || I % 2 != 0)
+    return fail(MABA_ERR_INVALID, "swiglu: gate_up [.., 2I] and out [.., I] with I even");
+  if (gate_up->dtype != out->dtype || (out->dtype != MABA_F32 && out->dtype != MABA_BF16))
+    return fail(MABA_ERR_DTYPE, "swiglu: f32 or bf16, one dtype");
+  SwigluArgs a;
+  int64_t R, R2;
+  if (!rows_of(gate_up, 2 * I, R, a.gus) || !rows_of(out, I, R2, a.os) || R2 != R)
+    return fail(MABA_ERR_UNSUPPORTED, "swiglu: rows with unit channel stride required");
+  a.gu = gate_up->data; a.out = out->data; a.R = R; a.I = I;
+  if (R == 0) return MABA_OK;
+  const int64_t total = R * (I / 2);
+  const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total, 256), 65536);
+  if (out->dtype == MABA_F32) hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);
+  else hipLaunchKernelGGL(swiglu_kernel<uint16_t>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch("swiglu");
+}

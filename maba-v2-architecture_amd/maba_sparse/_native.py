@@ -16,7 +16,8 @@ from typing import Optional, Sequence
 import torch
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib")
-LIB_PATH = os.path.join(LIB_DIR, "libmaba_hip.so")
+# MABA_HIP_LIBRARY names another build of the same library (a missing file still raises)
+LIB_PATH = os.environ.get("MABA_HIP_LIBRARY") or os.path.join(LIB_DIR, "libmaba_hip.so")
 
 MABA_F32, MABA_F16, MABA_BF16, MABA_F64, MABA_I64, MABA_I32 = 0, 1, 2, 3, 4, 5
 _DTYPE_CODES = {
@@ -48,6 +49,11 @@ EXPORTED_SYMBOLS = (
     "maba_hip_maba_sa_decode_static",
     "maba_hip_dgda_prologue",
     "maba_hip_maba_sa_prefill",
+    "maba_hip_cache_append",
+    "maba_hip_index_topk_decode_dev",
+    "maba_hip_maba_sa_decode_dev",
+    "maba_hip_rmsnorm",
+    "maba_hip_swiglu",
 )
 
 
@@ -91,6 +97,11 @@ def _declare(lib) -> None:
         "maba_hip_maba_sa_decode_static": ([T, T, T, T, T, i64, f, i, i, i, i, T, vp], i),
         "maba_hip_dgda_prologue": ([TA, TA, TA, f, TA, TA, vp], i),
         "maba_hip_maba_sa_prefill": ([T, T, T, T, T, T, T, T, f, i, i, i, i, T, vp], i),
+        "maba_hip_cache_append": ([T, T, vp, T, T, T, T, i, i, vp], i),
+        "maba_hip_index_topk_decode_dev": ([T, T, vp, i, f, i, T, vp, sz, vp], i),
+        "maba_hip_maba_sa_decode_dev": ([T, T, T, T, T, vp, i64, f, i, i, i, i, T, vp, sz, vp], i),
+        "maba_hip_rmsnorm": ([T, T, T, T, f, T, T, vp], i),
+        "maba_hip_swiglu": ([T, T, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -99,7 +99,9 @@ def hip_dgda_step(q, k, v, alpha=None, b=None, w=None, state=None, log_alpha=Non
     B, H, dk = q3.shape
     dv = v3.shape[-1]
     out = torch.empty(B, H, dv, dtype=out_dtype or q.dtype, device=dev)
-    new_state = torch.empty(B, H, dk, dv, dtype=state_dtype or q.dtype, device=dev)
+    new_state = kwargs.get("new_state")   # caller buffer; may be `state` itself (updated in place)
+    if new_state is None:
+        new_state = torch.empty(B, H, dk, dv, dtype=state_dtype or q.dtype, device=dev)
     lib = N.load()
     rc = lib.maba_hip_dgda_step(N.desc(q3), N.desc(k3), N.desc(v3), N.desc(a3), N.desc(la3), N.desc(b3),
                                 N.desc(w3), N.desc(state), N.desc(out), N.desc(new_state), N.stream_ptr(dev))
@@ -254,7 +256,11 @@ def hip_dgda_prologue(projections, conv_weights, history=None, n_heads: int = 10
     gates = torch.empty(4 if with_alpha else 3, B, L, C, dtype=gdt, device=dev)
     ys = [qkv[0], qkv[1], qkv[2], gates[0], gates[3] if with_alpha else None, gates[1], gates[2]]
     hdt = history[0].dtype if history is not None else dt
-    nh = list(torch.empty(3, B, C, 3, dtype=hdt, device=dev).unbind(0))
+    out_history = kwargs.get("out_history")
+    if out_history is not None:   # caller buffers; for one token they may be `history` itself
+        nh = list(out_history)
+    else:
+        nh = list(torch.empty(3, B, C, 3, dtype=hdt, device=dev).unbind(0))
     if L == 0:
         for h, old in zip(nh, history or (None,) * 3):
             h.copy_(old) if old is not None else h.zero_()
@@ -285,4 +291,81 @@ def hip_maba_sa_prefill(q, k, v, kh, vh, early, idx, gate_logits, scale: float, 
                                            int(n_sink), int(block_size), int(pool), N.desc(out),
                                            N.stream_ptr(dev))
     N.check(rc, "maba_sa_prefill")
+    return out
+
+
+# ----------------------------------------------------------------------------- serving path
+# Entry points for a decode step whose per-step scalars (the cache position) live in device
+# memory, so that one captured HIP graph serves every position.  Not dispatcher ops: the
+# reference keeps this code inline (layers/indexer.py:58-112, layers/sparse_attention.py:
+# 79-277, model.py:11-128).
+
+
+def hip_cache_append(c_new, k_new, pos, c_cache, k_cache, hca, centroids, pool: int = 64,
+                     block_size: int = 64) -> None:
+    """Writes row ``*pos`` of the latent and key caches and the centroid (and, on a completed
+    pool-block, the HCA mean) of the block holding it (layers/indexer.py:62-82,
+    layers/sparse_attention.py:206).  ``pos`` is a device int64 scalar view."""
+    dev = N.require_device([c_new, k_new, pos, c_cache, k_cache, hca, centroids], "cache_append")
+    rc = N.load().maba_hip_cache_append(N.desc(c_new), N.desc(k_new), pos.data_ptr(), N.desc(c_cache),
+                                        N.desc(k_cache), N.desc(hca), N.desc(centroids), int(pool), int(block_size),
+                                        N.stream_ptr(dev))
+    N.check(rc, "cache_append")
+
+
+def hip_index_topk_decode_dev(q, centroids, length, block_size: int, lambda_dist: float, top_k: int,
+                              workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode scoring + top-k over the first ``ceil(*length / block_size)`` rows of a centroid
+    buffer of fixed capacity (layers/indexer.py:101-112); ``length`` is a device int64 scalar
+    view and the count must reach ``top_k``."""
+    dev = N.require_device([q, centroids, length], "index_topk_decode_dev")
+    B, Hq, _ = q.shape
+    lib = N.load()
+    idx = torch.empty(B, Hq, int(top_k), dtype=torch.long, device=dev)
+    nbytes = lib.maba_hip_index_topk_decode_workspace_size(B, Hq, centroids.shape[1], int(top_k))
+    ws = workspace if workspace is not None and workspace.numel() >= nbytes else _workspace(nbytes, dev)
+    rc = lib.maba_hip_index_topk_decode_dev(N.desc(q), N.desc(centroids), length.data_ptr(), int(block_size),
+                                            float(lambda_dist), int(top_k), N.desc(idx), ws.data_ptr(), ws.numel(),
+                                            N.stream_ptr(dev))
+    N.check(rc, "index_topk_decode_dev")
+    return idx
+
+
+def hip_maba_sa_decode_dev(q_lat, c_cache, hca, idx, gate, length, L_cap: int, scale: float, window: int = 128,
+                           n_sink: int = 4, block_size: int = 64, pool: int = 64,
+                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``maba_sa_decode`` over the first ``*length`` rows of caches of capacity ``L_cap``
+    (``length`` a device int64 scalar view); returns fp32 ``[B, H, d_c]``."""
+    dev = N.require_device([q_lat, c_cache, hca, idx, gate, length], "maba_sa_decode_dev")
+    B, H, dc = q_lat.shape
+    lib = N.load()
+    out = torch.empty(B, H, dc, dtype=torch.float32, device=dev)
+    nbytes = lib.maba_hip_maba_sa_decode_workspace_size(B, H, dc, int(L_cap), idx.shape[-1], int(window),
+                                                        int(n_sink), int(pool))
+    ws = workspace if workspace is not None and workspace.numel() >= nbytes else _workspace(nbytes, dev)
+    rc = lib.maba_hip_maba_sa_decode_dev(N.desc(q_lat), N.desc(c_cache), N.desc(hca), N.desc(idx), N.desc(gate),
+                                         length.data_ptr(), int(L_cap), float(scale), int(window), int(n_sink),
+                                         int(block_size), int(pool), N.desc(out), ws.data_ptr(), ws.numel(),
+                                         N.stream_ptr(dev))
+    N.check(rc, "maba_sa_decode_dev")
+    return out
+
+
+def hip_rmsnorm(x, weight, eps: float, mo=None, gate=None, x_out=None) -> torch.Tensor:
+    """``RMSNorm(x) * weight`` (model.py:11-22); with ``mo`` and ``gate`` the gated residual
+    ``x + gate * mo`` is formed first (written to ``x_out`` when given) and normalised."""
+    dev = N.require_device([x, weight, mo, gate, x_out], "rmsnorm")
+    h = torch.empty_like(x)
+    rc = N.load().maba_hip_rmsnorm(N.desc(x), N.desc(mo), N.desc(gate), N.desc(weight), float(eps), N.desc(x_out),
+                                   N.desc(h), N.stream_ptr(dev))
+    N.check(rc, "rmsnorm")
+    return h
+
+
+def hip_swiglu(gate_up) -> torch.Tensor:
+    """``silu(g) * u`` for ``gate_up = [g | u]`` along the last dim (model.py:25-38)."""
+    dev = N.require_device([gate_up], "swiglu")
+    out = torch.empty(*gate_up.shape[:-1], gate_up.shape[-1] // 2, dtype=gate_up.dtype, device=dev)
+    rc = N.load().maba_hip_swiglu(N.desc(gate_up), N.desc(out), N.stream_ptr(dev))
+    N.check(rc, "swiglu")
     return out

@@ -58,6 +58,33 @@ class LatentCache:
             self.nh = full
 
 
+class DeviceCache:
+    """Decode caches of one MABA-SA layer for the serving path, in the format the
+    ``cache_append`` kernel maintains (all bf16, capacity ``cap`` tokens):
+    latent rows ``c [B, cap, d_c]``, indexer keys ``keys [B, cap, d_idx]``, the means of the
+    complete 64-token blocks ``hca [B, cap // 64, d_c]`` and the block centroids
+    ``cent [B, ceil(cap / 64), d_idx]`` (the last one the zero-padded tail centroid while its
+    block is incomplete).  The sequence length lives in a device counter shared by the
+    model's layers, so one captured decode step replays at every position."""
+
+    def __init__(self, c_kv: torch.Tensor, keys: torch.Tensor, cap: int, pool: int = 64, block: int = 64) -> None:
+        from maba_sparse.kernels import hip_backend as hb
+        B, L, dc = c_kv.shape
+        di = keys.shape[2]
+        dev, dt = c_kv.device, c_kv.dtype
+        self.cap, self.pool, self.block = cap, pool, block
+        self.c = torch.zeros(B, cap, dc, device=dev, dtype=dt)
+        self.keys = torch.zeros(B, cap, di, device=dev, dtype=dt)
+        self.hca = torch.zeros(B, max(1, cap // pool), dc, device=dev, dtype=dt)
+        self.cent = torch.zeros(B, (cap + block - 1) // block, di, device=dev, dtype=dt)
+        self.c[:, :L] = c_kv
+        self.keys[:, :L] = keys.to(dt)
+        if L >= pool:
+            self.hca[:, : L // pool] = hb.hip_hca_pool(c_kv[:, : (L // pool) * pool], pool=pool)
+        if L > 0:
+            self.cent[:, : (L + block - 1) // block] = hb.hip_compute_centroids(self.keys[:, :L], block_size=block)
+
+
 class MabaSparseAttention(WeightCacheMixin, nn.Module):
     def __init__(self, config: Optional[Any] = None, dim: int = 640, n_heads: int = 10, d_head: int = 64,
                  d_c: int = 128, window_size: int = 128, block_size: int = 64, top_k: int = 32,
@@ -180,6 +207,27 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         idx, _ = self.indexer.forward_projected(qi, ki, return_scores=False, past_centroids=past_centroids)
         hca = cache.hca[:, : max(cache.nh, 1)]
         return self._decode(x, cache.c, cache.n, hca, idx, q=q, gate_logits=gl)
+
+    def decode_step_device(self, x: torch.Tensor, cache: DeviceCache, counters: torch.Tensor,
+                           return_parts: bool = False):
+        """One token on the serving path: the token's row joins ``cache`` at position
+        ``counters[0]`` (device), the decode indexer and the fused three-stream decode run over
+        the first ``counters[1] = counters[0] + 1`` rows.  Same math as ``decode_step``; HIP
+        backend, bf16 caches and at least ``top_k`` blocks of history.  ``return_parts`` also
+        returns the selected blocks and the latent-space output ``z`` (for tests)."""
+        from maba_sparse.kernels import hip_backend as hb
+        B = x.shape[0]
+        q, c_new, qi, ki, gl = self._token_projections(x)
+        hb.hip_cache_append(c_new[:, 0], ki[:, 0], counters[0], cache.c, cache.keys, cache.hca, cache.cent,
+                            pool=self.hca_pool_size, block_size=self.block_size)
+        idx = hb.hip_index_topk_decode_dev(qi, cache.cent, counters[1], self.block_size, self.dist_lambda, self.top_k)
+        q_lat = torch.einsum("bhd,hdc->bhc", q.reshape(B, self.n_heads, self.d_head).float(),
+                             self._f32_heads(self.k_up_proj, "_wk_f32"))
+        z = hb.hip_maba_sa_decode_dev(q_lat, cache.c, cache.hca, idx, gl.view(-1, 3), counters[1], cache.cap,
+                                      self.scale, window=self.window_size, n_sink=self.n_sink_tokens,
+                                      block_size=self.block_size, pool=self.hca_pool_size)
+        out = self._heads_out(z, x.dtype)
+        return (out, idx, z) if return_parts else out
 
     # ------------------------------------------------------------ prefill (HIP)
     def _prefill_fusable(self, q: torch.Tensor, c_full: torch.Tensor, idx: torch.Tensor) -> bool:

@@ -20,8 +20,9 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from maba_sparse.layers._wcache import WeightCacheMixin, cached
+from maba_sparse.kernels.dispatcher import get_backend
 from maba_sparse.layers.dgda import DGDALayer
-from maba_sparse.layers.sparse_attention import LatentCache, MabaSparseAttention
+from maba_sparse.layers.sparse_attention import DeviceCache, LatentCache, MabaSparseAttention
 
 
 @dataclass
@@ -84,6 +85,12 @@ class SwiGLUFFN(WeightCacheMixin, nn.Module):
         g, u = F.linear(x, w).chunk(2, dim=-1)
         return self.w_down(F.silu(g) * u)
 
+    def forward_hip(self, x: torch.Tensor) -> torch.Tensor:
+        """``forward`` with the activation ``silu(g) * u`` as one HIP kernel."""
+        from maba_sparse.kernels import hip_backend as hb
+        w = _frozen(self, "gate_up", lambda a, b: torch.cat([a, b], dim=0), self.w_gate.weight, self.w_up.weight)
+        return self.w_down(hb.hip_swiglu(F.linear(x, w)))
+
 
 class FactorizedEmbeddings(nn.Module):
     def __init__(self, vocab_size: int, d_emb: int, dim: int) -> None:
@@ -139,6 +146,58 @@ class MabaBlock(WeightCacheMixin, nn.Module):
         return self._residual(x, mo), ns, ncv
 
 
+class ServingStep:
+    """Device-resident state of a greedy decode after a prefill, and one decode token over it.
+
+    Everything a step reads or writes sits in buffers that keep their addresses: the current
+    token, a device counter pair ``[n, n + 1]`` (rows held before the step and after it), the
+    DGDA states and conv histories (updated in place), and per MABA-SA block a
+    ``DeviceCache`` (appended on device).  So the step can be captured once as a HIP graph
+    and replayed for every position.  The residual stream runs through the fused HIP kernels:
+    gated residual + the next RMSNorm in one launch, SwiGLU's activation in one launch."""
+
+    def __init__(self, model: "MabaSparseForCausalLM", states, length: int, capacity: int,
+                 first_token: torch.Tensor) -> None:
+        self.model = model
+        dev = first_token.device
+        self.tok = first_token.clone()
+        self.counters = torch.tensor([length, length + 1], dtype=torch.long, device=dev)
+        self.capacity = capacity
+        self.dgda, self.caches = {}, {}
+        for i, (layer, (st, cv, ck)) in enumerate(zip(model.layers, states)):
+            if layer.is_attention:
+                keys = layer.mixer.indexer._cached_k_idx
+                self.caches[i] = DeviceCache(ck, keys, capacity, pool=layer.mixer.hca_pool_size,
+                                             block=layer.mixer.block_size)
+            else:
+                self.dgda[i] = (st.clone().contiguous(), [h.clone().contiguous() for h in cv])
+        self.last: Optional[torch.Tensor] = None
+
+    def step(self) -> None:
+        """Decode the token in ``tok``; leaves the next token in ``tok`` and its logits in ``last``."""
+        from maba_sparse.kernels import hip_backend as hb
+        m = self.model
+        layers = m.layers
+        x = m.embeddings(self.tok)
+        n1 = layers[0].norm1
+        h = hb.hip_rmsnorm(x, n1.weight, n1.eps)
+        for i, layer in enumerate(layers):
+            if layer.is_attention:
+                mo = layer.mixer.decode_step_device(h, self.caches[i], self.counters)
+            else:
+                st, hs = self.dgda[i]
+                mo = layer.mixer.step_device(h, st, hs)
+            g1 = _frozen(layer, "g1", torch.sigmoid, layer.res_gate1)
+            g2 = _frozen(layer, "g2", torch.sigmoid, layer.res_gate2)
+            h2 = hb.hip_rmsnorm(x, layer.norm2.weight, layer.norm2.eps, mo=mo, gate=g1, x_out=x)
+            f = layer.ffn.forward_hip(h2)
+            nxt = layers[i + 1].norm1 if i + 1 < len(layers) else m.final_norm
+            h = hb.hip_rmsnorm(x, nxt.weight, nxt.eps, mo=f, gate=g2, x_out=x)
+        self.last = m.lm_head(m.head_proj(h))[:, -1]
+        self.tok.copy_(self.last.argmax(dim=-1, keepdim=True))
+        self.counters += 1
+
+
 class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
     def __init__(self, config: Optional[MabaConfig] = None) -> None:
         super().__init__()
@@ -187,20 +246,51 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
             nps.append((nst, ncv, nck))
         return self._logits(x), nps
 
+    def serving_graph_ok(self, input_ids: torch.Tensor) -> bool:
+        """Whether ``generate_greedy`` can take the captured device-resident step: the HIP
+        backend, a bf16 model, and a prefill holding at least ``top_k`` blocks (the decode
+        indexer then always selects ``top_k`` of them)."""
+        c = self.config
+        if input_ids.device.type != "cuda" or get_backend(input_ids.device) != "hip":
+            return False
+        if next(self.parameters()).dtype != torch.bfloat16:
+            return False
+        if c.dim % 2 or c.dim > 2048 or c.intermediate_size % 2:       # the fused norm and SwiGLU kernels
+            return False
+        for layer in self.layers:
+            mx = layer.mixer
+            if layer.is_attention:
+                if mx.d_c % 32 or mx.d_c > 128 or mx.indexer.d_idx % 32 or mx.indexer.d_idx > 256:
+                    return False
+                if mx.n_heads > 16 or mx.top_k > 64 or mx.block_size > 64:
+                    return False
+            elif mx.d_k != 64 or mx.d_v != 64 or mx.kernel_size != 4 or mx.n_heads > 16:
+                return False
+        return input_ids.shape[1] >= c.top_k * c.block_size
+
     @torch.no_grad()
     def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
-                        on_prefill_done=None, return_logits: bool = False):
+                        on_prefill_done=None, return_logits: bool = False, graph: Optional[bool] = None):
         """Greedy decoding (reference model.py:272-305 at temperature 0): one prefill, then
         ``max_new_tokens - 1`` single-token steps over per-layer decode caches.  Returns the
         new tokens ``[B, max_new_tokens]``.  ``on_prefill_done()`` runs between the two phases
         (a timing hook).  With ``return_logits`` the last-position logits of the prefill and
         of every step come back too, ``[B, max_new_tokens, vocab]``.
 
+        ``graph`` (default: whenever ``serving_graph_ok``) takes the device-resident path: a
+        ``ServingStep`` whose first step runs eagerly (it also warms up the libraries), then
+        one HIP graph of a step, captured once and replayed for every further token.
+        Otherwise each step runs eagerly over ``LatentCache``s.
+
         The stacked and converted weights the decode path keeps are dropped on entry, so a
         weight written through ``.data`` since the last call takes effect."""
         self.clear_weight_caches()
         B, L = input_ids.shape
+        if graph is None:
+            graph = self.serving_graph_ok(input_ids)
         logits, states = self(input_ids)
+        if graph:
+            return self._generate_graph(logits, states, L, max_new_tokens, on_prefill_done, return_logits)
         caches: List[Optional[LatentCache]] = []
         for layer, (_, _, c_kv) in zip(self.layers, states):
             if layer.is_attention:
@@ -227,6 +317,38 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
             out.append(tok)
             if return_logits:
                 seen.append(last)
+        toks = torch.cat(out, dim=1)
+        return (toks, torch.stack(seen, dim=1)) if return_logits else toks
+
+    def _generate_graph(self, logits, states, L, max_new_tokens, on_prefill_done, return_logits):
+        last = logits[:, -1]
+        first = last.argmax(dim=-1, keepdim=True)
+        serv = ServingStep(self, states, L, L + max_new_tokens, first)
+        del states
+        if on_prefill_done is not None:
+            on_prefill_done()
+        out, seen = [first], ([last] if return_logits else None)
+
+        def keep():
+            out.append(serv.tok.clone())
+            if return_logits:
+                seen.append(serv.last.clone())
+
+        steps = max_new_tokens - 1
+        if steps > 0:
+            side = torch.cuda.Stream(device=first.device)
+            side.wait_stream(torch.cuda.current_stream(first.device))
+            with torch.cuda.stream(side):      # the first step, eager: lazy library set-up happens here
+                serv.step()
+            torch.cuda.current_stream(first.device).wait_stream(side)
+            keep()
+        if steps > 1:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):          # recorded, not run
+                serv.step()
+            for _ in range(steps - 1):
+                g.replay()
+                keep()
         toks = torch.cat(out, dim=1)
         return (toks, torch.stack(seen, dim=1)) if return_logits else toks
 

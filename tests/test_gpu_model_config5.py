@@ -1,13 +1,15 @@
 """BASELINE config 5 (the 101M model, bf16 weights ~ N(0, 0.02), B = 16) on the GPU.
 
-- The ``generate_greedy`` serving loop (LatentCache, incremental centroid and HCA caches,
-  stacked projections) against the reference-style ``forward``/``step`` state passing fed
-  the same tokens, across a 64-token block boundary: in bf16, last-position logits within
-  3e-2 of the logit scale (a few ulps of the bf16 logits: the two paths round different
-  GEMMs) and equal greedy tokens wherever a step's top-2 gap exceeds twice that step's
-  logit difference; in fp32, logits within 1e-5 of the scale and equal tokens.  The
-  prefill is 2,000 (bf16) or 1,000 (fp32) tokens instead of 131,072 (the property does not
-  depend on the length; the full length runs in bench.py).
+- The ``generate_greedy`` serving loop -- the captured device-resident step (DeviceCache
+  appends, device-length decode kernels, fused norms) and the eager LatentCache loop --
+  against the reference-style ``forward``/``step`` state passing fed
+  the same tokens, across a 64-token block boundary: in bf16 against the state passing in
+  fp32 (same bf16-rounded weights), last-position logits within 5e-2 of the logit scale
+  (about a dozen ulps of the bf16 logits), no growth over the steps, and equal greedy tokens
+  wherever a step's top-2 gap exceeds twice that step's logit difference; in fp32 (eager
+  loop) against fp32 state passing, logits within 1e-5 of the scale and equal tokens.
+  The prefill is 2,100 (bf16) or 1,000 (fp32) tokens instead of 131,072 (the property does
+  not depend on the length; the full length runs in bench.py).
 - One DGDA block at the model's widths against the float64 oracle, in two stages: the
   prologue kernel from the block's own bf16 projection GEMM output (q/k/v one bf16 ulp,
   gates 1e-5), then the chunked prefill from the prologue's outputs (rtol = atol = 2e-3).
@@ -47,14 +49,15 @@ def model():
     return _build(torch.bfloat16)
 
 
-def _two_loops(m, prefill, steps, seed):
+def _two_loops(m, prefill, steps, seed, graph=None):
     """Last-position logits [B, steps, V] of the serving loop and of the state-passing loop
     fed the serving loop's tokens, and those tokens."""
     dev = next(m.parameters()).device
     ids = torch.randint(0, m.config.vocab_size, (BATCH, prefill), generator=torch.Generator().manual_seed(seed)).to(dev)
-    print(f"\nconfig 5 serving loop: B={BATCH} prefill={prefill} steps={steps} {next(m.parameters()).dtype}", flush=True)
+    print(f"\nconfig 5 serving loop: B={BATCH} prefill={prefill} steps={steps} {next(m.parameters()).dtype} "
+          f"graph={graph}", flush=True)
     with torch.no_grad():
-        toks, lg_serve = m.generate_greedy(ids, steps, return_logits=True)
+        toks, lg_serve = m.generate_greedy(ids, steps, return_logits=True, graph=graph)
         logits, states = m(ids)
         ref = [logits[:, -1]]
         for t in range(steps - 1):
@@ -71,16 +74,35 @@ def _check_tokens(toks, got, ref, min_sure):
     assert torch.equal(toks[sure], ref.argmax(-1)[sure])
 
 
-def test_config5_serving_loop_matches_state_passing(model):
-    """bf16 (config 5's dtype).  The logits are themselves bf16: one ulp is about 0.4 % of their
-    scale, and the two paths' differently rounded projections move them by a few ulps from the
-    first decode step on, without growth."""
-    toks, got, ref = _two_loops(model, 2000, 60, 1)          # positions 2000..2059 cross 2048
+@pytest.mark.parametrize("graph", [True, False])
+def test_config5_serving_loop_matches_state_passing(model, graph):
+    """bf16 (config 5's dtype), through the captured device-resident step (graph) and the
+    eager LatentCache loop, against the same model's reference-style state passing run in
+    fp32 (the bf16-rounded weights, fed the serving loop's tokens).  The logits are bf16: one
+    ulp is about 0.4 % of their scale, and 20 bf16 blocks round every activation; the
+    measured error is flat over the steps (no drift) at 2-3.5 % of the scale."""
+    import copy
+    dev = next(model.parameters()).device
+    ids = torch.randint(0, model.config.vocab_size, (BATCH, 2100), generator=torch.Generator().manual_seed(1)).to(dev)
+    steps = 60                                                        # positions 2100..2159 cross 2112
+    print(f"\nconfig 5 serving loop vs fp32 state passing: graph={graph}", flush=True)
+    with torch.no_grad():
+        toks, got = model.generate_greedy(ids, steps, return_logits=True, graph=graph)
+        ref_model = copy.deepcopy(model).float()
+        logits, states = ref_model(ids)
+        ref = [logits[:, -1]]
+        for t in range(steps - 1):
+            lg, states = ref_model.step(toks[:, t:t + 1], past_states=states)
+            ref.append(lg[:, -1])
+        del ref_model
+    ref = torch.stack(ref, dim=1).float().cpu()
+    got = got.float().cpu()
     scale = ref.abs().max().item()
-    err = (got - ref).abs().max().item()
-    assert err <= 3e-2 * scale, f"serving-loop logits differ by {err:.3e} (scale {scale:.3e})"
-    assert (got[:, 0] == ref[:, 0]).all()                     # the shared prefill
-    _check_tokens(toks, got, ref, 0.3)
+    per_step = (got - ref).abs().amax(dim=(0, 2)) / scale
+    print("per-step error / scale:", [round(x, 4) for x in per_step.tolist()], flush=True)
+    assert per_step.max() <= 5e-2, f"serving-loop logits differ by {per_step.max():.3e} of the scale"
+    assert per_step[-10:].mean() <= 1.5 * per_step[1:11].mean() + 1e-3, "the error grows over the steps"
+    _check_tokens(toks.cpu(), got, ref, 0.2)
 
 
 def test_config5_serving_loop_fp32_exact():

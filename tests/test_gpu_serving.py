@@ -1,0 +1,238 @@
+"""Kernels of the device-resident decode step, on the GPU.
+
+- ``cache_append`` against ``oracle.indexer.decode_centroid_cache`` and
+  ``oracle.sparse_attn.hca_means`` after every appended token, across block boundaries
+  (centroids and means within half a bf16 ulp of the float64 values, plus fp32 slack;
+  appended rows bit-exact).
+- ``index_topk_decode_dev`` / ``maba_sa_decode_dev`` (length in device memory, buffers of
+  fixed capacity) against the host-length entry points on the same rows: indices
+  bit-exact, latent outputs within 1e-5, and the MABA-SA output within the north-star 2e-3
+  of the float64 oracle.
+- ``rmsnorm`` (with and without the gated residual) and ``swiglu`` against float64 torch
+  on the same bf16 inputs: one bf16 rounding of the result (half an ulp plus fp32 slack).
+- the DGDA step with a bf16 state (in place and out of place) and the single-token
+  prologue (in-place history) against the float64 oracle.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import assert_close, to_np
+from oracle import dgda as odgda
+from oracle import indexer as oidx
+from oracle import sparse_attn as osa
+
+pytestmark = pytest.mark.gpu
+
+
+def _hb():
+    from maba_sparse.kernels import hip_backend
+    return hip_backend
+
+
+def _ulp_close(got, exp, what):
+    g = to_np(got)
+    e = np.asarray(exp, np.float64)
+    bound = (2.0 ** -8 + 1e-5) * np.abs(e) + 1e-6
+    bad = np.abs(g - e) > bound
+    assert not bad.any(), f"{what}: {bad.sum()} values beyond half a bf16 ulp (max err {np.abs(g - e).max():.3e})"
+
+
+def test_cache_append_vs_oracle(dev):
+    hb = _hb()
+    g = torch.Generator().manual_seed(3)
+    B, dc, di, Lmax, L0, steps = 3, 128, 64, 320, 100, 170       # crosses 128, 192, 256
+    c_all = torch.randn(B, Lmax, dc, generator=g).bfloat16()
+    k_all = torch.randn(B, Lmax, di, generator=g).bfloat16()
+    c = torch.zeros(B, Lmax, dc, dtype=torch.bfloat16, device=dev)
+    k = torch.zeros(B, Lmax, di, dtype=torch.bfloat16, device=dev)
+    hca = torch.zeros(B, Lmax // 64, dc, dtype=torch.bfloat16, device=dev)
+    cent = torch.zeros(B, (Lmax + 63) // 64, di, dtype=torch.bfloat16, device=dev)
+    c[:, :L0] = c_all[:, :L0].to(dev)
+    k[:, :L0] = k_all[:, :L0].to(dev)
+    hca[:, : L0 // 64] = hb.hip_hca_pool(c[:, :L0], pool=64)
+    cent[:, : L0 // 64] = hb.hip_compute_centroids(k[:, : (L0 // 64) * 64], block_size=64)
+    pos = torch.tensor([L0], dtype=torch.long, device=dev)
+    for t in range(L0, L0 + steps):
+        hb.hip_cache_append(c_all[:, t].to(dev), k_all[:, t].to(dev), pos[0], c, k, hca, cent)
+        pos += 1
+        n = t + 1
+        assert torch.equal(c[:, t].cpu(), c_all[:, t]) and torch.equal(k[:, t].cpu(), k_all[:, t])
+        if n % 64 == 0 or n % 37 == 0 or t == L0 + steps - 1:
+            _ulp_close(hca[:, : n // 64], osa.hca_means(to_np(c_all[:, :n]), n, 64), f"hca means at n={n}")
+            _ulp_close(cent[:, : (n + 63) // 64], oidx.decode_centroid_cache(to_np(k_all[:, :n]), 64),
+                       f"centroid cache at n={n}")
+    assert int(pos) == L0 + steps
+
+
+@pytest.mark.parametrize("L", [2048 + 5, 6400, 25000])
+def test_index_topk_decode_dev_matches_host(dev, L):
+    hb = _hb()
+    g = torch.Generator().manual_seed(L)
+    B, Hq, d, ncap = 4, 3, 64, 400
+    cent = torch.randn(B, ncap, d, generator=g).bfloat16().to(dev)
+    q = torch.randn(B, Hq, d, generator=g).bfloat16().to(dev)
+    nb = (L + 63) // 64
+    length = torch.tensor([L], dtype=torch.long, device=dev)
+    got = hb.hip_index_topk_decode_dev(q, cent, length[0], 64, 0.1, 32)
+    exp = hb.hip_index_topk_decode(q, cent[:, :nb], lambda_dist=0.1, top_k=32)
+    assert torch.equal(got, exp)
+
+
+@pytest.mark.parametrize("L,Hi", [(700, 1), (5000, 4), (19999, 1), (20000, 4)])
+def test_maba_sa_decode_dev_matches_host(dev, L, Hi):
+    hb = _hb()
+    g = torch.Generator().manual_seed(L + Hi)
+    B, H, dh, dc, Lcap, K = 2, 4, 64, 128, 20000, 16
+    c = torch.randn(B, Lcap, dc, generator=g).bfloat16()
+    Wk = torch.randn(H * dh, dc, generator=g) * 0.05
+    Wv = torch.randn(H * dh, dc, generator=g) * 0.05
+    q = torch.randn(B, H, dh, generator=g)
+    nb = (L + 63) // 64
+    idx = torch.stack([torch.stack([torch.randperm(nb, generator=g)[:K] for _ in range(Hi)]) for _ in range(B)])
+    gate = torch.randn(B, 3, generator=g)
+    cd = c.to(dev)
+    hca = torch.zeros(B, Lcap // 64, dc, dtype=torch.bfloat16, device=dev)
+    hca[:, : L // 64] = hb.hip_hca_pool(cd[:, :L], pool=64)
+    q_lat = torch.einsum("bhd,hdc->bhc", q, Wk.view(H, dh, dc)).to(dev)
+    length = torch.tensor([L], dtype=torch.long, device=dev)
+    z_dev = hb.hip_maba_sa_decode_dev(q_lat, cd, hca, idx.to(dev), gate.to(dev), length[0], Lcap, 1 / math.sqrt(dh))
+    z_host = hb.hip_maba_sa_decode(q_lat, cd, hca[:, : max(L // 64, 1)], idx.to(dev), gate.to(dev), L=L,
+                                   scale=1 / math.sqrt(dh))
+    assert_close(z_dev, to_np(z_host), 1e-5, 1e-6, "device-length decode vs host length")
+    out = torch.einsum("bhc,hdc->bhd", z_dev.cpu(), Wv.view(H, dh, dc))
+    exp = osa.maba_sa_decode(to_np(q), to_np(c[:, :L]), to_np(Wk), to_np(Wv), to_np(idx).astype(np.int64),
+                             to_np(gate))
+    assert_close(out, exp, 2e-3, 2e-3, "device-length decode vs oracle")
+
+
+@pytest.mark.parametrize("rows,C,dtype", [((16, 1), 640, torch.bfloat16), ((3, 70), 640, torch.bfloat16),
+                                          ((5, 1), 1248, torch.float32), ((2, 9), 96, torch.bfloat16)])
+def test_rmsnorm_and_residual(dev, rows, C, dtype):
+    hb = _hb()
+    g = torch.Generator().manual_seed(C)
+    x = torch.randn(*rows, C, generator=g).to(dtype)
+    mo = torch.randn(*rows, C, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(C, generator=g)).to(dtype)
+    gate = torch.sigmoid(torch.randn(C, generator=g)).to(dtype)
+    eps = 1e-6
+    h = hb.hip_rmsnorm(x.to(dev), w.to(dev), eps)
+    xd = x.double()
+    ref = xd / torch.sqrt((xd * xd).mean(-1, keepdim=True) + eps) * w.double()
+    _ulp_close(h, ref.numpy(), "rmsnorm") if dtype == torch.bfloat16 else assert_close(h, ref.numpy(), 1e-5, 1e-6, "rmsnorm")
+    xo = torch.empty_like(x, device=dev)
+    h2 = hb.hip_rmsnorm(x.to(dev), w.to(dev), eps, mo=mo.to(dev), gate=gate.to(dev), x_out=xo)
+    xr = (x.double() + gate.double() * mo.double())
+    if dtype == torch.bfloat16:
+        _ulp_close(xo, xr.numpy(), "gated residual")
+    xs = xo.cpu().double()                                   # the norm reads the stored residual
+    ref2 = xs / torch.sqrt((xs * xs).mean(-1, keepdim=True) + eps) * w.double()
+    _ulp_close(h2, ref2.numpy(), "rmsnorm of the residual") if dtype == torch.bfloat16 else \
+        assert_close(h2, ref2.numpy(), 1e-5, 1e-6, "rmsnorm of the residual")
+
+
+@pytest.mark.parametrize("shape,dtype", [((16, 1, 2496), torch.bfloat16), ((3, 50, 96), torch.float32)])
+def test_swiglu(dev, shape, dtype):
+    hb = _hb()
+    gu = torch.randn(*shape, generator=torch.Generator().manual_seed(shape[-1])).to(dtype)
+    out = hb.hip_swiglu(gu.to(dev))
+    I = shape[-1] // 2
+    gd, ud = gu[..., :I].double(), gu[..., I:].double()
+    ref = gd / (1 + torch.exp(-gd)) * ud
+    if dtype == torch.bfloat16:
+        _ulp_close(out, ref.numpy(), "swiglu")
+    else:
+        assert_close(out, ref.numpy(), 1e-5, 1e-6, "swiglu")
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_dgda_step_bf16_state(dev, inplace):
+    hb = _hb()
+    g = torch.Generator().manual_seed(7)
+    B, H, d = 16, 10, 64
+    q = torch.nn.functional.normalize(torch.randn(B, H, d, generator=g), dim=-1).bfloat16()
+    k = torch.nn.functional.normalize(torch.randn(B, H, d, generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, H, d, generator=g).bfloat16()
+    la = -torch.nn.functional.softplus(torch.randn(B, H, d, generator=g))
+    b = torch.sigmoid(torch.randn(B, H, d, generator=g))
+    w = torch.sigmoid(torch.randn(B, H, d, generator=g))
+    S = (torch.randn(B, H, d, d, generator=g) * 0.3).bfloat16()
+    Sd = S.to(dev)
+    kw = dict(new_state=Sd) if inplace else {}
+    o, Sn = hb.hip_dgda_step(q.to(dev), k.to(dev), v.to(dev), log_alpha=la.to(dev), b=b.to(dev), w=w.to(dev),
+                             state=Sd, allow_mixed_dtypes=True, out_dtype=torch.float32, **kw)
+    if inplace:
+        assert Sn.data_ptr() == Sd.data_ptr()
+    eo, eS = odgda.dgda_step(to_np(q), to_np(k), to_np(v), alpha=np.exp(to_np(la)), b=to_np(b), w=to_np(w),
+                             state=to_np(S))
+    assert Sn.dtype == torch.bfloat16
+    assert_close(o, eo, 1e-4, 1e-4, "step output (fp32 from the bf16 state)")
+    _ulp_close(Sn, eS, "bf16 state")
+
+
+@pytest.mark.parametrize("hist_dtype", [torch.float32, torch.bfloat16])
+def test_prologue_single_token_in_place(dev, hist_dtype):
+    hb = _hb()
+    g = torch.Generator().manual_seed(11)
+    B, H = 16, 10
+    C = 64 * H
+    xs = [torch.randn(B, 1, C, generator=g).bfloat16() for _ in range(6)]
+    cw = [(torch.randn(C, 1, 4, generator=g) * 0.5).bfloat16() for _ in range(3)]
+    hist = [torch.randn(B, C, 3, generator=g).to(hist_dtype) for _ in range(3)]
+    hd = [h.to(dev) for h in hist]
+    outs = hb.hip_dgda_prologue([x.to(dev) for x in xs], [w.to(dev) for w in cw], history=hd, n_heads=H,
+                                eps=1e-6, gate_dtype=torch.float32, with_alpha=False, out_history=hd)
+    q, k, v, la, _, b, w, nh = outs
+    assert all(a.data_ptr() == c.data_ptr() for a, c in zip(nh, hd))
+    eq, ek, ev, ela, _, eb, ew, enh = odgda.layer_prologue(*[to_np(x) for x in xs], *[to_np(c)[:, 0, :] for c in cw],
+                                                           hist=[to_np(h) for h in hist], n_heads=H, eps=1e-6)
+    for name, got, e in (("q", q, eq), ("k", k, ek), ("v", v, ev)):
+        _ulp_close(got, e, f"single-token prologue {name}")
+    assert_close(la, ela, 1e-5, 1e-6, "log_alpha")
+    assert_close(b, eb, 1e-5, 1e-6, "erase gate")
+    assert_close(w, ew, 1e-5, 1e-6, "write gate")
+    for s in range(3):
+        assert_close(nh[s], enh[s], 0, 0, f"new history {s}")
+
+
+def test_maba_sa_device_decode_vs_oracle(dev):
+    """A bf16 MABA-SA layer at the 101M widths: prefill 2,100 tokens, then 70 decode tokens on
+    the device path (DeviceCache appends, device-length indexer and decode), crossing the
+    block boundaries at 2,112 and 2,176.  At several steps the output is checked against the
+    float64 oracle on the device cache's rows with oracle-computed means (2e-3), and the
+    indexer's picks against oracle scores of the centroids the cache holds."""
+    from maba_sparse.layers import MabaSparseAttention
+    from maba_sparse.layers.sparse_attention import DeviceCache
+    torch.manual_seed(5)
+    B, L0, steps = 4, 2100, 70
+    layer = MabaSparseAttention(dim=640, n_heads=10, d_head=64, d_c=128, d_idx=64, top_k=32,
+                                dist_lambda=0.1).eval()
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0.0, 0.05) if p.dim() > 1 else None
+    layer = layer.to(dev, torch.bfloat16)
+    g = torch.Generator().manual_seed(6)
+    xs = torch.randn(B, L0 + steps, 640, generator=g).bfloat16().to(dev)
+    with torch.no_grad():
+        _, c_full = layer(xs[:, :L0])
+        cache = DeviceCache(c_full, layer.indexer._cached_k_idx, L0 + steps)
+        counters = torch.tensor([L0, L0 + 1], dtype=torch.long, device=dev)
+        for t in range(L0, L0 + steps):
+            x = xs[:, t:t + 1]
+            out, idx, z = layer.decode_step_device(x, cache, counters, return_parts=True)
+            counters += 1
+            L = t + 1
+            if t - L0 in (0, 11, 12, 13, 45, 69):
+                q, _, qi, _, gl = layer._token_projections(x)
+                nb = (L + 63) // 64
+                ref_sc = oidx.decode_scores(to_np(qi), oidx.decode_centroid_cache(to_np(cache.keys[:, :L]), 64), 0.1)
+                from _helpers import topk_is_valid
+                topk_is_valid(idx.cpu().numpy(), ref_sc, 2e-2)          # centroids are bf16-rounded
+                assert idx.shape == (B, 1, 32) and int(idx.max()) < nb
+                got = torch.einsum("bhc,hdc->bhd", z.cpu(), layer.v_up_proj.weight.float().cpu().view(10, 64, 128))
+                exp = osa.maba_sa_decode(to_np(q.view(B, 10, 64)), to_np(cache.c[:, :L]),
+                                         to_np(layer.k_up_proj.weight), to_np(layer.v_up_proj.weight),
+                                         to_np(idx).astype(np.int64), to_np(gl.view(-1, 3)), L=L)
+                assert_close(got, exp, 2e-3, 2e-3, f"device decode at L={L}")
