@@ -466,7 +466,13 @@ def row_benches(dev):
         return hb.hip_index_topk(qi, cent, lambda_dist=0.5, top_k=K, block_size=64)
 
     ms, _ = time_op(topk_prefill, 5, 1)
+    # scoring flops: every query against the centroids of the blocks at or before its own
+    fl = 2 * di * Bq * sum(min(t // 64 + 1, L // 64) for t in range(0, L, 64)) * 64
     out["index_topk_prefill"] = {"ms_per_call": ms, "queries_per_s": Bq * L / (ms * 1e-3),
+                                 "roofline": {"bound": "mfma", "achieved": fl / (ms * 1e-3) / 1e12,
+                                              "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                              "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                                              "algorithmic_flops": fl, "traffic": None},
                                  "config": "B=1 L=32768 d=128 bf16, 512 centroids, top-32, causal"}
     log(f"index_topk prefill 32k x 512: {ms:.3f} ms")
     del qi, cent
@@ -514,8 +520,21 @@ def prefill_attention_bench(dev, B=1, H=10, L=32768, dh=64, K=32):
     u = idx.view(B, L // 16, 16 * K).sort(dim=-1).values
     distinct = (u[..., 1:] != u[..., :-1]).sum(-1).float().mean().item() + 1
     log(f"MABA-SA prefill streams 32k: {ms:.3f} ms ({distinct:.0f} distinct blocks per 16 queries)")
+    # algorithmic flops per query and head: 2 dh per score and per value accumulation, over the
+    # local keys (window + sinks, fewer at the start), the listed blocks' causal tokens and the
+    # complete means before the query
+    pos = torch.arange(L, device=dev)
+    n_loc = torch.clamp(pos + 1, max=128) + torch.clamp(torch.clamp(pos + 1 - 128, min=0), max=4)
+    blk = idx[0].to(torch.int64)
+    n_sp = torch.clamp(pos[:, None] - blk * 64 + 1, min=0, max=64).sum(-1)
+    n_hca = (pos + 1) // 64
+    keys = (n_loc + n_sp + n_hca).double().sum().item()
+    fl = keys * H * B * 4 * dh
+    rf = {"bound": "mfma", "achieved": fl / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+          "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "algorithmic_flops": fl, "traffic": None}
     return {"maba_sa_prefill_32k": {
         "ms_per_call": ms, "queries_per_s": B * L / (ms * 1e-3), "sparse_blocks_per_wave": distinct,
+        "roofline": rf,
         "config": "B=1 H=10 L=32768 d_head=64 bf16, window 128 + 4 sinks, top-32 causal blocks per query from "
                   "index_topk (lambda 0.5), 512 HCA means, one launch with the gate"}}
 
@@ -582,19 +601,44 @@ def model_decode_bench(dev, B=16, L=131072, steps=256):
         torch.cuda.synchronize()
         marks.append(time.perf_counter())
 
+    graph = model.serving_graph_ok(ids)
     mark()
     toks = model.generate_greedy(ids, steps, on_prefill_done=mark)
     mark()
     prefill_s, decode_s = marks[1] - marks[0], marks[2] - marks[1]
+    # the first decode step runs eagerly and captures nothing; the graph serves the rest
     per_step = decode_s / max(steps - 1, 1)
     log(f"model config 5: prefill {prefill_s:.2f} s ({B * L / prefill_s / 1e6:.2f} M tok/s), decode "
-        f"{per_step * 1e3:.2f} ms/step ({B / per_step:.0f} tok/s)")
+        f"{per_step * 1e3:.2f} ms/step ({B / per_step:.0f} tok/s), graph={graph}")
+    eager_steps = 17
+    marks.clear()
+    mark()
+    model.generate_greedy(ids, eager_steps, on_prefill_done=mark, graph=False)
+    mark()
+    eager_step = (marks[2] - marks[1]) / (eager_steps - 1)
+    log(f"model config 5, eager LatentCache loop: {eager_step * 1e3:.2f} ms/step")
+    # algorithmic bytes of one decode step: every weight once (the tied embedding matrix once, as
+    # the LM head), the DGDA states read and written, and per MABA-SA block its centroids, HCA
+    # means, selected blocks and local window at the final context
+    c = model.config
+    n_params = sum(p.numel() for p in model.parameters())
+    n_dgda = sum(1 for b in model.layers if not b.is_attention)
+    n_sa = len(model.layers) - n_dgda
+    Lf = L + steps
+    state = 2 * B * c.n_heads * c.d_head * c.d_head * 2
+    sa = B * ((Lf // 64) * c.d_idx * 2 + (Lf // 64) * c.d_c * 2 + c.top_k * 64 * c.d_c * 2 + 132 * c.d_c * 2)
+    step_bytes = n_params * 2 + n_dgda * state + n_sa * sa
     out = {"model_decode_config5": {
         "ms_per_token": per_step * 1e3, "tokens_per_s": B / per_step, "decode_steps": steps - 1,
+        "serving_path": "one captured HIP graph per decode step" if graph else "eager",
+        "eager_ms_per_token": eager_step * 1e3,
         "prefill_s": prefill_s, "prefill_tokens_per_s": B * L / prefill_s, "first_tokens": toks[0, :4].tolist(),
+        "roofline": {"bound": "hbm", "achieved": step_bytes / per_step / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": step_bytes / per_step / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": step_bytes,
+                     "traffic": None},
         "config": f"101M Maba v2 (20 layers, 3:1 DGDA:MABA-SA, d_model 640, factorised 32768->128->640 "
                   f"embedding, SwiGLU 1248, RMSNorm), bf16 weights ~N(0,0.02), B={B}, prefill {L} uniform "
-                  f"random ids, {steps} greedy tokens (one from the prefill, {steps - 1} decode steps), eager"}}
+                  f"random ids, {steps} greedy tokens (one from the prefill, {steps - 1} decode steps)"}}
     del model, ids
     torch.cuda.empty_cache()
     return out
@@ -639,11 +683,40 @@ def layer_decode_bench(dev, B=8, L0=1_000_000 - 10, steps=20):
     nb = cache.n // 64
     byts = B * (nb * 64 * 2 + nb * 128 * 2 + 32 * 64 * 128 * 2 + 132 * 128 * 2)   # centroids, HCA, sparse, local
     log(f"MABA-SA layer decode step at 1M (eager): {us:.1f} us")
-    del cache, layer
-    return {"us_per_step": us, "gbs": byts / (us * 1e-6) / 1e9, "hbm_frac": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-            "algorithmic_bytes": byts, "steps": steps,
+    # the serving path: DeviceCache appends and device-length kernels, one captured graph per step
+    from maba_sparse.layers.sparse_attention import DeviceCache
+    n0 = cache.n
+    dcache = DeviceCache(cache.c[:, :n0], layer.indexer._keys.view()[:, :n0], n0 + 2 * steps + 8)
+    del cache
+    counters = torch.tensor([n0, n0 + 1], dtype=torch.long, device=dev)
+    with torch.no_grad():
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            layer.decode_step_device(x, dcache, counters)
+            counters += 1
+        torch.cuda.current_stream(dev).wait_stream(side)
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            layer.decode_step_device(x, dcache, counters)
+            counters += 1
+        for _ in range(3):
+            gr.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+    gus = e0.elapsed_time(e1) / steps * 1e3
+    log(f"MABA-SA layer decode step at 1M (device-resident, graph replay): {gus:.1f} us")
+    del dcache, layer
+    return {"us_per_step": gus, "gbs": byts / (gus * 1e-6) / 1e9, "hbm_frac": byts / (gus * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "algorithmic_bytes": byts, "steps": steps, "eager_us_per_step": us,
+            "timing": "one captured HIP graph per step (cache append, decode indexer, fused streams, projections), "
+                      "events around back-to-back replays; eager_us_per_step: the LatentCache decode_step",
             "config": "B=8, context ~1M (synthetic latent, key and centroid caches), d_model 640, 10 heads x 64, "
-                      "d_c 128, d_idx 64, one indexer query shared by the heads, top-32, bf16, eager"}
+                      "d_c 128, d_idx 64, one indexer query shared by the heads, top-32, bf16"}
 
 
 def main():
