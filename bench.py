@@ -498,45 +498,68 @@ def row_benches(dev):
     return out
 
 
-def prefill_attention_bench(dev, B=1, H=10, L=32768, dh=64, K=32):
-    """MABA-SA prefill streams (local + sparse + HCA + gate) for a 32k-token sequence: per-head
-    bf16 q/k/v, up-projected means, and each query's top-32 blocks from the HIP causal
-    index_topk over random queries and centroids (lambda 0.5, the layer's default)."""
+def prefill_attention_bench(dev, B=1, H=10, L=32768, dh=64, dc=128, K=32):
+    """MABA-SA prefill streams (local + sparse + HCA + gate) for a 32k-token sequence at the
+    layer's default shape (10 heads of 64, d_c 128), each query's top-32 blocks from the HIP
+    causal index_topk over random queries and centroids (lambda 0.5, the layer's default).
+
+    The layer's path is the latent form: ``q_lat = W_k,h^T q_h``, one launch over the bf16
+    latent rows and their block means, ``o_h = W_v,h z_h``; the row times that composite and
+    the latent kernel alone (the roofline's kernel).  The head-space kernel over up-projected
+    keys and values (the previous path) is timed beside it."""
     import torch
     from maba_sparse.kernels import hip_backend as hb
     g = torch.Generator(device=dev).manual_seed(21)
     bf = lambda *sh: torch.randn(*sh, device=dev, generator=g, dtype=torch.bfloat16)  # noqa: E731
-    q, k, v = bf(B, H, L, dh), bf(B, H, L, dh), bf(B, H, L, dh)
-    kh, vh = bf(B, H, L // 64, dh), bf(B, H, L // 64, dh)
-    early = bf(B, H, 63, dh)
+    q = bf(B, H, L, dh)
+    c = bf(B, L, dc)
+    Wk = torch.randn(H, dh, dc, device=dev, generator=g) * dc ** -0.5
+    Wv = torch.randn(H, dh, dc, device=dev, generator=g) * dc ** -0.5
     gate = torch.randn(B, L, 3, device=dev, generator=g)
     idx = hb.hip_index_topk(bf(B, L, 64), bf(B, L // 64, 64), lambda_dist=0.5, top_k=K, block_size=64)
+    hca = hb.hip_hca_pool(c, pool=64)
+    q_lat = torch.einsum("bhtd,hdc->bthc", q.float(), Wk).contiguous()
+    z = torch.empty(B, L, H, dc, device=dev)
 
-    def call():
-        return hb.hip_maba_sa_prefill(q, k, v, kh, vh, early, idx, gate, scale=dh ** -0.5)
+    def kernel():
+        return hb.hip_maba_sa_prefill_latent(q_lat, c, hca, idx, gate, scale=dh ** -0.5, out=z)
 
-    ms, _ = time_op(call, 5, 1)
-    # distinct blocks per 16-query wave: the sparse stream's tiles
-    u = idx.view(B, L // 16, 16 * K).sort(dim=-1).values
-    distinct = (u[..., 1:] != u[..., :-1]).sum(-1).float().mean().item() + 1
-    log(f"MABA-SA prefill streams 32k: {ms:.3f} ms ({distinct:.0f} distinct blocks per 16 queries)")
-    # algorithmic flops per query and head: 2 dh per score and per value accumulation, over the
-    # local keys (window + sinks, fewer at the start), the listed blocks' causal tokens and the
-    # complete means before the query
+    def composite():
+        ql = torch.einsum("bhtd,hdc->bthc", q.float(), Wk).contiguous()
+        means = hb.hip_hca_pool(c, pool=64)
+        zz = hb.hip_maba_sa_prefill_latent(ql, c, means, idx, gate, scale=dh ** -0.5)
+        return torch.einsum("bthc,hdc->bthd", zz, Wv)
+
+    ms, _ = time_op(kernel, 10, 2)
+    ms_comp, _ = time_op(composite, 10, 2)
+    # the head-space kernel of the earlier path over up-projected keys and values
+    k = torch.einsum("blc,hdc->bhld", c.float(), Wk).bfloat16()
+    v = torch.einsum("blc,hdc->bhld", c.float(), Wv).bfloat16()
+    kh, vh = k[:, :, :L // 64].contiguous(), v[:, :, :L // 64].contiguous()
+    ms_heads, _ = time_op(lambda: hb.hip_maba_sa_prefill(q, k, v, kh, vh, v[:, :, :63].contiguous(), idx, gate,
+                                                          scale=dh ** -0.5), 3, 1)
+    del k, v, kh, vh
+    log(f"MABA-SA prefill 32k: latent kernel {ms:.3f} ms, composite {ms_comp:.3f} ms, "
+        f"head-space kernel {ms_heads:.3f} ms")
+    # algorithmic flops of the latent kernel per query and head: 2 d_c per score and per value
+    # accumulation, over the local keys (window + sinks, fewer at the start), the listed
+    # blocks' causal tokens and the complete means before the query
     pos = torch.arange(L, device=dev)
     n_loc = torch.clamp(pos + 1, max=128) + torch.clamp(torch.clamp(pos + 1 - 128, min=0), max=4)
     blk = idx[0].to(torch.int64)
-    n_sp = torch.clamp(pos[:, None] - blk * 64 + 1, min=0, max=64).sum(-1)
+    n_sp = torch.where(blk >= 0, torch.clamp(pos[:, None] - blk * 64 + 1, min=0, max=64), 0).sum(-1)
     n_hca = (pos + 1) // 64
     keys = (n_loc + n_sp + n_hca).double().sum().item()
-    fl = keys * H * B * 4 * dh
+    fl = keys * H * B * 4 * dc
     rf = {"bound": "mfma", "achieved": fl / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
           "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "algorithmic_flops": fl, "traffic": None}
     return {"maba_sa_prefill_32k": {
-        "ms_per_call": ms, "queries_per_s": B * L / (ms * 1e-3), "sparse_blocks_per_wave": distinct,
+        "ms_per_call": ms_comp, "kernel_ms": ms, "head_space_kernel_ms": ms_heads,
+        "queries_per_s": B * L / (ms_comp * 1e-3), "keys_per_query": keys / (B * L),
         "roofline": rf,
-        "config": "B=1 H=10 L=32768 d_head=64 bf16, window 128 + 4 sinks, top-32 causal blocks per query from "
-                  "index_topk (lambda 0.5), 512 HCA means, one launch with the gate"}}
+        "config": "B=1 H=10 d_head=64 d_c=128 L=32768 bf16 latent rows, window 128 + 4 sinks, top-32 causal "
+                  "blocks per query from index_topk (lambda 0.5), 512 HCA means; ms_per_call = q_lat "
+                  "projection + block means + latent kernel + W_v projection"}}
 
 
 def prologue_benches(dev, B=4, T=32768, dim=640, H=10):

@@ -32,6 +32,8 @@
  *   maba_hip_maba_sa_prefill        layers/sparse_attention.py:95-105,145-171,
  *                                   173-219,275 (the three prefill streams over
  *                                   dense masks and the gate; inline torch code)
+ *   maba_hip_maba_sa_prefill_latent the same streams over the latent cache with the
+ *                                   absorbed projections
  *   maba_hip_dgda_prologue          layers/dgda.py:103-121,186-207 (the DGDA
  *                                   layer's conv + SiLU with carried history,
  *                                   gate activations and key normalisation;
@@ -203,6 +205,23 @@ int maba_hip_maba_sa_prefill(const maba_tensor* q, const maba_tensor* k, const m
                              const maba_tensor* idx, const maba_tensor* gate, float scale,
                              int window, int n_sink, int block_size, int pool, maba_tensor* out,
                              void* stream);
+
+/*
+ * MABA-SA prefill in latent form (the same streams and gate as maba_hip_maba_sa_prefill,
+ * layers/sparse_attention.py:95-105,145-171,173-219,275): query t of q_lat [B,Lq,H,dc]
+ * (W_k,h^T q_h; f32/bf16) sits at position Lkv - Lq + t of the bf16 latent cache
+ * c_kv [B,Lkv,dc] (16-byte aligned rows, dc a multiple of 32 up to 128, H <= 16) and attends,
+ * per head, to the local window + sinks, the tokens <= pos of its blocks idx [B,Lq|1,K]
+ * (int64, K <= 64, block_size <= 64, a block listed twice counts twice), and the complete means of
+ * hca [B,>=Lkv/pool,dc] (bf16) with (e+1) pool - 1 <= pos, or the running mean of c[0..pos]
+ * before pool - 1; gate [B,Lq,3] or [B,H,Lq,3] logits.  out_lat f32 [B,Lq,H,dc] (unit
+ * channel stride) = sum_s g_s z_s; the caller applies W_v,h.  A stream without a valid key
+ * contributes zero.
+ */
+int maba_hip_maba_sa_prefill_latent(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                    const maba_tensor* hca, const maba_tensor* idx,
+                                    const maba_tensor* gate, float scale, int window, int n_sink,
+                                    int block_size, int pool, maba_tensor* out_lat, void* stream);
 
 /*
  * DGDA layer prologue.  xs[0..5]: the q, k, v, alpha, erase and write projections

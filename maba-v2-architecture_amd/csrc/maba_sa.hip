@@ -383,46 +383,198 @@ __device__ __forceinline__ SaSeg sa_segment(const SaArgs& a, int sid) {
   return g;
 }
 
-// Key rows 16 rb + c16 of tile tix of a segment, dims 32 p + 8 g .. +7.  Invalid rows
-// read row 0 of the stream (in bounds: L >= 1, and the HCA stream is only walked when it
-// has entries); their scores are masked to -inf, so they get zero weight.  blk is the
-// tile's block index for the sparse stream.  Bit 4 rb + i of okb says whether
-// key row 16 rb + 4 g + i (a row of this lane's score accumulators) is valid.
+// Where the key rows of the three streams of one query live: the latent rows c[0, L) and the
+// complete-block means hca[0, nc), with the local stream's geometry.
+struct SaRows {
+  const uint16_t* c; int64_t cs;     // latent rows of the sequence, row stride (unit channel stride)
+  const uint16_t* hca; int64_t hs;   // block means of the sequence
+  int64_t L;
+  int bs, ns, loc_start, nloc, nc;
+};
+
+__device__ __forceinline__ SaRows sa_rows(const SaArgs& a, int64_t b) {
+  SaRows r;
+  r.c = (const uint16_t*)a.c + b * a.csb; r.cs = a.csl;
+  r.hca = (const uint16_t*)a.hca + b * a.hsb; r.hs = a.hsn;
+  r.L = a.L; r.bs = a.bs; r.ns = a.ns; r.loc_start = a.loc_start; r.nloc = a.nloc; r.nc = a.nc;
+  return r;
+}
+
+// Key rows 16 rb + c16 of tile tix of a stream (0 local, 1 sparse, 2 HCA), dims 32 p + 8 g
+// .. +7.  Invalid rows read row 0 of the stream (in bounds: L >= 1, and the HCA stream is
+// only walked when it has entries); their scores are masked to -inf, so they get zero
+// weight.  blk is the tile's block index for the sparse stream.  Bit 4 rb + i of okb says
+// whether key row 16 rb + 4 g + i (a row of this lane's score accumulators) is valid.
 template <int NP>
-__device__ __forceinline__ void sa_load_tile(const SaArgs& a, const SaSeg& sg, int64_t b, int64_t tix, int64_t blk,
-                                             int c16, int g, s16x8 (&cv)[4][NP], uint32_t& okb) {
-  const uint16_t* base;
-  int64_t rstride;
-  if (sg.stream == 2) {
-    base = (const uint16_t*)a.hca + b * a.hsb;
-    rstride = a.hsn;
-  } else {
-    base = (const uint16_t*)a.c + b * a.csb;
-    rstride = a.csl;
-  }
-  const int64_t nblk = (a.L + a.bs - 1) / a.bs;
+__device__ __forceinline__ void sa_load_rows(const SaRows& r, int stream, int64_t tix, int64_t blk, int c16, int g,
+                                             s16x8 (&cv)[4][NP], uint32_t& okb) {
+  const uint16_t* base = stream == 2 ? r.hca : r.c;
+  const int64_t rstride = stream == 2 ? r.hs : r.cs;
+  const int64_t nblk = (r.L + r.bs - 1) / r.bs;
   okb = 0;
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
     const int j = 16 * rb + c16;
     int64_t pos;
     bool ok;
-    if (sg.stream == 0) {
+    if (stream == 0) {
       const int64_t li = tix * 64 + j;
-      ok = li < a.nloc;
-      pos = li < a.ns ? li : a.loc_start + (li - a.ns);
-    } else if (sg.stream == 1) {
-      pos = blk * a.bs + j;
-      ok = blk >= 0 && blk < nblk && j < a.bs && pos < a.L;
+      ok = li < r.nloc;
+      pos = li < r.ns ? li : r.loc_start + (li - r.ns);
+    } else if (stream == 1) {
+      pos = blk * r.bs + j;
+      ok = blk >= 0 && blk < nblk && j < r.bs && pos < r.L;
     } else {
       pos = tix * 64 + j;
-      ok = pos < a.nc;
+      ok = pos < r.nc;
     }
     const uint16_t* row = base + (ok ? pos : 0) * rstride + 8 * g;
 #pragma unroll
     for (int p = 0; p < NP; ++p) cv[rb][p] = *(const s16x8*)(row + 32 * p);
     // lanes 0-15 load rows 16 rb + c16: bits 4g .. 4g+3 of their ballot are this lane's rows
     okb |= (uint32_t)((__ballot(ok) >> (4 * g)) & 0xfu) << (4 * rb);
+  }
+}
+
+// Online-softmax state of one stream for the lane's MFMA column (head c16): running max,
+// running sum and Z[dim][head] as accumulator tiles (lane holds dims 16 dt + 4 g + i).
+template <int NP>
+struct SaAcc {
+  float m, l;
+  f32x4 z[2 * NP];
+};
+
+template <int NP>
+__device__ __forceinline__ void sa_acc_init(SaAcc<NP>& st) {
+  st.m = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int dt = 0; dt < 2 * NP; ++dt) st.z[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// One 64-key tile: scores D[key][head] = C Q^T with the scaled query in bf16 hi + lo (B
+// operand), online softmax, values Z[dim][head] += C^T P with the tile copied row-major into
+// the wave's LDS and read transposed, P in bf16 hi + lo.  head_on: the lane's column is a
+// head that attends to this stream.
+template <int NP>
+__device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t okb, bool head_on,
+                                             const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile, int c16,
+                                             int g, SaAcc<NP>& st) {
+  constexpr int DC = 32 * NP;
+  constexpr int TP = DC + 8;
+  f32x4 sc[4];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      *(s16x8*)(tile + (16 * rb + c16) * TP + 32 * p + 8 * g) = cv[rb][p];
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
+                                                    __builtin_bit_cast(bf16x8, qh[p]), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
+                                                    __builtin_bit_cast(bf16x8, ql[p]), acc, 0, 0, 0);
+    }
+    sc[rb] = acc;
+  }
+  // lane (head c16, group g) holds scores of keys 16 rb + 4g + i
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool kv = (okb >> (4 * rb + i)) & 1u;
+      const float x = (kv && head_on) ? sc[rb][i] : -INFINITY;
+      sc[rb][i] = x;
+      tmax = fmaxf(tmax, x);
+    }
+  }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+  const float m_new = fmaxf(st.m, tmax);
+  const float corr = (m_new == -INFINITY) ? 1.f : __expf(st.m - m_new);
+  const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;   // exp(-inf - m_sub) = 0 for masked keys
+  float psum = 0.f;
+  s16x4 ph[4], pl[4];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    f32x4 pv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pe = __expf(sc[rb][i] - m_sub);
+      pv[i] = pe;
+      psum += pe;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const short hb = __builtin_bit_cast(short, (__bf16)pv[i]);
+      ph[rb][i] = hb;
+      pl[rb][i] = __builtin_bit_cast(short, (__bf16)(pv[i] - bf16_bits_to_f32((uint16_t)hb)));
+    }
+  }
+  psum += __shfl_xor(psum, 16);
+  psum += __shfl_xor(psum, 32);
+  st.l = st.l * corr + psum;
+  st.m = m_new;
+  // z[dim][head] = corr * z + C^T P  (K = 64 keys as two permuted 32-steps)
+#pragma unroll
+  for (int dt = 0; dt < DC / 16; ++dt) {
+    f32x4 acc = st.z[dt] * corr;
+#pragma unroll
+    for (int p2 = 0; p2 < 2; ++p2) {
+      const s16x4 a0 = sa_ldsT4(tile, TP, 32 * p2, 16 * dt, c16, g);
+      const s16x4 a1 = sa_ldsT4(tile, TP, 32 * p2 + 16, 16 * dt, c16, g);
+      const s16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      const s16x8 bh = {ph[2 * p2][0], ph[2 * p2][1], ph[2 * p2][2], ph[2 * p2][3],
+                        ph[2 * p2 + 1][0], ph[2 * p2 + 1][1], ph[2 * p2 + 1][2], ph[2 * p2 + 1][3]};
+      const s16x8 bl = {pl[2 * p2][0], pl[2 * p2][1], pl[2 * p2][2], pl[2 * p2][3],
+                        pl[2 * p2 + 1][0], pl[2 * p2 + 1][1], pl[2 * p2 + 1][2], pl[2 * p2 + 1][3]};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bh),
+                                                    acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bl),
+                                                    acc, 0, 0, 0);
+    }
+    st.z[dt] = acc;
+  }
+}
+
+// The lane's query fragment for MFMA column c16 (head c16, dims 32 p + 8 g .. +7) times
+// the score scale, split bf16 hi + lo; heads >= H are zero.  qp: the fp32 query rows of
+// the sequence (head stride qsh, unit channel stride when vec).
+template <int NP>
+__device__ __forceinline__ void sa_query_split(const void* q, int qdt, int64_t qoff, int64_t qsh, int64_t qsd, bool vec,
+                                               int H, float scale, int c16, int g, s16x8 (&qh)[NP], s16x8 (&ql)[NP]) {
+  float qv[NP][8];
+  if (vec) {  // fp32 rows, 16-byte aligned: all of the lane's query loads in flight at once
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
+      if (c16 < H) {
+        const float* qp = (const float*)q + qoff + c16 * qsh + 32 * p + 8 * g;
+        x0 = *(const f32x4*)qp;
+        x1 = *(const f32x4*)(qp + 4);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qv[p][j] = x0[j];
+        qv[p][4 + j] = x1[j];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        qv[p][j] = (c16 < H) ? load_elem(q, qdt, qoff + c16 * qsh + (32 * p + 8 * g + j) * qsd) : 0.f;
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = qv[p][j] * scale;   // scores come out scaled
+      const short h = __builtin_bit_cast(short, (__bf16)x);
+      qh[p][j] = h;
+      ql[p][j] = __builtin_bit_cast(short, (__bf16)(x - bf16_bits_to_f32((uint16_t)h)));
+    }
   }
 }
 
@@ -442,47 +594,13 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a_in) {
   const int64_t t1 = min(sg.t_end, t0 + tpw);
   short* tile = s_tile[wave];
 
-  // queries times the score scale (B operand of the scores): head c16, dims 32p + 8g .. +7,
-  // split hi/lo
+  // queries times the score scale (B operand of the scores): head c16, split hi/lo
   s16x8 qh[NP], ql[NP];
-  float qv[NP][8];
-  if (a.qvec) {  // fp32 rows, 16-byte aligned: all of the lane's query loads in flight at once
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
-      if (c16 < a.H) {
-        const float* qp = (const float*)a.q + b * a.qsb + c16 * a.qsh + 32 * p + 8 * g;
-        x0 = *(const f32x4*)qp;
-        x1 = *(const f32x4*)(qp + 4);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        qv[p][j] = x0[j];
-        qv[p][4 + j] = x1[j];
-      }
-    }
-  } else {
-#pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        qv[p][j] = (c16 < a.H) ? load_elem(a.q, a.qdt, b * a.qsb + c16 * a.qsh + (32 * p + 8 * g + j) * a.qsd) : 0.f;
-  }
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float x = qv[p][j] * a.scale;   // scores come out scaled
-      const short h = __builtin_bit_cast(short, (__bf16)x);
-      qh[p][j] = h;
-      ql[p][j] = __builtin_bit_cast(short, (__bf16)(x - bf16_bits_to_f32((uint16_t)h)));
-    }
-  }
+  sa_query_split<NP>(a.q, a.qdt, b * a.qsb, a.qsh, a.qsd, a.qvec, a.H, a.scale, c16, g, qh, ql);
   const bool head_on = c16 < a.H && (sg.head_only < 0 || sg.head_only == c16);
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4 z[DC / 16];
-#pragma unroll
-  for (int dt = 0; dt < DC / 16; ++dt) z[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  SaAcc<NP> st;
+  sa_acc_init(st);
+  const SaRows rows = sa_rows(a, b);
 
   // sparse block indices of this wave's tiles, one per lane, fetched up front so that
   // the tile loads do not wait on a dependent index load
@@ -494,100 +612,24 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a_in) {
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)blk_l >> 32), src);
     return (int64_t)(((uint64_t)hi << 32) | lo);
   };
-  // One tile: scores, online softmax, values.  The key rows arrive in registers (cv,
-  // with their row validity ok) and are copied row-major into the wave's LDS tile for
-  // the transposed reads of the value product.
-  auto tile_step = [&](const s16x8 (&cv)[4][NP], uint32_t okb) {
-    f32x4 sc[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        *(s16x8*)(tile + (16 * rb + c16) * TP + 32 * p + 8 * g) = cv[rb][p];
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
-                                                      __builtin_bit_cast(bf16x8, qh[p]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cv[rb][p]),
-                                                      __builtin_bit_cast(bf16x8, ql[p]), acc, 0, 0, 0);
-      }
-      sc[rb] = acc;
-    }
-    // lane (head c16, group g) holds scores of keys 16 rb + 4g + i
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool kv = (okb >> (4 * rb + i)) & 1u;
-        const float x = (kv && head_on) ? sc[rb][i] : -INFINITY;
-        sc[rb][i] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float corr = (m_new == -INFINITY) ? 1.f : __expf(m_run - m_new);
-    const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;   // exp(-inf - m_sub) = 0 for masked keys
-    float psum = 0.f;
-    s16x4 ph[4], pl[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      f32x4 pv;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pe = __expf(sc[rb][i] - m_sub);
-        pv[i] = pe;
-        psum += pe;
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const short hb = __builtin_bit_cast(short, (__bf16)pv[i]);
-        ph[rb][i] = hb;
-        pl[rb][i] = __builtin_bit_cast(short, (__bf16)(pv[i] - bf16_bits_to_f32((uint16_t)hb)));
-      }
-    }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
-    l_run = l_run * corr + psum;
-    m_run = m_new;
-    // z[dim][head] = corr * z + C^T P  (K = 64 keys as two permuted 32-steps)
-#pragma unroll
-    for (int dt = 0; dt < DC / 16; ++dt) {
-      f32x4 acc = z[dt] * corr;
-#pragma unroll
-      for (int p2 = 0; p2 < 2; ++p2) {
-        const s16x4 a0 = sa_ldsT4(tile, TP, 32 * p2, 16 * dt, c16, g);
-        const s16x4 a1 = sa_ldsT4(tile, TP, 32 * p2 + 16, 16 * dt, c16, g);
-        const s16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        const s16x8 bh = {ph[2 * p2][0], ph[2 * p2][1], ph[2 * p2][2], ph[2 * p2][3],
-                          ph[2 * p2 + 1][0], ph[2 * p2 + 1][1], ph[2 * p2 + 1][2], ph[2 * p2 + 1][3]};
-        const s16x8 bl = {pl[2 * p2][0], pl[2 * p2][1], pl[2 * p2][2], pl[2 * p2][3],
-                          pl[2 * p2 + 1][0], pl[2 * p2 + 1][1], pl[2 * p2 + 1][2], pl[2 * p2 + 1][3]};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bh),
-                                                      acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bl),
-                                                      acc, 0, 0, 0);
-      }
-      z[dt] = acc;
-    }
-  };
   // two register sets in turn: the next tile's loads are in flight while a tile computes,
   // and no set is copied into the other (a copy would wait for the loads)
   s16x8 cvA[4][NP], cvB[4][NP];
   uint32_t okA = 0, okB = 0;
-  if (t0 < t1) sa_load_tile<NP>(a, sg, b, t0, blk_of(t0), c16, g, cvA, okA);
+  if (t0 < t1) sa_load_rows<NP>(rows, sg.stream, t0, blk_of(t0), c16, g, cvA, okA);
   for (int64_t tix = t0; tix < t1; tix += 2) {
     // loads past the wave's last tile re-read that tile (in bounds, unused); unconditional
     // loads keep the register pressure of the two sets at that of straight-line code
     const int64_t n1 = tix + 1 < t1 ? tix + 1 : tix;
-    sa_load_tile<NP>(a, sg, b, n1, blk_of(n1), c16, g, cvB, okB);
-    tile_step(cvA, okA);
+    sa_load_rows<NP>(rows, sg.stream, n1, blk_of(n1), c16, g, cvB, okB);
+    sa_tile_step<NP>(cvA, okA, head_on, qh, ql, tile, c16, g, st);
     if (tix + 1 >= t1) break;
     const int64_t n2 = tix + 2 < t1 ? tix + 2 : tix + 1;
-    sa_load_tile<NP>(a, sg, b, n2, blk_of(n2), c16, g, cvA, okA);
-    tile_step(cvB, okB);
+    sa_load_rows<NP>(rows, sg.stream, n2, blk_of(n2), c16, g, cvA, okA);
+    sa_tile_step<NP>(cvB, okB, head_on, qh, ql, tile, c16, g, st);
   }
+  const float m_run = st.m, l_run = st.l;
+  const f32x4* z = st.z;
   // merge the four wave partials: s_z[wave][head][dim], s_m / s_l[wave][head]
   __syncthreads();
   float* s_z = (float*)&s_tile[0][0];
@@ -627,6 +669,156 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a_in) {
       for (int w = 0; w < 4; ++w) zz = fmaf(e[w], s_z[(w * 16 + h) * DC + dd], zz);
       a.ws[o + 2 + dd] = zz;
     }
+  }
+}
+
+// ------------------------------------------------------------------ prefill, latent form
+// Every query t of a prefill (position pos = Lkv - Lq + t) attends, per head, to the three
+// streams of a decode step at length L = pos + 1 (layers/sparse_attention.py:95-105,
+// 145-171, 173-219, 275: the local window and sinks with j <= pos, the listed blocks'
+// tokens <= pos with multiplicity, the complete means with (e+1) pool - 1 <= pos or the
+// running mean before pool - 1), in latent space with the heads in the MFMA columns: the
+// key rows of a tile serve every head of the query, and no query of another position
+// shares the wave.  One workgroup of PL_W waves per query; the waves are split over the
+// streams in proportion to their tile counts (each wave one stream, one online softmax),
+// then the partials of each stream are merged in LDS, gated and written as
+// z[b, t, h] = sum_s g_s sum_j p_sj c_j (fp32); the caller applies W_v,h.
+constexpr int PL_W = 8;
+
+struct PlArgs {
+  const void* q; int qdt; int64_t qsb, qst, qsh, qsd; int qvec;   // q_lat [B, Lq, H, dc]
+  const uint16_t* c; int64_t csb, csl;                            // [B, Lkv, dc] bf16
+  const uint16_t* hca; int64_t hsb, hsn;                          // [B, >= Lkv/pool, dc] bf16
+  const int64_t* idx; int64_t isb, ist, isk;                      // [B, Lq | 1, K]
+  const void* gate; int gdt; int64_t gsb, gsh, gst, gsm;          // [B, Lq, 3] (gsh = 0) or [B, H, Lq, 3]
+  float* out; int64_t osb, ost, osh;                              // [B, Lq, H, dc] fp32, unit channel stride
+  int64_t Lq, Lkv;
+  int H, K, window, n_sink, bs, pool;
+  float scale;
+};
+
+template <int NP>
+__global__ __launch_bounds__(512, 1) void maba_sa_prefill_latent_kernel(PlArgs a) {
+  constexpr int DC = 32 * NP;
+  constexpr int TP = DC + 8;
+  __shared__ __attribute__((aligned(16))) short s_tile[PL_W][64 * TP];
+  __shared__ float s_ml[PL_W][2][16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t b = blockIdx.x / a.Lq, t = blockIdx.x % a.Lq;
+  const int64_t L = a.Lkv - a.Lq + t + 1;
+  // the three streams of a decode step at length L (as sa_geometry)
+  SaRows rows;
+  rows.c = a.c + b * a.csb; rows.cs = a.csl;
+  rows.hca = a.hca + b * a.hsb; rows.hs = a.hsn;
+  rows.L = L; rows.bs = a.bs;
+  const int64_t ns = L < a.n_sink ? L : a.n_sink;
+  const int64_t lst = (L - a.window) > ns ? (L - a.window) : ns;
+  rows.ns = (int)ns; rows.loc_start = (int)lst; rows.nloc = (int)(ns + (L - lst)); rows.nc = (int)(L / a.pool);
+  const int tc0 = (rows.nloc + 63) / 64, tc1 = a.K, tc2 = (L - 1 >= a.pool - 1) ? (rows.nc + 63) / 64 : 0;
+  // waves per stream: in proportion to the tile counts, at least one per nonempty stream
+  // (scalars throughout: a small array indexed by the stream would go to scratch memory)
+  const int T = tc0 + tc1 + tc2;
+  const int Tm = T > 0 ? T : 1;
+  int n0 = tc0 > 0 ? max(1, PL_W * tc0 / Tm) : 0;
+  int n1 = tc1 > 0 ? max(1, PL_W * tc1 / Tm) : 0;
+  int n2 = tc2 > 0 ? max(1, PL_W * tc2 / Tm) : 0;
+  while (n0 + n1 + n2 > PL_W) {   // take a wave from the stream with the most waves
+    if (n1 >= n0 && n1 >= n2 && n1 > 1) --n1;
+    else if (n2 >= n0 && n2 > 1) --n2;
+    else --n0;
+  }
+  while (n0 + n1 + n2 < PL_W) {   // give a wave to the stream with the most tiles per wave
+    const int p0 = n0 ? (tc0 + n0 - 1) / n0 : 0, p1 = n1 ? (tc1 + n1 - 1) / n1 : 0, p2 = n2 ? (tc2 + n2 - 1) / n2 : 0;
+    const int best = max(p0, max(p1, p2));
+    if (best <= 1) break;
+    if (p1 == best) ++n1; else if (p2 == best) ++n2; else ++n0;
+  }
+  const int wb1 = n0, wb2 = n0 + n1, wend = n0 + n1 + n2;   // waves [0,wb1) local, [wb1,wb2) sparse, [wb2,wend) HCA
+  const int stream = wave < wb1 ? 0 : (wave < wb2 ? 1 : (wave < wend ? 2 : -1));
+  const int j = stream == 0 ? wave : (stream == 1 ? wave - wb1 : wave - wb2);
+  const int tcs = stream == 0 ? tc0 : (stream == 1 ? tc1 : tc2);
+  const int nws = stream == 0 ? n0 : (stream == 1 ? n1 : n2);
+  int64_t t0 = 0, t1 = 0;
+  if (stream >= 0) {
+    const int per = (tcs + nws - 1) / nws;
+    t0 = (int64_t)j * per;
+    t1 = min((int64_t)tcs, t0 + per);
+  }
+  short* tile = s_tile[wave];
+  s16x8 qh[NP], ql[NP];
+  sa_query_split<NP>(a.q, a.qdt, b * a.qsb + t * a.qst, a.qsh, a.qsd, a.qvec, a.H, a.scale, c16, g, qh, ql);
+  const bool head_on = c16 < a.H;
+  SaAcc<NP> st;
+  sa_acc_init(st);
+  int64_t blk_l = 0;
+  if (stream == 1 && lane < t1 - t0) blk_l = a.idx[b * a.isb + t * a.ist + (t0 + lane) * a.isk];
+  auto blk_of = [&](int64_t tix) {
+    const int src = (int)(tix - t0);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)blk_l, src);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)blk_l >> 32), src);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+  if (t0 < t1) {
+    s16x8 cvA[4][NP], cvB[4][NP];
+    uint32_t okA = 0, okB = 0;
+    sa_load_rows<NP>(rows, stream, t0, blk_of(t0), c16, g, cvA, okA);
+    for (int64_t tix = t0; tix < t1; tix += 2) {
+      const int64_t n1 = tix + 1 < t1 ? tix + 1 : tix;
+      sa_load_rows<NP>(rows, stream, n1, blk_of(n1), c16, g, cvB, okB);
+      sa_tile_step<NP>(cvA, okA, head_on, qh, ql, tile, c16, g, st);
+      if (tix + 1 >= t1) break;
+      const int64_t n2 = tix + 2 < t1 ? tix + 2 : tix + 1;
+      sa_load_rows<NP>(rows, stream, n2, blk_of(n2), c16, g, cvA, okA);
+      sa_tile_step<NP>(cvB, okB, head_on, qh, ql, tile, c16, g, st);
+    }
+  }
+  // wave partials to LDS (the tiles are free once every wave is past its loop)
+  __syncthreads();
+  float* s_z = (float*)&s_tile[0][0];   // [PL_W][16][DC]
+#pragma unroll
+  for (int dt = 0; dt < DC / 16; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_z[(wave * 16 + c16) * DC + 16 * dt + 4 * g + i] = st.z[dt][i];
+  if (g == 0) {
+    s_ml[wave][0][c16] = stream >= 0 ? st.m : -INFINITY;
+    s_ml[wave][1][c16] = stream >= 0 ? st.l : 0.f;
+  }
+  __syncthreads();
+  const bool early = L - 1 < a.pool - 1;
+  const int wr[4] = {0, wb1, wb2, wend};
+  for (int e = threadIdx.x; e < a.H * DC; e += PL_W * 64) {
+    const int h = e / DC, d = e % DC;
+    const int64_t gb = b * a.gsb + h * a.gsh + t * a.gst;
+    float z0 = load_elem(a.gate, a.gdt, gb), z1 = load_elem(a.gate, a.gdt, gb + a.gsm),
+          z2 = load_elem(a.gate, a.gdt, gb + 2 * a.gsm);
+    const float gm = fmaxf(z0, fmaxf(z1, z2));
+    z0 = __expf(z0 - gm); z1 = __expf(z1 - gm); z2 = __expf(z2 - gm);
+    const float gi = 1.f / (z0 + z1 + z2);
+    const float gs[3] = {z0 * gi, z1 * gi, z2 * gi};
+    float res = 0.f;
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      if (s == 2 && early) continue;
+      float M = -INFINITY;
+      for (int w = wr[s]; w < wr[s + 1]; ++w) M = fmaxf(M, s_ml[w][0][h]);
+      if (M == -INFINITY) continue;   // no valid key: the stream gives 0
+      float Ls = 0.f, Zs = 0.f;
+      for (int w = wr[s]; w < wr[s + 1]; ++w) {
+        const float m = s_ml[w][0][h];
+        if (m == -INFINITY) continue;
+        const float f = __expf(m - M);
+        Ls = fmaf(f, s_ml[w][1][h], Ls);
+        Zs = fmaf(f, s_z[(w * 16 + h) * DC + d], Zs);
+      }
+      if (Ls > 0.f) res = fmaf(gs[s], Zs / Ls, res);
+    }
+    if (early) {   // HCA before the first complete block: running mean of c[0..pos]
+      float zs = 0.f;
+      for (int64_t r = 0; r < L; ++r) zs += bf16_bits_to_f32(rows.c[r * rows.cs + d]);
+      res = fmaf(gs[2], zs / (float)L, res);
+    }
+    a.out[b * a.osb + t * a.ost + h * a.osh + d] = res;
   }
 }
 
@@ -840,4 +1032,65 @@ extern "C" int maba_hip_maba_sa_decode_dev(const maba_tensor* q_lat, const maba_
   if (L_cap < pool) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_dev: L_cap must be at least pool");
   a.dlen = d_len;
   return sa_run(a, seg, (hipStream_t)stream);
+}
+
+extern "C" int maba_hip_maba_sa_prefill_latent(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                               const maba_tensor* hca, const maba_tensor* idx,
+                                               const maba_tensor* gate, float scale, int window, int n_sink,
+                                               int block_size, int pool, maba_tensor* out_lat, void* stream) {
+  if (!q_lat || q_lat->ndim != 4) return fail(MABA_ERR_INVALID, "maba_sa_prefill_latent: q_lat must be [B,Lq,H,dc]");
+  const int64_t B = q_lat->shape[0], Lq = q_lat->shape[1], H = q_lat->shape[2], dc = q_lat->shape[3];
+  if (!c_kv || c_kv->ndim != 3 || c_kv->shape[0] != B || c_kv->shape[2] != dc || c_kv->shape[1] < Lq)
+    return fail(MABA_ERR_INVALID, "maba_sa_prefill_latent: c_kv must be [B,Lkv>=Lq,dc]");
+  const int64_t Lkv = c_kv->shape[1];
+  if (window < 0 || n_sink < 0 || block_size <= 0 || pool <= 0)
+    return fail(MABA_ERR_INVALID, "maba_sa_prefill_latent: bad window/sink/block/pool");
+  if (!hca || hca->ndim != 3 || hca->shape[0] != B || hca->shape[2] != dc || hca->shape[1] < Lkv / pool)
+    return fail(MABA_ERR_INVALID, "maba_sa_prefill_latent: hca must be [B,>=Lkv/pool,dc]");
+  if (!idx || idx->ndim != 3 || idx->shape[0] != B || (idx->shape[1] != Lq && idx->shape[1] != 1))
+    return fail(MABA_ERR_INVALID, "maba_sa_prefill_latent: idx must be [B,Lq|1,K]");
+  if (idx->dtype != MABA_I64) return fail(MABA_ERR_DTYPE, "maba_sa_prefill_latent: idx must be int64");
+  if (!gate || !((gate->ndim == 3 && gate->shape[0] == B && gate->shape[1] == Lq && gate->shape[2] == 3) ||
+                 (gate->ndim == 4 && gate->shape[0] == B && gate->shape[1] == H && gate->shape[2] == Lq &&
+                  gate->shape[3] == 3)))
+    return fail(MABA_ERR_INVALID, "maba_sa_prefill_latent: gate must be [B,Lq,3] or [B,H,Lq,3]");
+  const int64_t so[4] = {B, Lq, H, dc};
+  if (!expect_shape(out_lat, "out_lat", 4, so)) return MABA_ERR_INVALID;
+  if (out_lat->dtype != MABA_F32 || out_lat->stride[3] != 1)
+    return fail(MABA_ERR_DTYPE, "maba_sa_prefill_latent: out_lat must be f32 with unit channel stride");
+  if (!expect_float(q_lat, "q_lat") || !expect_float(gate, "gate")) return MABA_ERR_DTYPE;
+  if (c_kv->dtype != MABA_BF16 || hca->dtype != MABA_BF16)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill_latent: bf16 c_kv and hca");
+  if (H > SA_MAXH || dc % 32 != 0 || dc > 128 || block_size > 64 || idx->shape[2] > 64)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill_latent: H <= %d, d_c a multiple of 32 up to 128, "
+                "block_size <= 64 and K <= 64", SA_MAXH);
+  if (B * Lq > INT32_MAX) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill_latent: B * Lq beyond one grid");
+  if (c_kv->stride[2] != 1 || hca->stride[2] != 1 || (uintptr_t)c_kv->data % 16 || (uintptr_t)hca->data % 16 ||
+      c_kv->stride[0] % 8 || c_kv->stride[1] % 8 || hca->stride[0] % 8 || hca->stride[1] % 8)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill_latent: 16-byte aligned bf16 rows with unit channel stride");
+  if (B * Lq * H == 0) return MABA_OK;
+  PlArgs a;
+  a.q = q_lat->data; a.qdt = q_lat->dtype; a.qsb = q_lat->stride[0]; a.qst = q_lat->stride[1];
+  a.qsh = q_lat->stride[2]; a.qsd = q_lat->stride[3];
+  a.qvec = q_lat->dtype == MABA_F32 && q_lat->stride[3] == 1 && (uintptr_t)q_lat->data % 16 == 0 &&
+           q_lat->stride[0] % 4 == 0 && q_lat->stride[1] % 4 == 0 && q_lat->stride[2] % 4 == 0;
+  a.c = (const uint16_t*)c_kv->data; a.csb = c_kv->stride[0]; a.csl = c_kv->stride[1];
+  a.hca = (const uint16_t*)hca->data; a.hsb = hca->stride[0]; a.hsn = hca->stride[1];
+  a.idx = (const int64_t*)idx->data; a.isb = idx->stride[0]; a.ist = idx->shape[1] == 1 ? 0 : idx->stride[1];
+  a.isk = idx->stride[2];
+  a.gate = gate->data; a.gdt = gate->dtype;
+  if (gate->ndim == 3) { a.gsb = gate->stride[0]; a.gsh = 0; a.gst = gate->stride[1]; a.gsm = gate->stride[2]; }
+  else { a.gsb = gate->stride[0]; a.gsh = gate->stride[1]; a.gst = gate->stride[2]; a.gsm = gate->stride[3]; }
+  a.out = (float*)out_lat->data; a.osb = out_lat->stride[0]; a.ost = out_lat->stride[1]; a.osh = out_lat->stride[2];
+  a.Lq = Lq; a.Lkv = Lkv; a.H = (int)H; a.K = (int)idx->shape[2];
+  a.window = window; a.n_sink = n_sink; a.bs = block_size; a.pool = pool; a.scale = scale;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)(B * Lq));
+  switch (dc / 32) {
+    case 1: hipLaunchKernelGGL(maba_sa_prefill_latent_kernel<1>, grid, dim3(PL_W * 64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(maba_sa_prefill_latent_kernel<2>, grid, dim3(PL_W * 64), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(maba_sa_prefill_latent_kernel<3>, grid, dim3(PL_W * 64), 0, s, a); break;
+    default: hipLaunchKernelGGL(maba_sa_prefill_latent_kernel<4>, grid, dim3(PL_W * 64), 0, s, a); break;
+  }
+  return check_launch("maba_sa_prefill_latent");
 }

@@ -54,6 +54,7 @@ EXPORTED_SYMBOLS = (
     "maba_hip_maba_sa_decode_dev",
     "maba_hip_rmsnorm",
     "maba_hip_swiglu",
+    "maba_hip_maba_sa_prefill_latent",
 )
 
 
@@ -102,6 +103,7 @@ def _declare(lib) -> None:
         "maba_hip_maba_sa_decode_dev": ([T, T, T, T, T, vp, i64, f, i, i, i, i, T, vp, sz, vp], i),
         "maba_hip_rmsnorm": ([T, T, T, T, f, T, T, vp], i),
         "maba_hip_swiglu": ([T, T, vp], i),
+        "maba_hip_maba_sa_prefill_latent": ([T, T, T, T, T, f, i, i, i, i, T, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -369,3 +369,24 @@ def hip_swiglu(gate_up) -> torch.Tensor:
     rc = N.load().maba_hip_swiglu(N.desc(gate_up), N.desc(out), N.stream_ptr(dev))
     N.check(rc, "swiglu")
     return out
+
+
+def hip_maba_sa_prefill_latent(q_lat, c_kv, hca, idx, gate_logits, scale: float, window: int = 128,
+                               n_sink: int = 4, block_size: int = 64, pool: int = 64,
+                               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The three MABA-SA prefill streams and their gate in latent form
+    (layers/sparse_attention.py:95-105, 145-171, 173-219, 275): query t of ``q_lat [B, Lq, H,
+    d_c]`` (``W_k,h^T q_h``, fp32) sits at position ``Lkv - Lq + t`` of the bf16 latent cache
+    ``c_kv [B, Lkv, d_c]``; ``hca`` holds its complete-block means.  Returns fp32 ``z [B, Lq, H,
+    d_c]`` (into ``out`` when given); the caller applies ``W_v,h``."""
+    _no_grad_needed("maba_sa_prefill_latent", q_lat, c_kv, hca, gate_logits)
+    dev = N.require_device([q_lat, c_kv, hca, idx, gate_logits], "maba_sa_prefill_latent")
+    if out is None:
+        out = torch.empty(q_lat.shape, dtype=torch.float32, device=dev)
+    if out.numel() == 0:
+        return out
+    rc = N.load().maba_hip_maba_sa_prefill_latent(N.desc(q_lat), N.desc(c_kv), N.desc(hca), N.desc(idx),
+                                                  N.desc(gate_logits), float(scale), int(window), int(n_sink),
+                                                  int(block_size), int(pool), N.desc(out), N.stream_ptr(dev))
+    N.check(rc, "maba_sa_prefill_latent")
+    return out

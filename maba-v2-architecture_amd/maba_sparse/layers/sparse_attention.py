@@ -239,9 +239,31 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
             return False
         if self.block_size != 64 or idx.shape[-1] > 64 or c_full.shape[1] > (1 << 20):
             return False
+        if self.d_c % 32 != 0 or self.d_c > 128 or self.n_heads > 16:
+            return False
         return not (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()))
 
     def _fused_prefill(self, x, q, c_full, idx):
+        """The three streams and the gate in latent form: ``q_lat = W_k,h^T q_h`` per query, one
+        ``maba_sa_prefill_latent`` launch over the bf16 latent rows and their complete-block
+        means, then ``o_h = W_v,h z_h``.  Keys and values are never up-projected (the cache is
+        read once per query tile instead of materialising ``[B, H, Lkv, dh]`` twice).
+        Returns ``[B, H, Lq, dh]`` (a transposed view)."""
+        from maba_sparse.kernels import hip_backend as hb
+        b, h, lq, dh = q.shape
+        r = self.hca_pool_size
+        nc = c_full.shape[1] // r
+        Wk = self._f32_heads(self.k_up_proj, "_wk_f32")
+        Wv = self._f32_heads(self.v_up_proj, "_wv_f32")
+        q_lat = torch.einsum("bhtd,hdc->bthc", q.float(), Wk)
+        hca = (hb.hip_hca_pool(c_full[:, : nc * r], pool=r) if nc > 0
+               else c_full.new_zeros(b, 1, self.d_c))
+        z = hb.hip_maba_sa_prefill_latent(q_lat.contiguous(), c_full.contiguous(), hca, idx, self.stream_gate(x),
+                                          scale=self.scale, window=self.window_size, n_sink=self.n_sink_tokens,
+                                          block_size=self.block_size, pool=r)
+        return torch.einsum("bthc,hdc->bthd", z, Wv).transpose(1, 2)
+
+    def _fused_prefill_heads(self, x, q, c_full, idx):
         """The streams' inputs as the dense path forms them (per-head keys and values, the
         up-projected complete-block means, the running-mean rows before ``pool - 1``), then
         one ``maba_sa_prefill`` launch with the gate.  Returns ``[B, H, Lq, dh]``."""

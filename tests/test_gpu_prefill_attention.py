@@ -115,3 +115,88 @@ def test_maba_sa_prefill_edges(dev, Lq, Lkv, window, n_sink, empty_sparse):
     exp = osa.maba_sa_prefill_heads(to_np(q), to_np(k), to_np(v), to_np(kh), to_np(vh), to_np(early), idx.numpy(),
                                     to_np(gate), window=window, n_sink=n_sink, scale=0.125)
     assert_close(out, exp, 2e-3, 2e-3, "maba_sa_prefill edge")
+
+
+def _latent_case(B, H, Lq, Lkv, dc, K, seed, shared=False, gate4=False, dup=False, dh=64):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, Lq, dh, generator=g).bfloat16()
+    c = torch.randn(B, Lkv, dc, generator=g).bfloat16()
+    Wk = (torch.randn(H * dh, dc, generator=g) * dc ** -0.5).bfloat16()
+    Wv = (torch.randn(H * dh, dc, generator=g) * dc ** -0.5).bfloat16()
+    nb = (Lkv + 63) // 64
+    idx = torch.randint(0, nb, (B, 1 if shared else Lq, K), generator=g)
+    if K > 2:
+        idx[:, :, 0] = -1                                       # an empty slot (ignored)
+    if dup and K > 2:
+        idx[:, ::3, 2] = idx[:, ::3, 1]                         # repeated blocks count twice
+    gate = torch.randn(B, H, Lq, 3, generator=g) if gate4 else torch.randn(B, Lq, 3, generator=g)
+    return q, c, Wk, Wv, idx, gate
+
+
+def _latent_run(dev, q, c, Wk, Wv, idx, gate, window, n_sink, pool=64):
+    """The layer's latent composition on the GPU: q_lat = W_k,h^T q_h (fp32), the kernel over the
+    bf16 latent rows and their bf16 block means, then W_v,h z."""
+    B, H, Lq, dh = q.shape
+    dc = c.shape[-1]
+    Wk_h = Wk.float().view(H, dh, dc).to(dev)
+    Wv_h = Wv.float().view(H, dh, dc).to(dev)
+    q_lat = torch.einsum("bhtd,hdc->bthc", q.to(dev).float(), Wk_h).contiguous()
+    cd = c.to(dev)
+    nc = c.shape[1] // pool
+    hca = (_hip().hip_hca_pool(cd[:, : nc * pool], pool=pool) if nc > 0
+           else torch.zeros(B, 1, dc, device=dev, dtype=torch.bfloat16))
+    z = _hip().hip_maba_sa_prefill_latent(q_lat, cd, hca, idx.to(dev), gate.to(dev), scale=dh ** -0.5,
+                                          window=window, n_sink=n_sink, block_size=64, pool=pool)
+    return torch.einsum("bthc,hdc->bhtd", z, Wv_h)
+
+
+@pytest.mark.parametrize("B,H,Lq,Lkv,dc,K,window,n_sink,shared,gate4,dup", [
+    (2, 3, 150, 150, 64, 4, 128, 4, False, False, True),    # early rows, two complete means, repeats
+    (1, 2, 77, 300, 128, 8, 40, 2, False, True, False),     # a past, per-head gates, narrow window
+    (2, 2, 64, 64, 32, 3, 16, 0, True, False, False),       # d_c 32, one index row for all queries
+    (1, 2, 40, 40, 128, 2, 128, 4, False, False, False),    # no complete block: all early
+    (1, 10, 600, 1000, 128, 32, 128, 4, False, False, True),  # the layer's head count and top-k
+    (1, 16, 300, 2000, 96, 16, 300, 70, False, False, False),  # 16 heads, sinks wider than one tile
+    (1, 4, 200, 4200, 128, 64, 128, 4, False, True, True),  # 64 index slots
+])
+def test_maba_sa_prefill_latent_vs_oracle(dev, B, H, Lq, Lkv, dc, K, window, n_sink, shared, gate4, dup):
+    q, c, Wk, Wv, idx, gate = _latent_case(B, H, Lq, Lkv, dc, K, B * 1000 + Lq + K, shared, gate4, dup)
+    out = _latent_run(dev, q, c, Wk, Wv, idx, gate, window, n_sink)
+    exp = osa.maba_sa_prefill(to_np(q), to_np(c), to_np(Wk), to_np(Wv), idx.numpy(), to_np(gate),
+                              window=window, n_sink=n_sink)
+    assert_close(out, exp, 2e-3, 2e-3, "maba_sa_prefill_latent")
+
+
+@pytest.mark.parametrize("Lq,Lkv,window,n_sink,empty_sparse", [
+    (1, 1, 128, 4, False),      # one token
+    (1, 500, 128, 4, False),    # one query over a past: a decode step
+    (50, 200, 0, 0, False),     # no local keys at all: the local stream contributes 0
+    (40, 100, 16, 200, True),   # sinks wider than the sequence; every index slot empty
+    (70, 70, 128, 4, False),    # queries on both sides of the first complete block
+])
+def test_maba_sa_prefill_latent_edges(dev, Lq, Lkv, window, n_sink, empty_sparse):
+    q, c, Wk, Wv, idx, gate = _latent_case(2, 3, Lq, Lkv, 64, 4, Lq * 7 + Lkv)
+    if empty_sparse:
+        idx[:] = -1
+    out = _latent_run(dev, q, c, Wk, Wv, idx, gate, window, n_sink)
+    exp = osa.maba_sa_prefill(to_np(q), to_np(c), to_np(Wk), to_np(Wv), idx.numpy(), to_np(gate),
+                              window=window, n_sink=n_sink)
+    assert_close(out, exp, 2e-3, 2e-3, "maba_sa_prefill_latent edge")
+
+
+def test_maba_sa_prefill_latent_matches_decode(dev):
+    """Every query row of the prefill equals a decode step at that prefix length (the decode
+    entry point, with the same index row)."""
+    B, H, Lq, Lkv, dc, K = 1, 4, 96, 400, 128, 8
+    q, c, Wk, Wv, idx, gate = _latent_case(B, H, Lq, Lkv, dc, K, 5)
+    Wk_h = Wk.float().view(H, 64, dc).to(dev)
+    q_lat = torch.einsum("bhtd,hdc->bthc", q.to(dev).float(), Wk_h).contiguous()
+    cd = c.to(dev)
+    hca = _hip().hip_hca_pool(cd, pool=64)
+    z = _hip().hip_maba_sa_prefill_latent(q_lat, cd, hca, idx.to(dev), gate.to(dev), scale=0.125)
+    for t in (0, 1, 37, Lq - 1):
+        L = Lkv - Lq + t + 1
+        zd = _hip().hip_maba_sa_decode(q_lat[:, t].contiguous(), cd, hca, idx[:, t: t + 1].to(dev),
+                                       gate[:, t].to(dev), L=L, scale=0.125)
+        err = (z[:, t] - zd).abs().max().item()
+        assert err <= 1e-4 * max(1.0, zd.abs().max().item()), (t, err)
