@@ -601,11 +601,27 @@ def prologue_benches(dev, B=4, T=32768, dim=640, H=10):
             return layer(x)[0]
 
     ms, _ = time_op(fwd, 5, 1)
+    layer.fuse_prologue = False
+    ms_u, _ = time_op(fwd, 5, 1)
+    layer.fuse_prologue = True
+    # the fused prologue + recurrence passes alone, from the projections
+    projs = torch.randn(B, T, 6 * Cc, device=dev, generator=g, dtype=torch.bfloat16).split(Cc, dim=-1)
+    convs = (layer.conv_q.weight, layer.conv_k.weight, layer.conv_v.weight)
+    ob = torch.empty(B, T, Cc, device=dev, dtype=torch.bfloat16)
+    def fused_passes():
+        with torch.no_grad():
+            return hb.hip_dgda_layer_prefill(projs, convs, None, out=ob)
+
+    ms_k, _ = time_op(fused_passes, 5, 1)
     out["dgda_layer_forward"] = {
-        "ms_per_call": ms, "tokens_per_s": B * T / (ms * 1e-3),
+        "ms_per_call": ms, "tokens_per_s": B * T / (ms * 1e-3), "unfused_ms_per_call": ms_u,
+        "fused_prefill_ms": ms_k,
         "config": "DGDALayer(dim=640, 10 heads) bf16, x [4, 32768, 640], no_grad: one 640x3840 projection GEMM, "
-                  "the HIP prologue, the per-channel-gate DGDA prefill, o_proj"}
-    log(f"dgda layer forward (bf16, B=4, T=32768): {ms:.3f} ms")
+                  "the per-channel-gate DGDA prefill with the prologue fused into its staging "
+                  "(fused_prefill_ms: those passes alone), o_proj; unfused: the one-pass prologue kernel, "
+                  "then the prefill on its stored outputs"}
+    log(f"dgda layer forward (bf16, B=4, T=32768): {ms:.3f} ms fused, {ms_u:.3f} ms unfused; "
+        f"fused prefill passes {ms_k:.3f} ms")
     return out
 
 

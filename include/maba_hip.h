@@ -38,6 +38,9 @@
  *                                   layer's conv + SiLU with carried history,
  *                                   gate activations and key normalisation;
  *                                   inline torch code in the reference)
+ *   maba_hip_dgda_layer_prefill     layers/dgda.py:103-121,186-233 (the prologue
+ *                                   above fused into the prefill kernels' input
+ *                                   staging, then the chunked recurrence)
  *   maba_hip_cache_append           layers/indexer.py:62-82 (key cache, complete
  *                                   and tail centroids), layers/sparse_attention.py:
  *                                   206, 241-251 (latent rows, HCA block means)
@@ -238,6 +241,22 @@ int maba_hip_maba_sa_prefill_latent(const maba_tensor* q_lat, const maba_tensor*
 int maba_hip_dgda_prologue(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
                            const maba_tensor* const* hist, float eps, maba_tensor* const* ys,
                            maba_tensor* const* new_hist, void* stream);
+
+/*
+ * DGDA layer prefill with the prologue fused into the recurrence kernels' input staging:
+ * q, k, v, the gates and the key norm are formed in fp32 inside the kernels and never
+ * stored.  xs: the six bf16 projections [B,L,C] (q, k, v, decay, erase, write; unit channel
+ * stride, 8-byte aligned rows, C = 64 H), conv_w [C,1,4] x3 (f32/bf16), hist [B,C,3] x3 bf16
+ * or NULL (zeros), eps the key-norm epsilon, initial_state [B,H,64,64] or NULL, out
+ * [B,H,L,64] (f32/bf16, unit channel stride; a [B,L,C] buffer viewed head-major), final_state
+ * [B,H,64,64], new_hist [B,C,3] x3 (f32/bf16; may alias hist: it is written last).  L >= 1.
+ * The workspace is sized by maba_hip_dgda_layer_prefill_workspace_size(B, H, L).
+ */
+size_t maba_hip_dgda_layer_prefill_workspace_size(int64_t B, int64_t H, int64_t L);
+int maba_hip_dgda_layer_prefill(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
+                                const maba_tensor* const* hist, float eps, const maba_tensor* initial_state,
+                                maba_tensor* out, maba_tensor* final_state, maba_tensor* const* new_hist,
+                                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Serving path: a decode step whose position lives in device memory, so that one captured

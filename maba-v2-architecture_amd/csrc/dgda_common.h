@@ -178,4 +178,24 @@ inline SlotGeom slot_geom(int64_t BH, int64_t nch, int64_t min_u) {
   return gm;
 }
 
+// ------------------------------------------------------------------ layer prologue math
+
+// The DGDA layer's activations (reference layers/dgda.py:103-121, 193-197) on the hardware
+// transcendentals (a few ulp in fp32; outputs are then rounded to their dtype).
+__device__ __forceinline__ float pro_sigmoid(float x) { return fast_rcp(1.f + fast_exp(-x)); }
+__device__ __forceinline__ float pro_silu(float x) { return x * pro_sigmoid(x); }
+// max(-softplus(x), -14) with torch's softplus (x itself above 20, where the clamp applies anyway);
+// log(1 + e^x) loses e^x below fp32's epsilon, an absolute error under 1.2e-7
+__device__ __forceinline__ float pro_log_decay(float x) {
+  const float sp = x > 20.f ? x : fast_log(1.f + fast_exp(x));
+  return fmaxf(-sp, -14.f);
+}
+// 1 / (||k|| + eps) from the sum of squares
+__device__ __forceinline__ float pro_knorm_inv(float ss, float eps) { return fast_rcp(fast_sqrt(ss) + eps); }
+
+// The conv history a fused layer prefill leaves (the inputs of its last three tokens per
+// stream and channel); defined with the prologue kernels.
+int launch_dgda_new_history(const maba_tensor* const* xs, const maba_tensor* const* hist,
+                            maba_tensor* const* new_hist, hipStream_t stream);
+
 }  // namespace maba

@@ -14,7 +14,7 @@
 // once (plus a three-row halo per run).  The per-head norm of k is a reduction over the
 // head's 32 threads (half a wave).  Arithmetic in fp32; each output is rounded once.
 // Bound: HBM (six input rows in, seven output rows out per token).
-#include "maba_common.h"
+#include "dgda_common.h"
 
 namespace maba {
 
@@ -49,17 +49,6 @@ template <> struct Pair<uint16_t> {   // bf16 bits
     *(uint32_t*)((uint16_t*)p + i) = (uint32_t)f32_to_bf16_bits(x0) | ((uint32_t)f32_to_bf16_bits(x1) << 16);
   }
 };
-
-// Hardware exp2/rcp based forms (a few ulp in fp32; the outputs are then rounded to the
-// output dtype): the kernel issues seven transcendentals per channel and token.
-__device__ __forceinline__ float pro_silu(float x) { return __fdividef(x, 1.f + __expf(-x)); }
-__device__ __forceinline__ float pro_sigmoid(float x) { return __fdividef(1.f, 1.f + __expf(-x)); }
-// max(-softplus(x), -14) with torch's softplus (x itself above 20, where the clamp applies anyway);
-// log(1 + e^x) loses e^x below fp32's epsilon, an absolute error under 1.2e-7
-__device__ __forceinline__ float pro_log_decay(float x) {
-  const float sp = x > 20.f ? x : __logf(1.f + __expf(x));
-  return fmaxf(-sp, -14.f);
-}
 
 // Conv input of stream s, channel ch, at token t (t >= -3): the projection for t >= 0,
 // the carried history for t < 0 (zeros without one).
@@ -141,7 +130,7 @@ __global__ __launch_bounds__(512) void dgda_prologue_kernel(ProArgs a) {
       float ss = y[1][0] * y[1][0] + y[1][1] * y[1][1];
 #pragma unroll
       for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off);
-      const float kinv = __fdividef(1.f, sqrtf(ss) + a.eps);
+      const float kinv = pro_knorm_inv(ss, a.eps);
       const float la0 = pro_log_decay(xv[3].x), la1 = pro_log_decay(xv[3].y);
       Pair<QT>::st(a.y[0], b * a.ysb[0] + t * a.ysl[0] + c, y[0][0], y[0][1]);
       Pair<QT>::st(a.y[1], b * a.ysb[1] + t * a.ysl[1] + c, y[1][0] * kinv, y[1][1] * kinv);
@@ -204,7 +193,7 @@ __global__ __launch_bounds__(64) void dgda_prologue_step_kernel(ProArgs a) {
   float ss = y[1] * y[1];
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
-  const float kinv = __fdividef(1.f, sqrtf(ss) + a.eps);
+  const float kinv = pro_knorm_inv(ss, a.eps);
   const float la = pro_log_decay(x[3]);
   pro_st1<QT>(a.y[0], b * a.ysb[0] + c, y[0]);
   pro_st1<QT>(a.y[1], b * a.ysb[1] + c, y[1] * kinv);
@@ -233,6 +222,51 @@ static void pro_launch_g(const ProArgs& a, int gdt, dim3 grid, dim3 block, hipSt
     if (step) hipLaunchKernelGGL((dgda_prologue_step_kernel<XT, QT, uint16_t>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((dgda_prologue_kernel<XT, QT, uint16_t>), grid, block, 0, s, a);
   }
+}
+
+// New conv history of a prefill whose conv runs inside the DGDA kernels (the fused layer
+// prefill): the conv inputs of tokens L-3 .. L-1 per stream and channel, from the
+// projections or, for L < 3, the old history.  One thread per channel reads its three
+// inputs before writing, so the new history may overwrite the old one in place.
+template <class XT>
+__global__ __launch_bounds__(256) void dgda_history_kernel(ProArgs a, int C) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (c >= C) return;
+  float v[3][PRO_KH];
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+#pragma unroll
+    for (int j = 0; j < PRO_KH; ++j) v[s][j] = pro_input<XT>(a, s, b, c, a.L - PRO_KH + j);
+#pragma unroll
+  for (int s = 0; s < 3; ++s)
+#pragma unroll
+    for (int j = 0; j < PRO_KH; ++j)
+      store_elem(a.nh[s], a.nhdt, b * a.nhsb[s] + c * a.nhsc[s] + j * a.nhst[s], v[s][j]);
+}
+
+// Host side of the above for the fused layer prefill, whose entry point has validated the
+// shapes ([B,L,C] projections with unit channel stride, [B,C,3] histories).
+int launch_dgda_new_history(const maba_tensor* const* xs, const maba_tensor* const* hist,
+                            maba_tensor* const* new_hist, hipStream_t stream) {
+  const int64_t B = xs[0]->shape[0], L = xs[0]->shape[1], C = xs[0]->shape[2];
+  if (B == 0) return MABA_OK;
+  ProArgs a = {};
+  for (int s = 0; s < 3; ++s) {
+    a.x[s] = xs[s]->data; a.xsb[s] = xs[s]->stride[0]; a.xsl[s] = xs[s]->stride[1];
+    a.hist[s] = hist ? hist[s]->data : nullptr;
+    a.hsb[s] = hist ? hist[s]->stride[0] : 0; a.hsc[s] = hist ? hist[s]->stride[1] : 0;
+    a.hst[s] = hist ? hist[s]->stride[2] : 0;
+    a.nh[s] = new_hist[s]->data; a.nhsb[s] = new_hist[s]->stride[0]; a.nhsc[s] = new_hist[s]->stride[1];
+    a.nhst[s] = new_hist[s]->stride[2];
+  }
+  a.hdt = hist ? hist[0]->dtype : MABA_F32;
+  a.nhdt = new_hist[0]->dtype;
+  a.L = L;
+  const dim3 grid((unsigned)ceil_div(C, 256), (unsigned)B);
+  if (xs[0]->dtype == MABA_F32) hipLaunchKernelGGL(dgda_history_kernel<float>, grid, dim3(256), 0, stream, a, (int)C);
+  else hipLaunchKernelGGL(dgda_history_kernel<uint16_t>, grid, dim3(256), 0, stream, a, (int)C);
+  return check_launch("dgda_layer_prefill/history");
 }
 
 }  // namespace maba

@@ -25,6 +25,16 @@
 //
 // Sequence parallelism, passes and modes: as the chunked path in dgda_chunk.hip (slots
 // of U sub-chunks, aggregate [N | M] pass, zero-start and fix-up output passes).
+//
+// Fused layer prologue (PRO, maba_hip_dgda_layer_prefill; reference layers/dgda.py:103-121,
+// 186-207): the kernels read the layer's six bf16 projections instead of q, k, v and the
+// gates, and form the op inputs in the staging step: the causal depthwise conv (kernel 4)
+// + SiLU of q, k, v over [history, projections], the per-head L2 norm of k, the decay
+// max(-softplus, -14) and the sigmoid erase and write gates, all in fp32 and never
+// written back.  A stager lane loads the four conv taps of its token (tokens t-3 .. t,
+// the earlier three mostly L1 hits from its neighbours' loads).  The key norm sums the
+// 64 channels of a token over four waves: each stager wave leaves its partial sums in LDS
+// before the loop-top barrier and the staging after it adds them.
 #include "dgda_common.h"
 
 namespace maba {
@@ -51,6 +61,13 @@ struct SubArgs {
   int64_t U;       // sub-chunks per slot
   int H, L, BH, nseg_max, nchunks, use_log, has_s0;
   int mode;        // output kernel: SUB_ZERO or SUB_FIX
+  // fused prologue (PRO): the six bf16 projections [B, L, C] (q, k, v, decay, erase, write;
+  // unit channel stride, head h at channels 64h ..), conv taps [C, 1, 4] (f32/bf16), the
+  // bf16 conv history [B, C, 3] (null: zeros) and the key-norm eps
+  const uint16_t* px[6]; int pxs0[6], pxs1[6];
+  const void* cw[3]; int cwdt; int cwsc[3], cwst[3];
+  const uint16_t* ph[3]; int phs0[3], phs1[3], phs2[3];
+  float eps;
 };
 typedef const __attribute__((address_space(4))) SubArgs KSubArgs;
 
@@ -70,6 +87,8 @@ struct SubSmem {
   SM_ALIGN_SUB short Ah[AGG ? 8 : SC * TP], Al[AGG ? 8 : SC * TP];           // A (lower, with diagonal)
   SM_ALIGN_SUB float Lq[SC][4][4];                                            // L[i][p + 4 r] at [i][p][r]
   SM_ALIGN_SUB float elast[64];                                               // e^{Lam_15}
+  SM_ALIGN_SUB float nrm[2][4][16];   // fused prologue: |k|^2 partials [sub-chunk parity][stager wave][token]
+  SM_ALIGN_SUB float cw[3][4][64];    // fused prologue: the head's conv taps [stream][tap][channel]
   int big[2];                               // some |Lam| exceeds SUB_MFMA_RANGE (by sub-chunk parity)
 };
 
@@ -110,7 +129,7 @@ __device__ __forceinline__ float row16_incl_scan(float x) {
 }
 
 // One segment: sub-chunks [c_begin, c_end) of sequence bh, segment k of n.
-template <bool AGG, bool F32IN, bool OBF>
+template <bool AGG, bool F32IN, bool OBF, bool PRO>
 __device__ __forceinline__ void sub_segment(KSubArgs& a, SubSmem<AGG>& sm, int* s_mzero, int tid,
                                             int bh, int k, int n, int c_begin, int c_end) {
   const int wave = tid >> 6, lane = tid & 63;
@@ -177,9 +196,42 @@ __device__ __forceinline__ void sub_segment(KSubArgs& a, SubSmem<AGG>& sm, int* 
   const int st = tid & 15, c4 = (tid >> 4) * 4;
   Raw4<F32IN> pq = {}, pk = {}, pv = {};
   f32x4 pg = {}, pb = {}, pw = {};
+  // fused prologue: conv taps of tokens t-3 .. t (bf16 bits; taps before token 0 are
+  // loaded at token 0 and replaced by the history in the first sub-chunk), the gate
+  // projections and SiLU(conv k) of the staged token.  The head's conv weights go to LDS
+  // once per segment (the previous segment's last reads of them were before its last
+  // post-staging barrier).
+  i16x4 tq[4] = {}, tk[4] = {}, tv[4] = {}, xg[3] = {};
+  f32x4 kc = {};
+  const int ch = hi * 64 + c4;   // the stager's first channel of the projection rows
+  if (PRO) {
+    for (int i = tid; i < 3 * 4 * 64; i += blockDim.x) {
+      const int s = i >> 8, j = (i >> 6) & 3, cl = i & 63;
+      sm.cw[s][j][cl] = load_elem(a.cw[s], a.cwdt, (int64_t)(hi * 64 + cl) * a.cwsc[s] + j * a.cwst[s]);
+    }
+    lds_barrier();
+  }
+  // row tr + st of projection s at the stager's channels: a uniform base pointer plus a
+  // 32-bit lane offset, clamped to row 0 (rows before token 0 are replaced by the history)
+  auto prow = [&](int s, int tr) {
+    const uint16_t* base = a.px[s] + (int64_t)bi * a.pxs0[s];
+    return *(const i16x4*)(base + max(st * a.pxs1[s] + ch + tr * a.pxs1[s], ch));
+  };
   auto prefetch = [&](int cc) {
     const int tok = cc * SC + st;
     if (!stager || tok >= a.L) return;
+    if constexpr (PRO) {
+      const int t0 = cc * SC;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (!AGG) tq[j] = prow(0, t0 - 3 + j);
+        tk[j] = prow(1, t0 - 3 + j);
+        tv[j] = prow(2, t0 - 3 + j);
+      }
+#pragma unroll
+      for (int s = 0; s < 3; ++s) xg[s] = prow(3 + s, t0);
+      return;
+    }
     pk = load_raw4<F32IN>(a.k, kb + (int64_t)tok * a.ks2 + c4);
     pv = load_raw4<F32IN>(a.vp, vb + (int64_t)tok * a.vs2 + c4);
     if (!AGG) pq = load_raw4<F32IN>(a.q, qb + (int64_t)tok * a.qs2 + c4);
@@ -206,6 +258,53 @@ __device__ __forceinline__ void sub_segment(KSubArgs& a, SubSmem<AGG>& sm, int* 
       }
     }
   };
+  // fused prologue: SiLU(depthwise conv) of the stager's four channels of stream s from
+  // the taps (oldest first)
+  auto conv4 = [&](int s, const i16x4 (&t)[4]) {
+    f32x4 w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = *(const f32x4*)&sm.cw[s][j][c4];
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float acc = w[3][e] * bf16_val(t[3][e]);
+      acc = fmaf(w[2][e], bf16_val(t[2][e]), acc);
+      acc = fmaf(w[1][e], bf16_val(t[1][e]), acc);
+      acc = fmaf(w[0][e], bf16_val(t[0][e]), acc);
+      y[e] = pro_silu(acc);
+    }
+    return y;
+  };
+  // taps before token 0 (first sub-chunk of the sequence) come from the history, or are zero
+  auto hist_taps = [&](int s, i16x4 (&t)[4]) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      if (st - 3 + j >= 0) continue;
+      i16x4 h = {0, 0, 0, 0};
+      if (a.ph[s]) {
+        const uint16_t* hp = a.ph[s] + (int64_t)bi * a.phs0[s] + (int64_t)ch * a.phs1[s] + (int64_t)(st + j) * a.phs2[s];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = (short)hp[(int64_t)e * a.phs1[s]];
+      }
+      t[j] = h;
+    }
+  };
+  // before the loop-top barrier of sub-chunk cc: SiLU(conv k) of the prefetched taps and the
+  // wave's |k|^2 partial per token (lanes 16 m + st hold channel groups 4 wave + m of token st)
+  auto pre_norm = [&](int cc) {
+    if (!PRO || !stager) return;
+    if (cc == 0) {
+      if (!AGG) hist_taps(0, tq);
+      hist_taps(1, tk);
+      hist_taps(2, tv);
+    }
+    kc = conv4(1, tk);
+    float ss = kc[0] * kc[0] + kc[1] * kc[1] + kc[2] * kc[2] + kc[3] * kc[3];
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    if (lane < 16) sm.nrm[cc & 1][wave][lane] = ss;
+  };
+
   bool idle = false;                     // aggregate pass, M waves: the slab is exactly zero
   if (AGG && tid < 4) s_mzero[tid] = 0;
   if (tid == 0) sm.big[c_begin & 1] = 0;   // read after the first loop-top barrier
@@ -214,6 +313,7 @@ __device__ __forceinline__ void sub_segment(KSubArgs& a, SubSmem<AGG>& sm, int* 
   for (int c = c_begin; c < c_end; ++c) {
     const int t0 = c * SC;
     const int nt = min(SC, a.L - t0);
+    pre_norm(c);
     lds_barrier();   // the previous sub-chunk is done with the shared buffers
     if (AGG && s_mzero[0] && s_mzero[1] && s_mzero[2] && s_mzero[3]) {  // workgroup-uniform
       c_stop = c;
@@ -225,8 +325,22 @@ __device__ __forceinline__ void sub_segment(KSubArgs& a, SubSmem<AGG>& sm, int* 
     if (stager) {
       const bool on = st < nt;
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-      const f32x4 rk = raw_f32<F32IN>(pk), rv = raw_f32<F32IN>(pv), rq = AGG ? z : raw_f32<F32IN>(pq);
-      const f32x4 rg = pg, rb = pb, rw = pw;
+      f32x4 rk, rv, rq, rg, rb, rw;
+      if constexpr (PRO) {
+        const float n2 = (sm.nrm[c & 1][0][st] + sm.nrm[c & 1][1][st]) + (sm.nrm[c & 1][2][st] + sm.nrm[c & 1][3][st]);
+        rk = kc * pro_knorm_inv(n2, a.eps);
+        rv = conv4(2, tv);
+        rq = AGG ? z : conv4(0, tq);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          rg[i] = pro_log_decay(bf16_val(xg[0][i]));
+          rb[i] = pro_sigmoid(bf16_val(xg[1][i]));
+          rw[i] = pro_sigmoid(bf16_val(xg[2][i]));
+        }
+      } else {
+        rk = raw_f32<F32IN>(pk); rv = raw_f32<F32IN>(pv); rq = AGG ? z : raw_f32<F32IN>(pq);
+        rg = pg; rb = pb; rw = pw;
+      }
       const f32x4 kk = on ? rk : z;
       f32x4 la, bk, wv, lam, l15;
       float mx = 0.f;
@@ -457,7 +571,7 @@ __device__ __forceinline__ void sub_segment(KSubArgs& a, SubSmem<AGG>& sm, int* 
   }
 }
 
-template <bool AGG, bool F32IN, bool OBF>
+template <bool AGG, bool F32IN, bool OBF, bool PRO>
 __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_sub_kernel(SubArgs a) {
   __shared__ SubSmem<AGG> sm;
   __shared__ int s_mzero[4];
@@ -493,7 +607,7 @@ __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_sub_kernel(
     asm volatile("" : "+v"(tid));
     KSubArgs* ap = (KSubArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(ap));
-    sub_segment<AGG, F32IN, OBF>(*ap, sm, s_mzero, tid, bh, k, n, c0, c1);
+    sub_segment<AGG, F32IN, OBF, PRO>(*ap, sm, s_mzero, tid, bh, k, n, c0, c1);
   }
 }
 
@@ -546,13 +660,16 @@ size_t dgda_sub_workspace(int64_t BH, int64_t L) {
   return (size_t)(BH * nseg * 64 * 128) * sizeof(float) + (size_t)(BH * nseg) * sizeof(int);
 }
 
+template <bool PRO>
+static int run_sub_passes(SubArgs& a, bool f32in, bool obf, hipStream_t stream);
+
 int launch_dgda_sub(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                     const maba_tensor* gate, int use_log, const maba_tensor* b,
                     const maba_tensor* w, const maba_tensor* s0, maba_tensor* out,
                     maba_tensor* sf, void* ws, size_t ws_bytes, hipStream_t stream) {
   const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2];
   const int64_t BH = B * H;
-  SubArgs a;
+  SubArgs a = {};
   // strides fit in int32 (dgda_sub_supported checks every operand)
   a.q = q->data; a.qs0 = (int)q->stride[0]; a.qs1 = (int)q->stride[1]; a.qs2 = (int)q->stride[2];
   a.k = k->data; a.ks0 = (int)k->stride[0]; a.ks1 = (int)k->stride[1]; a.ks2 = (int)k->stride[2];
@@ -577,14 +694,26 @@ int launch_dgda_sub(const maba_tensor* q, const maba_tensor* k, const maba_tenso
   const int64_t nsegs = BH * a.nseg_max;
   a.agg = (float*)ws;
   a.zc = (int*)(a.agg + nsegs * 64 * 128);
-  const bool f32in = q->dtype == MABA_F32, obf = out->dtype == MABA_BF16;
+  return run_sub_passes<false>(a, q->dtype == MABA_F32, out->dtype == MABA_BF16, stream);
+}
+
+// Workspace slots, then the aggregate, zero-start and fix-up passes (one zero-start pass
+// when every sequence fits one slot).  PRO: the fused-prologue inputs (bf16 projections).
+template <bool PRO>
+static int run_sub_passes(SubArgs& a, bool f32in, bool obf, hipStream_t stream) {
   auto launch_out = [&](int mode) {
     a.mode = mode;
-    const dim3 grid(mode == SUB_ZERO ? (unsigned)ceil_div(BH * a.nchunks, a.U) : (unsigned)(BH * (a.nseg_max - 1)));
-    if (f32in && obf) hipLaunchKernelGGL((dgda_sub_kernel<false, true, true>), grid, dim3(256), 0, stream, a);
-    else if (f32in) hipLaunchKernelGGL((dgda_sub_kernel<false, true, false>), grid, dim3(256), 0, stream, a);
-    else if (obf) hipLaunchKernelGGL((dgda_sub_kernel<false, false, true>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((dgda_sub_kernel<false, false, false>), grid, dim3(256), 0, stream, a);
+    const dim3 grid(mode == SUB_ZERO ? (unsigned)ceil_div((int64_t)a.BH * a.nchunks, a.U)
+                                     : (unsigned)(a.BH * (a.nseg_max - 1)));
+    if constexpr (PRO) {
+      if (obf) hipLaunchKernelGGL((dgda_sub_kernel<false, false, true, true>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((dgda_sub_kernel<false, false, false, true>), grid, dim3(256), 0, stream, a);
+    } else {
+      if (f32in && obf) hipLaunchKernelGGL((dgda_sub_kernel<false, true, true, false>), grid, dim3(256), 0, stream, a);
+      else if (f32in) hipLaunchKernelGGL((dgda_sub_kernel<false, true, false, false>), grid, dim3(256), 0, stream, a);
+      else if (obf) hipLaunchKernelGGL((dgda_sub_kernel<false, false, true, false>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((dgda_sub_kernel<false, false, false, false>), grid, dim3(256), 0, stream, a);
+    }
     return check_launch("dgda_prefill/sub-chunk output");
   };
   if (a.nseg_max == 1) {
@@ -592,9 +721,10 @@ int launch_dgda_sub(const maba_tensor* q, const maba_tensor* k, const maba_tenso
     return launch_out(SUB_ZERO);
   }
   a.mode = SUB_ZERO;
-  const dim3 agrid((unsigned)(BH * (a.nseg_max - 1)));
-  if (f32in) hipLaunchKernelGGL((dgda_sub_kernel<true, true, true>), agrid, dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((dgda_sub_kernel<true, false, true>), agrid, dim3(512), 0, stream, a);
+  const dim3 agrid((unsigned)(a.BH * (a.nseg_max - 1)));
+  if constexpr (PRO) hipLaunchKernelGGL((dgda_sub_kernel<true, false, true, true>), agrid, dim3(512), 0, stream, a);
+  else if (f32in) hipLaunchKernelGGL((dgda_sub_kernel<true, true, true, false>), agrid, dim3(512), 0, stream, a);
+  else hipLaunchKernelGGL((dgda_sub_kernel<true, false, true, false>), agrid, dim3(512), 0, stream, a);
   int rc = check_launch("dgda_prefill/sub-chunk aggregate");
   if (rc) return rc;
   if ((rc = launch_out(SUB_ZERO))) return rc;
@@ -602,3 +732,89 @@ int launch_dgda_sub(const maba_tensor* q, const maba_tensor* k, const maba_tenso
 }
 
 }  // namespace maba
+
+using namespace maba;
+
+extern "C" size_t maba_hip_dgda_layer_prefill_workspace_size(int64_t B, int64_t H, int64_t L) {
+  return dgda_sub_workspace(B * H, L);
+}
+
+extern "C" int maba_hip_dgda_layer_prefill(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
+                                           const maba_tensor* const* hist, float eps,
+                                           const maba_tensor* initial_state, maba_tensor* out,
+                                           maba_tensor* final_state, maba_tensor* const* new_hist, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  if (!xs || !conv_w || !new_hist || !out || !final_state)
+    return fail(MABA_ERR_INVALID, "dgda_layer_prefill: null argument");
+  for (int s = 0; s < 6; ++s)
+    if (!xs[s] || xs[s]->ndim != 3) return fail(MABA_ERR_INVALID, "dgda_layer_prefill: projection %d must be [B,L,C]", s);
+  const int64_t B = xs[0]->shape[0], L = xs[0]->shape[1], C = xs[0]->shape[2];
+  if (C % 64 != 0 || C == 0) return fail(MABA_ERR_UNSUPPORTED, "dgda_layer_prefill: C must be 64 * H");
+  if (L < 1) return fail(MABA_ERR_INVALID, "dgda_layer_prefill: at least one token");
+  if (L > ((int64_t)1 << 30)) return fail(MABA_ERR_UNSUPPORTED, "dgda_layer_prefill: L too large");
+  const int64_t H = C / 64, BH = B * H;
+  for (int s = 0; s < 6; ++s) {
+    const maba_tensor* t = xs[s];
+    if (t->shape[0] != B || t->shape[1] != L || t->shape[2] != C || t->dtype != MABA_BF16 || t->stride[2] != 1 ||
+        ((uintptr_t)t->data & 7) || t->stride[0] % 4 || t->stride[1] % 4 || !fits32s(t))
+      return fail(MABA_ERR_UNSUPPORTED, "dgda_layer_prefill: projections must be bf16 [B,L,C], unit channel "
+                  "stride, 8-byte aligned rows");
+    // the kernels address a sequence's rows with 32-bit offsets
+    if ((L + SC) * t->stride[1] + C > INT32_MAX)
+      return fail(MABA_ERR_UNSUPPORTED, "dgda_layer_prefill: L * row stride must stay below 2^31 elements");
+  }
+  const int64_t sw[3] = {C, 1, 4}, sh[3] = {B, C, 3};
+  for (int s = 0; s < 3; ++s) {
+    if (!expect_shape(conv_w[s], "conv weight", 3, sw) || !expect_float(conv_w[s], "conv weight"))
+      return MABA_ERR_INVALID;
+    if (conv_w[s]->dtype != conv_w[0]->dtype) return fail(MABA_ERR_DTYPE, "dgda_layer_prefill: conv weights differ in dtype");
+    if (!fits32s(conv_w[s])) return fail(MABA_ERR_UNSUPPORTED, "dgda_layer_prefill: conv weight strides");
+    if (hist) {
+      if (!expect_shape(hist[s], "conv history", 3, sh)) return MABA_ERR_INVALID;
+      if (hist[s]->dtype != MABA_BF16 || !fits32s(hist[s]))
+        return fail(MABA_ERR_DTYPE, "dgda_layer_prefill: the conv history must be bf16");
+    }
+    if (!expect_shape(new_hist[s], "new conv history", 3, sh) || !expect_float(new_hist[s], "new conv history"))
+      return MABA_ERR_INVALID;
+  }
+  const int64_t so[4] = {B, H, L, 64}, ss[4] = {B, H, 64, 64};
+  if (!expect_shape(out, "out", 4, so) || !expect_shape(final_state, "final_state", 4, ss)) return MABA_ERR_INVALID;
+  if (out->stride[3] != 1 || !fits32s(out) || (out->dtype != MABA_BF16 && out->dtype != MABA_F32))
+    return fail(MABA_ERR_UNSUPPORTED, "dgda_layer_prefill: out must be f32/bf16 with unit channel stride");
+  if (!expect_float(final_state, "final_state")) return MABA_ERR_DTYPE;
+  if (initial_state && (!expect_shape(initial_state, "initial_state", 4, ss) || !expect_float(initial_state, "initial_state")))
+    return MABA_ERR_INVALID;
+  const size_t need = dgda_sub_workspace(BH, L);
+  if (!workspace || workspace_bytes < need)
+    return fail(MABA_ERR_WORKSPACE, "dgda_layer_prefill: workspace of %zu bytes required", need);
+  if (B == 0) return MABA_OK;
+  SubArgs a = {};
+  for (int s = 0; s < 6; ++s) {
+    a.px[s] = (const uint16_t*)xs[s]->data; a.pxs0[s] = (int)xs[s]->stride[0]; a.pxs1[s] = (int)xs[s]->stride[1];
+  }
+  a.cwdt = conv_w[0]->dtype;
+  for (int s = 0; s < 3; ++s) {
+    a.cw[s] = conv_w[s]->data; a.cwsc[s] = (int)conv_w[s]->stride[0]; a.cwst[s] = (int)conv_w[s]->stride[2];
+    a.ph[s] = hist ? (const uint16_t*)hist[s]->data : nullptr;
+    a.phs0[s] = hist ? (int)hist[s]->stride[0] : 0; a.phs1[s] = hist ? (int)hist[s]->stride[1] : 0;
+    a.phs2[s] = hist ? (int)hist[s]->stride[2] : 0;
+  }
+  a.eps = eps;
+  a.s0 = view4(initial_state);
+  a.op = out->data; a.os0 = (int)out->stride[0]; a.os1 = (int)out->stride[1]; a.os2 = (int)out->stride[2];
+  a.sf = mview4(final_state);
+  a.H = (int)H; a.L = (int)L; a.BH = (int)BH;
+  a.nchunks = (int)ceil_div(L, SC);
+  const SlotGeom gm = sub_geom(BH, L);
+  a.U = gm.U;
+  a.nseg_max = gm.nseg_max;
+  a.use_log = 1; a.has_s0 = initial_state != nullptr;
+  const int64_t nsegs = BH * a.nseg_max;
+  a.agg = (float*)workspace;
+  a.zc = (int*)(a.agg + nsegs * 64 * 128);
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = run_sub_passes<true>(a, false, out->dtype == MABA_BF16, st);
+  if (rc) return rc;
+  // after the passes, which read the old history: the new one may overwrite it in place
+  return launch_dgda_new_history(xs, hist, new_hist, st);
+}

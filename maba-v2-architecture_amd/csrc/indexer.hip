@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void index_decode_score_kernel(DecArgs a) {
           if (h < Hq) acc[h] = fmaf(s_q[h * IDX_MAX_D + c], x, acc[h]);
       }
     }
-    const float pen = valid ? a.lam * log1pf((float)(a.nb - 1 - n)) : 0.f;
+    const float pen = valid ? a.lam * fast_log(1.f + (float)(a.nb - 1 - n)) : 0.f;
     if (__ballot(valid) == 0ull) break;
 #pragma unroll
     for (int h = 0; h < IDX_MAX_HEADS; ++h) {
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256) void index_decode_tile_kernel(DecTileArgs a) {
       float sc = -INFINITY;
       if (n < nb) {
         // log1p(m) = log(1 + m) with 1 + m exact for integer block distances m < 2^24
-        sc = acc[i] * a.scale - a.lam * __logf(1.f + (float)(nb - 1 - n));
+        sc = acc[i] * a.scale - a.lam * fast_log(1.f + (float)(nb - 1 - n));
         best = kmax(best, make_key(sc, (uint32_t)n));
         if (hv && a.scores) a.scores[bi * a.ssb + c16 * a.ssh + n * a.ssn] = sc;
       }
@@ -465,7 +465,7 @@ __global__ __launch_bounds__(256) void index_prefill_mfma_kernel(PreMfmaArgs a) 
       for (int j = 0; j < 4 && r0 - j >= 0; ++j) {
         const int64_t n = (int64_t)(r0 - j) * 64 + lane;
         key64 key = KEY_NONE;
-        if (n < nv) key = make_key(s_sc[j][4 * wave + r][lane] - a.lam * log1pf((float)(qblk - n)), (uint32_t)n);
+        if (n < nv) key = make_key(s_sc[j][4 * wave + r][lane] - a.lam * fast_log(1.f + (float)(qblk - n)), (uint32_t)n);
         list[r] = wave_merge_topk(list[r], key, a.K);
       }
     }
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(256) void index_prefill_kernel(PreArgs a) {
       float acc = 0.f;
       const int64_t cb = bi * a.csb + n * a.csn;
       for (int64_t c = 0; c < a.d; ++c) acc = fmaf(s_q[wave][c], load_elem(a.c, a.cdt, cb + c * a.csd), acc);
-      s = acc - a.lam * log1pf((float)(qblk - n));
+      s = acc - a.lam * fast_log(1.f + (float)(qblk - n));
     }
     if (a.scores && n < a.nb) store_elem(a.scores, a.sdt, bi * a.ssb + t * a.ssl + n * a.ssn, s);
     if (n0 < nvalid) list = wave_merge_topk(list, n < nvalid ? make_key(s, (uint32_t)n) : KEY_NONE, a.K);

@@ -28,6 +28,15 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
 
+// Hardware transcendentals (v_exp_f32, v_log_f32, v_rcp_f32, v_sqrt_f32: about one ulp,
+// without the IEEE division sequence or the denormal range scaling of the library forms,
+// which cost several times more instructions).  Results that leave fp32's normal range
+// saturate (exp to 0 or inf, rcp(inf) = 0); the log is taken of arguments >= 1 here.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float fast_log(float x) { return __builtin_amdgcn_logf(x) * 0.6931471805599453f; }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_sqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+
 // Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);

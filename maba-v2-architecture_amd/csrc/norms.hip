@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
     const int j = (int)(e - r * np);
     const float2 g = P2<T>::ld(a.gu, r * a.gus + 2 * j);
     const float2 u = P2<T>::ld(a.gu, r * a.gus + a.I + 2 * j);
-    const float s0 = __fdividef(g.x, 1.f + __expf(-g.x)), s1 = __fdividef(g.y, 1.f + __expf(-g.y));
+    const float s0 = g.x * fast_rcp(1.f + fast_exp(-g.x)), s1 = g.y * fast_rcp(1.f + fast_exp(-g.y));
     P2<T>::st(a.out, r * a.os + 2 * j, make_float2(s0 * u.x, s1 * u.y));
   }
 }

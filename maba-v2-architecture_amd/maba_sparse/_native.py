@@ -55,6 +55,8 @@ EXPORTED_SYMBOLS = (
     "maba_hip_rmsnorm",
     "maba_hip_swiglu",
     "maba_hip_maba_sa_prefill_latent",
+    "maba_hip_dgda_layer_prefill_workspace_size",
+    "maba_hip_dgda_layer_prefill",
 )
 
 
@@ -104,6 +106,8 @@ def _declare(lib) -> None:
         "maba_hip_rmsnorm": ([T, T, T, T, f, T, T, vp], i),
         "maba_hip_swiglu": ([T, T, vp], i),
         "maba_hip_maba_sa_prefill_latent": ([T, T, T, T, T, f, i, i, i, i, T, vp], i),
+        "maba_hip_dgda_layer_prefill_workspace_size": ([i64, i64, i64], sz),
+        "maba_hip_dgda_layer_prefill": ([TA, TA, TA, f, T, T, T, TA, vp, sz, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

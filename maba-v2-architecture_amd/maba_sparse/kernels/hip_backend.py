@@ -390,3 +390,30 @@ def hip_maba_sa_prefill_latent(q_lat, c_kv, hca, idx, gate_logits, scale: float,
                                                   int(block_size), int(pool), N.desc(out), N.stream_ptr(dev))
     N.check(rc, "maba_sa_prefill_latent")
     return out
+
+
+def hip_dgda_layer_prefill(projections, conv_weights, history=None, eps: float = 1e-6, initial_state=None,
+                           out=None, out_history=None, state_dtype: Optional[torch.dtype] = None):
+    """The DGDA layer prefill with its prologue fused into the kernels' staging
+    (layers/dgda.py:103-121, 186-233): from the six bf16 projections ``[B, L, C]`` straight to
+    the head outputs and the final state, q/k/v and the gates never stored.  Returns ``(o
+    [B, L, C] bf16, final state [B, H, 64, 64], new conv history (3 x [B, C, 3]))``; ``out``
+    may be a preallocated ``[B, L, C]`` buffer, ``out_history`` the new history's buffers."""
+    _no_grad_needed("dgda_layer_prefill", *projections, *conv_weights, *(history or ()), initial_state)
+    dev = N.require_device([*projections, *conv_weights, *(history or ()), initial_state], "dgda_layer_prefill")
+    B, L, C = projections[0].shape
+    H = C // 64
+    if out is None:
+        out = torch.empty(B, L, C, dtype=projections[0].dtype, device=dev)
+    state = torch.empty(B, H, 64, 64, dtype=state_dtype or projections[0].dtype, device=dev)
+    nh = list(out_history) if out_history is not None else \
+        list(torch.empty(3, B, C, 3, dtype=projections[0].dtype, device=dev).unbind(0))
+    lib = N.load()
+    ws = _workspace(lib.maba_hip_dgda_layer_prefill_workspace_size(B, H, L), dev)
+    o4 = out.view(B, L, H, 64).transpose(1, 2)   # the kernel's [B, H, L, 64] view of the [B, L, C] rows
+    rc = lib.maba_hip_dgda_layer_prefill(N.desc_array(projections), N.desc_array(conv_weights),
+                                         N.desc_array(history) if history is not None else None, float(eps),
+                                         N.desc(initial_state), N.desc(o4), N.desc(state), N.desc_array(nh),
+                                         ws.data_ptr(), ws.numel(), N.stream_ptr(dev))
+    N.check(rc, "dgda_layer_prefill")
+    return out, state, tuple(nh)

@@ -65,6 +65,9 @@ class DGDALayer(WeightCacheMixin, nn.Module):
         self.chunk_size = _cfg(config, ("chunk_size",), 16)
         self.inversion_method = _cfg(config, ("inversion_method",), "adaptive")
         self.adaptive_tol = _cfg(config, ("adaptive_tol",), 7e-5)
+        # bf16 prefill on the HIP backend: the prologue runs inside the recurrence kernels
+        # (False: the one-pass prologue kernel, then the op on its stored outputs)
+        self.fuse_prologue = True
 
         qk, vd = self.n_heads * self.d_k, self.n_heads * self.d_v
         lin = lambda i, o: nn.Linear(i, o, bias=False)  # noqa: E731
@@ -141,6 +144,33 @@ class DGDALayer(WeightCacheMixin, nn.Module):
             return False
         return not (torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())))
 
+    def _projections(self, x: torch.Tensor, hists):
+        """One GEMM for the six projections (``[B, L, C]`` views, row stride 6C) and the carried
+        conv history cut or zero-padded to ``kernel_size - 1`` taps (None without one)."""
+        C = self.n_heads * self.d_k
+        ws = [m.weight for m in (self.q_proj, self.k_proj, self.v_proj, self.gate_alpha, self.gate_erase,
+                                 self.gate_write)]
+        # restacked only after a weight changes (one stack per input dtype)
+        w6 = cached(self, f"w6_{x.dtype}", ws, lambda: torch.cat(ws, dim=0).to(x.dtype))
+        projs = F.linear(x, w6).split(C, dim=-1)
+        kh = self.kernel_size - 1
+        hist = None
+        if hists[0] is not None:
+            fit = lambda h: F.pad(h, (kh - h.shape[-1], 0)) if h.shape[-1] < kh else h[..., h.shape[-1] - kh:]  # noqa: E731
+            hist = tuple(fit(h) for h in hists)
+        return projs, hist
+
+    def _fused_forward(self, x: torch.Tensor, state, hists):
+        """The bf16 prefill with the prologue fused into the recurrence kernels' staging: the
+        six projections go straight to the head outputs, q/k/v and the gates are never
+        stored (one GEMM, the HIP passes, ``o_proj``)."""
+        from maba_sparse.kernels import hip_backend as hb
+        projs, hist = self._projections(x, hists)
+        convs = (self.conv_q.weight, self.conv_k.weight, self.conv_v.weight)
+        s0 = state.to(x.dtype) if state is not None else None
+        o, S, nh = hb.hip_dgda_layer_prefill(projs, convs, hist, eps=self.eps, initial_state=s0)
+        return self.o_proj(o), S, ConvState(nh)
+
     def _fused_op_inputs(self, x: torch.Tensor, state, hists):
         """One GEMM for the six projections, then the HIP prologue (conv + SiLU, gates, key
         norm) in one pass.  Gates come out in fp32 (the chunked kernels' gate format, more
@@ -148,17 +178,7 @@ class DGDALayer(WeightCacheMixin, nn.Module):
         ``allow_mixed_dtypes``."""
         B, L, _ = x.shape
         H, dk = self.n_heads, self.d_k
-        C = H * dk
-        ws = [m.weight for m in (self.q_proj, self.k_proj, self.v_proj, self.gate_alpha, self.gate_erase,
-                                 self.gate_write)]
-        # restacked only after a weight changes (one stack per input dtype)
-        w6 = cached(self, f"w6_{x.dtype}", ws, lambda: torch.cat(ws, dim=0).to(x.dtype))
-        projs = F.linear(x, w6).split(C, dim=-1)   # [B, L, C] views, row stride 6C
-        kh = self.kernel_size - 1
-        hist = None
-        if hists[0] is not None:
-            fit = lambda h: F.pad(h, (kh - h.shape[-1], 0)) if h.shape[-1] < kh else h[..., h.shape[-1] - kh:]  # noqa: E731
-            hist = tuple(fit(h) for h in hists)
+        projs, hist = self._projections(x, hists)
         q, k, v, la, _, b, w, nh = dispatch_dgda_prologue(
             projs, (self.conv_q.weight, self.conv_k.weight, self.conv_v.weight), hist, n_heads=H, eps=self.eps,
             gate_dtype=torch.float32, with_alpha=False)
@@ -209,6 +229,10 @@ class DGDALayer(WeightCacheMixin, nn.Module):
             zv = torch.zeros(B, H * dv, kh, dtype=x.dtype, device=x.device)
             st = state.clone() if state is not None else torch.zeros(B, H, dk, dv, dtype=x.dtype, device=x.device)
             return torch.empty(B, 0, D, dtype=x.dtype, device=x.device), st, ConvState((zq, zq, zv))
+        if self._prologue_fusable(x) and x.dtype == torch.bfloat16 and self.fuse_prologue:
+            hists = self._split_conv_state(conv_state, B, x.device, x.dtype)
+            if hists[0] is None or all(h.dtype == torch.bfloat16 for h in hists):
+                return self._fused_forward(x, state, hists)
         args, state, ncs = self._op_inputs(x, state, conv_state)
         o, S = dispatch_dgda_prefill(
             **args,

@@ -1,5 +1,7 @@
 """The DGDA layer prologue kernel (conv + SiLU with carried history, gates, key norm)
-against the float64 oracle (``oracle.dgda.layer_prologue``) on seeded inputs.
+against the float64 oracle (``oracle.dgda.layer_prologue``) on seeded inputs, and the
+layer prefill with the prologue fused into the recurrence kernels against the float64
+prologue composed with the float64 token recurrence (``oracle.dgda.dgda_prefill_seq``).
 
 Tolerances: fp32 outputs rtol 1e-5 / atol 1e-6 (fp32 arithmetic against float64);
 bf16 outputs rtol 5e-3 / atol 1e-6 (one rounding to bf16: at most half an ulp, 2^-8
@@ -86,3 +88,100 @@ def test_dgda_prologue_empty_and_fp32_history(dev):
     assert_close(res[3], exp[3], 1e-5, 1e-6, "log_alpha")
     for i in range(3):
         assert torch.equal(res[7][i].cpu(), torch.from_numpy(exp[7][i]).float()), i
+
+
+# ---------------------------------------------------------------- the fused layer prefill
+
+def _fused_case(B, L, H, seed, with_hist, with_state, slow):
+    C = 64 * H
+    g = torch.Generator().manual_seed(seed)
+    xs = [torch.randn(B, L, C, generator=g).bfloat16() for _ in range(6)]
+    if slow:   # decay projections far below zero: log alpha ~ -e^{x}, a long memory
+        xs[3] = (torch.randn(B, L, C, generator=g) - 6.0).bfloat16()
+    ws = [torch.randn(C, 1, 4, generator=g) * 0.4 for _ in range(3)]
+    hist = [torch.randn(B, C, 3, generator=g).bfloat16() for _ in range(3)] if with_hist else None
+    s0 = torch.randn(B, H, 64, 64, generator=g) * 0.1 if with_state else None
+    return xs, ws, hist, s0
+
+
+def _fused_oracle(xs, ws, hist, s0, H, eps=1e-6):
+    """The float64 prologue, then the float64 token recurrence on its outputs."""
+    B, L, C = xs[0].shape
+    q, k, v, la, _, b, w, nh = od.layer_prologue(*[to_np(x) for x in xs], *[to_np(c[:, 0]) for c in ws],
+                                                 hist=[to_np(h) for h in hist] if hist else None, n_heads=H, eps=eps)
+    heads = lambda t: t.reshape(B, L, H, 64).transpose(0, 2, 1, 3)  # noqa: E731
+    eo, eS = od.dgda_prefill_seq(heads(q), heads(k), heads(v), b=heads(b), w=heads(w),
+                                    initial_state=to_np(s0) if s0 is not None else None, log_alpha=heads(la))
+    return eo.transpose(0, 2, 1, 3).reshape(B, L, C), eS, nh
+
+
+@pytest.mark.parametrize("B,L,H,with_hist,with_state,slow", [
+    (2, 1, 2, True, True, False),       # one token: its three earlier taps from the history
+    (1, 2, 2, True, False, False),      # L < 3: the new history keeps the old one's tail
+    (2, 37, 3, False, True, False),     # ragged last sub-chunk, zero history
+    (1, 1500, 2, True, True, True),     # slow decay: the state reaches across sub-chunks
+    (2, 2500, 10, True, False, False),  # the layer's head count
+])
+def test_dgda_layer_prefill_fused_vs_oracle(dev, B, L, H, with_hist, with_state, slow):
+    """Rtol = atol = 2e-3 on the fp32 outputs and the final state (the north-star DGDA bar,
+    bf16 inputs with fp32 accumulation); the new history is a copy of inputs: exact."""
+    xs, ws, hist, s0 = _fused_case(B, L, H, L * 13 + H, with_hist, with_state, slow)
+    d = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    projs = torch.cat(xs, dim=-1).to(dev).split(64 * H, dim=-1)   # views of one GEMM output, row stride 6C
+    out = torch.empty(B, L, 64 * H, device=dev)
+    o, S, nh = _hip().hip_dgda_layer_prefill(projs, [d(w) for w in ws], [d(h) for h in hist] if hist else None,
+                                             eps=1e-6, initial_state=d(s0), out=out, state_dtype=torch.float32)
+    eo, eS, enh = _fused_oracle(xs, ws, hist, s0, H)
+    assert o.data_ptr() == out.data_ptr()
+    assert_close(o, eo, 2e-3, 2e-3, f"out L={L}")
+    assert_close(S, eS, 2e-3, 2e-3, f"state L={L}")
+    for i in range(3):
+        assert torch.equal(nh[i].cpu().float(), torch.from_numpy(enh[i]).float()), f"history {i}"
+
+
+def test_dgda_layer_prefill_fused_split_and_bf16_out(dev):
+    """A prefill cut in two, the state and the conv history carried (the history rewritten in
+    place), equals one pass; the bf16 output is the rounding of the fp32 one."""
+    B, L, H = 2, 700, 4
+    xs, ws, _, _ = _fused_case(B, L, H, 3, False, False, True)
+    projs = torch.cat(xs, dim=-1).to(dev).split(64 * H, dim=-1)
+    wd = [w.to(dev) for w in ws]
+    hb = _hip()
+    out = torch.empty(B, L, 64 * H, device=dev)
+    o, S, nh = hb.hip_dgda_layer_prefill(projs, wd, None, out=out, state_dtype=torch.float32)
+    cut = 301
+    o1, S1, nh1 = hb.hip_dgda_layer_prefill([p[:, :cut] for p in projs], wd, None, state_dtype=torch.float32,
+                                            out=torch.empty(B, cut, 64 * H, device=dev))
+    o2, S2, nh2 = hb.hip_dgda_layer_prefill([p[:, cut:] for p in projs], wd, nh1, initial_state=S1,
+                                            out_history=nh1, state_dtype=torch.float32,
+                                            out=torch.empty(B, L - cut, 64 * H, device=dev))
+    assert nh2[0].data_ptr() == nh1[0].data_ptr()
+    assert_close(torch.cat([o1, o2], dim=1), to_np(o), 2e-3, 2e-3, "split outputs")
+    assert_close(S2, to_np(S), 2e-3, 2e-3, "split state")
+    for i in range(3):
+        assert torch.equal(nh2[i], nh[i])
+    obf, _, _ = hb.hip_dgda_layer_prefill(projs, wd, None)
+    assert obf.dtype == torch.bfloat16
+    assert torch.equal(obf, o.bfloat16())
+
+
+def test_dgda_layer_fused_forward_matches_unfused(dev):
+    """The bf16 DGDALayer with the prologue fused against the same layer with the one-pass
+    prologue kernel and the op on its stored bf16 outputs (which round q, k, v once more):
+    within 2e-2 of the output's largest magnitude; then a second call continues from the
+    returned state and conv history in both."""
+    from maba_sparse.layers import DGDALayer
+    torch.manual_seed(2)
+    layer = DGDALayer(dim=256, n_heads=4).to(dev, torch.bfloat16).eval()
+    x = torch.randn(2, 900, 256, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        yf, sf, cf = layer(x[:, :500])
+        yf2, sf2, _ = layer(x[:, 500:], state=sf, conv_state=cf)
+        layer.fuse_prologue = False
+        yu, su, cu = layer(x[:, :500])
+        yu2, su2, _ = layer(x[:, 500:], state=su, conv_state=cu)
+    for a, b_, name in ((yf, yu, "y"), (yf2, yu2, "y2"), (sf, su, "S"), (sf2, su2, "S2")):
+        err = (a.float() - b_.float()).abs().max().item()
+        assert err <= 2e-2 * b_.float().abs().max().item(), (name, err)
+    for i in range(3):
+        assert torch.equal(cf[i], cu[i]), f"history {i}"
