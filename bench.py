@@ -199,75 +199,103 @@ def _timed(fn, min_seconds: float):
             return reps, dt
 
 
+def cpu_anchor_config1(min_seconds: float = 5.0):
+    """BASELINE config 1 on the host cores, the required CPU anchor: DGDA forward at B=1,
+    H=10, T=2048, d=64 in fp32 through the package's ``cpu`` backend (the chunked form of the
+    reference's CPU kernels, kernels/cpu_dgda.py; chunk 16, adaptive inversion) with the
+    config's distributions: q, k ~ N(0,1) L2-normalised, v ~ N(0,1), beta = sigmoid(N(0,1)),
+    log alpha = -softplus(N(0,1) + 2) per token, zero initial state."""
+    import torch
+    import torch.nn.functional as F
+    from maba_sparse.kernels.cpu_dgda import cpu_dgda_prefill
+    B, H, T, d = 1, 10, 2048, 64
+    g = torch.Generator().manual_seed(0)
+    q = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1)
+    k = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1)
+    v = torch.randn(B, H, T, d, generator=g)
+    be = torch.sigmoid(torch.randn(B, H, T, 1, generator=g)).expand(B, H, T, d)
+    la = (-F.softplus(torch.randn(B, H, T, 1, generator=g) + 2)).expand(B, H, T, d)
+    reps, dt = _timed(lambda: cpu_dgda_prefill(q, k, v, b=be, w=be, log_alpha=la, chunk_size=16), min_seconds)
+    return {"value": reps * B * T / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "config": "BASELINE config 1: DGDA forward B=1 H=10 T=2048 d_k=d_v=64 fp32, zero initial state",
+            "sample": f"the full config, {reps} repeats in {dt:.1f} s after one warm-up; the package's cpu "
+                      f"backend (maba_sparse/kernels/cpu_dgda.py, chunk 16, adaptive inversion) on torch's "
+                      f"intra-op threads"}
+
+
 def cpu_row_baselines(min_seconds: float = 2.0):
-    """The oracle timed on host cores beside each secondary row, on bounded samples of the
-    same workloads (float64 numpy for the indexer and MABA-SA restatements, the C/OpenMP
-    restatement for the per-channel DGDA prefill).  numpy's matrix products may use the
-    BLAS threads of the host; the Python loops are single-threaded."""
+    """The CPU baselines beside the secondary rows, on the host cores: the package's torch-CPU
+    ops (the ``cpu`` backend: chunked DGDA, the reference ops for the indexer and MABA-SA) at
+    the rows' full shapes where that fits a few seconds, otherwise on a stated sample; the
+    float64 oracle where no torch op exists at that shape (the dense prefill attention)."""
     import numpy as np
-    from oracle import dgda as odg, indexer as oix, sparse_attn as osa, dgda_c
+    import torch
+    import torch.nn.functional as F
+    from maba_sparse.kernels import common as C
+    from maba_sparse.kernels.cpu_dgda import cpu_dgda_prefill, cpu_dgda_step
+    from oracle import sparse_attn as osa
     out = {}
+    nthr = torch.get_num_threads()
     blas = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
     r = np.random.default_rng(7)
-    # DGDA decode step, B=64 H=10 d=64, fp64 numpy (oracle/dgda.py::dgda_step)
+    g = torch.Generator().manual_seed(7)
+    # DGDA decode step, B=64 H=10 d=64, fp32 (cpu backend's step)
     B, H, d = 64, 10, 64
-    q = r.standard_normal((B, H, d)); k = r.standard_normal((B, H, d)); v = r.standard_normal((B, H, d))
-    la = -np.log1p(np.exp(r.standard_normal((B, H, 1)) + 2)) * np.ones((1, 1, d))
-    be = 1 / (1 + np.exp(-r.standard_normal((B, H, 1)))) * np.ones((1, 1, d))
-    S = np.zeros((B, H, d, d))
-    reps, dt = _timed(lambda: odg.dgda_step(q, k, v, b=be, w=be, state=S, log_alpha=la), min_seconds)
-    out["dgda_step_B64"] = {"value": dt / reps * 1e6, "unit": "us/step", "cores": blas, "kind": "port",
-                            "sample": f"the full B=64 step, {reps} repeats in {dt:.1f} s, oracle/dgda.py (numpy fp64)"}
-    # DG-Indexer decode at 1M context: B=8, 10 heads, 15,625 centroids, d=128, top-32
+    q = F.normalize(torch.randn(B, H, d, generator=g), dim=-1)
+    k = F.normalize(torch.randn(B, H, d, generator=g), dim=-1)
+    v = torch.randn(B, H, d, generator=g)
+    la = (-F.softplus(torch.randn(B, H, 1, generator=g) + 2)).expand(B, H, d)
+    be = torch.sigmoid(torch.randn(B, H, 1, generator=g)).expand(B, H, d)
+    S = torch.zeros(B, H, d, d)
+    reps, dt = _timed(lambda: cpu_dgda_step(q, k, v, b=be, w=be, state=S, log_alpha=la), min_seconds)
+    out["dgda_step_B64"] = {"value": dt / reps * 1e6, "unit": "us/step", "cores": nthr, "kind": "port",
+                            "sample": f"the full B=64 step in fp32, {reps} repeats in {dt:.1f} s; "
+                                      f"maba_sparse/kernels/cpu_dgda.py cpu_dgda_step"}
+    # DG-Indexer decode at 1M context: B=8, 10 heads, 15,625 centroids, d=128, top-32 (full config 3 step)
     B, Hq, nb, dc = 8, 10, 15625, 128
-    qi = r.standard_normal((B, Hq, dc)); cent = r.standard_normal((B, nb, dc))
-
-    def idx_step():
-        oix.topk_desc(oix.decode_scores(qi, cent, 0.1), 32)
-
-    reps, dt = _timed(idx_step, min_seconds)
-    out["index_topk_decode_1M"] = {"value": dt / reps * 1e6, "unit": "us/step", "cores": blas, "kind": "port",
-                                   "sample": f"the full config-3 step, {reps} repeats in {dt:.1f} s, "
-                                             f"oracle/indexer.py decode_scores + topk_desc (numpy fp64)"}
-    # MABA-SA decode at 1M context, one batch element of config 4 (scaled by 8): latent
-    # queries as q with identity per-head projections, per-head top-32 index rows
+    qi = torch.randn(B, Hq, dc, generator=g)
+    cent = torch.randn(B, nb, dc, generator=g)
+    reps, dt = _timed(lambda: C.ref_index_topk_decode(qi, cent, lambda_dist=0.1, top_k=32), min_seconds)
+    out["index_topk_decode_1M"] = {"value": dt / reps * 1e6, "unit": "us/step", "cores": nthr, "kind": "port",
+                                   "sample": f"the full config-3 step in fp32, {reps} repeats in {dt:.1f} s; "
+                                             f"kernels/common.py ref_index_topk_decode (torch)"}
+    del cent
+    # MABA-SA decode at 1M context: one batch element of config 4 at full length (scaled by 8)
     Bs, L, H = 1, 1_000_000, 10
-    c = r.standard_normal((Bs, L, dc))          # fp64 already: the oracle's conversions are no-ops
-    means = c.reshape(Bs, L // 64, 64, dc).mean(axis=2)
-    eye = np.concatenate([np.eye(dc)] * H, axis=0)            # [H*dc, dc]: W_k,h = W_v,h = I
-    qs = r.standard_normal((Bs, H, dc)) * 0.1
-    idx = np.stack([np.stack([r.permutation(L // 64)[:32] for _ in range(H)]) for _ in range(Bs)])
-    gate = r.standard_normal((Bs, 3))
-    reps, dt = _timed(lambda: osa.maba_sa_decode(qs, c, eye, eye, idx, gate, means=means), min_seconds)
-    out["maba_sa_decode_1M"] = {"value": dt / reps * 1e6 * 8, "unit": "us/step", "cores": blas, "kind": "port",
+    c = torch.randn(Bs, L, dc, generator=g)
+    hca = C.ref_hca_pool(c, pool=64)
+    ql = torch.randn(Bs, H, dc, generator=g) * 0.1
+    idx = torch.stack([torch.randperm(L // 64, generator=g)[:32] for _ in range(H)]).unsqueeze(0)
+    gate = torch.randn(Bs, 3, generator=g)
+    reps, dt = _timed(lambda: C.ref_maba_sa_decode(ql, c, hca, idx, gate, L=L, scale=0.125), min_seconds)
+    out["maba_sa_decode_1M"] = {"value": dt / reps * 1e6 * 8, "unit": "us/step", "cores": nthr, "kind": "port",
                                 "sample": f"one of the 8 batch elements of config 4 (L=1M, H=10, d_c=128, per-head "
-                                          f"top-32 rows), {reps} repeats in {dt:.1f} s, times 8; "
-                                          f"oracle/sparse_attn.py maba_sa_decode (numpy fp64)"}
-    del c, means
-    # DGDA prefill with per-channel gates: B=1 H=10 T=1024 of the config-2 shape, C/OpenMP
-    dgda_c.build()
-    B, H, T, d = 1, 10, 1024, 64
-    q = r.standard_normal((B, H, T, d), dtype=np.float32); q /= np.linalg.norm(q, axis=-1, keepdims=True)
-    k = r.standard_normal((B, H, T, d), dtype=np.float32); k /= np.linalg.norm(k, axis=-1, keepdims=True)
-    v = r.standard_normal((B, H, T, d), dtype=np.float32)
-    la = (-np.log1p(np.exp(r.standard_normal((B, H, T, d), dtype=np.float32) + 2))).astype(np.float32)
-    be = (1 / (1 + np.exp(-r.standard_normal((B, H, T, d), dtype=np.float32)))).astype(np.float32)
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or 64, B * H)
-    reps, dt = _timed(lambda: dgda_c.dgda_prefill_chunked_c(q, k, v, la, be, be, chunk_size=64, nthreads=threads),
-                      min_seconds)
+                                          f"top-32 rows) in fp32, {reps} repeats in {dt:.1f} s, times 8; "
+                                          f"kernels/common.py ref_maba_sa_decode (torch)"}
+    del c, hca
+    # DGDA prefill with per-channel gates: B=1 H=10 T=2048 of the config-2 shape, fp32 chunked
+    B, H, T = 1, 10, 2048
+    q = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1)
+    k = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1)
+    v = torch.randn(B, H, T, d, generator=g)
+    la = -F.softplus(torch.randn(B, H, T, d, generator=g) + 2)
+    be = torch.sigmoid(torch.randn(B, H, T, d, generator=g))
+    reps, dt = _timed(lambda: cpu_dgda_prefill(q, k, v, b=be, w=be, log_alpha=la, chunk_size=16), min_seconds)
     out["dgda_prefill_per_channel_gates"] = {
-        "value": reps * B * T / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-        "sample": f"B=1 H=10 T=1024 d=64 of the config-2 shape with per-channel fp32 gates, {reps} repeats in "
-                  f"{dt:.1f} s, oracle/dgda_chunked.c (OpenMP over b*h)"}
-    # DGDA layer prologue: B=1, 512 of the 32,768 tokens, C=640, fp64 numpy (oracle/dgda.py::layer_prologue)
-    Tp, Cp = 512, 640
-    xs = [r.standard_normal((1, Tp, Cp)) for _ in range(6)]
-    wsp = [r.standard_normal((Cp, 4)) * 0.3 for _ in range(3)]
-    reps, dt = _timed(lambda: odg.layer_prologue(*xs, *wsp, n_heads=10), min_seconds)
-    out["dgda_layer_prologue"] = {"value": dt / reps * 1e6 * (4 * 32768 / Tp), "unit": "us/call", "cores": blas,
+        "value": reps * B * T / dt, "unit": "tokens/s", "cores": nthr, "kind": "port",
+        "sample": f"B=1 H=10 T=2048 d=64 of the config-2 shape with per-channel fp32 gates, {reps} repeats in "
+                  f"{dt:.1f} s; maba_sparse/kernels/cpu_dgda.py cpu_dgda_prefill (chunk 16)"}
+    # DGDA layer prologue: B=1, 8,192 of the 32,768 tokens, C=640, fp32 (the torch reference op)
+    Tp, Cp = 8192, 640
+    xs = [torch.randn(1, Tp, Cp, generator=g) for _ in range(6)]
+    wsp = [torch.randn(Cp, 1, 4, generator=g) * 0.3 for _ in range(3)]
+    reps, dt = _timed(lambda: C.ref_dgda_prologue(xs, wsp, None, n_heads=10, with_alpha=False), min_seconds)
+    out["dgda_layer_prologue"] = {"value": dt / reps * 1e6 * (4 * 32768 / Tp), "unit": "us/call", "cores": nthr,
                                   "kind": "port",
-                                  "sample": f"B=1, 512 of the 32,768 tokens (C=640), {reps} repeats in {dt:.1f} s, "
-                                            f"scaled by 256 to the B=4 call; oracle/dgda.py layer_prologue (numpy fp64)"}
+                                  "sample": f"B=1, 8,192 of the 32,768 tokens (C=640) in fp32, {reps} repeats in "
+                                            f"{dt:.1f} s, scaled by 16 to the B=4 call; kernels/common.py "
+                                            f"ref_dgda_prologue (torch)"}
+    del xs
     # MABA-SA prefill streams: the last 128 of the 32,768 queries of one head, scaled by 256 x 10 heads
     Lp, dhp, Kp = 32768, 64, 32
     qp1 = r.standard_normal((1, 1, 128, dhp)); kp1 = r.standard_normal((1, 1, Lp, dhp))
@@ -297,26 +325,20 @@ def cpu_row_baselines(min_seconds: float = 2.0):
                                    "sample": f"B=1, 256-token prefill ({marks[0] - t0:.1f} s), then 8 greedy steps; the "
                                              f"same stack in fp32 on the host through the torch reference ops"}
     del cm
-    # causal prefill index_topk: 4,096 of the 32,768 queries against 512 centroids, d=128
-    Lq, nbp = 4096, 512
-    qp = r.standard_normal((1, Lq, dc)); cp = r.standard_normal((1, nbp, dc))
-
-    def pre_step():
-        sc = oix.prefill_scores(qp, cp, 0.5)
-        oix.topk_desc(sc, 32)
-
-    # gate superposition: 4,096 of the 32,768 positions of [1,10,32768,64], fp64 numpy
-    o3 = [r.standard_normal((1, 10, 4096, 64)) for _ in range(3)]
-    gz = r.standard_normal((1, 4096, 3))
-    reps_s, dt_s = _timed(lambda: osa.superposition(o3[0], o3[1], o3[2], gate_logits=gz), min_seconds)
-    out["stream_superposition"] = {"value": dt_s / reps_s * 8 * 1e6, "unit": "us/call", "cores": 1, "kind": "port",
-                                   "sample": f"4,096 of the 32,768 positions, {reps_s} repeats in {dt_s:.1f} s, times 8; "
-                                             f"oracle/sparse_attn.py superposition (numpy fp64)"}
-    reps, dt = _timed(pre_step, min_seconds)
-    out["index_topk_prefill"] = {"value": reps * Lq / dt, "unit": "queries/s", "cores": blas, "kind": "port",
-                                 "sample": f"the first 4,096 of the 32,768 query rows (512 centroids, d=128, top-32), "
-                                           f"{reps} repeats in {dt:.1f} s, oracle/indexer.py prefill_scores + "
-                                           f"topk_desc (numpy fp64)"}
+    # causal prefill index_topk: the 32,768 query rows against 512 centroids, d=128 (full row shape)
+    qp = torch.randn(1, 32768, dc, generator=g)
+    cp = torch.randn(1, 512, dc, generator=g)
+    reps, dt = _timed(lambda: C.ref_index_topk(qp, cp, lambda_dist=0.5, top_k=32, block_size=64), min_seconds)
+    out["index_topk_prefill"] = {"value": reps * 32768 / dt, "unit": "queries/s", "cores": nthr, "kind": "port",
+                                 "sample": f"the full 32,768 query rows (512 centroids, d=128, top-32) in fp32, "
+                                           f"{reps} repeats in {dt:.1f} s; kernels/common.py ref_index_topk (torch)"}
+    # gate superposition at the full [1,10,32768,64] shape
+    o3 = [torch.randn(1, 10, 32768, 64, generator=g) for _ in range(3)]
+    gz = torch.randn(1, 32768, 3, generator=g)
+    reps, dt = _timed(lambda: C.ref_stream_superposition(o3[0], o3[1], o3[2], gate_logits=gz), min_seconds)
+    out["stream_superposition"] = {"value": dt / reps * 1e6, "unit": "us/call", "cores": nthr, "kind": "port",
+                                   "sample": f"the full shape in fp32, {reps} repeats in {dt:.1f} s; "
+                                             f"kernels/common.py ref_stream_superposition (torch)"}
     return out
 
 
@@ -833,6 +855,8 @@ def main():
     if not args.only_prefill and not args.skip_cpu:
         log("timing the CPU baseline")
         res["cpu_baseline"] = cpu_baseline()
+        log("timing the config-1 CPU anchor")
+        res["cpu_anchor_config1"] = cpu_anchor_config1()
         if not args.skip_decode:
             log("timing the CPU baselines of the secondary rows")
             rows_cpu = cpu_row_baselines()

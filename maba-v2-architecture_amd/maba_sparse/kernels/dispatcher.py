@@ -37,6 +37,7 @@ import torch
 
 from maba_sparse._native import HipLibraryMissing
 from maba_sparse.kernels import common as _c
+from maba_sparse.kernels import cpu_dgda as _cpu
 
 logger = logging.getLogger(__name__)
 
@@ -53,10 +54,11 @@ _KERNEL_REGISTRY: Dict[str, Dict[str, Callable]] = {
         "dgda_prologue": _c.ref_dgda_prologue,
         "maba_sa_prefill": _c.ref_maba_sa_prefill,
     },
-    # CPU tensors run the same torch code; no separate CPU kernels are built here.
+    # host cores: the chunked DGDA of the reference's CPU backend (cpu_dgda.py), the rest as
+    # the reference ops in torch
     "cpu": {
-        "dgda_prefill": _c.reference_dgda_prefill,
-        "dgda_step": _c.reference_dgda_step,
+        "dgda_prefill": _cpu.cpu_dgda_prefill,
+        "dgda_step": _cpu.cpu_dgda_step,
         "compute_centroids": _c.reference_compute_centroids,
         "index_topk": _c.reference_index_topk,
         "stream_superposition": _c.reference_stream_superposition,
