@@ -472,6 +472,26 @@ def row_benches(dev):
 
     ms, _ = time_op(pc_step, 3, 1)
     nbytes = B * H * T * (3 * d * 2 + 3 * d * 4 + d * 2) + B * H * d * d * 4
+    del la, beta, wg
+    # the headline kernel with slow decay (log alpha x 0.005, about 0.6% per token): segment
+    # transitions never vanish, so the aggregate, map-chain and fix-up passes do full work
+    sc = dgda_prefill_case(dev, B, H, T, d)
+    sc["log_alpha"] = (sc["log_alpha"][..., :1] * 0.005).expand(B, H, T, d)   # still per token (stride 0)
+
+    def slow_step():
+        return hb.hip_dgda_prefill(**sc, chunk_size=64, out_dtype=torch.bfloat16, state_dtype=torch.float32,
+                                   allow_mixed_dtypes=True)
+
+    ms_slow, _ = time_op(slow_step, 5, 1)
+    sb = prefill_bytes(B, H, T, d)
+    out["dgda_prefill_slow_decay"] = {
+        "ms_per_step": ms_slow, "tokens_per_s": B * T / (ms_slow * 1e-3), "gbs": sb / (ms_slow * 1e-3) / 1e9,
+        "hbm_frac": sb / (ms_slow * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": sb,
+        "mfma_frac": prefill_flops(B, H, T, d) / (ms_slow * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "config": "BASELINE config 2 (B=4 H=10 T=32768 d=64, bf16 q/k/v, fp32 per-token gates) with the log "
+                  "decay scaled by 0.005"}
+    log(f"dgda_prefill slow decay: {ms_slow:.3f} ms/step")
+    del sc
     out["dgda_prefill_per_channel_gates"] = {
         "ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3), "gbs": nbytes / (ms * 1e-3) / 1e9,
         "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes,

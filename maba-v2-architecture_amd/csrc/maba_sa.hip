@@ -400,35 +400,33 @@ __device__ __forceinline__ SaRows sa_rows(const SaArgs& a, int64_t b) {
   return r;
 }
 
-// Key rows 16 rb + c16 of tile tix of a stream (0 local, 1 sparse, 2 HCA), dims 32 p + 8 g
-// .. +7.  Invalid rows read row 0 of the stream (in bounds: L >= 1, and the HCA stream is
-// only walked when it has entries); their scores are masked to -inf, so they get zero
-// weight.  blk is the tile's block index for the sparse stream.  Bit 4 rb + i of okb says
-// whether key row 16 rb + 4 g + i (a row of this lane's score accumulators) is valid.
+// Key rows 16 rb + c16 of tile tix of a stream (0 local, 1 sparse, 2 HCA; wave-uniform),
+// dims 32 p + 8 g .. +7, without branches: a tile's first row and the row limits are
+// uniform, and a local row past the sinks shifts to the window.  Invalid rows read row 0 of
+// the stream (in bounds: L >= 1, and the HCA stream is only walked when it has entries);
+// their scores are masked to -inf, so they get zero weight.  blk is the tile's block index
+// for the sparse stream.  Bit 4 rb + i of okb says whether key row 16 rb + 4 g + i (a row of
+// this lane's score accumulators) is valid.  Row offsets are 32-bit (the hosts check that a
+// sequence's rows span fewer than 2^31 elements).
 template <int NP>
 __device__ __forceinline__ void sa_load_rows(const SaRows& r, int stream, int64_t tix, int64_t blk, int c16, int g,
                                              s16x8 (&cv)[4][NP], uint32_t& okb) {
   const uint16_t* base = stream == 2 ? r.hca : r.c;
-  const int64_t rstride = stream == 2 ? r.hs : r.cs;
+  const int rstride = (int)(stream == 2 ? r.hs : r.cs);
   const int64_t nblk = (r.L + r.bs - 1) / r.bs;
+  const bool blk_ok = blk >= 0 && blk < nblk;
+  const int first = (int)(stream == 1 ? (blk_ok ? blk * r.bs : 0) : tix * 64);
+  // rows [first, lim) are valid; local rows at or past the sinks move by `shift`
+  const int lim = stream == 0 ? r.nloc : stream == 2 ? r.nc : (blk_ok ? (int)min(r.L, (int64_t)first + r.bs) : 0);
+  const int thr = stream == 0 ? r.ns : INT32_MAX;
+  const int shift = stream == 0 ? r.loc_start - r.ns : 0;
   okb = 0;
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
-    const int j = 16 * rb + c16;
-    int64_t pos;
-    bool ok;
-    if (stream == 0) {
-      const int64_t li = tix * 64 + j;
-      ok = li < r.nloc;
-      pos = li < r.ns ? li : r.loc_start + (li - r.ns);
-    } else if (stream == 1) {
-      pos = blk * r.bs + j;
-      ok = blk >= 0 && blk < nblk && j < r.bs && pos < r.L;
-    } else {
-      pos = tix * 64 + j;
-      ok = pos < r.nc;
-    }
-    const uint16_t* row = base + (ok ? pos : 0) * rstride + 8 * g;
+    const int p0 = first + 16 * rb + c16;
+    const bool ok = p0 < lim;
+    const int pos = ok ? p0 + (p0 >= thr ? shift : 0) : 0;
+    const uint16_t* row = base + (uint32_t)(pos * rstride + 8 * g);
 #pragma unroll
     for (int p = 0; p < NP; ++p) cv[rb][p] = *(const s16x8*)(row + 32 * p);
     // lanes 0-15 load rows 16 rb + c16: bits 4g .. 4g+3 of their ballot are this lane's rows
@@ -452,12 +450,35 @@ __device__ __forceinline__ void sa_acc_init(SaAcc<NP>& st) {
   for (int dt = 0; dt < 2 * NP; ++dt) st.z[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
+// After a stream's tiles: a column whose head does not attend to the stream (heads >= H, or
+// other heads of a per-head sparse segment) leaves as no valid key (m = -inf, l = 0); every
+// merge gives such a partial zero weight without reading its Z.
+template <int NP>
+__device__ __forceinline__ void sa_acc_close(SaAcc<NP>& st, bool head_on) {
+  if (!head_on) {
+    st.m = -INFINITY;
+    st.l = 0.f;
+  }
+}
+
+// The tiles [t0, t1) of a stream through two register sets in turn: the next tile's
+// loads are in flight while a tile computes, and no set is copied into the other (a copy
+// would wait for the loads).  Loads past the last tile re-read it (in bounds, unused);
+// unconditional loads keep the register pressure at that of straight-line code.  blk_of(t)
+// is the sparse block index of tile t (wave-uniform).
+template <int NP, class BlkOf>
+__device__ __forceinline__ void sa_stream_tiles(const SaRows& rows, int stream, int64_t t0, int64_t t1, BlkOf blk_of,
+                                                const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile,
+                                                int c16, int g, SaAcc<NP>& st);
+
 // One 64-key tile: scores D[key][head] = C Q^T with the scaled query in bf16 hi + lo (B
 // operand), online softmax, values Z[dim][head] += C^T P with the tile copied row-major into
-// the wave's LDS and read transposed, P in bf16 hi + lo.  head_on: the lane's column is a
-// head that attends to this stream.
+// the wave's LDS and read transposed, P in bf16 hi + lo.  Every column runs the softmax (a
+// column of a head that does not attend to the stream is discarded by the caller, see
+// sa_acc_close); a tile whose 64 keys are all valid skips the masking, and the rescale of
+// Z is skipped when no column's running max moved (both tests wave-uniform).
 template <int NP>
-__device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t okb, bool head_on,
+__device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t okb,
                                              const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile, int c16,
                                              int g, SaAcc<NP>& st) {
   constexpr int DC = 32 * NP;
@@ -478,20 +499,26 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t 
   }
   // lane (head c16, group g) holds scores of keys 16 rb + 4g + i
   float tmax = -INFINITY;
+  if (__ballot(okb != 0xffffu) != 0ull) {   // some key of the tile is invalid
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool kv = (okb >> (4 * rb + i)) & 1u;
-      const float x = (kv && head_on) ? sc[rb][i] : -INFINITY;
-      sc[rb][i] = x;
-      tmax = fmaxf(tmax, x);
+      for (int i = 0; i < 4; ++i) {
+        const float x = ((okb >> (4 * rb + i)) & 1u) ? sc[rb][i] : -INFINITY;
+        sc[rb][i] = x;
+        tmax = fmaxf(tmax, x);
+      }
     }
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+      tmax = fmaxf(fmaxf(tmax, fmaxf(sc[rb][0], sc[rb][1])), fmaxf(sc[rb][2], sc[rb][3]));
   }
   tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
   tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
   const float m_new = fmaxf(st.m, tmax);
-  const float corr = (m_new == -INFINITY) ? 1.f : __expf(st.m - m_new);
+  const bool grow = __ballot(m_new != st.m) != 0ull;   // wave-uniform: some column's max moved
+  const float corr = (m_new == -INFINITY || !grow) ? 1.f : __expf(st.m - m_new);
   const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;   // exp(-inf - m_sub) = 0 for masked keys
   float psum = 0.f;
   s16x4 ph[4], pl[4];
@@ -518,7 +545,7 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t 
   // z[dim][head] = corr * z + C^T P  (K = 64 keys as two permuted 32-steps)
 #pragma unroll
   for (int dt = 0; dt < DC / 16; ++dt) {
-    f32x4 acc = st.z[dt] * corr;
+    f32x4 acc = grow ? st.z[dt] * corr : st.z[dt];
 #pragma unroll
     for (int p2 = 0; p2 < 2; ++p2) {
       const s16x4 a0 = sa_ldsT4(tile, TP, 32 * p2, 16 * dt, c16, g);
@@ -534,6 +561,25 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t 
                                                     acc, 0, 0, 0);
     }
     st.z[dt] = acc;
+  }
+}
+
+template <int NP, class BlkOf>
+__device__ __forceinline__ void sa_stream_tiles(const SaRows& rows, int stream, int64_t t0, int64_t t1, BlkOf blk_of,
+                                                const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile,
+                                                int c16, int g, SaAcc<NP>& st) {
+  if (t0 >= t1) return;
+  s16x8 cvA[4][NP], cvB[4][NP];
+  uint32_t okA = 0, okB = 0;
+  sa_load_rows<NP>(rows, stream, t0, blk_of(t0), c16, g, cvA, okA);
+  for (int64_t tix = t0; tix < t1; tix += 2) {
+    const int64_t n1 = tix + 1 < t1 ? tix + 1 : tix;
+    sa_load_rows<NP>(rows, stream, n1, blk_of(n1), c16, g, cvB, okB);
+    sa_tile_step<NP>(cvA, okA, qh, ql, tile, c16, g, st);
+    if (tix + 1 >= t1) break;
+    const int64_t n2 = tix + 2 < t1 ? tix + 2 : tix + 1;
+    sa_load_rows<NP>(rows, stream, n2, blk_of(n2), c16, g, cvA, okA);
+    sa_tile_step<NP>(cvB, okB, qh, ql, tile, c16, g, st);
   }
 }
 
@@ -612,22 +658,8 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a_in) {
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)blk_l >> 32), src);
     return (int64_t)(((uint64_t)hi << 32) | lo);
   };
-  // two register sets in turn: the next tile's loads are in flight while a tile computes,
-  // and no set is copied into the other (a copy would wait for the loads)
-  s16x8 cvA[4][NP], cvB[4][NP];
-  uint32_t okA = 0, okB = 0;
-  if (t0 < t1) sa_load_rows<NP>(rows, sg.stream, t0, blk_of(t0), c16, g, cvA, okA);
-  for (int64_t tix = t0; tix < t1; tix += 2) {
-    // loads past the wave's last tile re-read that tile (in bounds, unused); unconditional
-    // loads keep the register pressure of the two sets at that of straight-line code
-    const int64_t n1 = tix + 1 < t1 ? tix + 1 : tix;
-    sa_load_rows<NP>(rows, sg.stream, n1, blk_of(n1), c16, g, cvB, okB);
-    sa_tile_step<NP>(cvA, okA, head_on, qh, ql, tile, c16, g, st);
-    if (tix + 1 >= t1) break;
-    const int64_t n2 = tix + 2 < t1 ? tix + 2 : tix + 1;
-    sa_load_rows<NP>(rows, sg.stream, n2, blk_of(n2), c16, g, cvA, okA);
-    sa_tile_step<NP>(cvB, okB, head_on, qh, ql, tile, c16, g, st);
-  }
+  sa_stream_tiles<NP>(rows, sg.stream, t0, t1, blk_of, qh, ql, tile, c16, g, st);
+  sa_acc_close(st, head_on);
   const float m_run = st.m, l_run = st.l;
   const f32x4* z = st.z;
   // merge the four wave partials: s_z[wave][head][dim], s_m / s_l[wave][head]
@@ -703,7 +735,7 @@ __global__ __launch_bounds__(512, 1) void maba_sa_prefill_latent_kernel(PlArgs a
   constexpr int TP = DC + 8;
   __shared__ __attribute__((aligned(16))) short s_tile[PL_W][64 * TP];
   __shared__ float s_ml[PL_W][2][16];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int g = lane >> 4, c16 = lane & 15;
   const int64_t b = blockIdx.x / a.Lq, t = blockIdx.x % a.Lq;
   const int64_t L = a.Lkv - a.Lq + t + 1;
@@ -759,20 +791,8 @@ __global__ __launch_bounds__(512, 1) void maba_sa_prefill_latent_kernel(PlArgs a
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)blk_l >> 32), src);
     return (int64_t)(((uint64_t)hi << 32) | lo);
   };
-  if (t0 < t1) {
-    s16x8 cvA[4][NP], cvB[4][NP];
-    uint32_t okA = 0, okB = 0;
-    sa_load_rows<NP>(rows, stream, t0, blk_of(t0), c16, g, cvA, okA);
-    for (int64_t tix = t0; tix < t1; tix += 2) {
-      const int64_t n1 = tix + 1 < t1 ? tix + 1 : tix;
-      sa_load_rows<NP>(rows, stream, n1, blk_of(n1), c16, g, cvB, okB);
-      sa_tile_step<NP>(cvA, okA, head_on, qh, ql, tile, c16, g, st);
-      if (tix + 1 >= t1) break;
-      const int64_t n2 = tix + 2 < t1 ? tix + 2 : tix + 1;
-      sa_load_rows<NP>(rows, stream, n2, blk_of(n2), c16, g, cvA, okA);
-      sa_tile_step<NP>(cvB, okB, head_on, qh, ql, tile, c16, g, st);
-    }
-  }
+  if (stream >= 0) sa_stream_tiles<NP>(rows, stream, t0, t1, blk_of, qh, ql, tile, c16, g, st);
+  sa_acc_close(st, head_on);
   // wave partials to LDS (the tiles are free once every wave is past its loop)
   __syncthreads();
   float* s_z = (float*)&s_tile[0][0];   // [PL_W][16][DC]
@@ -887,7 +907,8 @@ static int sa_setup(const maba_tensor* q_lat, const maba_tensor* c_kv, const mab
   sa_geometry(a, L, window, n_sink, pool, a.Hi, a.K);
   seg = c_kv->dtype == MABA_BF16 && hca->dtype == MABA_BF16 && c_kv->stride[2] == 1 && hca->stride[2] == 1 &&
         dc % 32 == 0 && dc <= 128 && (uintptr_t)c_kv->data % 16 == 0 && (uintptr_t)hca->data % 16 == 0 &&
-        c_kv->stride[0] % 8 == 0 && c_kv->stride[1] % 8 == 0 && hca->stride[0] % 8 == 0 && hca->stride[1] % 8 == 0;
+        c_kv->stride[0] % 8 == 0 && c_kv->stride[1] % 8 == 0 && hca->stride[0] % 8 == 0 && hca->stride[1] % 8 == 0 &&
+        c_kv->shape[1] * c_kv->stride[1] <= INT32_MAX && hca->shape[1] * hca->stride[1] <= INT32_MAX;
   int64_t slots = a.ntiles;
   if (seg) {
     sa_segments(a, device_cu_count());
@@ -1068,6 +1089,8 @@ extern "C" int maba_hip_maba_sa_prefill_latent(const maba_tensor* q_lat, const m
   if (c_kv->stride[2] != 1 || hca->stride[2] != 1 || (uintptr_t)c_kv->data % 16 || (uintptr_t)hca->data % 16 ||
       c_kv->stride[0] % 8 || c_kv->stride[1] % 8 || hca->stride[0] % 8 || hca->stride[1] % 8)
     return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill_latent: 16-byte aligned bf16 rows with unit channel stride");
+  if (Lkv * c_kv->stride[1] > INT32_MAX || hca->shape[1] * hca->stride[1] > INT32_MAX)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_prefill_latent: a sequence's rows must span fewer than 2^31 elements");
   if (B * Lq * H == 0) return MABA_OK;
   PlArgs a;
   a.q = q_lat->data; a.qdt = q_lat->dtype; a.qsb = q_lat->stride[0]; a.qst = q_lat->stride[1];
