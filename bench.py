@@ -45,6 +45,16 @@ for _p in (REPO, os.path.join(REPO, "maba-v2-architecture_amd")):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
+TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE passes scaled by a device copy's "
+                  "readings (profiles/hbm_traffic_pmc.txt)")
+
+
+def measured_traffic(key):
+    """HBM bytes per call of a workload from the committed counter runs, or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as fh:
+        return json.load(fh).get(key)
 
 
 def log(msg: str) -> None:
@@ -63,6 +73,9 @@ def parse():
     ap.add_argument("--only-rows", action="store_true",
                     help="run only the secondary row benchmarks: per-channel-gate prefill, prefill top-k (for profiling)")
     ap.add_argument("--only-model", action="store_true", help="run only the config-5 full-model decode")
+    ap.add_argument("--row", default=None,
+                    help="with --only-rows: a comma-separated subset of the row groups dgda, prologue, topk, "
+                         "superposition, prefill_attention, layer_decode, model (for profiling)")
     ap.add_argument("--model-batch", type=int, default=16)
     ap.add_argument("--model-prefill", type=int, default=131072)
     ap.add_argument("--model-steps", type=int, default=256)
@@ -441,6 +454,8 @@ def decode_benches(dev, steps: int):
                                       "hbm_frac": tot_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
                                       "algorithmic_bytes": tot_bytes, "graph_us_per_step": step_ms * 1e3,
                                       "eager_us_per_step": step_eager_ms * 1e3,
+                                      "traffic": measured_traffic("decode_bytes_per_step"),
+                                      "traffic_source": TRAFFIC_SOURCE,
                                       "timing": timing + " (the two entry points per step)"}
     log(f"indexer decode 1M: graph {idx_ms * 1e3:.1f} us, eager {idx_eager_ms * 1e3:.1f} us")
     log(f"MABA-SA decode 1M: graph {sa_ms * 1e3:.1f} us, eager {sa_eager_ms * 1e3:.1f} us")
@@ -449,7 +464,7 @@ def decode_benches(dev, steps: int):
     return out
 
 
-def row_benches(dev):
+def row_benches(dev, only=None):
     """Secondary lines for hot-path rows outside the headline: DGDA prefill with
     per-channel gates (the layer's gate layout, config-2 shape) and the causal prefill
     index_topk."""
@@ -457,86 +472,94 @@ def row_benches(dev):
     import torch.nn.functional as F
     from maba_sparse.kernels import hip_backend as hb
     out = {}
-    B, H, T, d = 4, 10, 32768, 64
-    g = torch.Generator(device="cpu").manual_seed(5)
-    q = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1).to(dev, torch.bfloat16)
-    k = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1).to(dev, torch.bfloat16)
-    v = torch.randn(B, H, T, d, generator=g).to(dev, torch.bfloat16)
-    la = (-F.softplus(torch.randn(B, H, T, d, generator=g) + 2.0)).to(dev)
-    beta = torch.sigmoid(torch.randn(B, H, T, d, generator=g)).to(dev)
-    wg = torch.sigmoid(torch.randn(B, H, T, d, generator=g)).to(dev)
+    want = lambda name: only is None or name in only  # noqa: E731
+    if want("dgda"):
+        B, H, T, d = 4, 10, 32768, 64
+        g = torch.Generator(device="cpu").manual_seed(5)
+        q = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1).to(dev, torch.bfloat16)
+        k = F.normalize(torch.randn(B, H, T, d, generator=g), dim=-1).to(dev, torch.bfloat16)
+        v = torch.randn(B, H, T, d, generator=g).to(dev, torch.bfloat16)
+        la = (-F.softplus(torch.randn(B, H, T, d, generator=g) + 2.0)).to(dev)
+        beta = torch.sigmoid(torch.randn(B, H, T, d, generator=g)).to(dev)
+        wg = torch.sigmoid(torch.randn(B, H, T, d, generator=g)).to(dev)
 
-    def pc_step():
-        return hb.hip_dgda_prefill(q, k, v, log_alpha=la, b=beta, w=wg, chunk_size=64, out_dtype=torch.bfloat16,
-                                   state_dtype=torch.float32, allow_mixed_dtypes=True)
+        def pc_step():
+            return hb.hip_dgda_prefill(q, k, v, log_alpha=la, b=beta, w=wg, chunk_size=64, out_dtype=torch.bfloat16,
+                                       state_dtype=torch.float32, allow_mixed_dtypes=True)
 
-    ms, _ = time_op(pc_step, 3, 1)
-    nbytes = B * H * T * (3 * d * 2 + 3 * d * 4 + d * 2) + B * H * d * d * 4
-    del la, beta, wg
-    # the headline kernel with slow decay (log alpha x 0.005, about 0.6% per token): segment
-    # transitions never vanish, so the aggregate, map-chain and fix-up passes do full work
-    sc = dgda_prefill_case(dev, B, H, T, d)
-    sc["log_alpha"] = (sc["log_alpha"][..., :1] * 0.005).expand(B, H, T, d)   # still per token (stride 0)
+        ms, _ = time_op(pc_step, 3, 1)
+        nbytes = B * H * T * (3 * d * 2 + 3 * d * 4 + d * 2) + B * H * d * d * 4
+        del la, beta, wg
+        # the headline kernel with slow decay (log alpha x 0.005, about 0.6% per token): segment
+        # transitions never vanish, so the aggregate, map-chain and fix-up passes do full work
+        sc = dgda_prefill_case(dev, B, H, T, d)
+        sc["log_alpha"] = (sc["log_alpha"][..., :1] * 0.005).expand(B, H, T, d)   # still per token (stride 0)
 
-    def slow_step():
-        return hb.hip_dgda_prefill(**sc, chunk_size=64, out_dtype=torch.bfloat16, state_dtype=torch.float32,
-                                   allow_mixed_dtypes=True)
+        def slow_step():
+            return hb.hip_dgda_prefill(**sc, chunk_size=64, out_dtype=torch.bfloat16, state_dtype=torch.float32,
+                                       allow_mixed_dtypes=True)
 
-    ms_slow, _ = time_op(slow_step, 5, 1)
-    sb = prefill_bytes(B, H, T, d)
-    out["dgda_prefill_slow_decay"] = {
-        "ms_per_step": ms_slow, "tokens_per_s": B * T / (ms_slow * 1e-3), "gbs": sb / (ms_slow * 1e-3) / 1e9,
-        "hbm_frac": sb / (ms_slow * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": sb,
-        "mfma_frac": prefill_flops(B, H, T, d) / (ms_slow * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-        "config": "BASELINE config 2 (B=4 H=10 T=32768 d=64, bf16 q/k/v, fp32 per-token gates) with the log "
-                  "decay scaled by 0.005"}
-    log(f"dgda_prefill slow decay: {ms_slow:.3f} ms/step")
-    del sc
-    out["dgda_prefill_per_channel_gates"] = {
-        "ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3), "gbs": nbytes / (ms * 1e-3) / 1e9,
-        "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes,
-        "config": "B=4 H=10 T=32768 d=64, bf16 q/k/v, fp32 [B,H,T,64] decay/erase/write gates, bf16 out"}
-    log(f"dgda_prefill per-channel gates: {ms:.3f} ms/step")
-    del q, k, v, la, beta, wg
-    out.update(prologue_benches(dev))
-    # causal prefill index_topk: one sequence of 32,768 queries over 512 block centroids
-    Bq, L, di, K = 1, 32768, 128, 32
-    qi = torch.randn(Bq, L, di, device=dev, dtype=torch.bfloat16)
-    cent = torch.randn(Bq, L // 64, di, device=dev, dtype=torch.bfloat16)
+        ms_slow, _ = time_op(slow_step, 5, 1)
+        sb = prefill_bytes(B, H, T, d)
+        out["dgda_prefill_slow_decay"] = {
+            "ms_per_step": ms_slow, "tokens_per_s": B * T / (ms_slow * 1e-3), "gbs": sb / (ms_slow * 1e-3) / 1e9,
+            "hbm_frac": sb / (ms_slow * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": sb,
+            "mfma_frac": prefill_flops(B, H, T, d) / (ms_slow * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "config": "BASELINE config 2 (B=4 H=10 T=32768 d=64, bf16 q/k/v, fp32 per-token gates) with the log "
+                      "decay scaled by 0.005"}
+        log(f"dgda_prefill slow decay: {ms_slow:.3f} ms/step")
+        del sc
+        out["dgda_prefill_per_channel_gates"] = {
+            "ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3), "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes,
+            "config": "B=4 H=10 T=32768 d=64, bf16 q/k/v, fp32 [B,H,T,64] decay/erase/write gates, bf16 out"}
+        log(f"dgda_prefill per-channel gates: {ms:.3f} ms/step")
+        del q, k, v
+    if want("prologue"):
+        out.update(prologue_benches(dev))
+    if want("topk"):
+        # causal prefill index_topk: one sequence of 32,768 queries over 512 block centroids
+        Bq, L, di, K = 1, 32768, 128, 32
+        qi = torch.randn(Bq, L, di, device=dev, dtype=torch.bfloat16)
+        cent = torch.randn(Bq, L // 64, di, device=dev, dtype=torch.bfloat16)
 
-    def topk_prefill():
-        return hb.hip_index_topk(qi, cent, lambda_dist=0.5, top_k=K, block_size=64)
+        def topk_prefill():
+            return hb.hip_index_topk(qi, cent, lambda_dist=0.5, top_k=K, block_size=64)
 
-    ms, _ = time_op(topk_prefill, 5, 1)
-    # scoring flops: every query against the centroids of the blocks at or before its own
-    fl = 2 * di * Bq * sum(min(t // 64 + 1, L // 64) for t in range(0, L, 64)) * 64
-    out["index_topk_prefill"] = {"ms_per_call": ms, "queries_per_s": Bq * L / (ms * 1e-3),
-                                 "roofline": {"bound": "mfma", "achieved": fl / (ms * 1e-3) / 1e12,
-                                              "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                              "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-                                              "algorithmic_flops": fl, "traffic": None},
-                                 "config": "B=1 L=32768 d=128 bf16, 512 centroids, top-32, causal"}
-    log(f"index_topk prefill 32k x 512: {ms:.3f} ms")
-    del qi, cent
-    # gate superposition of three prefill stream outputs [1, 10, 32768, 64] bf16 with
-    # [1, 32768, 3] logits (the layer's prefill combine, sparse_attention.py:219)
-    Bs, Hs, Ls, Ds = 1, 10, 32768, 64
-    ol, os_, oh = (torch.randn(Bs, Hs, Ls, Ds, device=dev, dtype=torch.bfloat16) for _ in range(3))
-    gl = torch.randn(Bs, Ls, 3, device=dev, dtype=torch.bfloat16)
+        ms, _ = time_op(topk_prefill, 5, 1)
+        # scoring flops: every query against the centroids of the blocks at or before its own
+        fl = 2 * di * Bq * sum(min(t // 64 + 1, L // 64) for t in range(0, L, 64)) * 64
+        out["index_topk_prefill"] = {"ms_per_call": ms, "queries_per_s": Bq * L / (ms * 1e-3),
+                                     "roofline": {"bound": "mfma", "achieved": fl / (ms * 1e-3) / 1e12,
+                                                  "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                                  "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                                                  "algorithmic_flops": fl, "traffic": None},
+                                     "config": "B=1 L=32768 d=128 bf16, 512 centroids, top-32, causal"}
+        log(f"index_topk prefill 32k x 512: {ms:.3f} ms")
+        del qi, cent
+    if want("superposition"):
+        # gate superposition of three prefill stream outputs [1, 10, 32768, 64] bf16 with
+        # [1, 32768, 3] logits (the layer's prefill combine, sparse_attention.py:219)
+        Bs, Hs, Ls, Ds = 1, 10, 32768, 64
+        ol, os_, oh = (torch.randn(Bs, Hs, Ls, Ds, device=dev, dtype=torch.bfloat16) for _ in range(3))
+        gl = torch.randn(Bs, Ls, 3, device=dev, dtype=torch.bfloat16)
 
-    def superpose():
-        return hb.hip_stream_superposition(ol, os_, oh, gate_logits=gl)
+        def superpose():
+            return hb.hip_stream_superposition(ol, os_, oh, gate_logits=gl)
 
-    ms, _ = time_op(superpose, 20, 3)
-    sb = 4 * Bs * Hs * Ls * Ds * 2 + Bs * Ls * 3 * 2
-    out["stream_superposition"] = {"us_per_call": ms * 1e3, "gbs": sb / (ms * 1e-3) / 1e9,
-                                   "hbm_frac": sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": sb,
-                                   "config": "o_* [1,10,32768,64] bf16, gate logits [1,32768,3] bf16"}
-    log(f"stream superposition 1x10x32768x64: {ms * 1e3:.1f} us")
-    del ol, os_, oh, gl
-    out.update(prefill_attention_bench(dev))
-    out["maba_sa_layer_decode_1M"] = layer_decode_bench(dev)
-    out.update(model_decode_bench(dev))
+        ms, _ = time_op(superpose, 20, 3)
+        sb = 4 * Bs * Hs * Ls * Ds * 2 + Bs * Ls * 3 * 2
+        out["stream_superposition"] = {"us_per_call": ms * 1e3, "gbs": sb / (ms * 1e-3) / 1e9,
+                                       "hbm_frac": sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": sb,
+                                       "config": "o_* [1,10,32768,64] bf16, gate logits [1,32768,3] bf16"}
+        log(f"stream superposition 1x10x32768x64: {ms * 1e3:.1f} us")
+        del ol, os_, oh, gl
+    if want("prefill_attention"):
+        out.update(prefill_attention_bench(dev))
+    if want("layer_decode"):
+        out["maba_sa_layer_decode_1M"] = layer_decode_bench(dev)
+    if want("model"):
+        out.update(model_decode_bench(dev))
     return out
 
 
@@ -594,7 +617,8 @@ def prefill_attention_bench(dev, B=1, H=10, L=32768, dh=64, dc=128, K=32):
     keys = (n_loc + n_sp + n_hca).double().sum().item()
     fl = keys * H * B * 4 * dc
     rf = {"bound": "mfma", "achieved": fl / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-          "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "algorithmic_flops": fl, "traffic": None}
+          "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "algorithmic_flops": fl,
+          "traffic": measured_traffic("maba_sa_prefill_latent_bytes_per_call"), "traffic_source": TRAFFIC_SOURCE}
     return {"maba_sa_prefill_32k": {
         "ms_per_call": ms_comp, "kernel_ms": ms, "head_space_kernel_ms": ms_heads,
         "queries_per_s": B * L / (ms_comp * 1e-3), "keys_per_query": keys / (B * L),
@@ -822,7 +846,7 @@ def main():
         print(json.dumps({"decode": decode_benches(dev, args.steps)}), flush=True)
         return
     if args.only_rows:
-        print(json.dumps({"rows": row_benches(dev)}), flush=True)
+        print(json.dumps({"rows": row_benches(dev, args.row.split(",") if args.row else None)}), flush=True)
         return
     if args.only_model:
         print(json.dumps({"rows": model_decode_bench(dev, args.model_batch, args.model_prefill, args.model_steps)}),
@@ -842,10 +866,7 @@ def main():
     nbytes = prefill_bytes(B, H, T, d)
     flops = prefill_flops(B, H, T, d)
     achieved = nbytes / (ms * 1e-3) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as fh:
-            traffic = json.load(fh).get("dgda_prefill_bytes_per_step")
+    traffic = measured_traffic("dgda_prefill_bytes_per_step")
     res = {
         "metric": "DGDA prefill tok/s @T=32k; MABA-SA decode us/step @1M ctx; % roofline",
         "value": tok_s,
@@ -863,7 +884,7 @@ def main():
                    "d_k": d, "d_v": d, "chunk": 64, "qkv": "bf16", "gates": "fp32 per-token (stride-0)",
                    "state": "fp32", "out": "bf16", "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": TRAFFIC_SOURCE,
                      "kernel": "dgda_prefill op (aggregate + zero-start + fix-up launches)",
                      "algorithmic_bytes": nbytes},
         "mfma": {"achieved": flops / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
