@@ -400,29 +400,34 @@ __device__ __forceinline__ SaRows sa_rows(const SaArgs& a, int64_t b) {
   return r;
 }
 
-// Key rows 16 rb + c16 of tile tix of a stream (0 local, 1 sparse, 2 HCA; wave-uniform),
-// dims 32 p + 8 g .. +7, without branches: a tile's first row and the row limits are
-// uniform, and a local row past the sinks shifts to the window.  Invalid rows read row 0 of
+// Key rows 16 rb + c16 (rb < RB: tiles of 16 RB keys) of tile tix of a stream (0 local,
+// 1 sparse, 2 HCA; wave-uniform), dims 32 p + 8 g .. +7, without branches: a tile's first
+// row and the row limits are uniform, and a local row past the sinks shifts to the window.
+// A sparse block spans ceil(block_size / (16 RB)) tiles: tile tix is part tix % that of
+// its block.  Invalid rows read row 0 of
 // the stream (in bounds: L >= 1, and the HCA stream is only walked when it has entries);
 // their scores are masked to -inf, so they get zero weight.  blk is the tile's block index
 // for the sparse stream.  Bit 4 rb + i of okb says whether key row 16 rb + 4 g + i (a row of
 // this lane's score accumulators) is valid.  Row offsets are 32-bit (the hosts check that a
 // sequence's rows span fewer than 2^31 elements).
-template <int NP>
+template <int NP, int RB = 4>
 __device__ __forceinline__ void sa_load_rows(const SaRows& r, int stream, int64_t tix, int64_t blk, int c16, int g,
-                                             s16x8 (&cv)[4][NP], uint32_t& okb) {
+                                             s16x8 (&cv)[RB][NP], uint32_t& okb) {
+  constexpr int TK = 16 * RB;
   const uint16_t* base = stream == 2 ? r.hca : r.c;
   const int rstride = (int)(stream == 2 ? r.hs : r.cs);
   const int64_t nblk = (r.L + r.bs - 1) / r.bs;
   const bool blk_ok = blk >= 0 && blk < nblk;
-  const int first = (int)(stream == 1 ? (blk_ok ? blk * r.bs : 0) : tix * 64);
+  int part = 0;   // the tile's part of its sparse block (block_size <= 64: one part of a 64-key tile)
+  if constexpr (RB < 4) part = (int)(tix % ((r.bs + TK - 1) / TK));
+  const int first = (int)(stream == 1 ? (blk_ok ? blk * r.bs + part * TK : 0) : tix * TK);
   // rows [first, lim) are valid; local rows at or past the sinks move by `shift`
   const int lim = stream == 0 ? r.nloc : stream == 2 ? r.nc : (blk_ok ? (int)min(r.L, (int64_t)first + r.bs) : 0);
   const int thr = stream == 0 ? r.ns : INT32_MAX;
   const int shift = stream == 0 ? r.loc_start - r.ns : 0;
   okb = 0;
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
+  for (int rb = 0; rb < RB; ++rb) {
     const int p0 = first + 16 * rb + c16;
     const bool ok = p0 < lim;
     const int pos = ok ? p0 + (p0 >= thr ? shift : 0) : 0;
@@ -466,7 +471,7 @@ __device__ __forceinline__ void sa_acc_close(SaAcc<NP>& st, bool head_on) {
 // would wait for the loads).  Loads past the last tile re-read it (in bounds, unused);
 // unconditional loads keep the register pressure at that of straight-line code.  blk_of(t)
 // is the sparse block index of tile t (wave-uniform).
-template <int NP, class BlkOf>
+template <int NP, int RB = 4, class BlkOf>
 __device__ __forceinline__ void sa_stream_tiles(const SaRows& rows, int stream, int64_t t0, int64_t t1, BlkOf blk_of,
                                                 const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile,
                                                 int c16, int g, SaAcc<NP>& st);
@@ -477,15 +482,16 @@ __device__ __forceinline__ void sa_stream_tiles(const SaRows& rows, int stream, 
 // column of a head that does not attend to the stream is discarded by the caller, see
 // sa_acc_close); a tile whose 64 keys are all valid skips the masking, and the rescale of
 // Z is skipped when no column's running max moved (both tests wave-uniform).
-template <int NP>
-__device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t okb,
+template <int NP, int RB = 4>
+__device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[RB][NP], uint32_t okb,
                                              const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile, int c16,
                                              int g, SaAcc<NP>& st) {
+  static_assert(RB == 2 || RB == 4, "tiles of 32 or 64 keys");
   constexpr int DC = 32 * NP;
   constexpr int TP = DC + 8;
-  f32x4 sc[4];
+  f32x4 sc[RB];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
+  for (int rb = 0; rb < RB; ++rb) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -499,9 +505,9 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t 
   }
   // lane (head c16, group g) holds scores of keys 16 rb + 4g + i
   float tmax = -INFINITY;
-  if (__ballot(okb != 0xffffu) != 0ull) {   // some key of the tile is invalid
+  if (__ballot(okb != (1u << (4 * RB)) - 1u) != 0ull) {   // some key of the tile is invalid
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float x = ((okb >> (4 * rb + i)) & 1u) ? sc[rb][i] : -INFINITY;
@@ -511,7 +517,7 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t 
     }
   } else {
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
       tmax = fmaxf(fmaxf(tmax, fmaxf(sc[rb][0], sc[rb][1])), fmaxf(sc[rb][2], sc[rb][3]));
   }
   tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
@@ -521,9 +527,9 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t 
   const float corr = (m_new == -INFINITY || !grow) ? 1.f : __expf(st.m - m_new);
   const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;   // exp(-inf - m_sub) = 0 for masked keys
   float psum = 0.f;
-  s16x4 ph[4], pl[4];
+  s16x4 ph[RB], pl[RB];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
+  for (int rb = 0; rb < RB; ++rb) {
     f32x4 pv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -542,12 +548,12 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t 
   psum += __shfl_xor(psum, 32);
   st.l = st.l * corr + psum;
   st.m = m_new;
-  // z[dim][head] = corr * z + C^T P  (K = 64 keys as two permuted 32-steps)
+  // z[dim][head] = corr * z + C^T P  (the tile's keys as permuted 32-steps)
 #pragma unroll
   for (int dt = 0; dt < DC / 16; ++dt) {
     f32x4 acc = grow ? st.z[dt] * corr : st.z[dt];
 #pragma unroll
-    for (int p2 = 0; p2 < 2; ++p2) {
+    for (int p2 = 0; p2 < RB / 2; ++p2) {
       const s16x4 a0 = sa_ldsT4(tile, TP, 32 * p2, 16 * dt, c16, g);
       const s16x4 a1 = sa_ldsT4(tile, TP, 32 * p2 + 16, 16 * dt, c16, g);
       const s16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
@@ -564,22 +570,22 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[4][NP], uint32_t 
   }
 }
 
-template <int NP, class BlkOf>
+template <int NP, int RB, class BlkOf>
 __device__ __forceinline__ void sa_stream_tiles(const SaRows& rows, int stream, int64_t t0, int64_t t1, BlkOf blk_of,
                                                 const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile,
                                                 int c16, int g, SaAcc<NP>& st) {
   if (t0 >= t1) return;
-  s16x8 cvA[4][NP], cvB[4][NP];
+  s16x8 cvA[RB][NP], cvB[RB][NP];
   uint32_t okA = 0, okB = 0;
-  sa_load_rows<NP>(rows, stream, t0, blk_of(t0), c16, g, cvA, okA);
+  sa_load_rows<NP, RB>(rows, stream, t0, blk_of(t0), c16, g, cvA, okA);
   for (int64_t tix = t0; tix < t1; tix += 2) {
     const int64_t n1 = tix + 1 < t1 ? tix + 1 : tix;
-    sa_load_rows<NP>(rows, stream, n1, blk_of(n1), c16, g, cvB, okB);
-    sa_tile_step<NP>(cvA, okA, qh, ql, tile, c16, g, st);
+    sa_load_rows<NP, RB>(rows, stream, n1, blk_of(n1), c16, g, cvB, okB);
+    sa_tile_step<NP, RB>(cvA, okA, qh, ql, tile, c16, g, st);
     if (tix + 1 >= t1) break;
     const int64_t n2 = tix + 2 < t1 ? tix + 2 : tix + 1;
-    sa_load_rows<NP>(rows, stream, n2, blk_of(n2), c16, g, cvA, okA);
-    sa_tile_step<NP>(cvB, okB, qh, ql, tile, c16, g, st);
+    sa_load_rows<NP, RB>(rows, stream, n2, blk_of(n2), c16, g, cvA, okA);
+    sa_tile_step<NP, RB>(cvB, okB, qh, ql, tile, c16, g, st);
   }
 }
 
@@ -715,7 +721,13 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a_in) {
 // streams in proportion to their tile counts (each wave one stream, one online softmax),
 // then the partials of each stream are merged in LDS, gated and written as
 // z[b, t, h] = sum_s g_s sum_j p_sj c_j (fp32); the caller applies W_v,h.
+// Eight waves (two per SIMD) on 64-key tiles.  Twelve waves on 32-key tiles (three per SIMD
+// within 168 VGPRs, a few spilled) measured 4.84 ms against 4.02 ms at the 32k bench row: the
+// per-tile reductions and rescale are paid twice as often, and the third wave does not win
+// that back.
 constexpr int PL_W = 8;
+constexpr int PL_RB = 4;
+constexpr int PL_TK = 16 * PL_RB;
 
 struct PlArgs {
   const void* q; int qdt; int64_t qsb, qst, qsh, qsd; int qvec;   // q_lat [B, Lq, H, dc]
@@ -730,10 +742,11 @@ struct PlArgs {
 };
 
 template <int NP>
-__global__ __launch_bounds__(512, 1) void maba_sa_prefill_latent_kernel(PlArgs a) {
+__global__ __launch_bounds__(PL_W * 64, 1) void maba_sa_prefill_latent_kernel(PlArgs a) {
   constexpr int DC = 32 * NP;
   constexpr int TP = DC + 8;
-  __shared__ __attribute__((aligned(16))) short s_tile[PL_W][64 * TP];
+  __shared__ __attribute__((aligned(16))) short s_tile[PL_W][PL_TK * TP];
+  static_assert(PL_W * 16 * DC * sizeof(float) <= sizeof(s_tile), "the merge reuses the tiles' LDS");
   __shared__ float s_ml[PL_W][2][16];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int g = lane >> 4, c16 = lane & 15;
@@ -747,7 +760,10 @@ __global__ __launch_bounds__(512, 1) void maba_sa_prefill_latent_kernel(PlArgs a
   const int64_t ns = L < a.n_sink ? L : a.n_sink;
   const int64_t lst = (L - a.window) > ns ? (L - a.window) : ns;
   rows.ns = (int)ns; rows.loc_start = (int)lst; rows.nloc = (int)(ns + (L - lst)); rows.nc = (int)(L / a.pool);
-  const int tc0 = (rows.nloc + 63) / 64, tc1 = a.K, tc2 = (L - 1 >= a.pool - 1) ? (rows.nc + 63) / 64 : 0;
+  // tiles per stream (a sparse block is tpb tiles; the sparse waves split the K slots)
+  const int tpb = (a.bs + PL_TK - 1) / PL_TK;
+  const int tc0 = (rows.nloc + PL_TK - 1) / PL_TK, tc1 = a.K * tpb;
+  const int tc2 = (L - 1 >= a.pool - 1) ? (rows.nc + PL_TK - 1) / PL_TK : 0;
   // waves per stream: in proportion to the tile counts, at least one per nonempty stream
   // (scalars throughout: a small array indexed by the stream would go to scratch memory)
   const int T = tc0 + tc1 + tc2;
@@ -769,29 +785,32 @@ __global__ __launch_bounds__(512, 1) void maba_sa_prefill_latent_kernel(PlArgs a
   const int wb1 = n0, wb2 = n0 + n1, wend = n0 + n1 + n2;   // waves [0,wb1) local, [wb1,wb2) sparse, [wb2,wend) HCA
   const int stream = wave < wb1 ? 0 : (wave < wb2 ? 1 : (wave < wend ? 2 : -1));
   const int j = stream == 0 ? wave : (stream == 1 ? wave - wb1 : wave - wb2);
-  const int tcs = stream == 0 ? tc0 : (stream == 1 ? tc1 : tc2);
+  // units a wave's range is counted in: tiles, or K slots for the sparse stream
+  const int tcs = stream == 0 ? tc0 : (stream == 1 ? a.K : tc2);
   const int nws = stream == 0 ? n0 : (stream == 1 ? n1 : n2);
-  int64_t t0 = 0, t1 = 0;
+  int64_t u0 = 0, u1 = 0;
   if (stream >= 0) {
     const int per = (tcs + nws - 1) / nws;
-    t0 = (int64_t)j * per;
-    t1 = min((int64_t)tcs, t0 + per);
+    u0 = (int64_t)j * per;
+    u1 = min((int64_t)tcs, u0 + per);
   }
+  const int64_t t0 = stream == 1 ? u0 * tpb : u0, t1 = stream == 1 ? u1 * tpb : u1;
   short* tile = s_tile[wave];
   s16x8 qh[NP], ql[NP];
   sa_query_split<NP>(a.q, a.qdt, b * a.qsb + t * a.qst, a.qsh, a.qsd, a.qvec, a.H, a.scale, c16, g, qh, ql);
   const bool head_on = c16 < a.H;
   SaAcc<NP> st;
   sa_acc_init(st);
+  // the wave's sparse slots [u0, u1) (at most 64: K <= 64), one block index per lane
   int64_t blk_l = 0;
-  if (stream == 1 && lane < t1 - t0) blk_l = a.idx[b * a.isb + t * a.ist + (t0 + lane) * a.isk];
+  if (stream == 1 && lane < u1 - u0) blk_l = a.idx[b * a.isb + t * a.ist + (u0 + lane) * a.isk];
   auto blk_of = [&](int64_t tix) {
-    const int src = (int)(tix - t0);
+    const int src = (int)(tix / tpb - u0);
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)blk_l, src);
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)blk_l >> 32), src);
     return (int64_t)(((uint64_t)hi << 32) | lo);
   };
-  if (stream >= 0) sa_stream_tiles<NP>(rows, stream, t0, t1, blk_of, qh, ql, tile, c16, g, st);
+  if (stream >= 0) sa_stream_tiles<NP, PL_RB>(rows, stream, t0, t1, blk_of, qh, ql, tile, c16, g, st);
   sa_acc_close(st, head_on);
   // wave partials to LDS (the tiles are free once every wave is past its loop)
   __syncthreads();

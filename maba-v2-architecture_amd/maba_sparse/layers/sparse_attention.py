@@ -116,6 +116,10 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         self.indexer = DGIndexer(dim=self.dim, d_idx=d_idx, block_size=self.block_size, top_k=self.top_k,
                                  dist_lambda=self.dist_lambda)
         self._hca_means: Optional[_Growing] = None
+        # fused bf16 prefill: "auto" picks the latent or the head-space kernel from the
+        # selections' sharing (see _prefill_form); the union limit is in units of top_k
+        self.prefill_form = "auto"
+        self.prefill_union_limit = 4.0
         self._install_weight_cache_hooks()
 
     def reset_cache(self) -> None:
@@ -235,7 +239,7 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         kernel's head sizes and 64-token blocks, no gradients and the full three streams."""
         if q.device.type != "cuda" or get_backend(q.device) != "hip" or self.ablation_mode == "no_hca":
             return False
-        if q.dtype != torch.bfloat16 or c_full.dtype != torch.bfloat16 or self.d_head not in (32, 64, 128):
+        if q.dtype != torch.bfloat16 or c_full.dtype != torch.bfloat16:
             return False
         if self.block_size != 64 or idx.shape[-1] > 64 or c_full.shape[1] > (1 << 20):
             return False
@@ -243,7 +247,34 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
             return False
         return not (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()))
 
+    def _prefill_form(self, idx: torch.Tensor) -> str:
+        """``"latent"`` or ``"heads"`` for a fused prefill with selections ``idx [B, Lq, K]``.
+
+        The latent kernel does each query's tiles on its own (the ten heads share every key row,
+        as at decode); the head-space kernel gives each run of 16 queries the union of their
+        blocks (16 queries share every key tile, per head).  Per tile the head-space kernel
+        issues about a quarter of the latent kernel's MFMA work for the same 16 queries, so it
+        wins while the union of 16 consecutive queries' blocks stays below about 4 K (neighbouring
+        queries of a trained or randomly initialised model select nearly the same blocks) and
+        loses when the selections scatter (random queries give 5 K).  The union is counted on
+        the GPU from ``idx`` (one segmented sort); ``self.prefill_form`` may force either."""
+        if self.prefill_form != "auto":
+            return self.prefill_form
+        B, Lq, K = idx.shape
+        if Lq == 1:   # one selection shared by every query
+            return "heads"
+        if Lq < 16:
+            return "latent"
+        grp = idx[:, : (Lq // 16) * 16].reshape(B, Lq // 16, 16 * K).sort(dim=-1).values
+        distinct = (grp[..., 1:] != grp[..., :-1]).sum(dim=-1).float().mean().item() + 1.0
+        return "heads" if distinct < self.prefill_union_limit * K else "latent"
+
     def _fused_prefill(self, x, q, c_full, idx):
+        if self._prefill_form(idx) == "heads" and self.d_head in (32, 64, 128):
+            return self._fused_prefill_heads(x, q, c_full, idx)
+        return self._fused_prefill_latent(x, q, c_full, idx)
+
+    def _fused_prefill_latent(self, x, q, c_full, idx):
         """The three streams and the gate in latent form: ``q_lat = W_k,h^T q_h`` per query, one
         ``maba_sa_prefill_latent`` launch over the bf16 latent rows and their complete-block
         means, then ``o_h = W_v,h z_h``.  Keys and values are never up-projected (the cache is

@@ -80,13 +80,16 @@ def test_maba_sa_prefill_long_against_torch_reference(dev):
     assert_close(out, to_np(ref), 2e-3, 2e-3, "maba_sa_prefill 4k")
 
 
-def test_layer_prefill_fused_matches_dense_path(dev):
-    """The bf16 MabaSparseAttention prefill through the HIP kernel against the same layer's
-    dense torch path, then decode steps continue from either."""
+@pytest.mark.parametrize("form", ["latent", "heads", "auto"])
+def test_layer_prefill_fused_matches_dense_path(dev, form):
+    """The bf16 MabaSparseAttention prefill through either HIP kernel (the latent form, the
+    head-space union form, or the layer's choice between them) against the same layer's dense
+    torch path."""
     from maba_sparse.layers import MabaSparseAttention
     torch.manual_seed(8)
     layer = MabaSparseAttention(dim=256, n_heads=4, d_head=64, d_c=64, d_idx=32, top_k=8,
                                 dist_lambda=0.1).to(dev, torch.bfloat16).eval()
+    layer.prefill_form = form
     dense = copy.deepcopy(layer)
     dense._prefill_fusable = lambda *a: False
     x = torch.randn(2, 700, 256, device=dev, dtype=torch.bfloat16)

@@ -199,3 +199,20 @@ def test_sa_ablation_no_hca_uses_dense_path():
         y, c = layer(x)
         y1, _ = layer(x[:, 69:], past_c_kv=c[:, :69])
     assert y.shape == (1, 70, 64) and y1.shape == (1, 1, 64)
+
+
+def test_prefill_form_follows_selection_sharing():
+    """The fused prefill takes the head-space union kernel when 16 consecutive queries share
+    their blocks and the latent kernel when their selections scatter (the union of 16 query
+    rows is counted from the indices)."""
+    from maba_sparse.layers import MabaSparseAttention
+    layer = MabaSparseAttention(dim=64, n_heads=2, d_head=32, d_c=32, d_idx=16, top_k=8)
+    B, Lq, K = 2, 64, 8
+    shared = torch.arange(K).repeat(B, Lq, 1)                            # every query the same 8 blocks
+    assert layer._prefill_form(shared) == "heads"
+    g = torch.Generator().manual_seed(0)
+    scattered = torch.stack([torch.randperm(4096, generator=g)[:K] for _ in range(B * Lq)]).view(B, Lq, K)
+    assert layer._prefill_form(scattered) == "latent"
+    assert layer._prefill_form(shared[:, :1]) == "heads"                 # one row for all queries
+    layer.prefill_form = "latent"
+    assert layer._prefill_form(shared) == "latent"
