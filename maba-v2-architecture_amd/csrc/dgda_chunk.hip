@@ -162,6 +162,8 @@ struct ChunkSmem {
   SM_ALIGN short TL[4 * TILE_ELEMS];
   SM_ALIGN float LD[4 * DTILE_ELEMS];  // L_II in fp32 for the inverses
   SM_ALIGN float lam2[CH];   // inclusive cumulative log-decay, in log2 units
+  SM_ALIGN float rf[3][CH];  // 2^{lam2_i - lam2_{16J+15}}: row factors of the off-diagonal tiles (I,J)
+  SM_ALIGN float cf[CH];     // 2^{lam2_{16J+15} - lam2_j}, J = j/16: their column factors
   SM_ALIGN float elam[CH];   // e^Lam
   SM_ALIGN float eend[CH];   // e^{Lam_63 - Lam}
   SM_ALIGN float beta[CH];
@@ -324,7 +326,20 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
       const float s = wave_incl_scan(la);   // inclusive prefix sum of the log decay
       const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
       const float el = __expf(s);
-      sm.lam2[lane] = s * 1.4426950408889634f;
+      const float l2 = s * 1.4426950408889634f;
+      sm.lam2[lane] = l2;
+      // Off-diagonal decay factors: for i in block I > J and j in block J,
+      // 2^{l2_i - l2_j} = 2^{l2_i - r_J} 2^{r_J - l2_j} with r_J = l2 at token 16J + 15;
+      // l2 does not increase, so both factors are <= 1 (rows i <= 16J + 15 never use rf[J]).
+      const float rJ[3] = {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), 15)),
+                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), 31)),
+                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), 47))};
+      const float rown = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), 63));
+      const int jb = lane >> 4;
+      const float rj = jb == 0 ? rJ[0] : jb == 1 ? rJ[1] : jb == 2 ? rJ[2] : rown;
+      sm.cf[lane] = __builtin_amdgcn_exp2f(fminf(rj - l2, 0.f));
+#pragma unroll
+      for (int J = 0; J < 3; ++J) sm.rf[J][lane] = __builtin_amdgcn_exp2f(fminf(l2 - rJ[J], 0.f));
       sm.elam[lane] = el;
       sm.eend[lane] = __expf(last - s);
       sm.beta[lane] = pbe;
@@ -355,18 +370,26 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
         acc = mma32(acc, av, bv);
       }
       const int i = 16 * I + c16;
-      const float li = sm.lam2[i];
-      const f32x4 lj = *(const f32x4*)(sm.lam2 + 16 * J + 4 * g);
       f32x4 val;
+      if constexpr (I > J) {
+        // off-diagonal: the factored decay, row factor (with -beta_i for L: off-diagonal
+        // L tiles are stored negated, the solve accumulates -L_IJ u_J onto v_e_I) times
+        // the column factors
+        const float ri = ISA ? sm.rf[J][i] : -sm.beta[i] * sm.rf[J][i];
+        const f32x4 cj = *(const f32x4*)(sm.cf + 16 * J + 4 * g);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * J + 4 * g + r;
-        const float x = acc[r] * __builtin_amdgcn_exp2f(li - lj[r]);
-        if (I > J) val[r] = x;
-        else val[r] = (ISA ? j <= i : j < i) ? x : 0.f;
+        for (int r = 0; r < 4; ++r) val[r] = (acc[r] * ri) * cj[r];
+      } else {
+        const float li = sm.lam2[i];
+        const f32x4 lj = *(const f32x4*)(sm.lam2 + 16 * J + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * J + 4 * g + r;
+          const float x = acc[r] * __builtin_amdgcn_exp2f(li - lj[r]);
+          val[r] = (ISA ? j <= i : j < i) ? x : 0.f;
+        }
+        if (!ISA) val = val * sm.beta[i];
       }
-      // off-diagonal L tiles are stored negated: the solve accumulates -L_IJ u_J onto v_e_I
-      if (!ISA) val = val * (I == J ? sm.beta[i] : -sm.beta[i]);
       if (!ISA && I == J) {   // diagonal L tiles only feed the inverses, in fp32
         *(f32x4*)(sm.LD + I * DTILE_ELEMS + c16 * DPITCH + 4 * g) = val;
         return;

@@ -38,17 +38,24 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-// hi's fp32 values are unpacked from the two packed dwords (element 2m in the low half
-// of dword m).
+// x - hi for the element of a packed bf16 pair selected by SEL (0: low half), as one
+// v_dot2c_f32_bf16: (hi0, hi1) . (-1, -0) + x (or (-0, -1)).  The products are exact and
+// x - hi is representable in fp32, so the result is the exact remainder.  The unused
+// half is -0, not +0: the compiler encodes the pair (-1, +0) as the inline constant
+// -1.0, which the instruction reads as the 32-bit pattern (+0, -1) -- the wrong half --
+// while (-1, -0) and (-0, -1) stay literals (checked bit for bit against x - float(hi)
+// on 2^19 pairs of the gfx950 build).
+template <int SEL>
+__device__ __forceinline__ float bf16_rem(uint32_t hpair, float x) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+  const bf16x2 neg1 = __builtin_bit_cast(bf16x2, SEL ? 0xbf808000u : 0x8000bf80u);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, hpair), neg1, x, false);
+}
+
 __device__ __forceinline__ void split4(f32x4 x, i16x4& hi, i16x4& lo) {
   typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
   const uint32_t h01 = cvt_pk_bf16(x[0], x[1]), h23 = cvt_pk_bf16(x[2], x[3]);
-  f32x4 hf;
-  hf[0] = __uint_as_float(h01 << 16);
-  hf[1] = __uint_as_float(h01 & 0xffff0000u);
-  hf[2] = __uint_as_float(h23 << 16);
-  hf[3] = __uint_as_float(h23 & 0xffff0000u);
-  const f32x4 r = x - hf;
+  const f32x4 r = {bf16_rem<0>(h01, x[0]), bf16_rem<1>(h01, x[1]), bf16_rem<0>(h23, x[2]), bf16_rem<1>(h23, x[3])};
   const u32x2 hv = {h01, h23}, lv = {cvt_pk_bf16(r[0], r[1]), cvt_pk_bf16(r[2], r[3])};
   hi = __builtin_bit_cast(i16x4, hv);
   lo = __builtin_bit_cast(i16x4, lv);
