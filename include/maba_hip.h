@@ -41,6 +41,9 @@
  *   maba_hip_dgda_layer_prefill     layers/dgda.py:103-121,186-233 (the prologue
  *                                   above fused into the prefill kernels' input
  *                                   staging, then the chunked recurrence)
+ *   maba_hip_dgda_layer_step        layers/dgda.py:103-121,186-207 then
+ *                                   dispatcher.py:330-396 (the decode prologue above
+ *                                   and the step in one launch)
  *   maba_hip_cache_append           layers/indexer.py:62-82 (key cache, complete
  *                                   and tail centroids), layers/sparse_attention.py:
  *                                   206, 241-251 (latent rows, HCA block means)
@@ -289,6 +292,19 @@ int maba_hip_maba_sa_decode_dev(const maba_tensor* q_lat, const maba_tensor* c_k
                                 float scale, int window, int n_sink, int block_size, int pool,
                                 maba_tensor* out_lat, void* workspace, size_t workspace_bytes,
                                 void* stream);
+
+/* One decode token of the DGDA layer after its input projection: the single-token prologue
+ * of maba_hip_dgda_prologue (conv + SiLU over the carried history, key norm, gates, new
+ * history) and maba_hip_dgda_step in one launch, with q, k, v rounded to bf16 and the gates
+ * kept in fp32 as those two store them (the results equal theirs).  xs: the six bf16
+ * projections [B,C] or [B,1,C] (q, k, v, decay, erase, write; unit channel stride, C = 64 H),
+ * conv_w [C,1,4] x3 (f32/bf16, one dtype), hist [B,C,3] x3 bf16 or NULL (zeros), eps the
+ * key-norm epsilon, state [B,H,64,64] f32/bf16 or NULL (zero), out [B,H,64] f32/bf16,
+ * new_state like state (may alias it), new_hist [B,C,3] x3 bf16 (may alias hist). */
+int maba_hip_dgda_layer_step(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
+                             const maba_tensor* const* hist, float eps, const maba_tensor* state,
+                             maba_tensor* out, maba_tensor* new_state, maba_tensor* const* new_hist,
+                             void* stream);
 
 /* h = x' / sqrt(mean(x'^2) + eps) * weight over the last dim C (even, <= 2048), where
  * x' = x + gate * mo when mo is given (gate [C]), else x; x' is written to x_out when given

@@ -10,7 +10,7 @@
 // each thread owns one column c and a contiguous run of rows, keeps its slice
 // of S' in registers between the two reductions, and writes S_new once.  The
 // kernel is HBM-bound on the state read + write (8*dk*dv bytes per head).
-#include "maba_common.h"
+#include "dgda_common.h"
 
 namespace maba {
 
@@ -167,6 +167,104 @@ __global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
   store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
 }
 
+// One decode token of the DGDA layer after its input projection, in one launch: the
+// single-token prologue (layers/dgda.py:103-121, 186-207: causal depthwise conv + SiLU of
+// q, k, v over the carried history, the key's head L2 norm, the decay, erase and write
+// gates; the new history) followed by the step above, for one (b, h) per wave with
+// lane = channel of the head, the layout of both parts.  q, k, v are rounded to bf16
+// before the step and the gates kept in fp32, as the two separate launches store them,
+// so the results equal theirs.  Every input of the wave (state column, projections,
+// history) is read before its first store, so the state and the history update in place.
+struct LayerStepArgs {
+  const uint16_t* x[6]; int64_t xsb[6];                       // bf16 projection rows [B, C]
+  const void* cw[3]; int cwdt; int64_t cwsc[3], cwst[3];      // conv taps [C, 1, 4]
+  const uint16_t* hist[3]; int64_t hsb[3], hsc[3], hst[3];    // bf16 [B, C, 3] or null (zeros)
+  uint16_t* nh[3]; int64_t nhsb[3], nhsc[3], nhst[3];         // bf16 new history (may alias hist)
+  const void* state; int64_t ssb, ssh, ssr;                   // [B, H, 64, 64] (TS) or null (zero)
+  void* nst; int64_t nsb, nsh, nsr;                           // may alias state
+  void* out; int odt; int64_t osb, osh, osd;                  // o [B, H, 64]
+  int64_t BH;
+  int H;
+  float eps;
+};
+
+template <typename TS>
+__global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t bh = (int64_t)blockIdx.x * 4 + wave;
+  if (bh >= a.BH) return;  // wave-uniform; no barriers
+  const int64_t bi = bh / a.H, hi = bh % a.H;
+  const int64_t c = hi * 64 + lane;   // channel of the projection rows
+  float s[64];
+  if (a.state) {
+    const int64_t S = bi * a.ssb + hi * a.ssh + lane;
+#pragma unroll
+    for (int r = 0; r < 64; ++r) s[r] = ldf<TS>(a.state, S + r * a.ssr);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 64; ++r) s[r] = 0.f;
+  }
+  // ---- prologue (as dgda_prologue_step_kernel)
+  float x[6], w[3][4], h[3][3];
+#pragma unroll
+  for (int st = 0; st < 6; ++st) x[st] = bf16_bits_to_f32(a.x[st][bi * a.xsb[st] + c]);
+#pragma unroll
+  for (int st = 0; st < 3; ++st) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[st][j] = load_elem(a.cw[st], a.cwdt, c * a.cwsc[st] + j * a.cwst[st]);
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      h[st][j] = a.hist[st] ? bf16_bits_to_f32(a.hist[st][bi * a.hsb[st] + c * a.hsc[st] + j * a.hst[st]]) : 0.f;
+  }
+  float y[3];
+#pragma unroll
+  for (int st = 0; st < 3; ++st) {
+    float acc = w[st][3] * x[st];
+    acc = fmaf(w[st][2], h[st][2], acc);
+    acc = fmaf(w[st][1], h[st][1], acc);
+    acc = fmaf(w[st][0], h[st][0], acc);
+    y[st] = pro_silu(acc);
+  }
+#pragma unroll
+  for (int st = 0; st < 3; ++st) {   // new history: the inputs of tokens -2, -1, 0
+    uint16_t* nh = a.nh[st] + bi * a.nhsb[st] + c * a.nhsc[st];
+    nh[0] = f32_to_bf16_bits(h[st][1]);
+    nh[a.nhst[st]] = f32_to_bf16_bits(h[st][2]);
+    nh[2 * a.nhst[st]] = f32_to_bf16_bits(x[st]);
+  }
+  float ss = y[1] * y[1];
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
+  const float kinv = pro_knorm_inv(ss, a.eps);
+  // lane r holds the row-r scalars of the step (q, k, decay, erase), lane c the column ones (v, write)
+  const float qr = bf16_bits_to_f32(f32_to_bf16_bits(y[0]));
+  const float kr = bf16_bits_to_f32(f32_to_bf16_bits(y[1] * kinv));
+  const float vc = bf16_bits_to_f32(f32_to_bf16_bits(y[2]));
+  const float gr = pro_log_decay(x[3]);
+  const float br = pro_sigmoid(x[4]);
+  const float wc = pro_sigmoid(x[5]);
+  // ---- step (as dgda_step_wave_kernel with log_alpha)
+  const float al = __expf(gr);
+  const float bk = br * kr;
+  float pred = 0.f;
+#pragma unroll
+  for (int r = 0; r < 64; ++r) {
+    s[r] *= bcast(al, r);
+    pred = fmaf(bcast(bk, r), s[r], pred);
+  }
+  const float delta = wc * vc - pred;
+  float o = 0.f;
+  const int64_t N = bi * a.nsb + hi * a.nsh + lane;
+#pragma unroll
+  for (int r = 0; r < 64; ++r) {
+    const float sn = fmaf(bcast(kr, r), delta, s[r]);
+    if constexpr (sizeof(TS) == 4) ((float*)a.nst)[N + r * a.nsr] = sn;
+    else ((uint16_t*)a.nst)[N + r * a.nsr] = f32_to_bf16_bits(sn);
+    o = fmaf(bcast(qr, r), sn, o);
+  }
+  store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
+}
+
 }  // namespace maba
 
 using namespace maba;
@@ -247,4 +345,63 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
   else if (dv <= 64) hipLaunchKernelGGL(dgda_step_kernel<64>, grid, block, 0, s, a);
   else hipLaunchKernelGGL(dgda_step_kernel<128>, grid, block, 0, s, a);
   return check_launch("dgda_step");
+}
+
+extern "C" int maba_hip_dgda_layer_step(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
+                                        const maba_tensor* const* hist, float eps, const maba_tensor* state,
+                                        maba_tensor* out, maba_tensor* new_state, maba_tensor* const* new_hist,
+                                        void* stream) {
+  const char* who = "dgda_layer_step";
+  if (!xs || !conv_w || !new_hist || !out || !new_state)
+    return fail(MABA_ERR_INVALID, "%s: xs, conv_w and new_hist arrays, out and new_state required", who);
+  if (out->ndim != 3 || out->shape[2] != 64)
+    return fail(MABA_ERR_UNSUPPORTED, "%s: out must be [B,H,64] (64-channel heads)", who);
+  const int64_t B = out->shape[0], H = out->shape[1], C = 64 * H;
+  if (H < 1 || H > 16) return fail(MABA_ERR_UNSUPPORTED, "%s: 1 <= H <= 16", who);
+  if (out->dtype != MABA_F32 && out->dtype != MABA_BF16) return fail(MABA_ERR_DTYPE, "%s: out f32 or bf16", who);
+  LayerStepArgs a;
+  for (int st = 0; st < 6; ++st) {   // [B, C] or [B, 1, C] bf16 rows with unit channel stride
+    const maba_tensor* t = xs[st];
+    const bool ok = t && t->dtype == MABA_BF16 && t->shape[0] == B && t->shape[t->ndim - 1] == C &&
+                    t->stride[t->ndim - 1] == 1 && (t->ndim == 2 || (t->ndim == 3 && t->shape[1] == 1));
+    if (!ok) return fail(MABA_ERR_INVALID, "%s: projection %d must be bf16 [B,C] or [B,1,C], C = 64 H, unit channel stride", who, st);
+    a.x[st] = (const uint16_t*)t->data;
+    a.xsb[st] = t->stride[0];
+  }
+  for (int st = 0; st < 3; ++st) {
+    const maba_tensor* w = conv_w[st];
+    if (!w || w->ndim != 3 || w->shape[0] != C || w->shape[1] != 1 || w->shape[2] != 4 ||
+        (w->dtype != MABA_F32 && w->dtype != MABA_BF16))
+      return fail(MABA_ERR_INVALID, "%s: conv weight %d must be [C,1,4] f32/bf16", who, st);
+    if (st > 0 && w->dtype != conv_w[0]->dtype) return fail(MABA_ERR_DTYPE, "%s: conv weights of one dtype", who);
+    a.cw[st] = w->data; a.cwsc[st] = w->stride[0]; a.cwst[st] = w->stride[2];
+    const int64_t hs[3] = {B, C, 3};
+    const maba_tensor* hh = hist ? hist[st] : nullptr;   // no history array: zeros
+    if (hh && (!expect_shape(hh, "hist", 3, hs) || hh->dtype != MABA_BF16))
+      return fail(MABA_ERR_INVALID, "%s: history %d must be bf16 [B,C,3]", who, st);
+    a.hist[st] = hh ? (const uint16_t*)hh->data : nullptr;
+    a.hsb[st] = hh ? hh->stride[0] : 0; a.hsc[st] = hh ? hh->stride[1] : 0; a.hst[st] = hh ? hh->stride[2] : 0;
+    maba_tensor* nh = new_hist[st];
+    if (!nh || !expect_shape(nh, "new_hist", 3, hs) || nh->dtype != MABA_BF16)
+      return fail(MABA_ERR_INVALID, "%s: new history %d must be bf16 [B,C,3]", who, st);
+    a.nh[st] = (uint16_t*)nh->data; a.nhsb[st] = nh->stride[0]; a.nhsc[st] = nh->stride[1]; a.nhst[st] = nh->stride[2];
+  }
+  a.cwdt = conv_w[0]->dtype;
+  const int64_t ss4[4] = {B, H, 64, 64};
+  if (!expect_shape(new_state, "new_state", 4, ss4) || new_state->stride[3] != 1 ||
+      (new_state->dtype != MABA_F32 && new_state->dtype != MABA_BF16))
+    return fail(MABA_ERR_INVALID, "%s: new_state must be f32/bf16 [B,H,64,64] with unit column stride", who);
+  if (state && (!expect_shape(state, "state", 4, ss4) || state->stride[3] != 1 || state->dtype != new_state->dtype))
+    return fail(MABA_ERR_INVALID, "%s: state must match new_state", who);
+  a.state = state ? state->data : nullptr;
+  a.ssb = state ? state->stride[0] : 0; a.ssh = state ? state->stride[1] : 0; a.ssr = state ? state->stride[2] : 0;
+  a.nst = new_state->data; a.nsb = new_state->stride[0]; a.nsh = new_state->stride[1]; a.nsr = new_state->stride[2];
+  a.out = out->data; a.odt = out->dtype; a.osb = out->stride[0]; a.osh = out->stride[1]; a.osd = out->stride[2];
+  a.BH = B * H; a.H = (int)H; a.eps = eps;
+  if (B == 0) return MABA_OK;
+  const dim3 g4((unsigned)ceil_div(B * H, 4));
+  hipStream_t s = (hipStream_t)stream;
+  if (new_state->dtype == MABA_BF16) hipLaunchKernelGGL(dgda_layer_step_kernel<uint16_t>, g4, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(dgda_layer_step_kernel<float>, g4, dim3(256), 0, s, a);
+  return check_launch(who);
 }

@@ -57,6 +57,7 @@ EXPORTED_SYMBOLS = (
     "maba_hip_maba_sa_prefill_latent",
     "maba_hip_dgda_layer_prefill_workspace_size",
     "maba_hip_dgda_layer_prefill",
+    "maba_hip_dgda_layer_step",
 )
 
 
@@ -108,6 +109,7 @@ def _declare(lib) -> None:
         "maba_hip_maba_sa_prefill_latent": ([T, T, T, T, T, f, i, i, i, i, T, vp], i),
         "maba_hip_dgda_layer_prefill_workspace_size": ([i64, i64, i64], sz),
         "maba_hip_dgda_layer_prefill": ([TA, TA, TA, f, T, T, T, TA, vp, sz, vp], i),
+        "maba_hip_dgda_layer_step": ([TA, TA, TA, f, T, T, T, TA, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

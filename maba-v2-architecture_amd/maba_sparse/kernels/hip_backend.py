@@ -392,6 +392,25 @@ def hip_maba_sa_prefill_latent(q_lat, c_kv, hca, idx, gate_logits, scale: float,
     return out
 
 
+def hip_dgda_layer_step(projections, conv_weights, history, state, eps: float = 1e-6, out=None):
+    """One decode token of the DGDA layer after its input projection (layers/dgda.py:103-121,
+    186-207, then the step of dispatcher.py:330-396) in one launch: ``projections`` are the
+    six bf16 ``[B, 1, C]`` (or ``[B, C]``) rows, ``history`` the three ``[B, C, 3]`` bf16 conv
+    histories and ``state`` the ``[B, H, 64, 64]`` state, both updated in place.  Returns the
+    head outputs ``o [B, H, 64]`` in the projections' dtype; equal to ``hip_dgda_prologue``
+    followed by ``hip_dgda_step``."""
+    dev = N.require_device([*projections, *conv_weights, *history, state], "dgda_layer_step")
+    B, C = projections[0].shape[0], projections[0].shape[-1]
+    H = C // 64
+    if out is None:
+        out = torch.empty(B, H, 64, dtype=projections[0].dtype, device=dev)
+    hs = N.desc_array(history)
+    rc = N.load().maba_hip_dgda_layer_step(N.desc_array(projections), N.desc_array(conv_weights), hs, float(eps),
+                                           N.desc(state), N.desc(out), N.desc(state), hs, N.stream_ptr(dev))
+    N.check(rc, "dgda_layer_step")
+    return out
+
+
 def hip_dgda_layer_prefill(projections, conv_weights, history=None, eps: float = 1e-6, initial_state=None,
                            out=None, out_history=None, state_dtype: Optional[torch.dtype] = None):
     """The DGDA layer prefill with its prologue fused into the kernels' staging

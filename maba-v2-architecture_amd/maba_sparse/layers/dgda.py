@@ -267,6 +267,12 @@ class DGDALayer(WeightCacheMixin, nn.Module):
                                  self.gate_write)]
         w6 = cached(self, f"w6_{x.dtype}", ws, lambda: torch.cat(ws, dim=0).to(x.dtype))
         projs = F.linear(x, w6).split(H * dk, dim=-1)
+        convs = (self.conv_q.weight, self.conv_k.weight, self.conv_v.weight)
+        if (self.fuse_prologue and dk == dv == 64 and convs[0].shape[-1] == 4 and x.dtype == torch.bfloat16
+                and all(h.dtype == torch.bfloat16 for h in hists)):
+            # prologue and step in one launch; state and history updated in place
+            o = hb.hip_dgda_layer_step(projs, convs, tuple(hists), state, eps=self.eps)
+            return self.o_proj(o.reshape(B, 1, H * dv))
         q, k, v, la, _, b, w, _ = hb.hip_dgda_prologue(
             projs, (self.conv_q.weight, self.conv_k.weight, self.conv_v.weight), tuple(hists), n_heads=H,
             eps=self.eps, gate_dtype=torch.float32, with_alpha=False, out_history=tuple(hists))

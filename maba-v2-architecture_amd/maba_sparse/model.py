@@ -270,11 +270,13 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
 
     @torch.no_grad()
     def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int,
-                        on_prefill_done=None, return_logits: bool = False, graph: Optional[bool] = None):
+                        on_prefill_done=None, return_logits: bool = False, graph: Optional[bool] = None,
+                        on_graph_ready=None):
         """Greedy decoding (reference model.py:272-305 at temperature 0): one prefill, then
         ``max_new_tokens - 1`` single-token steps over per-layer decode caches.  Returns the
         new tokens ``[B, max_new_tokens]``.  ``on_prefill_done()`` runs between the two phases
-        (a timing hook).  With ``return_logits`` the last-position logits of the prefill and
+        and ``on_graph_ready()`` (graph path) once the step graph is captured, before its first
+        replay (timing hooks).  With ``return_logits`` the last-position logits of the prefill and
         of every step come back too, ``[B, max_new_tokens, vocab]``.
 
         ``graph`` (default: whenever ``serving_graph_ok``) takes the device-resident path: a
@@ -290,7 +292,8 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
             graph = self.serving_graph_ok(input_ids)
         logits, states = self(input_ids)
         if graph:
-            return self._generate_graph(logits, states, L, max_new_tokens, on_prefill_done, return_logits)
+            return self._generate_graph(logits, states, L, max_new_tokens, on_prefill_done, return_logits,
+                                        on_graph_ready)
         caches: List[Optional[LatentCache]] = []
         for layer, (_, _, c_kv) in zip(self.layers, states):
             if layer.is_attention:
@@ -320,7 +323,8 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
         toks = torch.cat(out, dim=1)
         return (toks, torch.stack(seen, dim=1)) if return_logits else toks
 
-    def _generate_graph(self, logits, states, L, max_new_tokens, on_prefill_done, return_logits):
+    def _generate_graph(self, logits, states, L, max_new_tokens, on_prefill_done, return_logits,
+                        on_graph_ready=None):
         last = logits[:, -1]
         first = last.argmax(dim=-1, keepdim=True)
         serv = ServingStep(self, states, L, L + max_new_tokens, first)
@@ -346,6 +350,8 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):          # recorded, not run
                 serv.step()
+            if on_graph_ready is not None:
+                on_graph_ready()
             for _ in range(steps - 1):
                 g.replay()
                 keep()

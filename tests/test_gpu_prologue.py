@@ -185,3 +185,61 @@ def test_dgda_layer_fused_forward_matches_unfused(dev):
         assert err <= 2e-2 * b_.float().abs().max().item(), (name, err)
     for i in range(3):
         assert torch.equal(cf[i], cu[i]), f"history {i}"
+
+
+@pytest.mark.parametrize("B,H,sdt,with_hist", [
+    (16, 10, torch.bfloat16, True),    # the serving model's decode shape and state dtype
+    (3, 4, torch.float32, True),
+    (2, 16, torch.bfloat16, False),    # no history: zero taps
+])
+def test_dgda_layer_step_equals_prologue_then_step(dev, B, H, sdt, with_hist):
+    """The one-launch decode token (prologue + step) against the two launches it replaces,
+    which the tests above and the decode tests pin to the oracle: equal bit for bit (the
+    same arithmetic, q/k/v rounded to bf16 and the gates kept in fp32 in both), the state
+    and the conv history updated in place."""
+    hb = _hip()
+    C = 64 * H
+    g = torch.Generator().manual_seed(B * 100 + H)
+    proj = torch.randn(B, 1, 6 * C, generator=g).to(dev, torch.bfloat16)
+    projs = proj.split(C, dim=-1)
+    ws = [(torch.randn(C, 1, 4, generator=g) * 0.4).to(dev) for _ in range(3)]
+    hist = [torch.randn(B, C, 3, generator=g).to(dev, torch.bfloat16) for _ in range(3)] if with_hist else None
+    state = (torch.randn(B, H, 64, 64, generator=g) * 0.3).to(dev, sdt)
+    # two launches
+    h1 = [h.clone() for h in hist] if with_hist else [torch.empty(B, C, 3, device=dev, dtype=torch.bfloat16)
+                                                      for _ in range(3)]
+    s1 = state.clone()
+    q, k, v, la, _, b, w, _ = hb.hip_dgda_prologue(projs, ws, tuple(h1) if with_hist else None, n_heads=H, eps=1e-6,
+                                                   gate_dtype=torch.float32, with_alpha=False, out_history=tuple(h1))
+    o1, _ = hb.hip_dgda_step(q.view(B, H, 64), k.view(B, H, 64), v.view(B, H, 64), log_alpha=la.view(B, H, 64),
+                             b=b.view(B, H, 64), w=w.view(B, H, 64), state=s1, new_state=s1, allow_mixed_dtypes=True)
+    # one launch
+    h2 = [h.clone() for h in hist] if with_hist else [torch.zeros(B, C, 3, device=dev, dtype=torch.bfloat16)
+                                                      for _ in range(3)]
+    s2 = state.clone()
+    o2 = hb.hip_dgda_layer_step(projs, ws, tuple(h2), s2, eps=1e-6)
+    assert o2.dtype == o1.dtype and o2.shape == (B, H, 64)
+    assert torch.equal(o2, o1.view(B, H, 64)), "o"
+    assert torch.equal(s2, s1), "state"
+    for i in range(3):
+        assert torch.equal(h2[i], h1[i]), f"history {i}"
+
+
+def test_dgda_layer_step_device_fused_matches_unfused(dev):
+    """DGDALayer.step_device (the serving path) with the fused launch against the same layer
+    with the prologue and the step as two launches, over two consecutive tokens."""
+    from maba_sparse.layers import DGDALayer
+    torch.manual_seed(4)
+    layer = DGDALayer(dim=640, n_heads=10).to(dev, torch.bfloat16).eval()
+    B, C = 16, 640
+    st = (torch.randn(B, 10, 64, 64, device=dev) * 0.2).to(torch.bfloat16)
+    hs = [torch.randn(B, C, 3, device=dev).to(torch.bfloat16) for _ in range(3)]
+    xs = [torch.randn(B, 1, C, device=dev, dtype=torch.bfloat16) for _ in range(2)]
+    outs = {}
+    for fused in (True, False):
+        layer.fuse_prologue = fused
+        s, h = st.clone(), [x.clone() for x in hs]
+        with torch.no_grad():
+            outs[fused] = [layer.step_device(x, s, h) for x in xs] + [s, *h]
+    for a, b_ in zip(outs[True], outs[False]):
+        assert torch.equal(a, b_)
