@@ -54,6 +54,11 @@
  *   maba_hip_rmsnorm                model.py:11-22 (RMSNorm) and the gated residual
  *                                   of MabaBlock, model.py:92-128
  *   maba_hip_swiglu                 model.py:25-38 (SwiGLU activation)
+ *   maba_hip_decode_linear          nn.Linear of one decode token per sequence
+ *                                   (model.py:25-38, 92-128, the layers' projections),
+ *                                   its input from RMSNorm, the gated residual +
+ *                                   RMSNorm or SwiGLU (model.py:11-38, 92-128) in the
+ *                                   same launch
  */
 #ifndef MABA_HIP_H
 #define MABA_HIP_H
@@ -298,7 +303,7 @@ int maba_hip_maba_sa_decode_dev(const maba_tensor* q_lat, const maba_tensor* c_k
  * history) and maba_hip_dgda_step in one launch, with q, k, v rounded to bf16 and the gates
  * kept in fp32 as those two store them (the results equal theirs).  xs: the six bf16
  * projections [B,C] or [B,1,C] (q, k, v, decay, erase, write; unit channel stride, C = 64 H),
- * conv_w [C,1,4] x3 (f32/bf16, one dtype), hist [B,C,3] x3 bf16 or NULL (zeros), eps the
+ * conv_w [C,1,4] x3 (f32/bf16, one dtype), hist [B,C,3] x3 bf16 (all three) or NULL (zeros), eps the
  * key-norm epsilon, state [B,H,64,64] f32/bf16 or NULL (zero), out [B,H,64] f32/bf16,
  * new_state like state (may alias it), new_hist [B,C,3] x3 bf16 (may alias hist). */
 int maba_hip_dgda_layer_step(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
@@ -315,6 +320,19 @@ int maba_hip_rmsnorm(const maba_tensor* x, const maba_tensor* mo, const maba_ten
 
 /* out [..,I] = silu(g) * u for gate_up [..,2I] = [g | u] (f32 or bf16, one dtype). */
 int maba_hip_swiglu(const maba_tensor* gate_up, maba_tensor* out, void* stream);
+
+/* y = A weight^T for a few rows (one decode token per sequence), bf16 with fp32 accumulation.
+ * weight [N,K] bf16 (unit K stride, 16-byte aligned rows, K a multiple of 32, K <= 2048).
+ * A is built in the same launch from a ([M,K] or [M,1,K] bf16 rows, 16-byte aligned):
+ *   act 0, norm_w NULL:       A = a
+ *   act 0, norm_w [K]:        A = bf16(a / sqrt(mean(a^2) + eps) * norm_w)          (K <= 1024)
+ *   act 0, norm_w, mo, gate:  x' = bf16(a + gate * mo) is written to x_out and A is the RMSNorm of
+ *                             x' as above; x_out may overlap neither a nor mo     (K <= 1024)
+ *   act 1:                    A = bf16(silu(a[:, :K]) * a[:, K:2K]) for a [M,2K]
+ * y [M,N] or [M,1,N] bf16, unit column stride, overlapping no input. */
+int maba_hip_decode_linear(const maba_tensor* a, const maba_tensor* mo, const maba_tensor* gate,
+                           const maba_tensor* norm_w, float eps, int act, const maba_tensor* weight,
+                           maba_tensor* x_out, maba_tensor* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,8 +17,8 @@
 //                              zero-padded tail centroid while its block is incomplete
 // The new row goes to index p = *pos (a device scalar, so that one captured launch serves
 // every position); the caller advances *pos after the step.  One workgroup per sequence:
-// it writes the two rows, then reduces the block that holds row p, taking row p from the
-// inputs and rows before it from the caches (written by earlier launches).
+// it reduces the block that holds row p, taking row p from the inputs and rows before it
+// from the caches (written by earlier launches), then writes the two rows.
 #include "maba_common.h"
 
 namespace maba {
@@ -40,7 +40,12 @@ struct AppendArgs {
 
 // Column reduction of rows [r0, p) of a cache plus the new row (newrow[col * nsd]): sum
 // (and max when WITH_MAX) per column; the threads split the rows in AP_T / d parts, and
-// thread `col` of the result holds column col.
+// thread `col` of the result holds column col.  Each thread loads AP_BATCH of its rows
+// before it adds the first (rows past p reread row rb, which is < p, and add nothing), so
+// a block costs one or two memory round trips rather than one per row; the rows are still
+// added in ascending order, one at a time.
+constexpr int AP_BATCH = 16;
+
 template <bool WITH_MAX>
 __device__ void ap_reduce(const uint16_t* base, int64_t rstride, int64_t r0, int64_t p, int d,
                           const uint16_t* newrow, int64_t nsd, float* s_sum, float* s_max, float& sum, float& mx) {
@@ -49,13 +54,23 @@ __device__ void ap_reduce(const uint16_t* base, int64_t rstride, int64_t r0, int
   const int col = tid % d, part = tid / d;
   float s = 0.f, m = -INFINITY;
   if (part < parts) {
-    for (int64_t r = r0 + part; r < p; r += parts) {
-      const float x = bf16_bits_to_f32(base[r * rstride + col]);
-      s += x;
-      if (WITH_MAX) m = fmaxf(m, x);
+    const float xn = bf16_bits_to_f32(newrow[col * nsd]);   // added by the last part only
+    for (int64_t rb = r0 + part; rb < p; rb += (int64_t)AP_BATCH * parts) {
+      uint16_t x[AP_BATCH];
+#pragma unroll
+      for (int k = 0; k < AP_BATCH; ++k) {
+        const int64_t r = rb + (int64_t)k * parts;
+        x[k] = base[(r < p ? r : rb) * rstride + col];
+      }
+#pragma unroll
+      for (int k = 0; k < AP_BATCH; ++k) {
+        const bool in = rb + (int64_t)k * parts < p;
+        const float v = bf16_bits_to_f32(x[k]);
+        s += in ? v : 0.f;   // s is never -0, so adding +0 leaves it unchanged
+        if (WITH_MAX) m = in ? fmaxf(m, v) : m;
+      }
     }
     if (part == parts - 1) {
-      const float xn = bf16_bits_to_f32(newrow[col * nsd]);
       s += xn;
       if (WITH_MAX) m = fmaxf(m, xn);
     }
@@ -78,21 +93,12 @@ __global__ __launch_bounds__(AP_T) void cache_append_kernel(AppendArgs a) {
   __shared__ float s_sum[AP_T], s_max[AP_T];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
+  // the new rows, loaded together with the position; they are stored last, so that no
+  // load of the reductions (rows before p only) waits behind their stores
+  const uint16_t xc = a.cn[b * a.cnsb + min(tid, a.dc - 1) * a.cnsd];
+  const uint16_t xk = a.kn[b * a.knsb + min(tid, a.di - 1) * a.knsd];
   const int64_t p = *a.pos;
   if (p < 0 || p >= a.Lmax) return;   // the host checks capacity; never write out of bounds
-  // the new rows
-  const uint16_t xc = tid < a.dc ? a.cn[b * a.cnsb + tid * a.cnsd] : 0;
-  const uint16_t xk = tid < a.di ? a.kn[b * a.knsb + tid * a.knsd] : 0;
-  if (tid < a.dc) a.c[b * a.csb + p * a.csl + tid] = xc;
-  if (tid < a.di) a.k[b * a.ksb + p * a.ksl + tid] = xk;
-  // HCA mean of the pool-block that row p completes
-  if ((p + 1) % a.pool == 0) {
-    const int64_t e = (p + 1) / a.pool - 1;
-    float sum, mx;
-    ap_reduce<false>(a.c + b * a.csb, a.csl, p + 1 - a.pool, p, a.dc, a.cn + b * a.cnsb, a.cnsd, s_sum, s_max,
-                     sum, mx);
-    if (tid < a.dc && e < a.nh_max) a.hca[b * a.hsb + e * a.hsn + tid] = f32_to_bf16_bits(sum * (1.0f / (float)a.pool));
-  }
   // centroid of the block holding row p: complete, or the zero-padded tail
   const int64_t blk = p / a.bs;
   const int64_t r0 = blk * a.bs;
@@ -103,6 +109,15 @@ __global__ __launch_bounds__(AP_T) void cache_append_kernel(AppendArgs a) {
     const float c = 0.5f * (sum * (1.0f / (float)a.bs) + mx);
     a.cent[b * a.esb + blk * a.esn + tid] = f32_to_bf16_bits(c);
   }
+  // HCA mean of the pool-block that row p completes
+  if ((p + 1) % a.pool == 0) {
+    const int64_t e = (p + 1) / a.pool - 1;
+    ap_reduce<false>(a.c + b * a.csb, a.csl, p + 1 - a.pool, p, a.dc, a.cn + b * a.cnsb, a.cnsd, s_sum, s_max,
+                     sum, mx);
+    if (tid < a.dc && e < a.nh_max) a.hca[b * a.hsb + e * a.hsn + tid] = f32_to_bf16_bits(sum * (1.0f / (float)a.pool));
+  }
+  if (tid < a.dc) a.c[b * a.csb + p * a.csl + tid] = xc;
+  if (tid < a.di) a.k[b * a.ksb + p * a.ksl + tid] = xk;
 }
 
 }  // namespace maba

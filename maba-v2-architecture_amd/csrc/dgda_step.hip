@@ -188,7 +188,13 @@ struct LayerStepArgs {
   float eps;
 };
 
-template <typename TS>
+// TW: dtype of the conv taps; HS / HH: a state / a history is given (else zeros).  The
+// dtype and the presence of each input are compile-time, so the wave issues every load
+// (state column, projections, taps, history) before it waits for the first: with a
+// run-time dtype switch or a null test around a load, the compiler converts or merges
+// each loaded value inside its branch and waits for that load alone, one memory round
+// trip per tap.
+template <typename TS, typename TW, bool HS, bool HH>
 __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t bh = (int64_t)blockIdx.x * 4 + wave;
@@ -196,7 +202,7 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
   const int64_t bi = bh / a.H, hi = bh % a.H;
   const int64_t c = hi * 64 + lane;   // channel of the projection rows
   float s[64];
-  if (a.state) {
+  if constexpr (HS) {
     const int64_t S = bi * a.ssb + hi * a.ssh + lane;
 #pragma unroll
     for (int r = 0; r < 64; ++r) s[r] = ldf<TS>(a.state, S + r * a.ssr);
@@ -211,10 +217,10 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
 #pragma unroll
   for (int st = 0; st < 3; ++st) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[st][j] = load_elem(a.cw[st], a.cwdt, c * a.cwsc[st] + j * a.cwst[st]);
+    for (int j = 0; j < 4; ++j) w[st][j] = ldf<TW>(a.cw[st], c * a.cwsc[st] + j * a.cwst[st]);
 #pragma unroll
     for (int j = 0; j < 3; ++j)
-      h[st][j] = a.hist[st] ? bf16_bits_to_f32(a.hist[st][bi * a.hsb[st] + c * a.hsc[st] + j * a.hst[st]]) : 0.f;
+      h[st][j] = HH ? bf16_bits_to_f32(a.hist[st][bi * a.hsb[st] + c * a.hsc[st] + j * a.hst[st]]) : 0.f;
   }
   float y[3];
 #pragma unroll
@@ -387,6 +393,8 @@ extern "C" int maba_hip_dgda_layer_step(const maba_tensor* const* xs, const maba
     a.nh[st] = (uint16_t*)nh->data; a.nhsb[st] = nh->stride[0]; a.nhsc[st] = nh->stride[1]; a.nhst[st] = nh->stride[2];
   }
   a.cwdt = conv_w[0]->dtype;
+  const int nhist = (int)(a.hist[0] != nullptr) + (a.hist[1] != nullptr) + (a.hist[2] != nullptr);
+  if (nhist != 0 && nhist != 3) return fail(MABA_ERR_INVALID, "%s: give all three histories or none", who);
   const int64_t ss4[4] = {B, H, 64, 64};
   if (!expect_shape(new_state, "new_state", 4, ss4) || new_state->stride[3] != 1 ||
       (new_state->dtype != MABA_F32 && new_state->dtype != MABA_BF16))
@@ -401,7 +409,14 @@ extern "C" int maba_hip_dgda_layer_step(const maba_tensor* const* xs, const maba
   if (B == 0) return MABA_OK;
   const dim3 g4((unsigned)ceil_div(B * H, 4));
   hipStream_t s = (hipStream_t)stream;
-  if (new_state->dtype == MABA_BF16) hipLaunchKernelGGL(dgda_layer_step_kernel<uint16_t>, g4, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(dgda_layer_step_kernel<float>, g4, dim3(256), 0, s, a);
+  const bool sb = new_state->dtype == MABA_BF16, wb = a.cwdt == MABA_BF16, hs = a.state != nullptr, hh = nhist == 3;
+  void (*k)(LayerStepArgs) = nullptr;
+#define MABA_LS_PICK(TS, TW)                                                                  \
+  k = hs ? (hh ? dgda_layer_step_kernel<TS, TW, true, true> : dgda_layer_step_kernel<TS, TW, true, false>) \
+         : (hh ? dgda_layer_step_kernel<TS, TW, false, true> : dgda_layer_step_kernel<TS, TW, false, false>)
+  if (sb) { if (wb) MABA_LS_PICK(uint16_t, uint16_t); else MABA_LS_PICK(uint16_t, float); }
+  else { if (wb) MABA_LS_PICK(float, uint16_t); else MABA_LS_PICK(float, float); }
+#undef MABA_LS_PICK
+  hipLaunchKernelGGL(k, g4, dim3(256), 0, s, a);
   return check_launch(who);
 }

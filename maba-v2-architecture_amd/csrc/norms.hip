@@ -29,60 +29,99 @@ struct NormArgs {
 
 template <class T> struct P2;
 template <> struct P2<float> {
-  static __device__ __forceinline__ float2 ld(const void* p, int64_t i) { return *(const float2*)((const float*)p + i); }
+  typedef float2 raw;   // the bits of a channel pair as loaded
+  static __device__ __forceinline__ raw ldr(const void* p, int64_t i) { return *(const float2*)((const float*)p + i); }
+  static __device__ __forceinline__ float2 cvt(raw u) { return u; }
+  static __device__ __forceinline__ raw zero(uint32_t z) { return make_float2(__uint_as_float(z), __uint_as_float(z)); }
+  static __device__ __forceinline__ float2 ld(const void* p, int64_t i) { return ldr(p, i); }
   static __device__ __forceinline__ void st(void* p, int64_t i, float2 v) { *(float2*)((float*)p + i) = v; }
 };
 template <> struct P2<uint16_t> {
-  static __device__ __forceinline__ float2 ld(const void* p, int64_t i) {
-    const uint32_t u = *(const uint32_t*)((const uint16_t*)p + i);
+  typedef uint32_t raw;
+  static __device__ __forceinline__ raw ldr(const void* p, int64_t i) { return *(const uint32_t*)((const uint16_t*)p + i); }
+  static __device__ __forceinline__ float2 cvt(raw u) {
     return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
   }
+  static __device__ __forceinline__ raw zero(uint32_t z) { return z; }
+  static __device__ __forceinline__ float2 ld(const void* p, int64_t i) { return cvt(ldr(p, i)); }
   static __device__ __forceinline__ void st(void* p, int64_t i, float2 v) {
     *(uint32_t*)((uint16_t*)p + i) = (uint32_t)f32_to_bf16_bits(v.x) | ((uint32_t)f32_to_bf16_bits(v.y) << 16);
   }
 };
 
-__device__ __forceinline__ float2 ld_any2(const void* p, int dt, int64_t i) {
-  return dt == MABA_F32 ? P2<float>::ld(p, i) : P2<uint16_t>::ld(p, i);
+// v as the row dtype stores it (the residual stream is normalised as stored).
+template <class T> __device__ __forceinline__ float2 as_stored(float2 v);
+template <> __device__ __forceinline__ float2 as_stored<float>(float2 v) { return v; }
+template <> __device__ __forceinline__ float2 as_stored<uint16_t>(float2 v) {
+  return make_float2(bf16_bits_to_f32(f32_to_bf16_bits(v.x)), bf16_bits_to_f32(f32_to_bf16_bits(v.y)));
 }
 
-template <class T>
+// T: row dtype; TG, TW: dtype of the residual gate and the norm weight; MODE 0: h = norm(x),
+// 1: x' = x + g * mo and h = norm(x'), 2: as 1 with x' written to xo in T and normalised as
+// written.  The wave first issues every load of its row as raw bits (channel indices clamped
+// into the row) and only then converts and computes, every chunk without a branch on the
+// chunk count.  A value used under the same test as its load, or converted inside a run-time
+// dtype switch, is waited for on its own, one memory round trip per chunk; the fill of the
+// chunks past the row comes from an instruction the optimiser cannot see through, which
+// keeps it from moving the conversions up into the loads' branches.
+template <class T, class TG, class TW, int MODE>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= a.R) return;   // wave-uniform; no barriers
-  const int np = a.C / 2;
-  float2 v[NRM_MAXP];
+  // a wave past the last row reads that row and stores nothing: with an early return the
+  // compiler reads the row count, waits and branches before it loads the other arguments
+  asm volatile("" ::"s"(a.x), "s"(a.xs), "s"(a.mo), "s"(a.ms), "s"(a.g), "s"(a.w), "s"(a.xo), "s"(a.xos),
+               "s"(a.h), "s"(a.hs), "s"(a.R), "s"(a.C), "s"(a.eps));   // every argument loaded at once
+  const int64_t r0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool live = r0 < a.R;
+  const int64_t r = live ? r0 : a.R - 1;
+  const int np = live ? a.C / 2 : 0, nit = (a.C / 2 + 63) >> 6;
+  uint32_t zr;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zr));
+  typename P2<T>::raw v[NRM_MAXP], m[NRM_MAXP];
+  typename P2<TG>::raw g[NRM_MAXP];
+  typename P2<TW>::raw w[NRM_MAXP];
+#pragma unroll
+  for (int i = 0; i < NRM_MAXP; ++i) {
+    v[i] = P2<T>::zero(zr); m[i] = P2<T>::zero(zr); g[i] = P2<TG>::zero(zr); w[i] = P2<TW>::zero(zr);
+    if (i < nit) {
+      const int j = min(lane + 64 * i, a.C / 2 - 1);
+      v[i] = P2<T>::ldr(a.x, r * a.xs + 2 * j);
+      if constexpr (MODE > 0) {
+        m[i] = P2<T>::ldr(a.mo, r * a.ms + 2 * j);
+        g[i] = P2<TG>::ldr(a.g, 2 * j);
+      }
+      w[i] = P2<TW>::ldr(a.w, 2 * j);
+    }
+  }
+  float2 xs[NRM_MAXP];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NRM_MAXP; ++i) {
     const int j = lane + 64 * i;
-    if (j < np) {
-      float2 x = P2<T>::ld(a.x, r * a.xs + 2 * j);
-      if (a.mo) {
-        const float2 m = P2<T>::ld(a.mo, r * a.ms + 2 * j);
-        const float2 g = ld_any2(a.g, a.gdt, 2 * j);
-        x.x = fmaf(g.x, m.x, x.x);
-        x.y = fmaf(g.y, m.y, x.y);
-        if (a.xo) {   // the residual stream is stored in the row dtype; the norm reads it as stored
-          P2<T>::st(a.xo, r * a.xos + 2 * j, x);
-          x = P2<T>::ld(a.xo, r * a.xos + 2 * j);
-        }
+    float2 x = P2<T>::cvt(v[i]);
+    if constexpr (MODE > 0) {
+      const float2 mm = P2<T>::cvt(m[i]), gg = P2<TG>::cvt(g[i]);
+      x.x = fmaf(gg.x, mm.x, x.x);
+      x.y = fmaf(gg.y, mm.y, x.y);
+      if constexpr (MODE == 2) {
+        x = as_stored<T>(x);
+        if (j < np) P2<T>::st(a.xo, r * a.xos + 2 * j, x);
       }
-      v[i] = x;
-      ss = fmaf(x.x, x.x, fmaf(x.y, x.y, ss));
     }
+    const bool in = j < np;
+    x.x = in ? x.x : 0.f;
+    x.y = in ? x.y : 0.f;
+    xs[i] = x;
+    ss = fmaf(x.x, x.x, fmaf(x.y, x.y, ss));
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-  const float inv = rsqrtf(ss / (float)a.C + a.eps);
+  const float inv = rsqrtf(ss / (float)a.C + a.eps);   // (np = 0 on a dead wave: no stores)
 #pragma unroll
   for (int i = 0; i < NRM_MAXP; ++i) {
     const int j = lane + 64 * i;
-    if (j < np) {
-      const float2 w = ld_any2(a.w, a.wdt, 2 * j);
-      P2<T>::st(a.h, r * a.hs + 2 * j, make_float2(v[i].x * inv * w.x, v[i].y * inv * w.y));
-    }
+    const float2 ww = P2<TW>::cvt(w[i]);
+    if (j < np) P2<T>::st(a.h, r * a.hs + 2 * j, make_float2(xs[i].x * inv * ww.x, xs[i].y * inv * ww.y));
   }
 }
 
@@ -161,8 +200,17 @@ extern "C" int maba_hip_rmsnorm(const maba_tensor* x, const maba_tensor* mo, con
   a.R = R; a.C = C; a.eps = eps;
   if (R == 0) return MABA_OK;
   const dim3 grid((unsigned)ceil_div(R, 4));
-  if (x->dtype == MABA_F32) hipLaunchKernelGGL(rmsnorm_kernel<float>, grid, dim3(256), 0, (hipStream_t)stream, a);
-  else hipLaunchKernelGGL(rmsnorm_kernel<uint16_t>, grid, dim3(256), 0, (hipStream_t)stream, a);
+  const int mode = !a.mo ? 0 : !a.xo ? 1 : 2;
+  const bool tb = x->dtype == MABA_BF16, gb = a.gdt == MABA_BF16, wb = a.wdt == MABA_BF16;
+  void (*k)(NormArgs) = nullptr;
+#define MABA_NRM_PICK(T, TW)                                                                           \
+  k = mode == 0 ? rmsnorm_kernel<T, float, TW, 0>                                                       \
+    : mode == 1 ? (gb ? rmsnorm_kernel<T, uint16_t, TW, 1> : rmsnorm_kernel<T, float, TW, 1>)          \
+                : (gb ? rmsnorm_kernel<T, uint16_t, TW, 2> : rmsnorm_kernel<T, float, TW, 2>)
+  if (tb) { if (wb) MABA_NRM_PICK(uint16_t, uint16_t); else MABA_NRM_PICK(uint16_t, float); }
+  else { if (wb) MABA_NRM_PICK(float, uint16_t); else MABA_NRM_PICK(float, float); }
+#undef MABA_NRM_PICK
+  hipLaunchKernelGGL(k, grid, dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("rmsnorm");
 }
 

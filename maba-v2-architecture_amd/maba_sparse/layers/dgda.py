@@ -255,31 +255,35 @@ class DGDALayer(WeightCacheMixin, nn.Module):
         return self.o_proj(oh.reshape(B, 1, self.n_heads * self.d_v)), S, ncs
 
 
-    def step_device(self, x: torch.Tensor, state: torch.Tensor, hists) -> torch.Tensor:
+    def step_device(self, x: torch.Tensor, state: torch.Tensor, hists, proj=None) -> torch.Tensor:
         """One token on the serving path: the prologue writes the new conv history over
         ``hists`` (three ``[B, C, 3]`` buffers) and the step updates ``state`` in place, so a
         captured launch sequence replays with the same buffers at every position.  Same math
-        as ``step``; HIP backend only."""
+        as ``step``; HIP backend only.  ``proj(weight)``, when given, stands for ``F.linear(x,
+        weight)`` of the layer input (a decode linear that builds its normalised input in the
+        same launch; ``x`` then only gives the batch and dtype), and ``o_proj`` runs as a
+        decode linear too."""
         from maba_sparse.kernels import hip_backend as hb
         B = x.shape[0]
         H, dk, dv = self.n_heads, self.d_k, self.d_v
         ws = [m.weight for m in (self.q_proj, self.k_proj, self.v_proj, self.gate_alpha, self.gate_erase,
                                  self.gate_write)]
         w6 = cached(self, f"w6_{x.dtype}", ws, lambda: torch.cat(ws, dim=0).to(x.dtype))
-        projs = F.linear(x, w6).split(H * dk, dim=-1)
+        projs = (proj(w6) if proj is not None else F.linear(x, w6)).split(H * dk, dim=-1)
         convs = (self.conv_q.weight, self.conv_k.weight, self.conv_v.weight)
         if (self.fuse_prologue and dk == dv == 64 and convs[0].shape[-1] == 4 and x.dtype == torch.bfloat16
                 and all(h.dtype == torch.bfloat16 for h in hists)):
             # prologue and step in one launch; state and history updated in place
-            o = hb.hip_dgda_layer_step(projs, convs, tuple(hists), state, eps=self.eps)
-            return self.o_proj(o.reshape(B, 1, H * dv))
+            o = hb.hip_dgda_layer_step(projs, convs, tuple(hists), state, eps=self.eps).reshape(B, 1, H * dv)
+            return hb.hip_decode_linear(o, self.o_proj.weight) if proj is not None else self.o_proj(o)
         q, k, v, la, _, b, w, _ = hb.hip_dgda_prologue(
             projs, (self.conv_q.weight, self.conv_k.weight, self.conv_v.weight), tuple(hists), n_heads=H,
             eps=self.eps, gate_dtype=torch.float32, with_alpha=False, out_history=tuple(hists))
         o, _ = hb.hip_dgda_step(q.view(B, H, dk), k.view(B, H, dk), v.view(B, H, dv), log_alpha=la.view(B, H, dk),
                                 b=b.view(B, H, dk), w=w.view(B, H, dv), state=state, new_state=state,
                                 allow_mixed_dtypes=True)
-        return self.o_proj(o.reshape(B, 1, H * dv))
+        o = o.reshape(B, 1, H * dv)
+        return hb.hip_decode_linear(o.to(x.dtype), self.o_proj.weight) if proj is not None else self.o_proj(o)
 
 
 DecoupledGatedDeltaAttention = DGDALayer

@@ -142,12 +142,16 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         q = self.q_proj(x).view(B, self.n_heads, self.d_head).float()
         return torch.einsum("bhd,hdc->bhc", q, self._f32_heads(self.k_up_proj, "_wk_f32"))
 
-    def _heads_out(self, z: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-        """``W_v,h z_h`` then ``o_proj``; ``z [B, H, d_c]`` -> ``[B, 1, dim]``."""
+    def _heads_out(self, z: torch.Tensor, dtype: torch.dtype, decode_linear: bool = False) -> torch.Tensor:
+        """``W_v,h z_h`` then ``o_proj``; ``z [B, H, d_c]`` -> ``[B, 1, dim]`` (``o_proj`` as a
+        HIP decode linear with ``decode_linear``)."""
         B = z.shape[0]
         Wv = self._f32_heads(self.v_up_proj, "_wv_f32")
-        o = torch.einsum("bhc,hdc->bhd", z.float(), Wv).reshape(B, 1, self.n_heads * self.d_head)
-        return self.o_proj(o.to(dtype))
+        o = torch.einsum("bhc,hdc->bhd", z.float(), Wv).reshape(B, 1, self.n_heads * self.d_head).to(dtype)
+        if decode_linear:
+            from maba_sparse.kernels import hip_backend as hb
+            return hb.hip_decode_linear(o, self.o_proj.weight)
+        return self.o_proj(o)
 
     def _hca_for(self, c_full: torch.Tensor) -> torch.Tensor:
         """Complete-block means of ``c_full``, extended incrementally across decode steps."""
@@ -175,7 +179,7 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
                                     block_size=self.block_size, pool=self.hca_pool_size)
         return self._heads_out(z, x.dtype)
 
-    def _token_projections(self, x: torch.Tensor):
+    def _token_projections(self, x: torch.Tensor, proj=None):
         """q, the new latent, the indexer's query and key and the gate logits of one token from
         one GEMM over the stacked weights (the stack is rebuilt only after a weight changes).
 
@@ -193,7 +197,8 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
             return torch.cat([st, st.new_zeros(pad, st.shape[1])], dim=0) if pad else st
 
         w5 = cached(self, "w5", ws, stack)
-        qi, ki, q, c_new, gl, _ = F.linear(x, w5).split(sizes + [pad], dim=-1)
+        y = proj(w5) if proj is not None else F.linear(x, w5)
+        qi, ki, q, c_new, gl, _ = y.split(sizes + [pad], dim=-1)
         return q, c_new, qi, ki, gl + self.stream_gate.bias
 
     def decode_step(self, x: torch.Tensor, cache: LatentCache,
@@ -213,15 +218,18 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         return self._decode(x, cache.c, cache.n, hca, idx, q=q, gate_logits=gl)
 
     def decode_step_device(self, x: torch.Tensor, cache: DeviceCache, counters: torch.Tensor,
-                           return_parts: bool = False):
+                           return_parts: bool = False, proj=None):
         """One token on the serving path: the token's row joins ``cache`` at position
         ``counters[0]`` (device), the decode indexer and the fused three-stream decode run over
         the first ``counters[1] = counters[0] + 1`` rows.  Same math as ``decode_step``; HIP
         backend, bf16 caches and at least ``top_k`` blocks of history.  ``return_parts`` also
-        returns the selected blocks and the latent-space output ``z`` (for tests)."""
+        returns the selected blocks and the latent-space output ``z`` (for tests).
+        ``proj(weight)``, when given, stands for ``F.linear(x, weight)`` of the layer input
+        (a decode linear that builds its normalised input in the same launch; ``x`` then only
+        gives the batch and dtype), and ``o_proj`` runs as a decode linear too."""
         from maba_sparse.kernels import hip_backend as hb
         B = x.shape[0]
-        q, c_new, qi, ki, gl = self._token_projections(x)
+        q, c_new, qi, ki, gl = self._token_projections(x, proj)
         hb.hip_cache_append(c_new[:, 0], ki[:, 0], counters[0], cache.c, cache.keys, cache.hca, cache.cent,
                             pool=self.hca_pool_size, block_size=self.block_size)
         idx = hb.hip_index_topk_decode_dev(qi, cache.cent, counters[1], self.block_size, self.dist_lambda, self.top_k)
@@ -230,7 +238,7 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         z = hb.hip_maba_sa_decode_dev(q_lat, cache.c, cache.hca, idx, gl.view(-1, 3), counters[1], cache.cap,
                                       self.scale, window=self.window_size, n_sink=self.n_sink_tokens,
                                       block_size=self.block_size, pool=self.hca_pool_size)
-        out = self._heads_out(z, x.dtype)
+        out = self._heads_out(z, x.dtype, decode_linear=proj is not None)
         return (out, idx, z) if return_parts else out
 
     # ------------------------------------------------------------ prefill (HIP)

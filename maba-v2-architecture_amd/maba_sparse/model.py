@@ -172,9 +172,23 @@ class ServingStep:
             else:
                 self.dgda[i] = (st.clone().contiguous(), [h.clone().contiguous() for h in cv])
         self.last: Optional[torch.Tensor] = None
+        self.decode_linear = ServingStep.decode_linear and _decode_linear_fits(model)
+
+    # every linear layer of a step as a HIP decode linear that builds its input in the same
+    # launch (see step); False keeps torch's GEMMs and the separate norm / SwiGLU kernels
+    decode_linear = True
 
     def step(self) -> None:
-        """Decode the token in ``tok``; leaves the next token in ``tok`` and its logits in ``last``."""
+        """Decode the token in ``tok``; leaves the next token in ``tok`` and its logits in ``last``.
+
+        With ``decode_linear`` each linear layer is one HIP launch that also makes its input:
+        the mixer's first projection normalises the layer input and, from the second layer on,
+        first adds the previous FFN output through the gated residual (writing the new residual
+        stream to a fresh buffer); the stacked gate/up projection does the same for the
+        mixer's output; the down projection applies SwiGLU's activation; and the head
+        projection takes the last residual through the final norm."""
+        if self.decode_linear:
+            return self._step_decode_linear()
         from maba_sparse.kernels import hip_backend as hb
         m = self.model
         layers = m.layers
@@ -196,6 +210,66 @@ class ServingStep:
         self.last = m.lm_head(m.head_proj(h))[:, -1]
         self.tok.copy_(self.last.argmax(dim=-1, keepdim=True))
         self.counters += 1
+
+    def _step_decode_linear(self) -> None:
+        from maba_sparse.kernels import hip_backend as hb
+        m = self.model
+        layers = m.layers
+        emb = m.embeddings
+        x = hb.hip_decode_linear(emb.in_emb(self.tok), emb.proj.weight)
+        n1 = layers[0].norm1
+        spec = dict(a=x, norm_w=n1.weight, eps=n1.eps)    # the input stage of the next projection
+        for i, layer in enumerate(layers):
+            def proj(w, spec=spec):
+                return hb.hip_decode_linear(weight=w, **spec)
+            if layer.is_attention:
+                mo = layer.mixer.decode_step_device(x, self.caches[i], self.counters, proj=proj)
+            else:
+                st, hs = self.dgda[i]
+                mo = layer.mixer.step_device(x, st, hs, proj=proj)
+            x = spec.get("x_out", x)                     # the residual stream after that stage
+            g1 = _frozen(layer, "g1", torch.sigmoid, layer.res_gate1)
+            g2 = _frozen(layer, "g2", torch.sigmoid, layer.res_gate2)
+            ffn = layer.ffn
+            w_gu = _frozen(ffn, "gate_up", lambda a, b: torch.cat([a, b], dim=0), ffn.w_gate.weight, ffn.w_up.weight)
+            x2 = torch.empty_like(x)
+            gu = hb.hip_decode_linear(x, w_gu, norm_w=layer.norm2.weight, eps=layer.norm2.eps, mo=mo, gate=g1,
+                                      x_out=x2)
+            f = hb.hip_decode_linear(gu, ffn.w_down.weight, swiglu=True)
+            x = x2
+            nxt = layers[i + 1].norm1 if i + 1 < len(layers) else m.final_norm
+            spec = dict(a=x, norm_w=nxt.weight, eps=nxt.eps, mo=f, gate=g2, x_out=torch.empty_like(x))
+        hp = hb.hip_decode_linear(weight=m.head_proj.weight, **spec)
+        self.last = hb.hip_decode_linear(hp, m.lm_head.weight)[:, -1]
+        self.tok.copy_(self.last.argmax(dim=-1, keepdim=True))
+        self.counters += 1
+
+
+def _decode_linear_fits(model: "MabaSparseForCausalLM") -> bool:
+    """Whether every linear layer of a serving step fits the HIP decode linear: bf16 weights,
+    no bias (the MABA-SA stream gate's is added after the stacked projection), input widths a
+    multiple of 32, at most 1024 where the input is normalised and 2048 elsewhere; bf16 norm
+    weights and residual gates."""
+    normed, plain = [model.head_proj], [model.embeddings.proj, model.lm_head]
+    for layer in model.layers:
+        mx = layer.mixer
+        normed += [layer.ffn.w_gate, layer.ffn.w_up]
+        plain += [layer.ffn.w_down, mx.o_proj]
+        if layer.is_attention:
+            normed += [mx.indexer.q_idx_proj, mx.indexer.k_idx_proj, mx.q_proj, mx.kv_down_proj]
+            if mx.stream_gate.weight.shape[1] % 32 or mx.stream_gate.weight.dtype != torch.bfloat16:
+                return False
+        else:
+            normed += [mx.q_proj, mx.k_proj, mx.v_proj, mx.gate_alpha, mx.gate_erase, mx.gate_write]
+    for lim, mods in ((1024, normed), (2048, plain)):
+        for mod in mods:
+            w = mod.weight
+            if (w.dtype != torch.bfloat16 or w.dim() != 2 or w.shape[1] % 32 or w.shape[1] > lim
+                    or getattr(mod, "bias", None) is not None):
+                return False
+    vecs = [model.final_norm.weight] + [t for l in model.layers
+                                        for t in (l.norm1.weight, l.norm2.weight, l.res_gate1, l.res_gate2)]
+    return all(t.dtype == torch.bfloat16 for t in vecs)
 
 
 class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):

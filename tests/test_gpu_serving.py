@@ -131,6 +131,22 @@ def test_rmsnorm_and_residual(dev, rows, C, dtype):
     ref2 = xs / torch.sqrt((xs * xs).mean(-1, keepdim=True) + eps) * w.double()
     _ulp_close(h2, ref2.numpy(), "rmsnorm of the residual") if dtype == torch.bfloat16 else \
         assert_close(h2, ref2.numpy(), 1e-5, 1e-6, "rmsnorm of the residual")
+    # the residual without x_out is normalised unrounded; gate and weight of the other dtype
+    other = torch.float32 if dtype == torch.bfloat16 else torch.bfloat16
+    w3, g3 = w.to(other), gate.to(other)
+    h3 = hb.hip_rmsnorm(x.to(dev), w3.to(dev), eps, mo=mo.to(dev), gate=g3.to(dev))
+    xr3 = x.double() + g3.double() * mo.double()
+    ref3 = xr3 / torch.sqrt((xr3 * xr3).mean(-1, keepdim=True) + eps) * w3.double()
+    _ulp_close(h3, ref3.numpy(), "rmsnorm of the unstored residual") if dtype == torch.bfloat16 else \
+        assert_close(h3, ref3.numpy(), 1e-5, 1e-6, "rmsnorm of the unstored residual")
+    xo4 = x.clone().to(dev)                                  # x_out aliasing x, mixed dtypes
+    h4 = hb.hip_rmsnorm(xo4, w3.to(dev), eps, mo=mo.to(dev), gate=g3.to(dev), x_out=xo4)
+    xs4 = xo4.cpu().double()
+    if dtype == torch.bfloat16:
+        _ulp_close(xo4, xr3.numpy(), "gated residual in place")
+    ref4 = xs4 / torch.sqrt((xs4 * xs4).mean(-1, keepdim=True) + eps) * w3.double()
+    _ulp_close(h4, ref4.numpy(), "rmsnorm in place") if dtype == torch.bfloat16 else \
+        assert_close(h4, ref4.numpy(), 1e-5, 1e-6, "rmsnorm in place")
 
 
 @pytest.mark.parametrize("shape,dtype", [((16, 1, 2496), torch.bfloat16), ((3, 50, 96), torch.float32)])
@@ -236,3 +252,89 @@ def test_maba_sa_device_decode_vs_oracle(dev):
                                          to_np(layer.k_up_proj.weight), to_np(layer.v_up_proj.weight),
                                          to_np(idx).astype(np.int64), to_np(gl.view(-1, 3)), L=L)
                 assert_close(got, exp, 2e-3, 2e-3, f"device decode at L={L}")
+
+
+def _dl_case(M, K, N, mode, seed):
+    """Inputs of one decode_linear case and the float64 product of its bf16 operand A."""
+    g = torch.Generator().manual_seed(seed)
+    bf = torch.bfloat16
+    a = torch.randn(M, 1, 2 * K if mode == "swiglu" else K, generator=g).to(bf)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(bf)
+    mo = torch.randn(M, 1, K, generator=g).to(bf)
+    gate = torch.sigmoid(torch.randn(K, generator=g)).to(bf)
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(bf)
+    return a, w, mo, gate, nw
+
+
+def _dl_ref(A, w):
+    """A [M, K] (float64 values of the bf16 operand) times w^T, and the absolute-sum scale."""
+    wd = w.double()
+    return A @ wd.T, A.abs() @ wd.abs().T
+
+
+def _bf16(x):
+    return x.to(torch.bfloat16).double()
+
+
+@pytest.mark.parametrize("M,K,N,mode", [
+    (16, 640, 640, "plain"), (3, 128, 200, "plain"), (20, 1248, 48, "plain"), (16, 640, 3840, "norm"),
+    (16, 640, 2496, "normres"), (5, 96, 40, "normres"), (16, 1024, 32, "normres"), (16, 1248, 640, "swiglu"),
+    (7, 2048, 64, "swiglu")])
+def test_decode_linear_modes(dev, M, K, N, mode):
+    """y = A W^T with A's input stage in the same launch, against float64 on the same bf16
+    operand: the output is one bf16 rounding (half an ulp) of the product; an element of A
+    that the kernel (fp32, then bf16) and float64 round to neighbouring bf16 values moves y
+    by at most an ulp of that one term, inside 1e-3 of the absolute-sum scale.  y and x_out
+    are views into larger buffers whose other elements must stay untouched."""
+    hb = _hb()
+    a, w, mo, gate, nw = _dl_case(M, K, N, mode, seed=K + N + M)
+    ybuf = torch.full((M + 2, 1, N + 16), 7.0, dtype=torch.bfloat16, device=dev)
+    y = ybuf[:M, :, :N]
+    xbuf = torch.full((M + 1, 1, K), 7.0, dtype=torch.bfloat16, device=dev)
+    kw = {}
+    if mode == "norm":
+        kw = dict(norm_w=nw.to(dev))
+    elif mode == "normres":
+        kw = dict(norm_w=nw.to(dev), mo=mo.to(dev), gate=gate.to(dev), x_out=xbuf[:M])
+    hb.hip_decode_linear(a.to(dev), w.to(dev), eps=1e-6, swiglu=mode == "swiglu", out=y, **kw)
+    torch.cuda.synchronize()
+    ad = a[:, 0].double()
+    if mode == "plain":
+        A, slack = ad, 1e-5
+    elif mode == "swiglu":
+        gg, uu = ad[:, :K], ad[:, K:]
+        A, slack = _bf16(gg * torch.sigmoid(gg) * uu), 1e-3
+    else:
+        x = ad
+        if mode == "normres":
+            xr = ad + gate.double() * mo[:, 0].double()
+            xo = xbuf[:M, 0].cpu().double()
+            _ulp_close(xo, xr.numpy(), "decode_linear x_out")
+            assert torch.all(xbuf[M:].cpu() == 7.0), "x_out written past its rows"
+            x = xo
+        A, slack = _bf16(x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6) * nw.double()), 1e-3
+    ref, scale = _dl_ref(A, w)
+    got = y[:, 0].cpu().double()
+    bad = (got - ref).abs() > 2.0 ** -8 * ref.abs() + slack * scale + 1e-6
+    assert not bad.any(), f"{mode}: {int(bad.sum())} of {bad.numel()} beyond bound (max err {(got - ref).abs().max():.3e})"
+    rest = ybuf.cpu().clone()
+    rest[:M, :, :N] = 7.0
+    assert torch.all(rest == 7.0), "y written outside its view"
+
+
+def test_decode_linear_rejects(dev):
+    hb = _hb()
+    bf = torch.bfloat16
+    a = torch.randn(4, 1, 640, device=dev).to(bf)
+    w = torch.randn(64, 640, device=dev).to(bf)
+    nw = torch.ones(640, device=dev, dtype=bf)
+    with pytest.raises(Exception, match="multiple of 32"):
+        hb.hip_decode_linear(a[..., :600], w[:, :600].contiguous())
+    with pytest.raises(Exception, match="1024 with a norm"):
+        hb.hip_decode_linear(torch.randn(4, 2048, device=dev).to(bf), torch.randn(8, 2048, device=dev).to(bf),
+                             norm_w=torch.ones(2048, device=dev, dtype=bf))
+    with pytest.raises(Exception, match="may not overlap"):
+        hb.hip_decode_linear(a, w, norm_w=nw, mo=a.clone(), gate=nw, x_out=a)
+    with pytest.raises(Exception, match="16-byte aligned"):
+        buf = torch.randn(4, 648, device=dev).to(bf)
+        hb.hip_decode_linear(buf[:, 1:641], w)
