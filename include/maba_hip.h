@@ -54,6 +54,7 @@
  *   maba_hip_rmsnorm                model.py:11-22 (RMSNorm) and the gated residual
  *                                   of MabaBlock, model.py:92-128
  *   maba_hip_swiglu                 model.py:25-38 (SwiGLU activation)
+ *   maba_hip_argmax_rows            model.py:279-313 (the greedy pick, torch.argmax)
  *   maba_hip_decode_linear          nn.Linear of one decode token per sequence
  *                                   (model.py:25-38, 92-128, the layers' projections),
  *                                   its input from RMSNorm, the gated residual +
@@ -322,17 +323,23 @@ int maba_hip_rmsnorm(const maba_tensor* x, const maba_tensor* mo, const maba_ten
 int maba_hip_swiglu(const maba_tensor* gate_up, maba_tensor* out, void* stream);
 
 /* y = A weight^T for a few rows (one decode token per sequence), bf16 with fp32 accumulation.
- * weight [N,K] bf16 (unit K stride, 16-byte aligned rows, K a multiple of 32, K <= 2048).
+ * weight [N,K] bf16 (unit K stride, 16-byte aligned rows, K a multiple of 32, K <= 4096).
  * A is built in the same launch from a ([M,K] or [M,1,K] bf16 rows, 16-byte aligned):
  *   act 0, norm_w NULL:       A = a
- *   act 0, norm_w [K]:        A = bf16(a / sqrt(mean(a^2) + eps) * norm_w)          (K <= 1024)
+ *   rows [M] or [M,1] int64:  A[m] = a[rows[m]] for a table a [V,K] (rows clamped into [0, V))
+ *   act 0, norm_w [K]:        A = bf16(a / sqrt(mean(a^2) + eps) * norm_w)          (K <= 2048)
  *   act 0, norm_w, mo, gate:  x' = bf16(a + gate * mo) is written to x_out and A is the RMSNorm of
- *                             x' as above; x_out may overlap neither a nor mo     (K <= 1024)
+ *                             x' as above; x_out may overlap neither a nor mo     (K <= 2048)
  *   act 1:                    A = bf16(silu(a[:, :K]) * a[:, K:2K]) for a [M,2K]
  * y [M,N] or [M,1,N] bf16, unit column stride, overlapping no input. */
-int maba_hip_decode_linear(const maba_tensor* a, const maba_tensor* mo, const maba_tensor* gate,
-                           const maba_tensor* norm_w, float eps, int act, const maba_tensor* weight,
-                           maba_tensor* x_out, maba_tensor* y, void* stream);
+int maba_hip_decode_linear(const maba_tensor* a, const maba_tensor* rows, const maba_tensor* mo,
+                           const maba_tensor* gate, const maba_tensor* norm_w, float eps, int act,
+                           const maba_tensor* weight, maba_tensor* x_out, maba_tensor* y, void* stream);
+
+/* out[m] = the index of the first maximum of row m of x ([M,V] or [M,1,V], bf16 or f32, unit
+ * column stride, 16-byte aligned rows, V a multiple of 8 (bf16) or 4 (f32)), as torch.argmax:
+ * NaN counts as the maximum and -0 equals +0.  out int64 [M] or [M,1]. */
+int maba_hip_argmax_rows(const maba_tensor* x, maba_tensor* out, void* stream);
 
 #ifdef __cplusplus
 }

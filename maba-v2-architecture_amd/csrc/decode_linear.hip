@@ -2,6 +2,8 @@
 // (M rows, one per sequence; W [N, K] bf16 in nn.Linear's layout), with the layer input stage
 // that feeds A done inside the same launch:
 //   PLAIN    A = a                                      rows [M, K]
+//   GATHER   A = a[rows[m]]                             rows of a table (an embedding lookup,
+//            model.py:95-102's in_emb before its projection)
 //   NORM     A = RMSNorm(a) * nw                        reference model.py:11-22
 //   NORMRES  A = RMSNorm(x') * nw, x' = a + g * mo      model.py:92-128 (MabaBlock's gated
 //            residual; x' is stored to xo in bf16 and normalised as stored, like the separate
@@ -25,10 +27,12 @@
 
 namespace maba {
 
-constexpr int DL_PLAIN = 0, DL_NORM = 1, DL_NORMRES = 2, DL_SWIGLU = 3;
+constexpr int DL_PLAIN = 0, DL_NORM = 1, DL_NORMRES = 2, DL_SWIGLU = 3, DL_GATHER = 4;
 
 struct DlArgs {
-  const uint16_t* a; int64_t as;      // input rows (SWIGLU: [M, 2K])
+  const uint16_t* a; int64_t as;      // input rows (SWIGLU: [M, 2K]; GATHER: the table)
+  const int64_t* rows; int64_t rs;    // GATHER: table row of each output row (clamped into the table)
+  int64_t nrows;                      // GATHER: rows of the table
   const uint16_t* mo; int64_t ms;     // NORMRES: residual branch rows [M, K]
   const uint16_t* g;                  // NORMRES: residual gate [K]
   const uint16_t* nw;                 // NORM, NORMRES: norm weight [K]
@@ -59,26 +63,29 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
   return u;
 }
 
-// CPW: chunk slots per wave (>= ceil(K / 128)).
-template <int MODE, int CPW>
-__global__ __launch_bounds__(256) void decode_linear_kernel(DlArgs a) {
-  __shared__ float s_ss[4][16];
-  __shared__ __attribute__((aligned(16))) float s_acc[4][64][4];
-  asm volatile("" ::"s"(a.a), "s"(a.as), "s"(a.mo), "s"(a.ms), "s"(a.g), "s"(a.nw), "s"(a.xo), "s"(a.xos),
+// NW: waves of the workgroup (they split K); CPW: chunk slots per wave (>= ceil(K / (32 NW))).
+template <int MODE, int NW, int CPW>
+__global__ __launch_bounds__(64 * NW) void decode_linear_kernel(DlArgs a) {
+  __shared__ float s_ss[NW][16];
+  __shared__ __attribute__((aligned(16))) float s_acc[NW][64][4];
+  asm volatile("" ::"s"(a.a), "s"(a.as), "s"(a.rows), "s"(a.rs), "s"(a.nrows), "s"(a.mo), "s"(a.ms), "s"(a.g), "s"(a.nw), "s"(a.xo), "s"(a.xos),
                "s"(a.w), "s"(a.ws), "s"(a.y), "s"(a.ys), "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.eps));
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = lane & 15, q = lane >> 4;   // A row / W row (y column) of the lane, K quarter of the chunk
   const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
-  const int64_t m = min(m0 + r, a.M - 1), n = min(n0 + r, a.N - 1);
+  int64_t m = min(m0 + r, a.M - 1);
+  const int64_t n = min(n0 + r, a.N - 1);
+  if constexpr (MODE == DL_GATHER) m = min(max(a.rows[m * a.rs], (int64_t)0), a.nrows - 1);   // ahead of the weight loads
   const int KC = a.K >> 5, c0 = wave * CPW;
   uint32_t zr;
   asm volatile("v_mov_b32 %0, 0" : "=v"(zr));   // an opaque zero: keeps every conversion out of the loads
   const u32x4 z4 = {zr, zr, zr, zr};
   u32x4 wb[CPW], xa[CPW], xm[CPW], xg[CPW], xn[CPW];
 #pragma unroll
+  for (int j = 0; j < CPW; ++j) wb[j] = *(const u32x4*)(a.w + n * a.ws + 32 * min(c0 + j, KC - 1) + 8 * q);
+#pragma unroll
   for (int j = 0; j < CPW; ++j) {
     const int k = 32 * min(c0 + j, KC - 1) + 8 * q;
-    wb[j] = *(const u32x4*)(a.w + n * a.ws + k);
     xa[j] = *(const u32x4*)(a.a + m * a.as + k);
     xm[j] = z4; xg[j] = z4; xn[j] = z4;
     if constexpr (MODE == DL_NORMRES) {
@@ -117,7 +124,10 @@ __global__ __launch_bounds__(256) void decode_linear_kernel(DlArgs a) {
     ss += __shfl_xor(ss, 32);
     if (q == 0) s_ss[wave][r] = ss;
     __syncthreads();
-    const float inv = rsqrtf((s_ss[0][r] + s_ss[1][r] + s_ss[2][r] + s_ss[3][r]) / (float)a.K + a.eps);
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += s_ss[w][r];
+    const float inv = rsqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
     for (int j = 0; j < CPW; ++j) {
       float nn[8], h[8];
@@ -150,10 +160,14 @@ __global__ __launch_bounds__(256) void decode_linear_kernel(DlArgs a) {
   }
   *(f32x4*)s_acc[wave][lane] = acc;
   __syncthreads();
-  // lane l holds y[m0 + 4 (l / 16) + i][n0 + l % 16], i < 4; wave w stores i = w
-  const float val = s_acc[0][lane][wave] + s_acc[1][lane][wave] + s_acc[2][lane][wave] + s_acc[3][lane][wave];
-  const int row = m0 + 4 * q + wave, col = n0 + r;
-  if (row < a.M && col < a.N) a.y[(int64_t)row * a.ys + col] = (uint16_t)bf16_bits_hw(val);
+  // lane l holds y[m0 + 4 (l / 16) + i][n0 + l % 16], i < 4; wave w < 4 stores i = w
+  if (wave < 4) {
+    float val = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) val += s_acc[w][lane][wave];
+    const int row = m0 + 4 * q + wave, col = n0 + r;
+    if (row < a.M && col < a.N) a.y[(int64_t)row * a.ys + col] = (uint16_t)bf16_bits_hw(val);
+  }
 }
 
 // Rows of a [M, C] / [M, 1, C] bf16 tensor with unit channel stride: the row stride.
@@ -183,42 +197,62 @@ static bool dl_vec(const maba_tensor* t, int64_t C) {
          (uintptr_t)t->data % 16 == 0;
 }
 
-// The kernel for `cpw` chunk slots per wave (the norm modes stop at 8: their per-slot
-// registers for 16 slots would spill).
-template <int MODE, int CPW>
+// The kernel for NW waves of `need` chunk slots each (the norm modes stop at 8 slots: their
+// per-slot registers for more would spill).
+template <int MODE, int NW, int CPW>
 static void (*dl_fit())(DlArgs) {
   if constexpr ((MODE == DL_NORM || MODE == DL_NORMRES) && CPW > 8) return nullptr;
-  else return decode_linear_kernel<MODE, CPW>;
+  else return decode_linear_kernel<MODE, NW, CPW>;
 }
 
-template <int MODE>
+template <int MODE, int NW>
 static void (*dl_pick(int need))(DlArgs) {
-  if (need <= 1) return dl_fit<MODE, 1>();
-  if (need <= 2) return dl_fit<MODE, 2>();
-  if (need <= 3) return dl_fit<MODE, 3>();
-  if (need <= 4) return dl_fit<MODE, 4>();
-  if (need <= 5) return dl_fit<MODE, 5>();
-  if (need <= 6) return dl_fit<MODE, 6>();
-  if (need <= 8) return dl_fit<MODE, 8>();
-  if (need <= 10) return dl_fit<MODE, 10>();
-  if (need <= 12) return dl_fit<MODE, 12>();
-  if (need <= 16) return dl_fit<MODE, 16>();
+  if (need <= 1) return dl_fit<MODE, NW, 1>();
+  if (need <= 2) return dl_fit<MODE, NW, 2>();
+  if (need <= 3) return dl_fit<MODE, NW, 3>();
+  if (need <= 4) return dl_fit<MODE, NW, 4>();
+  if (need <= 5) return dl_fit<MODE, NW, 5>();
+  if (need <= 6) return dl_fit<MODE, NW, 6>();
+  if (need <= 8) return dl_fit<MODE, NW, 8>();
+  if (need <= 10) return dl_fit<MODE, NW, 10>();
+  if (need <= 12) return dl_fit<MODE, NW, 12>();
+  if (need <= 16) return dl_fit<MODE, NW, 16>();
   return nullptr;
 }
+
+template <int NW>
+static void (*dl_pick_mode(int mode, int need))(DlArgs) {
+  return mode == DL_PLAIN ? dl_pick<DL_PLAIN, NW>(need)
+       : mode == DL_GATHER ? dl_pick<DL_GATHER, NW>(need)
+       : mode == DL_NORM ? dl_pick<DL_NORM, NW>(need)
+       : mode == DL_NORMRES ? dl_pick<DL_NORMRES, NW>(need) : dl_pick<DL_SWIGLU, NW>(need);
+}
+
+// Waves per workgroup: eight from K = 1024 (measured on the config-5 widths: K = 1248 with
+// SwiGLU input 5.7 -> 4.6 us per launch; at K <= 640 eight waves cost 0.3-0.5 us more).
+static int dl_waves(int64_t K) { return K >= 1024 ? 8 : 4; }
 
 }  // namespace maba
 
 using namespace maba;
 
-extern "C" int maba_hip_decode_linear(const maba_tensor* a, const maba_tensor* mo, const maba_tensor* gate,
-                                      const maba_tensor* norm_w, float eps, int act, const maba_tensor* weight,
-                                      maba_tensor* x_out, maba_tensor* y, void* stream) {
+extern "C" int maba_hip_decode_linear(const maba_tensor* a, const maba_tensor* rows, const maba_tensor* mo,
+                                      const maba_tensor* gate, const maba_tensor* norm_w, float eps, int act,
+                                      const maba_tensor* weight, maba_tensor* x_out, maba_tensor* y, void* stream) {
   const char* who = "decode_linear";
   if (!a || !weight || !y) return fail(MABA_ERR_INVALID, "%s: a, weight and y required", who);
+  if (rows && (act != 0 || norm_w || mo || gate || x_out))
+    return fail(MABA_ERR_INVALID, "%s: rows take a plain table input", who);
   if (weight->ndim != 2 || weight->dtype != MABA_BF16 || weight->stride[1] != 1 || weight->stride[0] % 8 != 0 ||
       (uintptr_t)weight->data % 16 != 0)
     return fail(MABA_ERR_INVALID, "%s: weight must be bf16 [N,K], unit K stride, 16-byte aligned rows", who);
-  const int64_t N = weight->shape[0], K = weight->shape[1], M = a->shape[0];
+  const int64_t N = weight->shape[0], K = weight->shape[1];
+  int64_t M = a->shape[0];
+  if (rows) {   // rows [M] or [M, 1] int64: table rows
+    if (rows->dtype != MABA_I64 || rows->ndim < 1 || rows->ndim > 2 || (rows->ndim == 2 && rows->shape[1] != 1))
+      return fail(MABA_ERR_INVALID, "%s: rows must be int64 [M] or [M,1]", who);
+    M = rows->shape[0];
+  }
   if (K < 32 || K % 32 != 0) return fail(MABA_ERR_UNSUPPORTED, "%s: K must be a positive multiple of 32", who);
   if (N < 1 || N > (int64_t)INT32_MAX || M > (int64_t)16 * 65535)
     return fail(MABA_ERR_UNSUPPORTED, "%s: N or M out of range", who);
@@ -227,14 +261,20 @@ extern "C" int maba_hip_decode_linear(const maba_tensor* a, const maba_tensor* m
   if ((mo || gate || x_out) && !(mo && gate && x_out && norm_w))
     return fail(MABA_ERR_INVALID, "%s: the gated residual needs mo, gate, x_out and norm_w", who);
   DlArgs d = {};
-  if (!dl_rows(a, M, act == 1 ? 2 * K : K, d.as))
+  if (rows) {
+    if (a->ndim != 2 || a->dtype != MABA_BF16 || a->shape[1] != K || a->stride[1] != 1 || a->stride[0] % 8 != 0 ||
+        (uintptr_t)a->data % 16 != 0 || a->shape[0] < 1)
+      return fail(MABA_ERR_INVALID, "%s: the table must be bf16 [V,K], unit K stride, 16-byte aligned rows", who);
+    d.as = a->stride[0];
+    d.rows = (const int64_t*)rows->data; d.rs = rows->stride[0]; d.nrows = a->shape[0];
+  } else if (!dl_rows(a, M, act == 1 ? 2 * K : K, d.as))
     return fail(MABA_ERR_INVALID, "%s: a must be bf16 [M,%s] or [M,1,%s] rows, unit channel stride, 16-byte aligned",
                 who, act == 1 ? "2K" : "K", act == 1 ? "2K" : "K");
   if (y->dtype != MABA_BF16 || y->shape[0] != M || y->shape[y->ndim - 1] != N || y->stride[y->ndim - 1] != 1 ||
       !(y->ndim == 2 || (y->ndim == 3 && y->shape[1] == 1)))
     return fail(MABA_ERR_INVALID, "%s: y must be bf16 [M,N] or [M,1,N] with unit column stride", who);
   const int64_t ys = y->stride[0];
-  int mode = act == 1 ? DL_SWIGLU : DL_PLAIN;
+  int mode = act == 1 ? DL_SWIGLU : rows ? DL_GATHER : DL_PLAIN;
   if (norm_w) {
     if (!dl_vec(norm_w, K)) return fail(MABA_ERR_INVALID, "%s: norm_w must be bf16 [K], 16-byte aligned", who);
     mode = DL_NORM;
@@ -250,18 +290,17 @@ extern "C" int maba_hip_decode_linear(const maba_tensor* a, const maba_tensor* m
     mode = DL_NORMRES;
     d.mo = (const uint16_t*)mo->data; d.g = (const uint16_t*)gate->data; d.xo = (uint16_t*)x_out->data;
   }
-  if (M > 0 && overlaps(y, ys, N, a, d.as, act == 1 ? 2 * K : K))
+  if (M > 0 && !rows && overlaps(y, ys, N, a, d.as, act == 1 ? 2 * K : K))
     return fail(MABA_ERR_INVALID, "%s: y may not overlap a", who);
-  const int need = (int)((K / 32 + 3) / 4);   // chunk slots per wave
-  void (*k)(DlArgs) = mode == DL_PLAIN ? dl_pick<DL_PLAIN>(need)
-                    : mode == DL_NORM ? dl_pick<DL_NORM>(need)
-                    : mode == DL_NORMRES ? dl_pick<DL_NORMRES>(need) : dl_pick<DL_SWIGLU>(need);
-  if (!k) return fail(MABA_ERR_UNSUPPORTED, "%s: K <= 2048 (1024 with a norm)", who);
+  const int nw = dl_waves(K);
+  const int need = (int)((K / 32 + nw - 1) / nw);   // chunk slots per wave
+  void (*k)(DlArgs) = nw == 8 ? dl_pick_mode<8>(mode, need) : dl_pick_mode<4>(mode, need);
+  if (!k) return fail(MABA_ERR_UNSUPPORTED, "%s: K <= 4096 (2048 with a norm)", who);
   d.a = (const uint16_t*)a->data; d.w = (const uint16_t*)weight->data; d.ws = weight->stride[0];
   d.y = (uint16_t*)y->data; d.ys = ys;
   d.M = (int)M; d.N = (int)N; d.K = (int)K; d.eps = eps;
   if (M == 0) return MABA_OK;
   const dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + 15) / 16));
-  hipLaunchKernelGGL(k, grid, dim3(256), 0, (hipStream_t)stream, d);
+  hipLaunchKernelGGL(k, grid, dim3(64 * nw), 0, (hipStream_t)stream, d);
   return check_launch(who);
 }

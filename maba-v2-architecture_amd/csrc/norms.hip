@@ -146,6 +146,73 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
   }
 }
 
+// Greedy pick (model.py:279-313, torch.argmax over the vocabulary): one workgroup per row.
+// Each thread loads AM_BATCH 16-byte vectors of the row before it reads the first, then keeps
+// the largest key: the value mapped to an unsigned integer in float order (NaN above
+// everything, -0 as +0) in the high word, the complement of the index in the low word, so the
+// largest key of a row is its first maximum.
+constexpr int AM_T = 1024, AM_BATCH = 4;
+
+struct ArgmaxArgs {
+  const void* x; int64_t xs;   // rows [M, V]
+  int64_t* out; int64_t os;
+  int V;
+};
+
+__device__ __forceinline__ uint64_t am_key(float v, int idx) {
+  uint32_t o;
+  if (v != v) {
+    o = 0xffffffffu;
+  } else {
+    const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+    o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  return ((uint64_t)o << 32) | (uint32_t)(0xffffffffu - (uint32_t)idx);
+}
+
+template <class T>
+__global__ __launch_bounds__(AM_T) void argmax_rows_kernel(ArgmaxArgs a) {
+  __shared__ uint64_t s_best[AM_T / 64];
+  typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+  constexpr int E = 16 / sizeof(T);   // elements per vector
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nv = a.V / E;
+  const char* base = (const char*)a.x + (int64_t)blockIdx.x * a.xs * (int64_t)sizeof(T);
+  uint64_t best = 0;
+  for (int v0 = 0; v0 < nv; v0 += AM_T * AM_BATCH) {
+    u32x4 raw[AM_BATCH];
+#pragma unroll
+    for (int b = 0; b < AM_BATCH; ++b) raw[b] = *(const u32x4*)(base + (int64_t)min(v0 + b * AM_T + tid, nv - 1) * 16);
+#pragma unroll
+    for (int b = 0; b < AM_BATCH; ++b) {
+      const int v = v0 + b * AM_T + tid;
+      if (v < nv) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          float f;
+          if constexpr (sizeof(T) == 2) f = __uint_as_float(e & 1 ? raw[b][e / 2] & 0xffff0000u : raw[b][e / 2] << 16);
+          else f = __uint_as_float(raw[b][e]);
+          const uint64_t k = am_key(f, v * E + e);
+          best = k > best ? k : best;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t o = __shfl_xor(best, off);
+    best = o > best ? o : best;
+  }
+  if (lane == 0) s_best[wave] = best;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t b = s_best[0];
+#pragma unroll
+    for (int w = 1; w < AM_T / 64; ++w) b = s_best[w] > b ? s_best[w] : b;
+    a.out[(int64_t)blockIdx.x * a.os] = (int64_t)(0xffffffffu - (uint32_t)b);
+  }
+}
+
 // Rows of a [..., C] tensor: leading dims collapse into one when they are contiguous.
 static bool rows_of(const maba_tensor* t, int C, int64_t& R, int64_t& rs) {
   if (!t || t->ndim < 1 || t->ndim > 3 || t->shape[t->ndim - 1] != C || t->stride[t->ndim - 1] != 1) return false;
@@ -232,4 +299,25 @@ extern "C" int maba_hip_swiglu(const maba_tensor* gate_up, maba_tensor* out, voi
   if (out->dtype == MABA_F32) hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);
   else hipLaunchKernelGGL(swiglu_kernel<uint16_t>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("swiglu");
+}
+
+extern "C" int maba_hip_argmax_rows(const maba_tensor* x, maba_tensor* out, void* stream) {
+  if (!x || !out) return fail(MABA_ERR_INVALID, "argmax_rows: x and out required");
+  if (x->dtype != MABA_F32 && x->dtype != MABA_BF16) return fail(MABA_ERR_DTYPE, "argmax_rows: f32 or bf16 rows");
+  const int64_t V = x->shape[x->ndim - 1], E = x->dtype == MABA_F32 ? 4 : 8;
+  ArgmaxArgs a;
+  int64_t R;
+  if (V < 1 || V > (int64_t)INT32_MAX - 16 || V % E != 0 || !rows_of(x, (int)V, R, a.xs) ||
+      (a.xs * (16 / E)) % 16 != 0 || (uintptr_t)x->data % 16 != 0 || (x->ndim == 3 && x->shape[1] != 1))
+    return fail(MABA_ERR_UNSUPPORTED, "argmax_rows: rows [M,V] or [M,1,V] with unit stride, 16-byte aligned, "
+                "V a multiple of %d", (int)E);
+  if (out->dtype != MABA_I64 || out->shape[0] != R || out->ndim < 1 || out->ndim > 2 ||
+      (out->ndim == 2 && out->shape[1] != 1))
+    return fail(MABA_ERR_INVALID, "argmax_rows: out must be int64 [M] or [M,1]");
+  a.x = x->data; a.out = (int64_t*)out->data; a.os = out->stride[0]; a.V = (int)V;
+  if (R == 0) return MABA_OK;
+  if (R > 0x7fffffff) return fail(MABA_ERR_UNSUPPORTED, "argmax_rows: too many rows");
+  if (x->dtype == MABA_F32) hipLaunchKernelGGL(argmax_rows_kernel<float>, dim3((unsigned)R), dim3(AM_T), 0, (hipStream_t)stream, a);
+  else hipLaunchKernelGGL(argmax_rows_kernel<uint16_t>, dim3((unsigned)R), dim3(AM_T), 0, (hipStream_t)stream, a);
+  return check_launch("argmax_rows");
 }

@@ -59,6 +59,7 @@ EXPORTED_SYMBOLS = (
     "maba_hip_dgda_layer_prefill",
     "maba_hip_dgda_layer_step",
     "maba_hip_decode_linear",
+    "maba_hip_argmax_rows",
 )
 
 
@@ -111,7 +112,8 @@ def _declare(lib) -> None:
         "maba_hip_dgda_layer_prefill_workspace_size": ([i64, i64, i64], sz),
         "maba_hip_dgda_layer_prefill": ([TA, TA, TA, f, T, T, T, TA, vp, sz, vp], i),
         "maba_hip_dgda_layer_step": ([TA, TA, TA, f, T, T, T, TA, vp], i),
-        "maba_hip_decode_linear": ([T, T, T, T, f, i, T, T, T, vp], i),
+        "maba_hip_decode_linear": ([T, T, T, T, T, f, i, T, T, T, vp], i),
+        "maba_hip_argmax_rows": ([T, T, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -363,20 +363,34 @@ def hip_rmsnorm(x, weight, eps: float, mo=None, gate=None, x_out=None) -> torch.
 
 
 def hip_decode_linear(a, weight, norm_w=None, eps: float = 1e-6, mo=None, gate=None, x_out=None,
-                      swiglu: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      swiglu: bool = False, rows=None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``A @ weight.T`` for the few rows of one decode token per sequence (``nn.Linear``,
-    model.py), with A built in the same launch: ``a``; ``RMSNorm(a) * norm_w``
+    model.py), with A built in the same launch: ``a``; ``a[rows]`` for a table ``a [V, K]`` and
+    int64 ``rows [M]`` / ``[M, 1]`` (an embedding lookup); ``RMSNorm(a) * norm_w``
     (model.py:11-22); ``RMSNorm(a + gate * mo) * norm_w`` with the sum written to ``x_out``
     (the gated residual, model.py:92-128); or, with ``swiglu``, ``silu(a[..., :K]) *
     a[..., K:]`` (model.py:25-38).  bf16 rows ``[M, K]`` or ``[M, 1, K]`` (``[.., 2K]`` for
-    swiglu), ``weight [N, K]``; returns bf16 ``[M, N]`` / ``[M, 1, N]`` (into ``out``)."""
-    dev = N.require_device([a, weight, norm_w, mo, gate, x_out, out], "decode_linear")
+    swiglu), ``weight [N, K]``; returns bf16 ``[M, N]`` / ``[M, 1, N]`` (``rows``' shape then N;
+    into ``out``)."""
+    dev = N.require_device([a, rows, weight, norm_w, mo, gate, x_out, out], "decode_linear")
     if out is None:
-        out = torch.empty(*a.shape[:-1], weight.shape[0], dtype=torch.bfloat16, device=dev)
-    rc = N.load().maba_hip_decode_linear(N.desc(a), N.desc(mo), N.desc(gate), N.desc(norm_w), float(eps),
-                                         1 if swiglu else 0, N.desc(weight), N.desc(x_out), N.desc(out),
-                                         N.stream_ptr(dev))
+        lead = rows.shape if rows is not None else a.shape[:-1]
+        out = torch.empty(*lead, weight.shape[0], dtype=torch.bfloat16, device=dev)
+    rc = N.load().maba_hip_decode_linear(N.desc(a), N.desc(rows), N.desc(mo), N.desc(gate), N.desc(norm_w),
+                                         float(eps), 1 if swiglu else 0, N.desc(weight), N.desc(x_out),
+                                         N.desc(out), N.stream_ptr(dev))
     N.check(rc, "decode_linear")
+    return out
+
+
+def hip_argmax_rows(x, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``x.argmax(dim=-1, keepdim=True)`` for bf16 / f32 rows ``[M, V]`` or ``[M, 1, V]`` (the
+    greedy pick of model.py:279-313): int64 ``[M, 1]`` (into ``out``)."""
+    dev = N.require_device([x, out], "argmax_rows")
+    if out is None:
+        out = torch.empty(x.shape[0], 1, dtype=torch.long, device=dev)
+    rc = N.load().maba_hip_argmax_rows(N.desc(x), N.desc(out), N.stream_ptr(dev))
+    N.check(rc, "argmax_rows")
     return out
 
 

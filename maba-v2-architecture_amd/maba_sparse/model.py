@@ -182,11 +182,13 @@ class ServingStep:
         """Decode the token in ``tok``; leaves the next token in ``tok`` and its logits in ``last``.
 
         With ``decode_linear`` each linear layer is one HIP launch that also makes its input:
-        the mixer's first projection normalises the layer input and, from the second layer on,
+        the embedding projection gathers the token's table rows, the mixer's first projection
+        normalises the layer input and, from the second layer on,
         first adds the previous FFN output through the gated residual (writing the new residual
         stream to a fresh buffer); the stacked gate/up projection does the same for the
         mixer's output; the down projection applies SwiGLU's activation; and the head
-        projection takes the last residual through the final norm."""
+        projection takes the last residual through the final norm; the greedy pick is one
+        HIP argmax launch."""
         if self.decode_linear:
             return self._step_decode_linear()
         from maba_sparse.kernels import hip_backend as hb
@@ -216,7 +218,7 @@ class ServingStep:
         m = self.model
         layers = m.layers
         emb = m.embeddings
-        x = hb.hip_decode_linear(emb.in_emb(self.tok), emb.proj.weight)
+        x = hb.hip_decode_linear(emb.in_emb.weight, emb.proj.weight, rows=self.tok)
         n1 = layers[0].norm1
         spec = dict(a=x, norm_w=n1.weight, eps=n1.eps)    # the input stage of the next projection
         for i, layer in enumerate(layers):
@@ -240,17 +242,21 @@ class ServingStep:
             nxt = layers[i + 1].norm1 if i + 1 < len(layers) else m.final_norm
             spec = dict(a=x, norm_w=nxt.weight, eps=nxt.eps, mo=f, gate=g2, x_out=torch.empty_like(x))
         hp = hb.hip_decode_linear(weight=m.head_proj.weight, **spec)
-        self.last = hb.hip_decode_linear(hp, m.lm_head.weight)[:, -1]
-        self.tok.copy_(self.last.argmax(dim=-1, keepdim=True))
+        logits = hb.hip_decode_linear(hp, m.lm_head.weight)
+        self.last = logits[:, -1]
+        hb.hip_argmax_rows(logits, out=self.tok)
         self.counters += 1
 
 
 def _decode_linear_fits(model: "MabaSparseForCausalLM") -> bool:
-    """Whether every linear layer of a serving step fits the HIP decode linear: bf16 weights,
-    no bias (the MABA-SA stream gate's is added after the stacked projection), input widths a
-    multiple of 32, at most 1024 where the input is normalised and 2048 elsewhere; bf16 norm
-    weights and residual gates."""
-    normed, plain = [model.head_proj], [model.embeddings.proj, model.lm_head]
+    """Whether every linear layer of a serving step fits the HIP decode linear: bf16 weights
+    (and embedding table), no bias (the MABA-SA stream gate's is added after the stacked
+    projection), input widths a multiple of 32, at most 2048 where the input is normalised and
+    4096 elsewhere; bf16 norm weights and residual gates; a vocabulary of whole 8-wide vectors
+    for the argmax."""
+    normed, plain = [model.head_proj], [model.embeddings.in_emb, model.embeddings.proj, model.lm_head]
+    if model.config.vocab_size % 8:
+        return False                                       # the argmax kernel's row vectors
     for layer in model.layers:
         mx = layer.mixer
         normed += [layer.ffn.w_gate, layer.ffn.w_up]
@@ -261,7 +267,7 @@ def _decode_linear_fits(model: "MabaSparseForCausalLM") -> bool:
                 return False
         else:
             normed += [mx.q_proj, mx.k_proj, mx.v_proj, mx.gate_alpha, mx.gate_erase, mx.gate_write]
-    for lim, mods in ((1024, normed), (2048, plain)):
+    for lim, mods in ((2048, normed), (4096, plain)):
         for mod in mods:
             w = mod.weight
             if (w.dtype != torch.bfloat16 or w.dim() != 2 or w.shape[1] % 32 or w.shape[1] > lim

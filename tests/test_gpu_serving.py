@@ -278,8 +278,8 @@ def _bf16(x):
 
 @pytest.mark.parametrize("M,K,N,mode", [
     (16, 640, 640, "plain"), (3, 128, 200, "plain"), (20, 1248, 48, "plain"), (16, 640, 3840, "norm"),
-    (16, 640, 2496, "normres"), (5, 96, 40, "normres"), (16, 1024, 32, "normres"), (16, 1248, 640, "swiglu"),
-    (7, 2048, 64, "swiglu")])
+    (16, 640, 2496, "normres"), (5, 96, 40, "normres"), (16, 1024, 32, "normres"), (4, 2048, 48, "norm"),
+    (16, 1248, 640, "swiglu"), (7, 2048, 64, "swiglu"), (3, 4096, 32, "plain")])
 def test_decode_linear_modes(dev, M, K, N, mode):
     """y = A W^T with A's input stage in the same launch, against float64 on the same bf16
     operand: the output is one bf16 rounding (half an ulp) of the product; an element of A
@@ -330,11 +330,45 @@ def test_decode_linear_rejects(dev):
     nw = torch.ones(640, device=dev, dtype=bf)
     with pytest.raises(Exception, match="multiple of 32"):
         hb.hip_decode_linear(a[..., :600], w[:, :600].contiguous())
-    with pytest.raises(Exception, match="1024 with a norm"):
-        hb.hip_decode_linear(torch.randn(4, 2048, device=dev).to(bf), torch.randn(8, 2048, device=dev).to(bf),
-                             norm_w=torch.ones(2048, device=dev, dtype=bf))
+    with pytest.raises(Exception, match="2048 with a norm"):
+        hb.hip_decode_linear(torch.randn(4, 2080, device=dev).to(bf), torch.randn(8, 2080, device=dev).to(bf),
+                             norm_w=torch.ones(2080, device=dev, dtype=bf))
     with pytest.raises(Exception, match="may not overlap"):
         hb.hip_decode_linear(a, w, norm_w=nw, mo=a.clone(), gate=nw, x_out=a)
     with pytest.raises(Exception, match="16-byte aligned"):
         buf = torch.randn(4, 648, device=dev).to(bf)
         hb.hip_decode_linear(buf[:, 1:641], w)
+
+
+def test_decode_linear_gather(dev):
+    """Table rows picked by int64 ids (the embedding lookup before its projection), ids
+    outside the table clamped into it: equal to the plain decode linear on the gathered rows."""
+    hb = _hb()
+    g = torch.Generator().manual_seed(11)
+    table = torch.randn(1000, 128, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(640, 128, generator=g) / 12).to(torch.bfloat16).to(dev)
+    ids = torch.tensor([[5], [999], [0], [17], [5]], dtype=torch.long, device=dev)
+    got = hb.hip_decode_linear(table, w, rows=ids)
+    assert got.shape == (5, 1, 640)
+    exp = hb.hip_decode_linear(table[ids[:, 0]].unsqueeze(1).contiguous(), w)
+    assert torch.equal(got, exp)
+    far = hb.hip_decode_linear(table, w, rows=torch.tensor([-3, 5000], dtype=torch.long, device=dev))
+    assert torch.equal(far, hb.hip_decode_linear(table[[0, 999]].contiguous(), w))
+
+
+@pytest.mark.parametrize("M,V,dtype", [(16, 32768, torch.bfloat16), (3, 1000, torch.float32), (2, 40000, torch.bfloat16)])
+def test_argmax_rows(dev, M, V, dtype):
+    """torch.argmax's pick, including ties (first index), -0 against +0, and NaN."""
+    hb = _hb()
+    g = torch.Generator().manual_seed(V)
+    x = torch.randn(M, 1, V, generator=g).to(dtype)
+    x[0, 0, [7, V - 3]] = 50.0                                    # a tie: the first wins
+    if M > 1:
+        x[1, 0, :] = -1.0
+        x[1, 0, [V // 2, 3]] = torch.tensor([0.0, -0.0], dtype=dtype)   # -0 and +0 equal
+    if M > 2:
+        x[2, 0, [V - 1, 9]] = float("nan")                       # NaN is the maximum
+    xd = x.to(dev)
+    got = hb.hip_argmax_rows(xd)
+    assert torch.equal(got.cpu(), xd.argmax(dim=-1).cpu())
+    assert int(got[0, 0]) == 7
