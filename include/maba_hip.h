@@ -51,6 +51,12 @@
  *                                   count read from device memory
  *   maba_hip_maba_sa_decode_dev     layers/sparse_attention.py:79-219,263-275 with
  *                                   the sequence length read from device memory
+ *   maba_hip_cache_append_heads     maba_hip_cache_append plus the token's absorbed
+ *                                   queries W_k,h^T q_h and gate logits W_g x + b
+ *                                   (layers/sparse_attention.py:79-219, 274)
+ *   maba_hip_maba_sa_decode_dev_heads  maba_hip_maba_sa_decode_dev plus the value
+ *                                   up-projection W_v,h z_h of each head
+ *                                   (layers/sparse_attention.py:208, absorbed)
  *   maba_hip_rmsnorm                model.py:11-22 (RMSNorm) and the gated residual
  *                                   of MabaBlock, model.py:92-128
  *   maba_hip_swiglu                 model.py:25-38 (SwiGLU activation)
@@ -282,6 +288,17 @@ int maba_hip_cache_append(const maba_tensor* c_new, const maba_tensor* k_new, co
                           maba_tensor* c_cache, maba_tensor* k_cache, maba_tensor* hca,
                           maba_tensor* centroids, int pool, int block_size, void* stream);
 
+/* maba_hip_cache_append, and in the same launch the token's absorbed queries and gate logits:
+ * q_lat [B,H,dc] f32 (unit channel stride) = W_k,h^T q_h for q_heads [B,H*dh] and
+ * w_k [H*dh,dc] (unit column stride), summed in fp32; gate_out [B,3] = bf16(gate_in + gate_bias)
+ * for gate_in [B,3], gate_bias [3].  All bf16 but q_lat. */
+int maba_hip_cache_append_heads(const maba_tensor* c_new, const maba_tensor* k_new, const int64_t* pos,
+                                maba_tensor* c_cache, maba_tensor* k_cache, maba_tensor* hca,
+                                maba_tensor* centroids, int pool, int block_size,
+                                const maba_tensor* q_heads, const maba_tensor* w_k,
+                                const maba_tensor* gate_in, const maba_tensor* gate_bias,
+                                maba_tensor* q_lat, maba_tensor* gate_out, void* stream);
+
 /* maba_hip_index_topk_decode over the first nb = ceil(*d_len / block_size) rows of centroids
  * [B,Ncap,d] (bf16 MFMA path; nb must reach top_k).  out_idx int64 [B,Hq,top_k]; workspace
  * sized by maba_hip_index_topk_decode_workspace_size(B, Hq, Ncap, top_k). */
@@ -298,6 +315,17 @@ int maba_hip_maba_sa_decode_dev(const maba_tensor* q_lat, const maba_tensor* c_k
                                 float scale, int window, int n_sink, int block_size, int pool,
                                 maba_tensor* out_lat, void* workspace, size_t workspace_bytes,
                                 void* stream);
+
+/* maba_hip_maba_sa_decode_dev, and in its merge launch the value up-projection of each head:
+ * out_heads [B,H*dh] bf16 = bf16(W_v,h z_h) for w_v [H*dh,dc] bf16 (dh <= 64, unit column
+ * stride, 8-byte aligned rows), summed in fp32; out_lat still receives z. */
+int maba_hip_maba_sa_decode_dev_heads(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                      const maba_tensor* hca, const maba_tensor* idx,
+                                      const maba_tensor* gate, const int64_t* d_len, int64_t L_cap,
+                                      float scale, int window, int n_sink, int block_size, int pool,
+                                      const maba_tensor* w_v, maba_tensor* out_heads,
+                                      maba_tensor* out_lat, void* workspace, size_t workspace_bytes,
+                                      void* stream);
 
 /* One decode token of the DGDA layer after its input projection: the single-token prologue
  * of maba_hip_dgda_prologue (conv + SiLU over the carried history, key norm, gates, new

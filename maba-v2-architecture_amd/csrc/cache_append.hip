@@ -19,6 +19,13 @@
 // every position); the caller advances *pos after the step.  One workgroup per sequence:
 // it reduces the block that holds row p, taking row p from the inputs and rows before it
 // from the caches (written by earlier launches), then writes the two rows.
+//
+// The same launch can also form the token's absorbed queries and gate logits, which the
+// decode streams read next (layers/sparse_attention.py:79-219 with the latent absorption
+// <q_h, W_k,h c> = <W_k,h^T q_h, c>, and :274, W_g x + b): B * H more workgroups, one per
+// (b, h), write q_lat[b, h, :] = W_k,h^T q_h in fp32 (bf16 products, exact in fp32, summed
+// in fp32), and the first of each sequence writes the gate logits plus bias, rounded to bf16
+// as the bf16 addition of the two would be.
 #include "maba_common.h"
 
 namespace maba {
@@ -36,6 +43,14 @@ struct AppendArgs {
   const int64_t* pos;
   int64_t Lmax, nh_max, nc_max;
   int dc, di, pool, bs;
+  // absorbed queries and gate logits (qh null: not formed)
+  const uint16_t* qh; int64_t qhsb, qhsd;   // q projection [B, H * dh] bf16
+  const uint16_t* wk; int64_t wks;          // W_k [H * dh, dc] bf16, unit column stride
+  float* ql; int64_t qlsb, qlsh;            // q_lat [B, H, dc] fp32, unit channel stride
+  const uint16_t* gin; int64_t ginsb, ginsd;   // gate logits [B, 3] bf16
+  const uint16_t* gbias; int64_t gbsd;         // gate bias [3] bf16
+  uint16_t* gout; int64_t goutsb, goutsd;      // gate logits + bias [B, 3] bf16
+  int H, dh;
 };
 
 // Column reduction of rows [r0, p) of a cache plus the new row (newrow[col * nsd]): sum
@@ -89,8 +104,51 @@ __device__ void ap_reduce(const uint16_t* base, int64_t rstride, int64_t r0, int
   __syncthreads();
 }
 
-__global__ __launch_bounds__(AP_T) void cache_append_kernel(AppendArgs a) {
+// q_lat[b, h, c] = sum_d q[b, h dh + d] W_k[h dh + d, c]: thread (part, c) sums its part of
+// the d range in ascending order, the parts are added in a fixed order (deterministic).
+__device__ void ap_absorbed_query(const AppendArgs& a, int64_t b, int h, float* s_part) {
+  const int tid = threadIdx.x;
+  const int parts = AP_T / a.dc;
+  const int c = tid % a.dc, part = tid / a.dc;
+  const int per = (a.dh + parts - 1) / parts;
+  float acc = 0.f;
+  if (part < parts) {
+    const int d0 = part * per, d1 = min(a.dh, d0 + per);
+    const uint16_t* q = a.qh + b * a.qhsb + (int64_t)h * a.dh * a.qhsd;
+    const uint16_t* w = a.wk + (int64_t)h * a.dh * a.wks + c;
+    for (int d = d0; d < d1; d += AP_BATCH) {   // a batch of loads in flight, then its products in order
+      uint16_t qv[AP_BATCH], wv[AP_BATCH];
+#pragma unroll
+      for (int k = 0; k < AP_BATCH; ++k) {
+        const int dd = min(d + k, d1 - 1);
+        qv[k] = q[dd * a.qhsd];
+        wv[k] = w[dd * a.wks];
+      }
+#pragma unroll
+      for (int k = 0; k < AP_BATCH; ++k)
+        if (d + k < d1) acc = fmaf(bf16_bits_to_f32(qv[k]), bf16_bits_to_f32(wv[k]), acc);
+    }
+    s_part[part * a.dc + c] = acc;
+  }
+  __syncthreads();
+  if (tid < a.dc) {
+    float r = 0.f;
+    for (int q = 0; q < parts; ++q) r += s_part[q * a.dc + tid];
+    a.ql[b * a.qlsb + (int64_t)h * a.qlsh + tid] = r;
+  }
+  if (h == 0 && tid < 3) {
+    const float g = bf16_bits_to_f32(a.gin[b * a.ginsb + tid * a.ginsd]) + bf16_bits_to_f32(a.gbias[tid * a.gbsd]);
+    a.gout[b * a.goutsb + tid * a.goutsd] = f32_to_bf16_bits(g);
+  }
+}
+
+__global__ __launch_bounds__(AP_T) void cache_append_kernel(AppendArgs a, int64_t B) {
   __shared__ float s_sum[AP_T], s_max[AP_T];
+  if ((int64_t)blockIdx.x >= B) {   // absorbed query of one (b, h)
+    const int64_t j = blockIdx.x - B;
+    ap_absorbed_query(a, j / a.H, (int)(j % a.H), s_sum);
+    return;
+  }
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   // the new rows, loaded together with the position; they are stored last, so that no
@@ -124,9 +182,11 @@ __global__ __launch_bounds__(AP_T) void cache_append_kernel(AppendArgs a) {
 
 using namespace maba;
 
-extern "C" int maba_hip_cache_append(const maba_tensor* c_new, const maba_tensor* k_new, const int64_t* pos,
-                                     maba_tensor* c_cache, maba_tensor* k_cache, maba_tensor* hca,
-                                     maba_tensor* centroids, int pool, int block_size, void* stream) {
+static int cache_append(const maba_tensor* c_new, const maba_tensor* k_new, const int64_t* pos,
+                        maba_tensor* c_cache, maba_tensor* k_cache, maba_tensor* hca, maba_tensor* centroids,
+                        int pool, int block_size, const maba_tensor* q_heads, const maba_tensor* w_k,
+                        const maba_tensor* gate_in, const maba_tensor* gate_bias, maba_tensor* q_lat,
+                        maba_tensor* gate_out, void* stream) {
   if (!c_new || c_new->ndim != 2 || !k_new || k_new->ndim != 2)
     return fail(MABA_ERR_INVALID, "cache_append: c_new must be [B,dc] and k_new [B,di]");
   const int64_t B = c_new->shape[0], dc = c_new->shape[1], di = k_new->shape[1];
@@ -161,6 +221,49 @@ extern "C" int maba_hip_cache_append(const maba_tensor* c_new, const maba_tensor
   a.pos = pos;
   a.Lmax = Lmax; a.nh_max = hca->shape[1]; a.nc_max = centroids->shape[1];
   a.dc = (int)dc; a.di = (int)di; a.pool = pool; a.bs = block_size;
-  hipLaunchKernelGGL(cache_append_kernel, dim3((unsigned)B), dim3(AP_T), 0, (hipStream_t)stream, a);
+  a.qh = nullptr; a.H = 0; a.dh = 0;
+  int64_t nq = 0;
+  if (q_heads) {   // absorbed queries and gate logits in the same launch
+    if (q_heads->ndim != 2 || q_heads->shape[0] != B || !w_k || w_k->ndim != 2 || w_k->shape[1] != dc ||
+        w_k->shape[0] != q_heads->shape[1] || !q_lat || q_lat->ndim != 3 || q_lat->shape[0] != B ||
+        q_lat->shape[2] != dc || w_k->shape[0] % q_lat->shape[1] != 0)
+      return fail(MABA_ERR_INVALID, "cache_append: q_heads [B,H*dh], w_k [H*dh,dc], q_lat [B,H,dc] required");
+    const int64_t so[2] = {B, 3}, sb[1] = {3};
+    if (!expect_shape(gate_in, "gate_in", 2, so) || !expect_shape(gate_out, "gate_out", 2, so) ||
+        !expect_shape(gate_bias, "gate_bias", 1, sb))
+      return MABA_ERR_INVALID;
+    for (const maba_tensor* t : {q_heads, w_k, gate_in, gate_bias, (const maba_tensor*)gate_out})
+      if (t->dtype != MABA_BF16) return fail(MABA_ERR_DTYPE, "cache_append: bf16 q_heads, w_k and gate tensors");
+    if (q_lat->dtype != MABA_F32 || q_lat->stride[2] != 1 || w_k->stride[1] != 1)
+      return fail(MABA_ERR_DTYPE, "cache_append: q_lat f32 and w_k with unit channel strides");
+    a.qh = (const uint16_t*)q_heads->data; a.qhsb = q_heads->stride[0]; a.qhsd = q_heads->stride[1];
+    a.wk = (const uint16_t*)w_k->data; a.wks = w_k->stride[0];
+    a.ql = (float*)q_lat->data; a.qlsb = q_lat->stride[0]; a.qlsh = q_lat->stride[1];
+    a.gin = (const uint16_t*)gate_in->data; a.ginsb = gate_in->stride[0]; a.ginsd = gate_in->stride[1];
+    a.gbias = (const uint16_t*)gate_bias->data; a.gbsd = gate_bias->stride[0];
+    a.gout = (uint16_t*)gate_out->data; a.goutsb = gate_out->stride[0]; a.goutsd = gate_out->stride[1];
+    a.H = (int)q_lat->shape[1];
+    a.dh = (int)(w_k->shape[0] / a.H);
+    nq = B * a.H;
+  }
+  hipLaunchKernelGGL(cache_append_kernel, dim3((unsigned)(B + nq)), dim3(AP_T), 0, (hipStream_t)stream, a, B);
   return check_launch("cache_append");
+}
+
+extern "C" int maba_hip_cache_append(const maba_tensor* c_new, const maba_tensor* k_new, const int64_t* pos,
+                                     maba_tensor* c_cache, maba_tensor* k_cache, maba_tensor* hca,
+                                     maba_tensor* centroids, int pool, int block_size, void* stream) {
+  return cache_append(c_new, k_new, pos, c_cache, k_cache, hca, centroids, pool, block_size, nullptr, nullptr,
+                      nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int maba_hip_cache_append_heads(const maba_tensor* c_new, const maba_tensor* k_new, const int64_t* pos,
+                                           maba_tensor* c_cache, maba_tensor* k_cache, maba_tensor* hca,
+                                           maba_tensor* centroids, int pool, int block_size,
+                                           const maba_tensor* q_heads, const maba_tensor* w_k,
+                                           const maba_tensor* gate_in, const maba_tensor* gate_bias,
+                                           maba_tensor* q_lat, maba_tensor* gate_out, void* stream) {
+  if (!q_heads) return fail(MABA_ERR_INVALID, "cache_append_heads: q_heads required");
+  return cache_append(c_new, k_new, pos, c_cache, k_cache, hca, centroids, pool, block_size, q_heads, w_k,
+                      gate_in, gate_bias, q_lat, gate_out, stream);
 }

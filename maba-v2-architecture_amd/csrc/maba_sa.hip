@@ -47,6 +47,10 @@ struct SaArgs {
   int tpw, s_loc, s_hca, s_sp1, s_sp;
   float scale;
   const int64_t* dlen;   // device sequence length (null: L as given); the geometry above is then re-derived
+  // value up-projection in the merge (wv null: not applied): oh[b, h dh + d] = bf16(sum_c W_v[h dh + d, c] z[b, h, c])
+  const uint16_t* wv; int64_t wvs;    // W_v [H * dh, dc] bf16, unit column stride
+  uint16_t* oh; int64_t ohsb, ohsd;   // [B, H * dh] bf16
+  int dh;
 };
 
 // Tile geometry of the three streams (per batch element).
@@ -200,7 +204,8 @@ __global__ __launch_bounds__(256) void maba_sa_tile_kernel(SaArgs a) {
 // weighted sums.  lds holds at least 2 NT + 8 floats.
 constexpr int SA_PRE = 16;   // partials per thread whose latent sums are loaded up front
 template <int NT, class Src>
-__device__ void sa_merge(const SaArgs& a, const SaMerge& mg, int64_t b, int h, float* lds, const Src& src) {
+__device__ void sa_merge(const SaArgs& a, const SaMerge& mg, int64_t b, int h, float* lds, const Src& src,
+                         float* zkeep = nullptr) {
   float* s_w = lds;
   float* s_acc = lds + NT;
   float* s_M = lds + 2 * NT;
@@ -292,7 +297,33 @@ __device__ void sa_merge(const SaArgs& a, const SaMerge& mg, int64_t b, int h, f
       res = fmaf(gate_of(2), zs / (float)a.L, res);
     }
     a.out[b * a.osb + h * a.osh + tid * a.osd] = res;
+    if (zkeep) zkeep[tid] = res;
   }
+}
+
+// o[b, h dh + d] = bf16(sum_c W_v[h dh + d, c] z[c]) for the merged z of (b, h) in LDS (the
+// caller's sa_merge left it in zk): four threads per output, eight bf16 weights per load,
+// the four partial sums added by shuffles (layers/sparse_attention.py:208, absorbed:
+// sum_j p_j W_v,h c_j = W_v,h z_h).
+template <int NT>
+__device__ __forceinline__ void sa_value_up(const SaArgs& a, int64_t b, int h, const float* zk) {
+  const int tid = threadIdx.x;
+  const int d = tid >> 2, part = tid & 3;
+  const int per = a.dc / 4;   // a multiple of 8 (dc a multiple of 32)
+  float acc = 0.f;
+  if (d < a.dh) {
+    const uint16_t* w = a.wv + ((int64_t)h * a.dh + d) * a.wvs + part * per;
+    for (int c = 0; c < per; c += 8) {
+      const i16x4 lo4 = *(const i16x4*)(w + c), hi4 = *(const i16x4*)(w + c + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = fmaf(bf16_bits_to_f32((uint16_t)lo4[j]), zk[part * per + c + j], acc);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = fmaf(bf16_bits_to_f32((uint16_t)hi4[j]), zk[part * per + c + 4 + j], acc);
+    }
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  if (d < a.dh && part == 0) a.oh[b * a.ohsb + ((int64_t)h * a.dh + d) * a.ohsd] = f32_to_bf16_bits(acc);
 }
 
 // Partials of (b, h) in the workspace: virtual partial t at slot t (t < na), else at
@@ -319,10 +350,15 @@ __device__ __forceinline__ SaWsSrc sa_ws_src(const SaArgs& a, const SaMerge& mg,
 // One workgroup per (b, h) over the per-tile partials of the generic path.
 __global__ __launch_bounds__(256) void maba_sa_combine_kernel(SaArgs a_in, SaMerge mg) {
   __shared__ float lds[2 * 256 + 8];
+  __shared__ float zk[SA_MAXDC];
   const SaArgs a = sa_live(a_in);
   const int64_t b = blockIdx.x / a.H;
   const int h = blockIdx.x % a.H;
-  sa_merge<256>(a, mg, b, h, lds, sa_ws_src(a, mg, b, h));
+  sa_merge<256>(a, mg, b, h, lds, sa_ws_src(a, mg, b, h), a.wv ? zk : nullptr);
+  if (a.wv) {
+    __syncthreads();
+    sa_value_up<256>(a, b, h, zk);
+  }
 }
 
 // ------------------------------------------------------------------ MFMA path
@@ -1070,6 +1106,39 @@ extern "C" int maba_hip_maba_sa_decode_dev(const maba_tensor* q_lat, const maba_
     return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_dev: bf16 caches with 16-byte aligned rows and d_c a "
                                       "multiple of 32 up to 128 required");
   if (L_cap < pool) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_dev: L_cap must be at least pool");
+  a.dlen = d_len;
+  return sa_run(a, seg, (hipStream_t)stream);
+}
+
+extern "C" int maba_hip_maba_sa_decode_dev_heads(const maba_tensor* q_lat, const maba_tensor* c_kv,
+                                                 const maba_tensor* hca, const maba_tensor* idx,
+                                                 const maba_tensor* gate, const int64_t* d_len, int64_t L_cap,
+                                                 float scale, int window, int n_sink, int block_size, int pool,
+                                                 const maba_tensor* w_v, maba_tensor* out_heads,
+                                                 maba_tensor* out_lat, void* workspace, size_t workspace_bytes,
+                                                 void* stream) {
+  if (!d_len) return fail(MABA_ERR_INVALID, "maba_sa_decode_dev_heads: d_len (device int64) required");
+  SaArgs a;
+  bool seg = false, empty = false;
+  size_t need = 0;
+  int rc = sa_setup(q_lat, c_kv, hca, idx, gate, out_lat, L_cap, scale, window, n_sink, block_size, pool,
+                    workspace, workspace_bytes, a, seg, empty, need);
+  if (rc || empty) return rc;
+  if (!seg)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_dev_heads: bf16 caches with 16-byte aligned rows and d_c a "
+                                      "multiple of 32 up to 128 required");
+  if (L_cap < pool) return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_dev_heads: L_cap must be at least pool");
+  const int64_t B = a.B, H = a.H, dc = a.dc;
+  if (!w_v || w_v->ndim != 2 || w_v->shape[1] != dc || w_v->shape[0] % H != 0 || w_v->shape[0] / H > 64 ||
+      !out_heads || out_heads->ndim != 2 || out_heads->shape[0] != B || out_heads->shape[1] != w_v->shape[0])
+    return fail(MABA_ERR_INVALID, "maba_sa_decode_dev_heads: w_v [H*dh,dc] (dh <= 64) and out_heads [B,H*dh] required");
+  if (w_v->dtype != MABA_BF16 || out_heads->dtype != MABA_BF16)
+    return fail(MABA_ERR_DTYPE, "maba_sa_decode_dev_heads: bf16 w_v and out_heads");
+  if (w_v->stride[1] != 1 || (uintptr_t)w_v->data % 8 != 0 || w_v->stride[0] % 4 != 0)
+    return fail(MABA_ERR_UNSUPPORTED, "maba_sa_decode_dev_heads: w_v rows 8-byte aligned with unit column stride");
+  a.wv = (const uint16_t*)w_v->data; a.wvs = w_v->stride[0];
+  a.oh = (uint16_t*)out_heads->data; a.ohsb = out_heads->stride[0]; a.ohsd = out_heads->stride[1];
+  a.dh = (int)(w_v->shape[0] / H);
   a.dlen = d_len;
   return sa_run(a, seg, (hipStream_t)stream);
 }

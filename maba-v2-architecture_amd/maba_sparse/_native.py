@@ -60,6 +60,8 @@ EXPORTED_SYMBOLS = (
     "maba_hip_dgda_layer_step",
     "maba_hip_decode_linear",
     "maba_hip_argmax_rows",
+    "maba_hip_cache_append_heads",
+    "maba_hip_maba_sa_decode_dev_heads",
 )
 
 
@@ -114,6 +116,8 @@ def _declare(lib) -> None:
         "maba_hip_dgda_layer_step": ([TA, TA, TA, f, T, T, T, TA, vp], i),
         "maba_hip_decode_linear": ([T, T, T, T, T, f, i, T, T, T, vp], i),
         "maba_hip_argmax_rows": ([T, T, vp], i),
+        "maba_hip_cache_append_heads": ([T, T, vp, T, T, T, T, i, i, T, T, T, T, T, T, vp], i),
+        "maba_hip_maba_sa_decode_dev_heads": ([T, T, T, T, T, vp, i64, f, i, i, i, i, T, T, T, vp, sz, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -313,6 +313,21 @@ def hip_cache_append(c_new, k_new, pos, c_cache, k_cache, hca, centroids, pool: 
     N.check(rc, "cache_append")
 
 
+def hip_cache_append_heads(c_new, k_new, pos, c_cache, k_cache, hca, centroids, q_heads, w_k, gate_in, gate_bias,
+                           q_lat, gate_out, pool: int = 64, block_size: int = 64) -> None:
+    """``hip_cache_append`` plus, in the same launch, the token's absorbed queries
+    ``q_lat [B, H, d_c] = W_k,h^T q_h`` (fp32) for ``q_heads [B, H * d_head]`` and the gate
+    logits ``gate_out = gate_in + gate_bias`` (bf16), which the decode streams read next
+    (layers/sparse_attention.py:79-219, 274)."""
+    dev = N.require_device([c_new, k_new, pos, c_cache, k_cache, hca, centroids, q_heads, w_k, gate_in, gate_bias,
+                            q_lat, gate_out], "cache_append_heads")
+    rc = N.load().maba_hip_cache_append_heads(N.desc(c_new), N.desc(k_new), pos.data_ptr(), N.desc(c_cache),
+                                              N.desc(k_cache), N.desc(hca), N.desc(centroids), int(pool),
+                                              int(block_size), N.desc(q_heads), N.desc(w_k), N.desc(gate_in),
+                                              N.desc(gate_bias), N.desc(q_lat), N.desc(gate_out), N.stream_ptr(dev))
+    N.check(rc, "cache_append_heads")
+
+
 def hip_index_topk_decode_dev(q, centroids, length, block_size: int, lambda_dist: float, top_k: int,
                               workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Decode scoring + top-k over the first ``ceil(*length / block_size)`` rows of a centroid
@@ -348,6 +363,28 @@ def hip_maba_sa_decode_dev(q_lat, c_cache, hca, idx, gate, length, L_cap: int, s
                                          int(block_size), int(pool), N.desc(out), ws.data_ptr(), ws.numel(),
                                          N.stream_ptr(dev))
     N.check(rc, "maba_sa_decode_dev")
+    return out
+
+
+def hip_maba_sa_decode_dev_heads(q_lat, c_cache, hca, idx, gate, length, L_cap: int, scale: float, w_v,
+                                 out_heads, window: int = 128, n_sink: int = 4, block_size: int = 64, pool: int = 64,
+                                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``hip_maba_sa_decode_dev`` with each head's value up-projection in its merge launch:
+    ``out_heads [B, H * d_head] = W_v,h z_h`` in bf16 (layers/sparse_attention.py:208,
+    absorbed).  Returns ``z`` fp32 ``[B, H, d_c]`` as well."""
+    dev = N.require_device([q_lat, c_cache, hca, idx, gate, length, w_v, out_heads], "maba_sa_decode_dev_heads")
+    B, H, dc = q_lat.shape
+    lib = N.load()
+    out = torch.empty(B, H, dc, dtype=torch.float32, device=dev)
+    nbytes = lib.maba_hip_maba_sa_decode_workspace_size(B, H, dc, int(L_cap), idx.shape[-1], int(window),
+                                                        int(n_sink), int(pool))
+    ws = workspace if workspace is not None and workspace.numel() >= nbytes else _workspace(nbytes, dev)
+    rc = lib.maba_hip_maba_sa_decode_dev_heads(N.desc(q_lat), N.desc(c_cache), N.desc(hca), N.desc(idx),
+                                               N.desc(gate), length.data_ptr(), int(L_cap), float(scale),
+                                               int(window), int(n_sink), int(block_size), int(pool), N.desc(w_v),
+                                               N.desc(out_heads), N.desc(out), ws.data_ptr(), ws.numel(),
+                                               N.stream_ptr(dev))
+    N.check(rc, "maba_sa_decode_dev_heads")
     return out
 
 

@@ -179,7 +179,7 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
                                     block_size=self.block_size, pool=self.hca_pool_size)
         return self._heads_out(z, x.dtype)
 
-    def _token_projections(self, x: torch.Tensor, proj=None):
+    def _token_projections(self, x: torch.Tensor, proj=None, gate_bias: bool = True):
         """q, the new latent, the indexer's query and key and the gate logits of one token from
         one GEMM over the stacked weights (the stack is rebuilt only after a weight changes).
 
@@ -199,7 +199,7 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         w5 = cached(self, "w5", ws, stack)
         y = proj(w5) if proj is not None else F.linear(x, w5)
         qi, ki, q, c_new, gl, _ = y.split(sizes + [pad], dim=-1)
-        return q, c_new, qi, ki, gl + self.stream_gate.bias
+        return q, c_new, qi, ki, (gl + self.stream_gate.bias if gate_bias else gl)
 
     def decode_step(self, x: torch.Tensor, cache: LatentCache,
                     past_centroids: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -229,6 +229,24 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         gives the batch and dtype), and ``o_proj`` runs as a decode linear too."""
         from maba_sparse.kernels import hip_backend as hb
         B = x.shape[0]
+        if x.dtype == torch.bfloat16 and self._heads_fusable():
+            # five launches for the streams: the append also forms the absorbed queries and the
+            # gate logits, the merge also applies each head's value up-projection
+            q, c_new, qi, ki, gl = self._token_projections(x, proj, gate_bias=False)
+            q_lat = torch.empty(B, self.n_heads, self.d_c, dtype=torch.float32, device=x.device)
+            gate = torch.empty(B, 3, dtype=torch.bfloat16, device=x.device)
+            hb.hip_cache_append_heads(c_new[:, 0], ki[:, 0], counters[0], cache.c, cache.keys, cache.hca, cache.cent,
+                                      q[:, 0], self.k_up_proj.weight, gl[:, 0], self.stream_gate.bias, q_lat, gate,
+                                      pool=self.hca_pool_size, block_size=self.block_size)
+            idx = hb.hip_index_topk_decode_dev(qi, cache.cent, counters[1], self.block_size, self.dist_lambda,
+                                               self.top_k)
+            o = torch.empty(B, 1, self.n_heads * self.d_head, dtype=torch.bfloat16, device=x.device)
+            z = hb.hip_maba_sa_decode_dev_heads(q_lat, cache.c, cache.hca, idx, gate, counters[1], cache.cap,
+                                                self.scale, self.v_up_proj.weight, o[:, 0],
+                                                window=self.window_size, n_sink=self.n_sink_tokens,
+                                                block_size=self.block_size, pool=self.hca_pool_size)
+            out = hb.hip_decode_linear(o, self.o_proj.weight) if proj is not None else self.o_proj(o)
+            return (out, idx, z) if return_parts else out
         q, c_new, qi, ki, gl = self._token_projections(x, proj)
         hb.hip_cache_append(c_new[:, 0], ki[:, 0], counters[0], cache.c, cache.keys, cache.hca, cache.cent,
                             pool=self.hca_pool_size, block_size=self.block_size)
@@ -240,6 +258,15 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
                                       block_size=self.block_size, pool=self.hca_pool_size)
         out = self._heads_out(z, x.dtype, decode_linear=proj is not None)
         return (out, idx, z) if return_parts else out
+
+    def _heads_fusable(self) -> bool:
+        """Whether the serving step's append and merge launches also form the absorbed queries,
+        the gate logits and the value up-projection: bf16 weights, a gate bias, heads of at most
+        64 channels."""
+        ws = (self.k_up_proj.weight, self.v_up_proj.weight, self.stream_gate.weight)
+        return (all(w.dtype == torch.bfloat16 for w in ws) and self.stream_gate.bias is not None
+                and self.stream_gate.bias.dtype == torch.bfloat16 and self.d_head <= 64
+                and self.k_up_proj.bias is None and self.v_up_proj.bias is None)
 
     # ------------------------------------------------------------ prefill (HIP)
     def _prefill_fusable(self, q: torch.Tensor, c_full: torch.Tensor, idx: torch.Tensor) -> bool:

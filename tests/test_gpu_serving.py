@@ -254,6 +254,99 @@ def test_maba_sa_device_decode_vs_oracle(dev):
                 assert_close(got, exp, 2e-3, 2e-3, f"device decode at L={L}")
 
 
+def test_cache_append_heads_and_value_up(dev):
+    """The serving step's fused extras: ``cache_append_heads`` appends like ``cache_append``
+    (bit-exact caches) and forms ``q_lat = W_k,h^T q_h`` (float64 reference, fp32 slack) and
+    ``bf16(gate + bias)`` (exact); ``maba_sa_decode_dev_heads`` returns the same ``z`` as
+    ``maba_sa_decode_dev`` (bit-exact: same kernels) and ``W_v,h z_h`` rounded to bf16 within
+    half an ulp of the float64 product of that ``z``."""
+    hb = _hb()
+    g = torch.Generator().manual_seed(11)
+    B, L0, cap, H, dh, dc, di = 3, 700, 800, 10, 64, 128, 64
+    bf = torch.bfloat16
+    c_all = torch.randn(B, L0 + 1, dc, generator=g).to(bf)
+    k_all = torch.randn(B, L0 + 1, di, generator=g).to(bf)
+
+    def caches():
+        c = torch.zeros(B, cap, dc, dtype=bf, device=dev)
+        k = torch.zeros(B, cap, di, dtype=bf, device=dev)
+        c[:, :L0] = c_all[:, :L0].to(dev)
+        k[:, :L0] = k_all[:, :L0].to(dev)
+        hca = torch.zeros(B, cap // 64, dc, dtype=bf, device=dev)
+        hca[:, : L0 // 64] = hb.hip_hca_pool(c[:, : (L0 // 64) * 64])
+        cent = torch.zeros(B, (cap + 63) // 64, di, dtype=bf, device=dev)
+        cent[:, : (L0 + 63) // 64] = hb.hip_compute_centroids(k[:, :L0])
+        return c, k, hca, cent
+
+    qh = torch.randn(B, 1, H * dh, generator=g).to(bf).to(dev)
+    wk = (0.05 * torch.randn(H * dh, dc, generator=g)).to(bf).to(dev)
+    wv = (0.05 * torch.randn(H * dh, dc, generator=g)).to(bf).to(dev)
+    gin = torch.randn(B, 1, 3, generator=g).to(bf).to(dev)
+    gbias = torch.randn(3, generator=g).to(bf).to(dev)
+    pos = torch.tensor([L0, L0 + 1], dtype=torch.long, device=dev)
+    c1, k1, hca1, cent1 = caches()
+    c2, k2, hca2, cent2 = caches()
+    cn, kn = c_all[:, L0].to(dev), k_all[:, L0].to(dev)
+    hb.hip_cache_append(cn, kn, pos[0], c1, k1, hca1, cent1)
+    q_lat = torch.empty(B, H, dc, dtype=torch.float32, device=dev)
+    gate = torch.empty(B, 3, dtype=bf, device=dev)
+    hb.hip_cache_append_heads(cn, kn, pos[0], c2, k2, hca2, cent2, qh[:, 0], wk, gin[:, 0], gbias, q_lat, gate)
+    for x, y, what in ((c1, c2, "latent rows"), (k1, k2, "keys"), (hca1, hca2, "means"), (cent1, cent2, "centroids")):
+        assert torch.equal(x, y), what
+    q64 = qh[:, 0].double().cpu().view(B, H, dh)
+    exp = torch.einsum("bhd,hdc->bhc", q64, wk.double().cpu().view(H, dh, dc))
+    scale = torch.einsum("bhd,hdc->bhc", q64.abs(), wk.double().cpu().abs().view(H, dh, dc))
+    assert ((q_lat.double().cpu() - exp).abs() <= 1e-6 * scale + 1e-9).all(), "absorbed query"
+    assert torch.equal(gate.cpu(), (gin[:, 0] + gbias).cpu()), "gate logits + bias"
+
+    idx = torch.randint(0, (L0 + 1) // 64, (B, 1, 32), generator=g).to(dev)
+    z1 = hb.hip_maba_sa_decode_dev(q_lat, c2, hca2, idx, gate, pos[1], cap, 1 / math.sqrt(dh))
+    o = torch.empty(B, H * dh, dtype=bf, device=dev)
+    z2 = hb.hip_maba_sa_decode_dev_heads(q_lat, c2, hca2, idx, gate, pos[1], cap, 1 / math.sqrt(dh), wv, o)
+    assert torch.equal(z1, z2), "z"
+    o_exp = torch.einsum("bhc,hdc->bhd", z2.double().cpu(), wv.double().cpu().view(H, dh, dc)).reshape(B, H * dh)
+    _ulp_close(o, o_exp, "value up-projection")
+
+
+def test_serving_layer_step_fused_heads_matches_unfused(dev, monkeypatch):
+    """``decode_step_device`` with the fused extras against the same step with the separate
+    torch launches (absorbed query, gate bias, value up-projection): identical selections, ``z``
+    within 1e-4 (the absorbed query's fp32 sums run in another order, and the softmax carries
+    that through) and the layer outputs within two bf16 ulps of the output scale."""
+    from maba_sparse.layers import MabaSparseAttention
+    from maba_sparse.layers.sparse_attention import DeviceCache
+    torch.manual_seed(7)
+    B, L0, steps = 4, 2100, 8   # the device-length indexer needs at least top_k blocks
+    layer = MabaSparseAttention(dim=640, n_heads=10, d_head=64, d_c=128, d_idx=64, top_k=32,
+                                dist_lambda=0.1).eval()
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0.0, 0.05) if p.dim() > 1 else p.normal_(0.0, 0.5)
+    layer = layer.to(dev, torch.bfloat16)
+    assert layer._heads_fusable()
+    g = torch.Generator().manual_seed(8)
+    xs = torch.randn(B, L0 + steps, 640, generator=g).bfloat16().to(dev)
+    with torch.no_grad():
+        _, c_full = layer(xs[:, :L0])
+        keys = layer.indexer._cached_k_idx
+        ca = DeviceCache(c_full, keys, L0 + steps)
+        cb = DeviceCache(c_full, keys, L0 + steps)
+        cnt_a = torch.tensor([L0, L0 + 1], dtype=torch.long, device=dev)
+        cnt_b = cnt_a.clone()
+        for t in range(L0, L0 + steps):
+            x = xs[:, t:t + 1]
+            oa, ia, za = layer.decode_step_device(x, ca, cnt_a, return_parts=True)
+            with monkeypatch.context() as m:
+                m.setattr(type(layer), "_heads_fusable", lambda self: False)
+                ob, ib, zb = layer.decode_step_device(x, cb, cnt_b, return_parts=True)
+            cnt_a += 1
+            cnt_b += 1
+            assert torch.equal(ia, ib), f"selections at {t}"
+            assert_close(za, to_np(zb), 1e-4, 1e-5, f"z at {t}")   # q_lat summed in another order
+            sc = ob.float().abs().max().item()
+            assert (oa.float() - ob.float()).abs().max().item() <= 2 * 2.0 ** -8 * sc, f"output at {t}"
+
+
 def _dl_case(M, K, N, mode, seed):
     """Inputs of one decode_linear case and the float64 product of its bf16 operand A."""
     g = torch.Generator().manual_seed(seed)
