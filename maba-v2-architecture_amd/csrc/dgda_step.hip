@@ -91,11 +91,13 @@ __global__ __launch_bounds__(256) void dgda_step_kernel(StepArgs a) {
   }
 }
 
-// Fast path for dk = dv = 64 with fp32 state rows of unit column stride, q/k/v of
-// one dtype (bf16 or fp32) and fp32 gates: one wave per (b, h), lane = state
-// column.  All 64 row loads of the column are issued at once and the state stays
-// in registers; per-row scalars (decay, b*k, k, q) are broadcast from the lane
-// that loaded them with readlane, so neither reduction leaves the lane.
+// Fast path for dk = dv = 64 with state rows of unit column stride (fp32 or bf16), q/k/v
+// of one dtype (bf16 or fp32) and fp32 gates: one 256-thread workgroup per (b, h), wave w
+// owning state rows 16w .. 16w+15 and lane c the state column c.  Each lane issues its 16
+// row loads at once and keeps them in registers; the per-row scalars (decay, b*k, k, q) are
+// broadcast from the lane that loaded them with readlane, and the two column reductions
+// over the rows (b k^T S' and q^T S_new) are summed per wave, then over the four waves in
+// LDS in a fixed order.
 struct StepFast {
   const void* q; const void* k; const void* v;
   int64_t qsb, qsh, qsd, ksb, ksh, ksd, vsb, vsh, vsd;
@@ -122,22 +124,55 @@ __device__ __forceinline__ float bcast(float x, int r) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), r));
 }
 
-// T: dtype of q, k, v; TS: dtype of the state in and out (fp32 or bf16).  Every row of the
-// lane's column is loaded before the first store, so the new state may alias the old one.
+// The step on the rows of wave w (lane = column): s[i] holds S[16w + i][lane] on entry;
+// al, bk, kr, qr are the row scalars of row `lane`, vw = w_lane v_lane.  Writes the new state
+// rows (N: element offset of S_new[0][lane], nsr its row stride) and, from wave 0, o[lane].
+// Every state load of the caller precedes the first store, so S_new may alias S.
+template <typename TS>
+__device__ __forceinline__ float step_rows(float (&s)[16], float al, float bk, float kr, float qr, float vw,
+                                           void* nst, int64_t N, int64_t nsr, float (*s_red)[64]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float pred = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = 16 * wave + i;
+    s[i] *= bcast(al, r);
+    pred = fmaf(bcast(bk, r), s[i], pred);
+  }
+  s_red[wave][lane] = pred;
+  __syncthreads();
+  pred = (s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane]);
+  const float delta = vw - pred;
+  float o = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = 16 * wave + i;
+    const float sn = fmaf(bcast(kr, r), delta, s[i]);
+    if constexpr (sizeof(TS) == 4) ((float*)nst)[N + r * nsr] = sn;
+    else ((uint16_t*)nst)[N + r * nsr] = f32_to_bf16_bits(sn);
+    o = fmaf(bcast(qr, r), sn, o);   // the fp32 state before its rounding, as the generic kernel
+  }
+  __syncthreads();   // every wave has read s_red before it is reused
+  s_red[wave][lane] = o;
+  __syncthreads();
+  return (s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane]);
+}
+
+// T: dtype of q, k, v; TS: dtype of the state in and out (fp32 or bf16).
 template <typename T, typename TS>
 __global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
+  __shared__ float s_red[4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t bh = (int64_t)blockIdx.x * 4 + wave;
-  if (bh >= a.BH) return;  // wave-uniform; no barriers
+  const int64_t bh = blockIdx.x;
   const int64_t bi = bh / a.H, hi = bh % a.H;
-  float s[64];
+  float s[16];
   if (a.state) {
     const int64_t S = bi * a.ssb + hi * a.ssh + lane;
 #pragma unroll
-    for (int r = 0; r < 64; ++r) s[r] = ldf<TS>(a.state, S + r * a.ssr);
+    for (int i = 0; i < 16; ++i) s[i] = ldf<TS>(a.state, S + (16 * wave + i) * a.ssr);
   } else {
 #pragma unroll
-    for (int r = 0; r < 64; ++r) s[r] = 0.f;
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
   }
   // lane r holds the row-r scalars; lane c holds w_c v_c
   const float kr = ldf<T>(a.k, bi * a.ksb + hi * a.ksh + lane * a.ksd);
@@ -147,24 +182,8 @@ __global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
   const float br = a.bb[bi * a.bsb + hi * a.bsh + lane * a.bsd];
   const float wc = a.ww[bi * a.wsb + hi * a.wsh + lane * a.wsd];
   const float al = a.use_log ? __expf(gr) : gr;
-  const float bk = br * kr;
-  float pred = 0.f;
-#pragma unroll
-  for (int r = 0; r < 64; ++r) {
-    s[r] *= bcast(al, r);
-    pred = fmaf(bcast(bk, r), s[r], pred);
-  }
-  const float delta = wc * vc - pred;
-  float o = 0.f;
-  const int64_t N = bi * a.nsb + hi * a.nsh + lane;
-#pragma unroll
-  for (int r = 0; r < 64; ++r) {
-    const float sn = fmaf(bcast(kr, r), delta, s[r]);
-    if constexpr (sizeof(TS) == 4) ((float*)a.nst)[N + r * a.nsr] = sn;
-    else ((uint16_t*)a.nst)[N + r * a.nsr] = f32_to_bf16_bits(sn);
-    o = fmaf(bcast(qr, r), sn, o);   // the fp32 state before its rounding, as the generic kernel
-  }
-  store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
+  const float o = step_rows<TS>(s, al, br * kr, kr, qr, wc * vc, a.nst, bi * a.nsb + hi * a.nsh + lane, a.nsr, s_red);
+  if (wave == 0) store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
 }
 
 // One decode token of the DGDA layer after its input projection, in one launch: the
@@ -196,21 +215,21 @@ struct LayerStepArgs {
 // trip per tap.
 template <typename TS, typename TW, bool HS, bool HH>
 __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
+  __shared__ float s_red[4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t bh = (int64_t)blockIdx.x * 4 + wave;
-  if (bh >= a.BH) return;  // wave-uniform; no barriers
+  const int64_t bh = blockIdx.x;
   const int64_t bi = bh / a.H, hi = bh % a.H;
   const int64_t c = hi * 64 + lane;   // channel of the projection rows
-  float s[64];
+  float s[16];
   if constexpr (HS) {
     const int64_t S = bi * a.ssb + hi * a.ssh + lane;
 #pragma unroll
-    for (int r = 0; r < 64; ++r) s[r] = ldf<TS>(a.state, S + r * a.ssr);
+    for (int i = 0; i < 16; ++i) s[i] = ldf<TS>(a.state, S + (16 * wave + i) * a.ssr);
   } else {
 #pragma unroll
-    for (int r = 0; r < 64; ++r) s[r] = 0.f;
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
   }
-  // ---- prologue (as dgda_prologue_step_kernel)
+  // ---- prologue (as dgda_prologue_step_kernel); every wave forms all 64 channels
   float x[6], w[3][4], h[3][3];
 #pragma unroll
   for (int st = 0; st < 6; ++st) x[st] = bf16_bits_to_f32(a.x[st][bi * a.xsb[st] + c]);
@@ -231,13 +250,6 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
     acc = fmaf(w[st][0], h[st][0], acc);
     y[st] = pro_silu(acc);
   }
-#pragma unroll
-  for (int st = 0; st < 3; ++st) {   // new history: the inputs of tokens -2, -1, 0
-    uint16_t* nh = a.nh[st] + bi * a.nhsb[st] + c * a.nhsc[st];
-    nh[0] = f32_to_bf16_bits(h[st][1]);
-    nh[a.nhst[st]] = f32_to_bf16_bits(h[st][2]);
-    nh[2 * a.nhst[st]] = f32_to_bf16_bits(x[st]);
-  }
   float ss = y[1] * y[1];
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
@@ -249,26 +261,22 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
   const float gr = pro_log_decay(x[3]);
   const float br = pro_sigmoid(x[4]);
   const float wc = pro_sigmoid(x[5]);
-  // ---- step (as dgda_step_wave_kernel with log_alpha)
+  // ---- step (as dgda_step_wave_kernel with log_alpha).  Every wave's loads complete here,
+  // before the step's first barrier, so no wave still reads the history when wave 0
+  // overwrites it (in place) after the barriers below.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   const float al = __expf(gr);
-  const float bk = br * kr;
-  float pred = 0.f;
+  const float o = step_rows<TS>(s, al, br * kr, kr, qr, wc * vc, a.nst, bi * a.nsb + hi * a.nsh + lane, a.nsr, s_red);
+  if (wave == 0) {
 #pragma unroll
-  for (int r = 0; r < 64; ++r) {
-    s[r] *= bcast(al, r);
-    pred = fmaf(bcast(bk, r), s[r], pred);
+    for (int st = 0; st < 3; ++st) {   // new history: the inputs of tokens -2, -1, 0
+      uint16_t* nh = a.nh[st] + bi * a.nhsb[st] + c * a.nhsc[st];
+      nh[0] = f32_to_bf16_bits(h[st][1]);
+      nh[a.nhst[st]] = f32_to_bf16_bits(h[st][2]);
+      nh[2 * a.nhst[st]] = f32_to_bf16_bits(x[st]);
+    }
+    store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
   }
-  const float delta = wc * vc - pred;
-  float o = 0.f;
-  const int64_t N = bi * a.nsb + hi * a.nsh + lane;
-#pragma unroll
-  for (int r = 0; r < 64; ++r) {
-    const float sn = fmaf(bcast(kr, r), delta, s[r]);
-    if constexpr (sizeof(TS) == 4) ((float*)a.nst)[N + r * a.nsr] = sn;
-    else ((uint16_t*)a.nst)[N + r * a.nsr] = f32_to_bf16_bits(sn);
-    o = fmaf(bcast(qr, r), sn, o);
-  }
-  store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
 }
 
 }  // namespace maba
@@ -338,7 +346,7 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
     f.nsr = new_state->stride[2];
     f.out = out->data; f.odt = out->dtype; f.osb = out->stride[0]; f.osh = out->stride[1]; f.osd = out->stride[2];
     f.BH = B * H; f.H = (int)H; f.use_log = log_alpha != nullptr;
-    const dim3 g4((unsigned)ceil_div(B * H, 4));
+    const dim3 g4((unsigned)(B * H));   // one workgroup per (b, h)
     const bool sbf = sdt == MABA_BF16;
     if (q->dtype == MABA_BF16 && sbf) hipLaunchKernelGGL((dgda_step_wave_kernel<uint16_t, uint16_t>), g4, dim3(256), 0, s, f);
     else if (q->dtype == MABA_BF16) hipLaunchKernelGGL((dgda_step_wave_kernel<uint16_t, float>), g4, dim3(256), 0, s, f);
@@ -407,7 +415,7 @@ extern "C" int maba_hip_dgda_layer_step(const maba_tensor* const* xs, const maba
   a.out = out->data; a.odt = out->dtype; a.osb = out->stride[0]; a.osh = out->stride[1]; a.osd = out->stride[2];
   a.BH = B * H; a.H = (int)H; a.eps = eps;
   if (B == 0) return MABA_OK;
-  const dim3 g4((unsigned)ceil_div(B * H, 4));
+  const dim3 g4((unsigned)(B * H));   // one workgroup per (b, h)
   hipStream_t s = (hipStream_t)stream;
   const bool sb = new_state->dtype == MABA_BF16, wb = a.cwdt == MABA_BF16, hs = a.state != nullptr, hh = nhist == 3;
   void (*k)(LayerStepArgs) = nullptr;
