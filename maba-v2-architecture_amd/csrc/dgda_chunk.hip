@@ -9,7 +9,8 @@
 //   u    = (I + L)^-1 v_e
 //   o    = diag(e^Lam) (q S0) + A u
 //   S    = e^{Lam_63} S0 + k^T diag(e^{Lam_63 - Lam}) u
-// All decay factors are <= 1, so nothing overflows for any gate values.
+// With decays <= 1 every factor is <= 1, so nothing overflows; decays above one are
+// taken as they are (the factors then grow as the recurrence's state does).
 //
 // Sequence parallelism (only B*H = 40 recurrences at the BASELINE shape, but
 // 256 CUs): the (b,h)-major sequence of all B*H*nchunks chunks is cut into slots
@@ -48,6 +49,12 @@ constexpr int CH = 64;        // chunk length (tokens)
 constexpr int DK = 64;        // key / value head size
 constexpr int TPITCH = 20;    // bf16 row pitch of the 16x16 inverse blocks
 constexpr int CPS = 16;       // chunks per segment
+// The aggregate pass's bound (see chunk_segment): chunks probed, the log-decay at which the start
+// state no longer counts, and the largest b |k|^2 taken as a contraction (2, less a margin for
+// the rounding of the fp32 sums).
+constexpr int ZC_PROBE = 4;
+constexpr float ZC_LOG = -80.f;
+constexpr float ZC_CONTRACT = 1.99f;
 
 // Output-kernel modes.  Pass 1 records zc[s] for every segment s >= 1 of a (b,h):
 // the number of chunks after which its transition M is exactly zero in fp32 (-1 if
@@ -248,6 +255,61 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
   const int role = (wave + rot) & 3;
   const bool gate_wave = AGG ? wave == 0 : role == 2;   // forms the per-token gate arrays
 
+  // ---- pass 1: a bound from the gates.  The segment's transition is M = prod_t (I - b_t k_t
+  // k_t^T) alpha_t (per-token decay and erase gates); while every token has b_t |k_t|^2 <= 2
+  // (and >= 0) each factor I - b_t k_t k_t^T is a contraction (its eigenvalues are 1 and
+  // 1 - b_t |k_t|^2), so |M| <= exp(sum_t log alpha_t).  Once
+  // that sum falls to ZC_LOG the start state adds less than e^ZC_LOG |S_start| to any later
+  // state or output (e^-80 < 2e-35), and the zero-start pass's results from there on stand.
+  // Wave 0 sums the log-decays of up to ZC_PROBE chunks (all their gate and key loads issued
+  // at once) and checks b_t |k_t|^2 per token; when the bound is reached it records zc as the
+  // chunks up to that point and the workgroup ends without a product.  Otherwise (slow decay,
+  // or large erase gates or keys) the segment runs on [N | M] below, and zc records where M
+  // became exactly zero, or -1.
+  if constexpr (AGG) {
+    if (wave == 0) {
+      float la[ZC_PROBE], kk[ZC_PROBE], be[ZC_PROBE];
+#pragma unroll
+      for (int j = 0; j < ZC_PROBE; ++j) {
+        const int t = (c_begin + j) * CH + lane;
+        const bool in = c_begin + j < c_end && t < a.L;
+        la[j] = in ? gb[(int64_t)(in ? t : 0) * a.gs2] : 0.f;
+        be[j] = in ? bb[(int64_t)(in ? t : 0) * a.bs2] : 0.f;
+        kk[j] = 0.f;
+        i16x8 kv[8];
+#pragma unroll
+        for (int c8 = 0; c8 < 8; ++c8) {
+          const i16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+          kv[c8] = in ? *(const i16x8*)(kb + (int64_t)(in ? t : 0) * a.ks2 + 8 * c8) : z;
+        }
+#pragma unroll
+        for (int c8 = 0; c8 < 8; ++c8)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kk[j] = fmaf(bf16_val(kv[c8][e]), bf16_val(kv[c8][e]), kk[j]);
+      }
+      int zb = -1;
+      float cum = 0.f;
+#pragma unroll
+      for (int j = 0; j < ZC_PROBE; ++j) {
+        if (zb >= 0 || c_begin + j >= c_end) continue;
+        float l = a.use_log ? la[j] : __logf(fmaxf(la[j], 1e-20f));
+        // A decay above one raises the sum as it should; a NaN never satisfies the bound.
+        l = (c_begin + j) * CH + lane < a.L ? l : 0.f;
+        const float bk2 = be[j] * kk[j];
+        if (__ballot(!(bk2 >= 0.f && bk2 <= ZC_CONTRACT)) != 0ull) break;   // a factor may expand
+        cum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_incl_scan(l)), 63));
+        if (cum <= ZC_LOG) zb = j + 1;
+      }
+      if (lane == 0) s_mzero[4] = zb;
+    }
+    lds_barrier();
+    const int zb = s_mzero[4];
+    if (zb >= 0) {
+      if (tid == 0) a.zc[sidx] = zb;
+      return;
+    }
+  }
+
   // ---- register prefetch of one chunk's k, v, q rows and per-token gates
   i16x8 pk[IPT], pv[IPT], pq[IPT];
   float pla = 0.f, pbe = 0.f, pwt = 0.f;
@@ -322,7 +384,7 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
     }
     if (gate_wave) {   // one wave, lane = token
       float la = a.use_log ? pla : __logf(fmaxf(pla, 1e-20f));
-      la = (t0 + lane < a.L) ? fminf(la, 0.f) : 0.f;
+      la = (t0 + lane < a.L) ? la : 0.f;
       const float s = wave_incl_scan(la);   // inclusive prefix sum of the log decay
       const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
       const float el = __expf(s);
@@ -330,16 +392,18 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
       sm.lam2[lane] = l2;
       // Off-diagonal decay factors: for i in block I > J and j in block J,
       // 2^{l2_i - l2_j} = 2^{l2_i - r_J} 2^{r_J - l2_j} with r_J = l2 at token 16J + 15;
-      // l2 does not increase, so both factors are <= 1 (rows i <= 16J + 15 never use rf[J]).
+      // when no decay exceeds one, l2 does not increase and both factors are <= 1 (rows
+      // i <= 16J + 15 never use rf[J]); decays above one give factors above one, as in the
+      // recurrence.
       const float rJ[3] = {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), 15)),
                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), 31)),
                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), 47))};
       const float rown = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l2), 63));
       const int jb = lane >> 4;
       const float rj = jb == 0 ? rJ[0] : jb == 1 ? rJ[1] : jb == 2 ? rJ[2] : rown;
-      sm.cf[lane] = __builtin_amdgcn_exp2f(fminf(rj - l2, 0.f));
+      sm.cf[lane] = __builtin_amdgcn_exp2f(rj - l2);
 #pragma unroll
-      for (int J = 0; J < 3; ++J) sm.rf[J][lane] = __builtin_amdgcn_exp2f(fminf(l2 - rJ[J], 0.f));
+      for (int J = 0; J < 3; ++J) sm.rf[J][lane] = __builtin_amdgcn_exp2f(l2 - rJ[J]);
       sm.elam[lane] = el;
       sm.eend[lane] = __expf(last - s);
       sm.beta[lane] = pbe;
@@ -619,7 +683,7 @@ __device__ __forceinline__ void chunk_segment(KArgs& a, ChunkSmem<AGG>& sm, int*
 template <bool AGG, bool WTOK, bool OBF>
 __global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_chunk_kernel(ChunkArgs a) {
   __shared__ ChunkSmem<AGG> sm;
-  __shared__ int s_mzero[4];
+  __shared__ int s_mzero[5];   // [0, 4): the M slabs' zero flags; [4]: the bound's chunk count
   // Pass 1 and OUT_FIX: one workgroup per segment k >= 1.  OUT_ZERO: slot w covers
   // the chunks [U w, U w + U) of the (b,h)-major order, one segment per sequence it
   // touches.  Both walk the same loop so the segment body is inlined once.

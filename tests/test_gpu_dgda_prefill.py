@@ -145,6 +145,30 @@ def test_chunk_mixed_decay_segments(dev):
     assert_close(S, eS, 2e-3, 2e-3, "state")
 
 
+@pytest.mark.parametrize("case", ["expanding_erase", "decay_above_one"])
+def test_chunk_gate_bound_fallbacks(dev, case):
+    """The aggregate pass skips a segment from its gates alone when the summed log-decay of its
+    first chunks falls below -80 and every factor I - b k k^T is a contraction.  Erase gates
+    of 2.6 on every 37th token (b |k|^2 > 2, a factor that expands) must send the segment to
+    the exact test instead; decays above one on the first tokens of every chunk must count in
+    the sum (here the sum still reaches the bound, a few tokens later)."""
+    L = 4100
+    inp = dgda_inputs(1, 2, L, seed=91, device=dev, with_state=True)
+    t = torch.arange(L, device=dev)
+    if case == "expanding_erase":
+        b = inp["b"][..., :1].clone()
+        b[:, :, t % 37 == 5] = 2.6
+        inp["b"] = b.expand(1, 2, L, 64)
+    else:
+        la = inp["log_alpha"][..., :1].clone()
+        la[:, :, t % 64 < 4] = 0.3
+        inp["log_alpha"] = la.expand(1, 2, L, 64)
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, f"out {case}")
+    assert_close(S, eS, 2e-3, 2e-3, f"state {case}")
+
+
 @pytest.mark.parametrize("decay", ["baseline", "slow"])
 def test_chunk_slot_boundaries_multi_head(dev, decay):
     """Six heads of 65 chunks: the output pass's 16-chunk slots start inside sequences
