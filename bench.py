@@ -568,12 +568,15 @@ def prefill_attention_bench(dev, B=1, H=10, L=32768, dh=64, dc=128, K=32):
     layer's default shape (10 heads of 64, d_c 128), each query's top-32 blocks from the HIP
     causal index_topk over random queries and centroids (lambda 0.5, the layer's default).
 
-    The layer's path is the latent form: ``q_lat = W_k,h^T q_h``, one launch over the bf16
-    latent rows and their block means, ``o_h = W_v,h z_h``; the row times that composite and
-    the latent kernel alone (the roofline's kernel).  The head-space kernel over up-projected
-    keys and values (the previous path) is timed beside it."""
+    Both fused forms of ``MabaSparseAttention`` are timed, as composites and as kernels: the
+    latent form (``q_lat = W_k,h^T q_h``, one launch over the bf16 latent rows and their block
+    means, ``o_h = W_v,h z_h``) and the head-space form (keys, values, block means and the
+    early running means up-projected, one ``maba_sa_prefill`` launch).  ``ms_per_call`` and the
+    roofline follow the form the layer picks for these selections (``_prefill_form``).  The
+    roofline counts the reference's work: 4 d_head flops per key and head."""
     import torch
     from maba_sparse.kernels import hip_backend as hb
+    from maba_sparse.layers.sparse_attention import PREFILL_UNION_LIMIT
     g = torch.Generator(device=dev).manual_seed(21)
     bf = lambda *sh: torch.randn(*sh, device=dev, generator=g, dtype=torch.bfloat16)  # noqa: E731
     q = bf(B, H, L, dh)
@@ -582,50 +585,74 @@ def prefill_attention_bench(dev, B=1, H=10, L=32768, dh=64, dc=128, K=32):
     Wv = torch.randn(H, dh, dc, device=dev, generator=g) * dc ** -0.5
     gate = torch.randn(B, L, 3, device=dev, generator=g)
     idx = hb.hip_index_topk(bf(B, L, 64), bf(B, L // 64, 64), lambda_dist=0.5, top_k=K, block_size=64)
+    grp = idx[:, : (L // 16) * 16].reshape(B, L // 16, 16 * K).sort(dim=-1).values
+    distinct = (grp[..., 1:] != grp[..., :-1]).sum(dim=-1).float().mean().item() + 1.0
+    form = "heads" if distinct < PREFILL_UNION_LIMIT * K else "latent"
     hca = hb.hip_hca_pool(c, pool=64)
     q_lat = torch.einsum("bhtd,hdc->bthc", q.float(), Wk).contiguous()
     z = torch.empty(B, L, H, dc, device=dev)
 
-    def kernel():
+    def kernel_latent():
         return hb.hip_maba_sa_prefill_latent(q_lat, c, hca, idx, gate, scale=dh ** -0.5, out=z)
 
-    def composite():
+    def composite_latent():
         ql = torch.einsum("bhtd,hdc->bthc", q.float(), Wk).contiguous()
         means = hb.hip_hca_pool(c, pool=64)
         zz = hb.hip_maba_sa_prefill_latent(ql, c, means, idx, gate, scale=dh ** -0.5)
         return torch.einsum("bthc,hdc->bthd", zz, Wv)
 
-    ms, _ = time_op(kernel, 10, 2)
-    ms_comp, _ = time_op(composite, 10, 2)
-    # the head-space kernel of the earlier path over up-projected keys and values
-    k = torch.einsum("blc,hdc->bhld", c.float(), Wk).bfloat16()
-    v = torch.einsum("blc,hdc->bhld", c.float(), Wv).bfloat16()
-    kh, vh = k[:, :, :L // 64].contiguous(), v[:, :, :L // 64].contiguous()
-    ms_heads, _ = time_op(lambda: hb.hip_maba_sa_prefill(q, k, v, kh, vh, v[:, :, :63].contiguous(), idx, gate,
-                                                          scale=dh ** -0.5), 3, 1)
-    del k, v, kh, vh
-    log(f"MABA-SA prefill 32k: latent kernel {ms:.3f} ms, composite {ms_comp:.3f} ms, "
-        f"head-space kernel {ms_heads:.3f} ms")
-    # algorithmic flops of the latent kernel per query and head: 2 d_c per score and per value
-    # accumulation, over the local keys (window + sinks, fewer at the start), the listed
-    # blocks' causal tokens and the complete means before the query
+    Wkb, Wvb = Wk.reshape(H * dh, dc).bfloat16(), Wv.reshape(H * dh, dc).bfloat16()
+    heads = lambda t, n: t.view(B, n, H, dh).transpose(1, 2)  # noqa: E731
+    cnt = torch.arange(1, 64, device=dev, dtype=torch.bfloat16).view(1, -1, 1)
+
+    def head_inputs():   # as MabaSparseAttention._fused_prefill_heads forms them
+        k, v = heads(c @ Wkb.t(), L), heads(c @ Wvb.t(), L)
+        means = c.reshape(B, L // 64, 64, dc).mean(dim=2)
+        kh, vh = heads(means @ Wkb.t(), L // 64), heads(means @ Wvb.t(), L // 64)
+        early = heads((torch.cumsum(c[:, :63], dim=1) / cnt) @ Wvb.t(), 63)
+        return k, v, kh, vh, early
+
+    hin = head_inputs()
+
+    def kernel_heads():
+        return hb.hip_maba_sa_prefill(q, *hin, idx, gate, scale=dh ** -0.5)
+
+    def composite_heads():
+        return hb.hip_maba_sa_prefill(q, *head_inputs(), idx, gate, scale=dh ** -0.5)
+
+    ms_l, _ = time_op(kernel_latent, 10, 2)
+    ms_lc, _ = time_op(composite_latent, 10, 2)
+    ms_h, _ = time_op(kernel_heads, 10, 2)
+    ms_hc, _ = time_op(composite_heads, 10, 2)
+    del hin
+    ms, ms_comp = (ms_h, ms_hc) if form == "heads" else (ms_l, ms_lc)
+    log(f"MABA-SA prefill 32k ({distinct / K:.2f} K distinct blocks per 16 queries, layer form {form}): "
+        f"latent kernel {ms_l:.3f} ms (composite {ms_lc:.3f}), head-space kernel {ms_h:.3f} ms "
+        f"(composite {ms_hc:.3f})")
+    # keys per query: the local keys (window + sinks, fewer at the start), the listed blocks'
+    # causal tokens and the complete means before the query
     pos = torch.arange(L, device=dev)
     n_loc = torch.clamp(pos + 1, max=128) + torch.clamp(torch.clamp(pos + 1 - 128, min=0), max=4)
     blk = idx[0].to(torch.int64)
     n_sp = torch.where(blk >= 0, torch.clamp(pos[:, None] - blk * 64 + 1, min=0, max=64), 0).sum(-1)
     n_hca = (pos + 1) // 64
     keys = (n_loc + n_sp + n_hca).double().sum().item()
-    fl = keys * H * B * 4 * dc
+    fl = keys * H * B * 4 * dh
     rf = {"bound": "mfma", "achieved": fl / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
           "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "algorithmic_flops": fl,
-          "traffic": measured_traffic("maba_sa_prefill_latent_bytes_per_call"), "traffic_source": TRAFFIC_SOURCE}
+          "kernel": "maba_sa_prefill_kernel" if form == "heads" else "maba_sa_prefill_latent_kernel",
+          "traffic": (measured_traffic("maba_sa_prefill_latent_bytes_per_call") if form == "latent" else None),
+          "traffic_source": TRAFFIC_SOURCE}
     return {"maba_sa_prefill_32k": {
-        "ms_per_call": ms_comp, "kernel_ms": ms, "head_space_kernel_ms": ms_heads,
+        "ms_per_call": ms_comp, "kernel_ms": ms, "form": form, "distinct_blocks_per_16_queries": distinct,
+        "latent_kernel_ms": ms_l, "latent_composite_ms": ms_lc,
+        "head_space_kernel_ms": ms_h, "head_space_composite_ms": ms_hc,
+        "latent_form_flops": keys * H * B * 4 * dc,
         "queries_per_s": B * L / (ms_comp * 1e-3), "keys_per_query": keys / (B * L),
         "roofline": rf,
-        "config": "B=1 H=10 d_head=64 d_c=128 L=32768 bf16 latent rows, window 128 + 4 sinks, top-32 causal "
-                  "blocks per query from index_topk (lambda 0.5), 512 HCA means; ms_per_call = q_lat "
-                  "projection + block means + latent kernel + W_v projection"}}
+        "config": "B=1 H=10 d_head=64 d_c=128 L=32768 bf16, window 128 + 4 sinks, top-32 causal blocks per "
+                  "query from index_topk (lambda 0.5), 512 HCA means; ms_per_call = the layer's form as a "
+                  "composite (up-projections or q_lat / W_v projections, block means, kernel)"}}
 
 
 def prologue_benches(dev, B=4, T=32768, dim=640, H=10):

@@ -11,16 +11,18 @@
 //                     running-mean row early[t]
 //   gate   (:275)     out = sum_s softmax(logits)_s o_s; a stream with no valid key gives 0
 //
-// One wave per 16 consecutive queries of one (b, h); four independent waves per workgroup
-// (no barrier).  Per 64-key tile, on bf16 MFMA with fp32 accumulation:
-//   scores  S^T[key][query] = K Q^T     (A: key rows from global memory, B: the wave's
+// One workgroup per 64 consecutive queries of one (b, h), one wave per 16 of them.  The
+// workgroup walks one list of 64-key tiles -- local (sinks, then the window of all 64
+// queries), sparse (the union of the 64 queries' blocks, from an LDS bitmap compacted in
+// ascending block order), HCA (the means any of them sees) -- staging each key and value tile
+// once into double-buffered LDS, the next tile's loads in flight while the current one
+// computes, one barrier per tile.  Per tile and wave, on bf16 MFMA with fp32 accumulation:
+//   scores  S^T[key][query] = K Q^T     (A: key rows from the LDS tile, B: the wave's
 //                                        16 queries in registers)
-//   values  O^T[dim][query] += V^T P    (A: V^T fragments read transposed from the tile
-//                                        kept row-major in the wave's LDS, B: the
-//                                        probabilities in bf16 hi + lo)
-// with an online softmax per query and stream.  The sparse stream walks the union of the
-// 16 queries' blocks (an LDS bitmap, compacted in ascending block order) and weights each
-// key by how often the lane's query lists its block.
+//   values  O^T[dim][query] += V^T P    (A: V^T fragments read transposed from the LDS
+//                                        tile, B: the probabilities in bf16 hi + lo)
+// with an online softmax per query and stream; each sparse key is weighted by how often the
+// lane's query lists its block.  A wave skips the tiles none of its queries weights.
 #include <algorithm>
 
 #include "maba_common.h"
@@ -28,8 +30,8 @@
 namespace maba {
 
 constexpr int PF_MAXK = 64;          // index slots per query
-constexpr int PF_WORDS = 512;        // bitmap words per wave: blocks below 16384
-constexpr int PF_LIST = 16 * PF_MAXK;
+constexpr int PF_WORDS = 512;        // bitmap words per workgroup: blocks below 16384
+constexpr int PF_LIST = 64 * PF_MAXK;   // the union of a workgroup's 64 queries' slots
 
 typedef __attribute__((ext_vector_type(8))) short pf16x8;
 typedef __attribute__((ext_vector_type(4))) short pf16x4;
@@ -65,26 +67,28 @@ struct PfAcc {
 };
 
 template <int NP>   // dh = 32 NP
-__global__ __launch_bounds__(256) void maba_sa_prefill_kernel(PfArgs a) {
+__global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(PfArgs a) {
   constexpr int DH = 32 * NP;
-  constexpr int TP = DH + 8;      // row pitch (bf16) of the wave's value tile
+  constexpr int TP = DH + 8;      // row pitch (bf16) of the LDS key and value tiles
   constexpr int NDT = DH / 16;
-  __shared__ __attribute__((aligned(16))) short s_v[4][64 * TP];
-  __shared__ uint32_t s_bits[4][PF_WORDS];
-  __shared__ int s_list[4][PF_LIST];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int TE = 64 * TP;
+  __shared__ __attribute__((aligned(16))) short s_k[2][TE];
+  __shared__ __attribute__((aligned(16))) short s_v[2][TE];
+  __shared__ uint32_t s_bits[PF_WORDS];
+  __shared__ uint16_t s_list[PF_LIST];
+  __shared__ int s_nlist;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c16 = lane & 15;
   const int64_t b = blockIdx.z;
   const int h = blockIdx.y;
-  const int64_t tq0 = (int64_t)blockIdx.x * 64 + wave * 16;   // the wave's first query
-  if (tq0 >= a.Lq) return;                                     // whole wave; no barriers below
+  const int64_t tw0 = (int64_t)blockIdx.x * 64;                // the workgroup's first query (< Lq)
+  const int64_t tq0 = tw0 + wave * 16;                         // the wave's first query
   const bool qvalid = tq0 + c16 < a.Lq;
   const int64_t tq = qvalid ? tq0 + c16 : a.Lq - 1;            // extra columns repeat the last query
   const int64_t off = a.Lkv - a.Lq;
-  const int64_t pos = off + tq;
-  const int64_t pos_lo = off + tq0;
-  const int64_t pos_hi = off + min(tq0 + 15, a.Lq - 1);
-  short* vt = s_v[wave];
+  const int pos = (int)(off + tq);   // key positions fit 32 bits: Lkv <= PF_WORDS * 32 * 64
+  const int64_t wpos_lo = off + tw0;
+  const int64_t wpos_hi = off + min(tw0 + 63, a.Lq - 1);
 
   pf16x8 qb[NP];   // lane (query c16, group g): dims 32 p + 8 g .. +7
 #pragma unroll
@@ -104,39 +108,141 @@ __global__ __launch_bounds__(256) void maba_sa_prefill_kernel(PfArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // One 64-key tile: krow(j) / vrow(j) give in-bounds rows for tile row j; mult(j) the
-  // weight (0 = masked) of tile row j for the lane's query.
-  auto tile = [&](PfAcc<NDT>& st, auto krow, auto vrow, auto mult) {
-    pf16x8 kv[4][NP];
+  // ---- the workgroup's tiles, in stream order: local (sink tiles below the first window
+  // tile, then the window tiles of all 64 queries), sparse (the union of the 64 queries'
+  // blocks, ascending), HCA (the means any of the 64 queries can see).
+  const int64_t ns = min((int64_t)a.n_sink, a.Lkv);
+  const int64_t lo = max((int64_t)0, wpos_lo - a.window + 1);
+  const int64_t wt0 = (lo / 64) * 64;
+  const int64_t sink_end = min(ns, wt0);
+  const int n_st = (int)((sink_end + 63) / 64);
+  const int n_loc = n_st + (wpos_hi >= wt0 ? (int)((wpos_hi - wt0) / 64 + 1) : 0);
+
+  // this lane's share of its query's index slots, k = g + 4 r, two per register (slot 2 m in
+  // the low half): the block, or 0xffff for an empty or out-of-range slot (blocks are below
+  // PF_WORDS * 32 = 16384)
+  uint32_t myblk[PF_MAXK / 8];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const uint16_t* kr = krow(16 * rb + c16);
-      const uint16_t* vr = vrow(16 * rb + c16);
+  for (int m = 0; m < PF_MAXK / 8; ++m) {
+    uint32_t pr = 0u;
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        kv[rb][p] = *(const pf16x8*)(kr + 32 * p + 8 * g);
-        *(pf16x8*)(vt + (16 * rb + c16) * TP + 32 * p + 8 * g) = *(const pf16x8*)(vr + 32 * p + 8 * g);
-      }
+    for (int hf = 0; hf < 2; ++hf) {
+      const int kk = g + 4 * (2 * m + hf);
+      const int64_t v = kk < a.K ? a.idx[b * a.isb + tq * a.ist + kk * a.isk] : -1;
+      pr |= (uint32_t)((v >= 0 && v < a.nb) ? (int)v : 0xffff) << (16 * hf);
     }
+    myblk[m] = pr;
+  }
+  const int64_t nbl = min(a.nb, wpos_hi / 64 + 1);   // blocks that hold a key <= wpos_hi
+  const int nwords = (int)((nbl + 31) / 32);
+  for (int wd = tid; wd < nwords; wd += 256) s_bits[wd] = 0u;
+  __syncthreads();
+  if (qvalid) {
+#pragma unroll
+    for (int r = 0; r < PF_MAXK / 4; ++r) {
+      const int bk = (int)((myblk[r >> 1] >> (16 * (r & 1))) & 0xffffu);
+      if (bk < nbl) atomicOr(&s_bits[bk >> 5], 1u << (bk & 31));
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {   // compaction in ascending block order: word wd's set bits at base + (bits before it)
+    int nlist = 0;
+    for (int w0 = 0; w0 < nwords; w0 += 64) {
+      const int wd = w0 + lane;
+      const uint32_t word = wd < nwords ? s_bits[wd] : 0u;
+      const int cnt = __popc(word);
+      int incl = cnt;
+#pragma unroll
+      for (int o2 = 1; o2 < 64; o2 <<= 1) {
+        const int y = __shfl_up(incl, o2);
+        if (lane >= o2) incl += y;
+      }
+      int at = nlist + incl - cnt;
+      uint32_t rest = word;
+      while (rest) {
+        const int bit = __ffs(rest) - 1;
+        s_list[at++] = (uint16_t)(wd * 32 + bit);
+        rest &= rest - 1;
+      }
+      nlist += __shfl(incl, 63);
+    }
+    if (lane == 0) s_nlist = nlist;
+  }
+  const int64_t e_hi = min(a.nc - 1, (wpos_hi + 1) / a.pool - 1);
+  const int n_hca = e_hi >= 0 ? (int)(e_hi / 64 + 1) : 0;
+  __syncthreads();
+  const int n_sp = s_nlist;
+  const int n_ls = n_loc + n_sp;
+  const int nt = n_ls + n_hca;
+
+  // ---- tile staging: thread tid copies row tid / 4, 16-byte chunks (tid % 4) + 4 p, of the
+  // key and value tiles; the next tile's loads are in flight while the current one computes.
+  const uint16_t* kbase = a.k + b * a.ksb + h * a.ksh;
+  const uint16_t* vbase = a.v + b * a.vsb + h * a.vsh;
+  const uint16_t* khbase = a.kh ? a.kh + b * a.khb + h * a.khh : nullptr;
+  const uint16_t* vhbase = a.vh ? a.vh + b * a.vhb + h * a.vhh : nullptr;
+  const int srow = tid >> 2, spart = tid & 3;
+  pf16x8 pk[NP], pv[NP];
+  auto fetch = [&](int i) {
+    const uint16_t* kr;
+    const uint16_t* vr;
+    if (i < n_ls) {
+      const int64_t tb = i < n_st ? 64 * (int64_t)i
+                       : i < n_loc ? wt0 + 64 * (int64_t)(i - n_st) : 64 * (int64_t)s_list[i - n_loc];
+      const int64_t j = min(tb + srow, a.Lkv - 1);
+      kr = kbase + j * a.kst;
+      vr = vbase + j * a.vst;
+    } else {
+      const int64_t e = min(64 * (int64_t)(i - n_ls) + srow, a.nc - 1);
+      kr = khbase + e * a.khe;
+      vr = vhbase + e * a.vhe;
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      pk[p] = *(const pf16x8*)(kr + 8 * (spart + 4 * p));
+      pv[p] = *(const pf16x8*)(vr + 8 * (spart + 4 * p));
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      *(pf16x8*)(s_k[buf] + srow * TP + 8 * (spart + 4 * p)) = pk[p];
+      *(pf16x8*)(s_v[buf] + srow * TP + 8 * (spart + 4 * p)) = pv[p];
+    }
+  };
+
+  // One 64-key tile from LDS buffer buf: tile row j has weight fc for the lane's query where
+  // valid(j) holds and 0 elsewhere.  A wave none of whose queries weights any row skips the
+  // tile: for such a lane the tile would leave (m, l, z) exactly as they are.
+  auto tile = [&](PfAcc<NDT>& st, int buf, float fc, auto valid) {
+    uint32_t vmask = 0u;   // bit 4 rb + i: key 16 rb + 4 g + i weighted
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vmask |= (uint32_t)valid(16 * rb + 4 * g + i) << (4 * rb + i);
+    if (!qvalid || !(fc > 0.f)) vmask = 0u;
+    if (__ballot(vmask != 0u) == 0ull) return;   // wave-uniform
+    const short* ks = s_k[buf];
+    const short* vt = s_v[buf];
     f32x4 sc[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < NP; ++p)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kv[rb][p]),
+      for (int p = 0; p < NP; ++p) {
+        const pf16x8 kv = *(const pf16x8*)(ks + (16 * rb + c16) * TP + 32 * p + 8 * g);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kv),
                                                       __builtin_bit_cast(bf16x8, qb[p]), acc, 0, 0, 0);
+      }
       sc[rb] = acc;
     }
     // lane (query c16, g) holds the scores of keys 16 rb + 4 g + i
-    float wgt[4][4];
     float tmax = -INFINITY;
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        wgt[rb][i] = mult(16 * rb + 4 * g + i);
-        const float x = wgt[rb][i] > 0.f ? sc[rb][i] * a.scale : -INFINITY;
+        const float x = (vmask >> (4 * rb + i)) & 1u ? sc[rb][i] * a.scale : -INFINITY;
         sc[rb][i] = x;
         tmax = fmaxf(tmax, x);
       }
@@ -151,7 +257,7 @@ __global__ __launch_bounds__(256) void maba_sa_prefill_kernel(PfArgs a) {
     for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float pe = wgt[rb][i] * __expf(sc[rb][i] - m_sub);   // exp(-inf) = 0 for masked keys
+        const float pe = fc * __expf(sc[rb][i] - m_sub);   // exp(-inf) = 0 for masked keys
         psum += pe;
         const short hb = __builtin_bit_cast(short, (__bf16)pe);
         ph[rb][i] = hb;
@@ -195,115 +301,78 @@ __global__ __launch_bounds__(256) void maba_sa_prefill_kernel(PfArgs a) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[dt] += st.z[dt] * w;
   };
-
-  const uint16_t* kbase = a.k + b * a.ksb + h * a.ksh;
-  const uint16_t* vbase = a.v + b * a.vsb + h * a.vsh;
-  auto krow_at = [&](int64_t j) { return kbase + min(j, a.Lkv - 1) * a.kst; };
-  auto vrow_at = [&](int64_t j) { return vbase + min(j, a.Lkv - 1) * a.vst; };
+  // tiles [i, i_end): prefetch tile i + 1 (of whichever stream), compute tile i, stage the
+  // prefetched tile into the other buffer, one barrier per tile.  valid_of(i) gives tile i's
+  // row predicate, weight_of(i) the weight of its valid rows.
+  int i = 0;
+  auto run = [&](PfAcc<NDT>& st, int i_end, auto weight_of, auto valid_of) {
+    for (; i < i_end; ++i) {
+      if (i + 1 < nt) fetch(i + 1);
+      tile(st, i & 1, weight_of(i), valid_of(i));
+      if (i + 1 < nt) stash((i + 1) & 1);
+      __syncthreads();
+    }
+  };
+  if (nt > 0) {
+    fetch(0);
+    stash(0);
+  }
+  __syncthreads();
   PfAcc<NDT> st;
 
-  // ---- local stream: the sink tiles below the first window tile, then the window tiles
-  {
-    reset(st);
-    const int64_t ns = min((int64_t)a.n_sink, a.Lkv);
-    const int64_t lo = max((int64_t)0, pos_lo - a.window + 1);
-    const int64_t wt0 = (lo / 64) * 64;
-    const int64_t sink_end = min(ns, wt0);
-    for (int64_t tb = 0; tb < sink_end; tb += 64)
-      tile(st, [&](int j) { return krow_at(tb + j); }, [&](int j) { return vrow_at(tb + j); },
-           [&](int j) { const int64_t kj = tb + j; return (kj < sink_end && kj <= pos) ? 1.f : 0.f; });
-    for (int64_t tb = wt0; tb <= pos_hi; tb += 64)
-      tile(st, [&](int j) { return krow_at(tb + j); }, [&](int j) { return vrow_at(tb + j); },
-           [&](int j) {
-             const int64_t kj = tb + j;
-             return (kj <= pos && (pos - kj < a.window || kj < ns)) ? 1.f : 0.f;
-           });
-    fold(st, g0);
-  }
+  // ---- local stream
+  reset(st);
+  run(st, n_loc, [](int) { return 1.f; }, [&](int ti) {
+    const int tb = ti < n_st ? 64 * ti : (int)wt0 + 64 * (ti - n_st);
+    const bool sink = ti < n_st;
+    const int se = (int)sink_end, ns32 = (int)ns;
+    return [=](int j) {
+      const int kj = tb + j;
+      if (sink) return kj < se && kj <= pos;
+      return kj <= pos && (pos - kj < a.window || kj < ns32);
+    };
+  });
+  fold(st, g0);
 
-  // ---- sparse stream: union of the 16 queries' blocks, ascending
-  {
-    reset(st);
-    // this lane's share of its query's index slots: k = g, g + 4, ...
-    int64_t myblk[PF_MAXK / 4];
+  // ---- sparse stream: each key weighted by how often the lane's query lists its block
+  reset(st);
+  run(st, n_ls, [&](int ti) {
+    const int blk = s_list[ti - n_loc];   // wave-uniform
+    int cnt = 0;
 #pragma unroll
-    for (int r = 0; r < PF_MAXK / 4; ++r) {
-      const int kk = g + 4 * r;
-      myblk[r] = kk < a.K ? a.idx[b * a.isb + tq * a.ist + kk * a.isk] : -1;
-    }
-    const int64_t nbl = min(a.nb, pos_hi / 64 + 1);   // blocks that hold a key <= pos_hi
-    const int nwords = (int)((nbl + 31) / 32);
-    uint32_t* bits = s_bits[wave];
-    int* list = s_list[wave];
-    for (int wd = lane; wd < nwords; wd += 64) bits[wd] = 0u;
-    if (qvalid) {
-#pragma unroll
-      for (int r = 0; r < PF_MAXK / 4; ++r) {
-        const int64_t bk = myblk[r];
-        if (bk >= 0 && bk < nbl) atomicOr(&bits[bk >> 5], 1u << (bk & 31));
-      }
-    }
-    // compaction in ascending block order: word wd's set bits at base + (bits before it)
-    int nlist = 0;
-    for (int w0 = 0; w0 < nwords; w0 += 64) {
-      const int wd = w0 + lane;
-      const uint32_t word = wd < nwords ? bits[wd] : 0u;
-      const int cnt = __popc(word);
-      int incl = cnt;
-#pragma unroll
-      for (int o2 = 1; o2 < 64; o2 <<= 1) {
-        const int y = __shfl_up(incl, o2);
-        if (lane >= o2) incl += y;
-      }
-      int at = nlist + incl - cnt;
-      uint32_t rest = word;
-      while (rest) {
-        const int bit = __ffs(rest) - 1;
-        list[at++] = wd * 32 + bit;
-        rest &= rest - 1;
-      }
-      nlist += __shfl(incl, 63);
-    }
-    for (int u = 0; u < nlist; ++u) {
-      const int64_t blk = list[u];           // wave-uniform
-      int cnt = 0;                           // times the lane's query lists blk
-#pragma unroll
-      for (int r = 0; r < PF_MAXK / 4; ++r) cnt += myblk[r] == blk;
-      cnt += __shfl_xor(cnt, 16);
-      cnt += __shfl_xor(cnt, 32);
-      const float fc = qvalid ? (float)cnt : 0.f;
-      const int64_t tb = blk * 64;
-      tile(st, [&](int j) { return krow_at(tb + j); }, [&](int j) { return vrow_at(tb + j); },
-           [&](int j) { return (tb + j <= pos) ? fc : 0.f; });
-    }
-    fold(st, g1);
-  }
+    for (int m = 0; m < PF_MAXK / 8; ++m)
+      cnt += (int)((myblk[m] & 0xffffu) == (uint32_t)blk) + (int)((myblk[m] >> 16) == (uint32_t)blk);
+    cnt += __shfl_xor(cnt, 16);
+    cnt += __shfl_xor(cnt, 32);
+    return (float)cnt;
+  }, [&](int ti) {
+    const int tb = 64 * (int)s_list[ti - n_loc];
+    return [=](int j) { return tb + j <= pos; };
+  });
+  fold(st, g1);
 
   // ---- HCA stream: means e with (e + 1) pool - 1 <= pos; early queries take their row
-  {
-    reset(st);
-    const int64_t e_hi = min(a.nc - 1, (pos_hi + 1) / a.pool - 1);
-    if (e_hi >= 0) {
-      const uint16_t* khb = a.kh + b * a.khb + h * a.khh;
-      const uint16_t* vhb = a.vh + b * a.vhb + h * a.vhh;
-      for (int64_t eb = 0; eb <= e_hi; eb += 64)
-        tile(st, [&](int j) { return khb + min(eb + j, a.nc - 1) * a.khe; },
-             [&](int j) { return vhb + min(eb + j, a.nc - 1) * a.vhe; },
-             [&](int j) { const int64_t e = eb + j; return (e < a.nc && (e + 1) * a.pool - 1 <= pos) ? 1.f : 0.f; });
-    }
-    if (pos < a.pool - 1) {   // running mean of c[0..pos] through W_v (the caller's row)
-      const bool have = a.early && tq < a.n_early;
+  reset(st);
+  run(st, nt, [](int) { return 1.f; }, [&](int ti) {
+    const int eb = 64 * (ti - n_ls);
+    const int nc32 = (int)a.nc;
+    return [=](int j) {
+      const int e = eb + j;
+      return e < nc32 && (e + 1) * a.pool - 1 <= pos;
+    };
+  });
+  if (pos < a.pool - 1) {   // running mean of c[0..pos] through W_v (the caller's row)
+    const bool have = a.early && tq < a.n_early;
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = 16 * dt + 4 * g + i;
-          const float x = have ? load_elem(a.early, a.edt, b * a.esb + h * a.esh + tq * a.est + d * a.esd) : 0.f;
-          o[dt][i] += g2 * x;
-        }
-    } else {
-      fold(st, g2);
-    }
+      for (int i2 = 0; i2 < 4; ++i2) {
+        const int d = 16 * dt + 4 * g + i2;
+        const float x = have ? load_elem(a.early, a.edt, b * a.esb + h * a.esh + tq * a.est + d * a.esd) : 0.f;
+        o[dt][i2] += g2 * x;
+      }
+  } else {
+    fold(st, g2);
   }
 
   if (!qvalid) return;

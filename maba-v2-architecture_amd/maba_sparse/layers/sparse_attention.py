@@ -13,10 +13,11 @@ cache (:206): HCA means are kept and extended by one mean per completed block.
 (``decode_step``), avoiding the O(L) ``torch.cat`` that the reference's
 ``forward(x, past_c_kv)`` interface implies.
 
-Prefill (several tokens) follows the reference streams with dense torch code:
-causal sliding window + sinks (:95-105), per-query gathered blocks (:145-171),
-HCA over complete-block means with the early running-mean rule (:173-219), then
-``stream_superposition``.  A prefill-side fused kernel is future work.
+Prefill (several tokens) follows the reference streams: causal sliding window + sinks
+(:95-105), per-query gathered blocks (:145-171), HCA over complete-block means with the
+early running-mean rule (:173-219), then ``stream_superposition``.  In bf16 without
+gradients one fused launch does all three streams and the gate, in latent form or in head
+space (``_prefill_form`` picks); otherwise the dense torch path runs.
 """
 from __future__ import annotations
 
@@ -31,6 +32,10 @@ from maba_sparse.kernels.dispatcher import (dispatch_hca_pool, dispatch_maba_sa_
                                             dispatch_stream_superposition, get_backend)
 from maba_sparse.layers._wcache import WeightCacheMixin, cached
 from maba_sparse.layers.indexer import DGIndexer, _Growing
+
+# Fused prefill: the head-space kernel is taken while 16 consecutive queries list fewer than
+# this many distinct blocks, in units of top_k (the measured crossover with the latent kernel)
+PREFILL_UNION_LIMIT = 5.25
 
 
 class LatentCache:
@@ -119,7 +124,7 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         # fused bf16 prefill: "auto" picks the latent or the head-space kernel from the
         # selections' sharing (see _prefill_form); the union limit is in units of top_k
         self.prefill_form = "auto"
-        self.prefill_union_limit = 4.0
+        self.prefill_union_limit = PREFILL_UNION_LIMIT
         self._install_weight_cache_hooks()
 
     def reset_cache(self) -> None:
@@ -286,13 +291,15 @@ class MabaSparseAttention(WeightCacheMixin, nn.Module):
         """``"latent"`` or ``"heads"`` for a fused prefill with selections ``idx [B, Lq, K]``.
 
         The latent kernel does each query's tiles on its own (the ten heads share every key row,
-        as at decode); the head-space kernel gives each run of 16 queries the union of their
-        blocks (16 queries share every key tile, per head).  Per tile the head-space kernel
-        issues about a quarter of the latent kernel's MFMA work for the same 16 queries, so it
-        wins while the union of 16 consecutive queries' blocks stays below about 4 K (neighbouring
-        queries of a trained or randomly initialised model select nearly the same blocks) and
-        loses when the selections scatter (random queries give 5 K).  The union is counted on
-        the GPU from ``idx`` (one segmented sort); ``self.prefill_form`` may force either."""
+        as at decode); the head-space kernel gives each run of 64 queries the union of their
+        blocks, staged once per tile and computed by each 16-query wave that lists it (16
+        queries share every key tile, per head).  Its cost grows with the union of 16
+        consecutive queries' blocks, the latent kernel's does not: measured at 10 heads of 64,
+        d_c 128, top-32, the two are equal near 5.25 K distinct blocks per 16 queries (random
+        queries at 32k tokens give 5.1 K, at 64k 6.5 K, at 128k 7.6 K), and neighbouring queries
+        of a trained or randomly initialised model select nearly the same blocks (about 3 K, where
+        the head-space kernel is 2.5 times faster).  The union is counted on the GPU from ``idx``
+        (one segmented sort); ``self.prefill_form`` may force either."""
         if self.prefill_form != "auto":
             return self.prefill_form
         B, Lq, K = idx.shape
