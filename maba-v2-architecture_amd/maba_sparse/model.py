@@ -307,12 +307,50 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
         """Prefill: ``(logits, past_states)`` with ``(state, conv_state, c_kv)`` per block
         (reference model.py:207-234; the loss and MTP head are left out)."""
         x = self.embeddings(input_ids)
+        if self._fused_norms_ok(x):
+            return self._forward_fused_norms(x, past_states)
         nps = []
         for i, layer in enumerate(self.layers):
             st, cv, pk = past_states[i] if past_states is not None else (None, None, None)
             x, nst, ncv, nck = layer(x, state=st, conv_state=cv, past_c_kv=pk)
             nps.append((nst, ncv, nck))
         return self._logits(x), nps
+
+    def _fused_norms_ok(self, x: torch.Tensor) -> bool:
+        """Whether ``forward`` runs its norms, gated residuals and SwiGLU activations as HIP
+        kernels: the ``hip`` backend, a bf16 model, the kernels' widths, no gradients."""
+        c = self.config
+        if x.device.type != "cuda" or get_backend(x.device) != "hip" or x.dtype != torch.bfloat16:
+            return False
+        if c.dim % 2 or c.dim > 2048 or c.intermediate_size % 2:
+            return False
+        return not (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()))
+
+    def _forward_fused_norms(self, x: torch.Tensor, past_states):
+        """``forward`` with each block's ``x + g1 * mo`` and ``RMSNorm`` in one HIP launch, its
+        ``x + g2 * ffn`` folded into the next block's (or the final) norm, and the SwiGLU
+        activation as one kernel (the block structure of model.py:92-128; the mixers as in
+        ``MabaBlock.forward``).  The residual stream is updated in place in ``x``."""
+        from maba_sparse.kernels import hip_backend as hb
+        layers = self.layers
+        n1 = layers[0].norm1
+        h = hb.hip_rmsnorm(x, n1.weight, n1.eps)
+        nps = []
+        for i, layer in enumerate(layers):
+            st, cv, pk = past_states[i] if past_states is not None else (None, None, None)
+            nst = ncv = nck = None
+            if layer.is_attention:
+                mo, nck = layer.mixer(h, past_c_kv=pk)
+            else:
+                mo, nst, ncv = layer.mixer(h, state=st, conv_state=cv)
+            g1 = _frozen(layer, "g1", torch.sigmoid, layer.res_gate1)
+            g2 = _frozen(layer, "g2", torch.sigmoid, layer.res_gate2)
+            h2 = hb.hip_rmsnorm(x, layer.norm2.weight, layer.norm2.eps, mo=mo, gate=g1, x_out=x)
+            f = layer.ffn.forward_hip(h2)
+            nxt = layers[i + 1].norm1 if i + 1 < len(layers) else self.final_norm
+            h = hb.hip_rmsnorm(x, nxt.weight, nxt.eps, mo=f, gate=g2, x_out=x)
+            nps.append((nst, ncv, nck))
+        return self.lm_head(self.head_proj(h)), nps
 
     def step(self, input_ids: torch.Tensor, past_states: Optional[List[Any]] = None):
         """One token with the reference's state passing (model.py:251-270)."""
