@@ -64,7 +64,9 @@ template <> __device__ __forceinline__ float2 as_stored<uint16_t>(float2 v) {
 // dtype switch, is waited for on its own, one memory round trip per chunk; the fill of the
 // chunks past the row comes from an instruction the optimiser cannot see through, which
 // keeps it from moving the conversions up into the loads' branches.
-template <class T, class TG, class TW, int MODE>
+// MAXP: channel pairs per lane the arrays hold (4, 8 or NRM_MAXP, the smallest that covers C:
+// fewer registers, more waves per SIMD, more rows in flight).
+template <class T, class TG, class TW, int MODE, int MAXP>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
   const int lane = threadIdx.x & 63;
   // a wave past the last row reads that row and stores nothing: with an early return the
@@ -77,11 +79,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
   const int np = live ? a.C / 2 : 0, nit = (a.C / 2 + 63) >> 6;
   uint32_t zr;
   asm volatile("v_mov_b32 %0, 0" : "=v"(zr));
-  typename P2<T>::raw v[NRM_MAXP], m[NRM_MAXP];
-  typename P2<TG>::raw g[NRM_MAXP];
-  typename P2<TW>::raw w[NRM_MAXP];
+  typename P2<T>::raw v[MAXP], m[MAXP];
+  typename P2<TG>::raw g[MAXP];
+  typename P2<TW>::raw w[MAXP];
 #pragma unroll
-  for (int i = 0; i < NRM_MAXP; ++i) {
+  for (int i = 0; i < MAXP; ++i) {
     v[i] = P2<T>::zero(zr); m[i] = P2<T>::zero(zr); g[i] = P2<TG>::zero(zr); w[i] = P2<TW>::zero(zr);
     if (i < nit) {
       const int j = min(lane + 64 * i, a.C / 2 - 1);
@@ -93,10 +95,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
       w[i] = P2<TW>::ldr(a.w, 2 * j);
     }
   }
-  float2 xs[NRM_MAXP];
+  float2 xs[MAXP];
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < NRM_MAXP; ++i) {
+  for (int i = 0; i < MAXP; ++i) {
     const int j = lane + 64 * i;
     float2 x = P2<T>::cvt(v[i]);
     if constexpr (MODE > 0) {
@@ -118,7 +120,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
   for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
   const float inv = rsqrtf(ss / (float)a.C + a.eps);   // (np = 0 on a dead wave: no stores)
 #pragma unroll
-  for (int i = 0; i < NRM_MAXP; ++i) {
+  for (int i = 0; i < MAXP; ++i) {
     const int j = lane + 64 * i;
     const float2 ww = P2<TW>::cvt(w[i]);
     if (j < np) P2<T>::st(a.h, r * a.hs + 2 * j, make_float2(xs[i].x * inv * ww.x, xs[i].y * inv * ww.y));
@@ -143,6 +145,43 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
     const float2 u = P2<T>::ld(a.gu, r * a.gus + a.I + 2 * j);
     const float s0 = g.x * fast_rcp(1.f + fast_exp(-g.x)), s1 = g.y * fast_rcp(1.f + fast_exp(-g.y));
     P2<T>::st(a.out, r * a.os + 2 * j, make_float2(s0 * u.x, s1 * u.y));
+  }
+}
+
+// bf16 rows with I % 8 == 0 and 16-byte aligned rows: one wave per row, 16-byte loads of
+// eight gate and eight up channels per lane and chunk, no index division; the same
+// per-element arithmetic as swiglu_kernel.
+constexpr int SW_MAXQ = 4;   // 16-byte chunks per lane: I <= 64 * 8 * SW_MAXQ
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(SwigluArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.R) return;   // whole wave
+  const int nq = a.I / 8;
+  const uint16_t* gp = (const uint16_t*)a.gu + r * a.gus;
+  uint16_t* op = (uint16_t*)a.out + r * a.os;
+  uint4 g[SW_MAXQ], u[SW_MAXQ];
+#pragma unroll
+  for (int q = 0; q < SW_MAXQ; ++q) {
+    const int c = lane + 64 * q;
+    if (c < nq) {
+      g[q] = *(const uint4*)(gp + 8 * c);
+      u[q] = *(const uint4*)(gp + a.I + 8 * c);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < SW_MAXQ; ++q) {
+    const int c = lane + 64 * q;
+    if (c < nq) {
+      const uint32_t gw[4] = {g[q].x, g[q].y, g[q].z, g[q].w}, uw[4] = {u[q].x, u[q].y, u[q].z, u[q].w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float2 gg = P2<uint16_t>::cvt(gw[e]), uu = P2<uint16_t>::cvt(uw[e]);
+        const float s0 = gg.x * fast_rcp(1.f + fast_exp(-gg.x)), s1 = gg.y * fast_rcp(1.f + fast_exp(-gg.y));
+        ow[e] = (uint32_t)f32_to_bf16_bits(s0 * uu.x) | ((uint32_t)f32_to_bf16_bits(s1 * uu.y) << 16);
+      }
+      *(uint4*)(op + 8 * c) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
   }
 }
 
@@ -270,13 +309,19 @@ extern "C" int maba_hip_rmsnorm(const maba_tensor* x, const maba_tensor* mo, con
   const int mode = !a.mo ? 0 : !a.xo ? 1 : 2;
   const bool tb = x->dtype == MABA_BF16, gb = a.gdt == MABA_BF16, wb = a.wdt == MABA_BF16;
   void (*k)(NormArgs) = nullptr;
+  const int nit = (C / 2 + 63) / 64;
+#define MABA_NRM_PICKP(T, TW, P)                                                                       \
+  k = mode == 0 ? rmsnorm_kernel<T, float, TW, 0, P>                                                    \
+    : mode == 1 ? (gb ? rmsnorm_kernel<T, uint16_t, TW, 1, P> : rmsnorm_kernel<T, float, TW, 1, P>)    \
+                : (gb ? rmsnorm_kernel<T, uint16_t, TW, 2, P> : rmsnorm_kernel<T, float, TW, 2, P>)
 #define MABA_NRM_PICK(T, TW)                                                                           \
-  k = mode == 0 ? rmsnorm_kernel<T, float, TW, 0>                                                       \
-    : mode == 1 ? (gb ? rmsnorm_kernel<T, uint16_t, TW, 1> : rmsnorm_kernel<T, float, TW, 1>)          \
-                : (gb ? rmsnorm_kernel<T, uint16_t, TW, 2> : rmsnorm_kernel<T, float, TW, 2>)
-  if (tb) { if (wb) MABA_NRM_PICK(uint16_t, uint16_t); else MABA_NRM_PICK(uint16_t, float); }
-  else { if (wb) MABA_NRM_PICK(float, uint16_t); else MABA_NRM_PICK(float, float); }
+  if (nit <= 4) { MABA_NRM_PICKP(T, TW, 4); }                                                          \
+  else if (nit <= 8) { MABA_NRM_PICKP(T, TW, 8); }                                                     \
+  else { MABA_NRM_PICKP(T, TW, NRM_MAXP); }
+  if (tb) { if (wb) { MABA_NRM_PICK(uint16_t, uint16_t); } else { MABA_NRM_PICK(uint16_t, float); } }
+  else { if (wb) { MABA_NRM_PICK(float, uint16_t); } else { MABA_NRM_PICK(float, float); } }
 #undef MABA_NRM_PICK
+#undef MABA_NRM_PICKP
   hipLaunchKernelGGL(k, grid, dim3(256), 0, (hipStream_t)stream, a);
   return check_launch("rmsnorm");
 }
@@ -294,6 +339,13 @@ extern "C" int maba_hip_swiglu(const maba_tensor* gate_up, maba_tensor* out, voi
     return fail(MABA_ERR_UNSUPPORTED, "swiglu: rows with unit channel stride required");
   a.gu = gate_up->data; a.out = out->data; a.R = R; a.I = I;
   if (R == 0) return MABA_OK;
+  const bool rows16 = out->dtype == MABA_BF16 && I % 8 == 0 && I <= 64 * 8 * SW_MAXQ &&
+                      (uintptr_t)a.gu % 16 == 0 && (uintptr_t)a.out % 16 == 0 &&
+                      (R == 1 || (a.gus % 8 == 0 && a.os % 8 == 0)) && ceil_div(R, 4) <= 0x7fffffff;
+  if (rows16) {
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)ceil_div(R, 4)), dim3(256), 0, (hipStream_t)stream, a);
+    return check_launch("swiglu");
+  }
   const int64_t total = R * (I / 2);
   const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total, 256), 65536);
   if (out->dtype == MABA_F32) hipLaunchKernelGGL(swiglu_kernel<float>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);

@@ -303,18 +303,19 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
     def _logits(self, x: torch.Tensor) -> torch.Tensor:
         return self.lm_head(self.head_proj(self.final_norm(x)))
 
-    def forward(self, input_ids: torch.Tensor, past_states: Optional[List[Any]] = None):
+    def forward(self, input_ids: torch.Tensor, past_states: Optional[List[Any]] = None, last_only: bool = False):
         """Prefill: ``(logits, past_states)`` with ``(state, conv_state, c_kv)`` per block
-        (reference model.py:207-234; the loss and MTP head are left out)."""
+        (reference model.py:207-234; the loss and MTP head are left out).  ``last_only`` returns
+        the logits of the last position only, ``[B, 1, vocab]`` (what generation reads)."""
         x = self.embeddings(input_ids)
         if self._fused_norms_ok(x):
-            return self._forward_fused_norms(x, past_states)
+            return self._forward_fused_norms(x, past_states, last_only)
         nps = []
         for i, layer in enumerate(self.layers):
             st, cv, pk = past_states[i] if past_states is not None else (None, None, None)
             x, nst, ncv, nck = layer(x, state=st, conv_state=cv, past_c_kv=pk)
             nps.append((nst, ncv, nck))
-        return self._logits(x), nps
+        return self._logits(x[:, -1:] if last_only else x), nps
 
     def _fused_norms_ok(self, x: torch.Tensor) -> bool:
         """Whether ``forward`` runs its norms, gated residuals and SwiGLU activations as HIP
@@ -326,7 +327,7 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
             return False
         return not (torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()))
 
-    def _forward_fused_norms(self, x: torch.Tensor, past_states):
+    def _forward_fused_norms(self, x: torch.Tensor, past_states, last_only: bool = False):
         """``forward`` with each block's ``x + g1 * mo`` and ``RMSNorm`` in one HIP launch, its
         ``x + g2 * ffn`` folded into the next block's (or the final) norm, and the SwiGLU
         activation as one kernel (the block structure of model.py:92-128; the mixers as in
@@ -350,7 +351,7 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
             nxt = layers[i + 1].norm1 if i + 1 < len(layers) else self.final_norm
             h = hb.hip_rmsnorm(x, nxt.weight, nxt.eps, mo=f, gate=g2, x_out=x)
             nps.append((nst, ncv, nck))
-        return self.lm_head(self.head_proj(h)), nps
+        return self.lm_head(self.head_proj(h[:, -1:] if last_only else h)), nps
 
     def step(self, input_ids: torch.Tensor, past_states: Optional[List[Any]] = None):
         """One token with the reference's state passing (model.py:251-270)."""
@@ -408,7 +409,7 @@ class MabaSparseForCausalLM(WeightCacheMixin, nn.Module):
         B, L = input_ids.shape
         if graph is None:
             graph = self.serving_graph_ok(input_ids)
-        logits, states = self(input_ids)
+        logits, states = self(input_ids, last_only=True)
         if graph:
             return self._generate_graph(logits, states, L, max_new_tokens, on_prefill_done, return_logits,
                                         on_graph_ready)

@@ -163,6 +163,23 @@ def test_swiglu(dev, shape, dtype):
         assert_close(out, ref.numpy(), 1e-5, 1e-6, "swiglu")
 
 
+def test_swiglu_row_kernel_matches_generic(dev):
+    """bf16 rows of 16-byte aligned width take the one-wave-per-row kernel; the same rows at
+    a 4-byte offset (not 16-byte aligned) take the element-pair kernel: equal bits."""
+    hb = _hb()
+    shape = (3, 333, 2 * 1248)
+    gu = torch.randn(*shape, generator=torch.Generator().manual_seed(9)).bfloat16().to(dev)
+    out = hb.hip_swiglu(gu)
+    buf = torch.empty(gu.numel() + 8, dtype=torch.bfloat16, device=dev)
+    shifted = buf[2: 2 + gu.numel()].view(shape)
+    shifted.copy_(gu)
+    assert shifted.data_ptr() % 16 != 0
+    assert torch.equal(hb.hip_swiglu(shifted), out)
+    I = shape[-1] // 2
+    gd, ud = gu[..., :I].double().cpu(), gu[..., I:].double().cpu()
+    _ulp_close(out, (gd / (1 + torch.exp(-gd)) * ud).numpy(), "swiglu rows")
+
+
 @pytest.mark.parametrize("inplace", [False, True])
 def test_dgda_step_bf16_state(dev, inplace):
     hb = _hb()
