@@ -25,7 +25,7 @@
 // lane's query lists its block.  A wave skips the tiles none of its queries weights.
 #include <algorithm>
 
-#include "maba_common.h"
+#include "dgda_common.h"
 
 namespace maba {
 
@@ -59,7 +59,18 @@ __device__ __forceinline__ pf16x4 pf_ldsT4(const short* tile, int pitch, int r0,
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) pf16x4*)p);
 }
 
-// Running softmax state of one stream for the lane's query.
+// Bits 4 rb + i of the lane's 16 tile rows j = 16 rb + 4 g + i that lie in [lo, hi]
+// (tile-relative, either bound may fall outside [0, 63]).
+__device__ __forceinline__ uint32_t pf_range_bits(int lo, int hi, int g) {
+  auto lowmask = [](int n) -> uint32_t { return n <= 0 ? 0u : n >= 32 ? 0xffffffffu : (1u << n) - 1u; };
+  const uint32_t m0 = lowmask(hi + 1) & ~lowmask(lo);
+  const uint32_t m1 = lowmask(hi - 31) & ~lowmask(lo - 32);
+  const int sh = 4 * g;
+  return ((m0 >> sh) & 0xfu) | (((m0 >> (16 + sh)) & 0xfu) << 4) | (((m1 >> sh) & 0xfu) << 8) |
+         (((m1 >> (16 + sh)) & 0xfu) << 12);
+}
+
+// Running softmax state of one stream for the lane's query (m in log2 units).
 template <int NDT>
 struct PfAcc {
   float m, l;
@@ -76,7 +87,12 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
   __shared__ __attribute__((aligned(16))) short s_v[2][TE];
   __shared__ uint32_t s_bits[PF_WORDS];
   __shared__ uint16_t s_list[PF_LIST];
-  __shared__ int s_nlist;
+  __shared__ uint32_t s_need[4][PF_LIST / 32];    // per wave: the list entries its queries list
+  // Set-up only, in value buffer 1 (first written by the first tile's prefetch, after the
+  // set-up's last barrier): the list position of each bitmap word's first block, the list length.
+  int* s_wpre = (int*)&s_v[1][0];
+  int* s_nlist = s_wpre + PF_WORDS;
+  static_assert((PF_WORDS + 1) * 4 <= TE * 2, "set-up tables fit one value buffer");
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c16 = lane & 15;
   const int64_t b = blockIdx.z;
@@ -158,6 +174,7 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
         if (lane >= o2) incl += y;
       }
       int at = nlist + incl - cnt;
+      if (wd < nwords) s_wpre[wd] = at;
       uint32_t rest = word;
       while (rest) {
         const int bit = __ffs(rest) - 1;
@@ -166,12 +183,24 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
       }
       nlist += __shfl(incl, 63);
     }
-    if (lane == 0) s_nlist = nlist;
+    if (lane == 0) *s_nlist = nlist;
   }
   const int64_t e_hi = min(a.nc - 1, (wpos_hi + 1) / a.pool - 1);
   const int n_hca = e_hi >= 0 ? (int)(e_hi / 64 + 1) : 0;
+  for (int wd = tid; wd < 4 * (PF_LIST / 32); wd += 256) (&s_need[0][0])[wd] = 0u;
   __syncthreads();
-  const int n_sp = s_nlist;
+  const int n_sp = *s_nlist;
+  if (qvalid) {   // mark the list entries of the lane's slots for its wave
+#pragma unroll
+    for (int r = 0; r < PF_MAXK / 4; ++r) {
+      const int bk = (int)((myblk[r >> 1] >> (16 * (r & 1))) & 0xffffu);
+      if (bk < nbl) {
+        const int u = s_wpre[bk >> 5] + __popc(s_bits[bk >> 5] & ((1u << (bk & 31)) - 1u));
+        atomicOr(&s_need[wave][u >> 5], 1u << (u & 31));
+      }
+    }
+  }
+  __syncthreads();
   const int n_ls = n_loc + n_sp;
   const int nt = n_ls + n_hca;
 
@@ -211,17 +240,16 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
     }
   };
 
-  // One 64-key tile from LDS buffer buf: tile row j has weight fc for the lane's query where
-  // valid(j) holds and 0 elsewhere.  A wave none of whose queries weights any row skips the
-  // tile: for such a lane the tile would leave (m, l, z) exactly as they are.
-  auto tile = [&](PfAcc<NDT>& st, int buf, float fc, auto valid) {
-    uint32_t vmask = 0u;   // bit 4 rb + i: key 16 rb + 4 g + i weighted
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vmask |= (uint32_t)valid(16 * rb + 4 * g + i) << (4 * rb + i);
+  // One 64-key tile from LDS buffer buf: the lane's rows with bit 4 rb + i of vmask set
+  // (row 16 rb + 4 g + i) have weight fc, the others 0.  A wave none of whose queries weights
+  // any row skips the tile: for such a lane the tile would leave (m, l, z) exactly as they
+  // are.  Scores are scaled to log2 units (scale * log2 e) so that each probability is one
+  // exp2; a tile whose 64 rows are valid for every lane of the wave skips the masking.
+  const float sl2 = a.scale * 1.4426950408889634f;
+  auto tile = [&](PfAcc<NDT>& st, int buf, float fc, uint32_t vmask) {
     if (!qvalid || !(fc > 0.f)) vmask = 0u;
     if (__ballot(vmask != 0u) == 0ull) return;   // wave-uniform
+    const bool full = __ballot(qvalid && vmask != 0xffffu) == 0ull;
     const short* ks = s_k[buf];
     const short* vt = s_v[buf];
     f32x4 sc[4];
@@ -242,27 +270,26 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
     for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x = (vmask >> (4 * rb + i)) & 1u ? sc[rb][i] * a.scale : -INFINITY;
+        const float x = (full || ((vmask >> (4 * rb + i)) & 1u)) ? sc[rb][i] * sl2 : -INFINITY;
         sc[rb][i] = x;
         tmax = fmaxf(tmax, x);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float m_new = fmaxf(st.m, tmax);
-    const float corr = (m_new == -INFINITY) ? 1.f : __expf(st.m - m_new);
+    const float corr = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(st.m - m_new);
     const float m_sub = (m_new == -INFINITY) ? 0.f : m_new;
     float psum = 0.f;
-    pf16x4 ph[4], pl[4];
+    i16x4 ph[4], pl[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
+      f32x4 pe;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float pe = fc * __expf(sc[rb][i] - m_sub);   // exp(-inf) = 0 for masked keys
-        psum += pe;
-        const short hb = __builtin_bit_cast(short, (__bf16)pe);
-        ph[rb][i] = hb;
-        pl[rb][i] = __builtin_bit_cast(short, (__bf16)(pe - bf16_bits_to_f32((uint16_t)hb)));
+        pe[i] = fc * __builtin_amdgcn_exp2f(sc[rb][i] - m_sub);   // exp2(-inf) = 0 for masked keys
+        psum += pe[i];
       }
+      split4(pe, ph[rb], pl[rb]);
     }
     psum += __shfl_xor(psum, 16);
     psum += __shfl_xor(psum, 32);
@@ -278,10 +305,7 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
         const pf16x4 a0 = pf_ldsT4(vt, TP, 32 * p2, 16 * dt, c16, g);
         const pf16x4 a1 = pf_ldsT4(vt, TP, 32 * p2 + 16, 16 * dt, c16, g);
         const pf16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        const pf16x8 bh = {ph[2 * p2][0], ph[2 * p2][1], ph[2 * p2][2], ph[2 * p2][3],
-                           ph[2 * p2 + 1][0], ph[2 * p2 + 1][1], ph[2 * p2 + 1][2], ph[2 * p2 + 1][3]};
-        const pf16x8 bl = {pl[2 * p2][0], pl[2 * p2][1], pl[2 * p2][2], pl[2 * p2][3],
-                           pl[2 * p2 + 1][0], pl[2 * p2 + 1][1], pl[2 * p2 + 1][2], pl[2 * p2 + 1][3]};
+        const i16x8 bh = cat8(ph[2 * p2], ph[2 * p2 + 1]), bl = cat8(pl[2 * p2], pl[2 * p2 + 1]);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bh),
                                                       acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bl),
@@ -302,13 +326,14 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
     for (int dt = 0; dt < NDT; ++dt) o[dt] += st.z[dt] * w;
   };
   // tiles [i, i_end): prefetch tile i + 1 (of whichever stream), compute tile i, stage the
-  // prefetched tile into the other buffer, one barrier per tile.  valid_of(i) gives tile i's
-  // row predicate, weight_of(i) the weight of its valid rows.
+  // prefetched tile into the other buffer, one barrier per tile.  weight_of(i) gives tile i's
+  // weight for the lane's query and mask_of(i) its row mask (pf_range_bits).
   int i = 0;
-  auto run = [&](PfAcc<NDT>& st, int i_end, auto weight_of, auto valid_of) {
+  auto run = [&](PfAcc<NDT>& st, int i_end, auto weight_of, auto mask_of) {
     for (; i < i_end; ++i) {
       if (i + 1 < nt) fetch(i + 1);
-      tile(st, i & 1, weight_of(i), valid_of(i));
+      const float fc = weight_of(i);
+      tile(st, i & 1, fc, fc > 0.f ? mask_of(i) : 0u);
       if (i + 1 < nt) stash((i + 1) & 1);
       __syncthreads();
     }
@@ -320,24 +345,24 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
   __syncthreads();
   PfAcc<NDT> st;
 
-  // ---- local stream
+  // ---- local stream: sink tiles hold keys [0, min(sink_end, pos + 1)); window tiles the keys
+  // in (pos - window, pos] and the sinks below min(ns, pos + 1)
   reset(st);
   run(st, n_loc, [](int) { return 1.f; }, [&](int ti) {
-    const int tb = ti < n_st ? 64 * ti : (int)wt0 + 64 * (ti - n_st);
-    const bool sink = ti < n_st;
-    const int se = (int)sink_end, ns32 = (int)ns;
-    return [=](int j) {
-      const int kj = tb + j;
-      if (sink) return kj < se && kj <= pos;
-      return kj <= pos && (pos - kj < a.window || kj < ns32);
-    };
+    if (ti < n_st) return pf_range_bits(-64 * ti, min((int)sink_end - 1, pos) - 64 * ti, g);
+    const int tb = (int)wt0 + 64 * (ti - n_st);
+    return pf_range_bits(pos - a.window + 1 - tb, pos - tb, g) |
+           pf_range_bits(-tb, min((int)ns - 1, pos) - tb, g);
   });
   fold(st, g0);
 
-  // ---- sparse stream: each key weighted by how often the lane's query lists its block
+  // ---- sparse stream: each key weighted by how often the lane's query lists its block; a
+  // wave skips the entries none of its queries lists without counting
   reset(st);
   run(st, n_ls, [&](int ti) {
-    const int blk = s_list[ti - n_loc];   // wave-uniform
+    const int u = ti - n_loc;
+    if (((s_need[wave][u >> 5] >> (u & 31)) & 1u) == 0u) return 0.f;   // wave-uniform
+    const int blk = s_list[u];
     int cnt = 0;
 #pragma unroll
     for (int m = 0; m < PF_MAXK / 8; ++m)
@@ -345,22 +370,14 @@ __global__ __launch_bounds__(256, NP == 4 ? 2 : 3) void maba_sa_prefill_kernel(P
     cnt += __shfl_xor(cnt, 16);
     cnt += __shfl_xor(cnt, 32);
     return (float)cnt;
-  }, [&](int ti) {
-    const int tb = 64 * (int)s_list[ti - n_loc];
-    return [=](int j) { return tb + j <= pos; };
-  });
+  }, [&](int ti) { return pf_range_bits(0, pos - 64 * (int)s_list[ti - n_loc], g); });
   fold(st, g1);
 
-  // ---- HCA stream: means e with (e + 1) pool - 1 <= pos; early queries take their row
+  // ---- HCA stream: means e <= e_max, the last complete block's mean before the lane's query;
+  // early queries take their row
   reset(st);
-  run(st, nt, [](int) { return 1.f; }, [&](int ti) {
-    const int eb = 64 * (ti - n_ls);
-    const int nc32 = (int)a.nc;
-    return [=](int j) {
-      const int e = eb + j;
-      return e < nc32 && (e + 1) * a.pool - 1 <= pos;
-    };
-  });
+  const int e_max = (int)min(a.nc - 1, (int64_t)((pos + 1) / a.pool) - 1);
+  run(st, nt, [](int) { return 1.f; }, [&](int ti) { return pf_range_bits(0, e_max - 64 * (ti - n_ls), g); });
   if (pos < a.pool - 1) {   // running mean of c[0..pos] through W_v (the caller's row)
     const bool have = a.early && tq < a.n_early;
 #pragma unroll
