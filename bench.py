@@ -641,7 +641,8 @@ def prefill_attention_bench(dev, B=1, H=10, L=32768, dh=64, dc=128, K=32):
     rf = {"bound": "mfma", "achieved": fl / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
           "frac": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, "algorithmic_flops": fl,
           "kernel": "maba_sa_prefill_kernel" if form == "heads" else "maba_sa_prefill_latent_kernel",
-          "traffic": (measured_traffic("maba_sa_prefill_latent_bytes_per_call") if form == "latent" else None),
+          "traffic": measured_traffic("maba_sa_prefill_heads_bytes_per_call" if form == "heads"
+                                      else "maba_sa_prefill_latent_bytes_per_call"),
           "traffic_source": TRAFFIC_SOURCE}
     return {"maba_sa_prefill_32k": {
         "ms_per_call": ms_comp, "kernel_ms": ms, "form": form, "distinct_blocks_per_16_queries": distinct,
