@@ -123,3 +123,35 @@ def test_model_harness_gpu(dev):
         assert (lb.float().cpu() - lc).abs().max().item() <= 0.1 * scale
         toks = bf.generate_greedy(ids.to(dev), 6)
         assert toks.shape == (2, 6) and int(toks.min()) >= 0 and int(toks.max()) < 97
+
+
+def test_model_fused_norm_prefill_matches_unfused(dev):
+    """A bf16 model's ``forward`` on the HIP backend runs its norms, gated residuals and SwiGLU
+    activations as HIP kernels: against the same model's torch elementwise path, for a whole
+    prefill and for a prefill continued from the first half's states; ``last_only`` returns the
+    last position's row of the full logits.  Tolerance: 3e-2 of the logits' largest magnitude (the
+    two paths round the residual stream to bf16 at different points)."""
+    from maba_sparse.model import MabaSparseForCausalLM, get_101m_config
+    torch.manual_seed(3)
+    cfg = get_101m_config(dim=128, n_layers=4, n_heads=2, d_head=64, vocab_size=97, d_emb=16, d_c=32, d_idx=16,
+                          intermediate_size=96, top_k=4, dist_lambda=0.1)
+    m = MabaSparseForCausalLM(cfg).init_normal(0.02).to(dev, torch.bfloat16).eval()
+    ids = torch.randint(0, 97, (2, 300), generator=torch.Generator().manual_seed(4)).to(dev)
+    with torch.no_grad():
+        assert m._fused_norms_ok(m.embeddings(ids))
+        lf, _ = m(ids)
+        lf1, st = m(ids[:, :150])
+        lf2, _ = m(ids[:, 150:], past_states=st)
+        ll, _ = m(ids, last_only=True)
+        m._fused_norms_ok = lambda x: False           # the torch elementwise path
+        lu, _ = m(ids)
+        lu1, su = m(ids[:, :150])
+        lu2, _ = m(ids[:, 150:], past_states=su)
+    scale = lu.float().abs().max().item()
+    assert torch.isfinite(lf.float()).all()
+    assert (lf.float() - lu.float()).abs().max().item() <= 3e-2 * scale
+    assert (lf2.float() - lu2.float()).abs().max().item() <= 3e-2 * scale
+    assert (torch.cat([lf1, lf2], dim=1).float() - lf.float()).abs().max().item() <= 3e-2 * scale
+    assert ll.shape == (2, 1, 97)
+    # the head GEMM over 2 rows or over 600 may sum in another order
+    assert (ll[:, 0].float() - lf[:, -1].float()).abs().max().item() <= 1e-2 * scale
