@@ -224,9 +224,11 @@ static int cache_append(const maba_tensor* c_new, const maba_tensor* k_new, cons
   a.qh = nullptr; a.H = 0; a.dh = 0;
   int64_t nq = 0;
   if (q_heads) {   // absorbed queries and gate logits in the same launch
+    // q_lat's head count is checked positive before it divides anything
     if (q_heads->ndim != 2 || q_heads->shape[0] != B || !w_k || w_k->ndim != 2 || w_k->shape[1] != dc ||
         w_k->shape[0] != q_heads->shape[1] || !q_lat || q_lat->ndim != 3 || q_lat->shape[0] != B ||
-        q_lat->shape[2] != dc || w_k->shape[0] % q_lat->shape[1] != 0)
+        q_lat->shape[2] != dc || q_lat->shape[1] < 1 || w_k->shape[0] < q_lat->shape[1] ||
+        w_k->shape[0] % q_lat->shape[1] != 0)
       return fail(MABA_ERR_INVALID, "cache_append: q_heads [B,H*dh], w_k [H*dh,dc], q_lat [B,H,dc] required");
     const int64_t so[2] = {B, 3}, sb[1] = {3};
     if (!expect_shape(gate_in, "gate_in", 2, so) || !expect_shape(gate_out, "gate_out", 2, so) ||

@@ -287,6 +287,10 @@ extern "C" int maba_hip_decode_linear(const maba_tensor* a, const maba_tensor* r
     // x_out is written while other workgroups read a and mo: it may overlap neither
     if (overlaps(x_out, d.xos, K, a, d.as, K) || overlaps(x_out, d.xos, K, mo, d.ms, K))
       return fail(MABA_ERR_INVALID, "%s: x_out may not overlap a or mo", who);
+    // every workgroup reads mo and the first column of workgroups writes x_out while others
+    // write y: y may overlap neither
+    if (M > 0 && (overlaps(y, ys, N, mo, d.ms, K) || overlaps(y, ys, N, x_out, d.xos, K)))
+      return fail(MABA_ERR_INVALID, "%s: y may not overlap mo or x_out", who);
     mode = DL_NORMRES;
     d.mo = (const uint16_t*)mo->data; d.g = (const uint16_t*)gate->data; d.xo = (uint16_t*)x_out->data;
   }

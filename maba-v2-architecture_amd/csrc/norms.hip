@@ -278,6 +278,7 @@ extern "C" int maba_hip_rmsnorm(const maba_tensor* x, const maba_tensor* mo, con
                                 void* stream) {
   if (!x || !weight || !h) return fail(MABA_ERR_INVALID, "rmsnorm: x, weight and h required");
   const int C = (int)x->shape[x->ndim - 1];
+  if (C < 2) return fail(MABA_ERR_INVALID, "rmsnorm: the last dimension must hold at least 2 channels");
   if (C % 2 != 0 || C > 2 * 64 * NRM_MAXP) return fail(MABA_ERR_UNSUPPORTED, "rmsnorm: C even and <= %d", 128 * NRM_MAXP);
   if (x->dtype != MABA_F32 && x->dtype != MABA_BF16) return fail(MABA_ERR_DTYPE, "rmsnorm: f32 or bf16 rows");
   NormArgs a;

@@ -33,10 +33,14 @@ def _work_dtype(t: torch.Tensor) -> torch.dtype:
 
 
 def _log_decay(alpha, log_alpha):
-    """The reference's decay forms (cpu_dgda.py:63-68): log of alpha clamped to [1e-20, 1],
-    or log_alpha clamped to [-46, 0]."""
+    """The reference's decay forms (cpu_dgda.py:63-68), branch for branch: log_alpha alone is
+    taken as given; alpha alone as log(alpha clamped to [1e-20, 1]); both given, log_alpha
+    clamped to [-46, 0].  (Within a chunk every decay ratio is clamped to <= 1 below, as in the
+    reference, so a growing gate only counts across chunk boundaries.)"""
     if log_alpha is None:
         return torch.log(alpha.clamp(min=1e-20, max=1.0))
+    if alpha is None:
+        return log_alpha
     return torch.clamp(log_alpha, min=-46.0, max=0.0)
 
 

@@ -19,7 +19,8 @@ Functions
                        ``-0.75*ln 3`` known answer (test_indexer.py:143-164),
                        the causal pattern (test_triton_indexer.py:222-244) and
                        the penalty order ``[3,2,1,0]``
-                       (test_triton_indexer.py:247-255).
+                       (test_triton_indexer.py:247-255).  Chosen rows
+                       (``positions``) equal the same rows of the full matrix.
 ``decode_scores``      decode scores with ``q_blk = nb-1`` and no mask
                        (layers/indexer.py:101-107).  Pinned by the same
                        penalty closed form and brute force on tiny inputs.
@@ -52,15 +53,19 @@ def compute_centroids(k_idx, block_size=64):
     return 0.5 * (kb.mean(axis=2) + kb.max(axis=2))
 
 
-def prefill_scores(q_idx, centroids, lam, block_size=64):
-    """Causal prefill score matrix ``[B, L, nb]`` (cpu_indexer.py:91-102)."""
+def prefill_scores(q_idx, centroids, lam, block_size=64, positions=None):
+    """Causal prefill score matrix ``[B, L, nb]`` (cpu_indexer.py:91-102).
+
+    ``positions`` (default ``0 .. L-1``) are the token positions of the query rows, so that
+    chosen rows of a long prefill can be scored without the whole matrix."""
     q = np.asarray(q_idx, np.float64)
     c = np.asarray(centroids, np.float64)
     B, L, d = q.shape
     nb = c.shape[1]
     scale = 1.0 / math.sqrt(d)
     s = np.einsum("bld,bnd->bln", q * scale, c)
-    qi = (np.arange(L) // block_size)[:, None]
+    pos = np.arange(L) if positions is None else np.asarray(positions, np.int64)
+    qi = (pos // block_size)[:, None]
     ni = np.arange(nb)[None, :]
     pen = lam * np.log1p(np.abs(qi - ni).astype(np.float64))
     sc = s - pen[None]

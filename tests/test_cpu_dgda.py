@@ -93,3 +93,40 @@ def test_cpu_backend_selected_for_host_tensors():
     eo, eS = od.dgda_prefill_seq(**oracle_dgda_args(inp))
     assert_close(o, eo, 1e-4, 1e-4, "dispatched out")
     assert np.isfinite(to_np(S)).all()
+
+
+def test_cpu_backend_config1_shape():
+    """BASELINE config 1 (B=1, H=10, T=2048, d=64, fp32, per-token gates, zero state) through
+    the dispatcher on host tensors -- the ``cpu`` backend, chunk_size 16 and the adaptive
+    inversion as the layer calls it -- against the float64 token recurrence."""
+    from maba_sparse.kernels import dispatcher as D
+    inp = dgda_inputs(1, 10, 2048, qkv_dtype=torch.float32, seed=101)
+    inp["alpha"] = torch.exp(inp["log_alpha"][..., :1]).expand(inp["log_alpha"].shape)
+    o, S = D.dispatch_dgda_prefill(**inp, chunk_size=16, inversion_method="adaptive", adaptive_tol=7e-5)
+    assert o.shape == (1, 10, 2048, 64) and o.dtype == torch.float32
+    eo, eS = od.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 1e-4, 1e-4, "config 1 out")
+    assert_close(S, eS, 1e-4, 1e-4, "config 1 state")
+
+
+def test_cpu_growing_decay_follows_reference_cpu_branches():
+    """Decays above one (log_alpha > 0 on some tokens) take the reference CPU's branches
+    (cpu_dgda.py:63-68, 101-103):
+    - log_alpha alone is used as given.  With chunk_size 1 no decay ratio lies inside a chunk,
+      so the chunked algorithm is the token recurrence itself: it must equal the float64
+      recurrence on the unclamped gates;
+    - alpha and log_alpha both given: log_alpha is clamped to [-46, 0], so the result is the
+      recurrence on the clamped gates (no ratio then exceeds one, and the chunk size does
+      not matter)."""
+    inp = dgda_inputs(1, 2, 90, dk=16, dv=16, qkv_dtype=torch.float32, gates="channel", seed=5, with_state=True)
+    la = inp["log_alpha"].clone()
+    la[:, :, ::7] = 0.05                              # growing on every seventh token
+    inp["log_alpha"] = la
+    o, S = _cpu().cpu_dgda_prefill(**inp, chunk_size=1)
+    eo, eS = od.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 1e-4, 1e-4, "log_alpha alone, chunk 1")
+    assert_close(S, eS, 1e-4, 1e-4, "log_alpha alone, chunk 1 state")
+    o2, S2 = _cpu().cpu_dgda_prefill(**inp, alpha=torch.exp(la), chunk_size=16)
+    eo2, eS2 = od.dgda_prefill_seq(**oracle_dgda_args(dict(inp, log_alpha=la.clamp(-46.0, 0.0))))
+    assert_close(o2, eo2, 1e-4, 1e-4, "both forms: clamped")
+    assert_close(S2, eS2, 1e-4, 1e-4, "both forms: clamped state")

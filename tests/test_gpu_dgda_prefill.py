@@ -111,10 +111,15 @@ def test_baseline_shape_two_heads_vs_c_oracle(dev):
     assert_close(S, eS, 2e-3, 2e-3, "state")
 
 
-def test_baseline_shape_split_chaining(dev):
-    """Full BASELINE config 2 shape: prefill(T) == prefill(T/2) -> prefill(T/2, initial_state)."""
+@pytest.mark.parametrize("decay", ["baseline", "slow"])
+def test_baseline_shape_split_chaining(dev, decay):
+    """Full BASELINE config 2 shape: prefill(T) == prefill(T/2) -> prefill(T/2, initial_state).
+    With the BASELINE decay the segment transitions vanish within a chunk or two (the
+    zero-start pass and the gate-bound skip carry the run); with the slow decay none does
+    (aggregate, zero-start and fix-up passes all do full work)."""
     B, H, T = 4, 10, 32768
-    inp = dgda_inputs(B, H, T, seed=3, decay="slow", device=dev)
+    print(f"\nconfig 2 split chaining: decay={decay}", flush=True)
+    inp = dgda_inputs(B, H, T, seed=3, decay=decay, device=dev)
     o, S = _run(inp)
     assert torch.isfinite(o).all() and torch.isfinite(S).all()
     h = T // 2
@@ -125,6 +130,44 @@ def test_baseline_shape_split_chaining(dev):
     o2, S2 = _run(second)
     assert_close(torch.cat([o1, o2], dim=2), to_np(o), 2e-3, 2e-3, "chained out")
     assert_close(S2, to_np(S), 2e-3, 2e-3, "chained state")
+
+
+def _slot_chunks(B, H, T):
+    """Chunks per slot of the output pass at this shape on this device (U = max(16,
+    ceil(chunks / (2 CUs)))), the slot cut of the zero-start launch."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    total = B * H * (T // 64)
+    return max(16, -(-total // (2 * cus)))
+
+
+def test_baseline_shape_full_run_heads_vs_c_oracle(dev):
+    """The headline run itself -- B=4, H=10, T=32768, BASELINE decay, bf16 q/k/v, fp32
+    per-token gates, bf16 output as the bench writes it -- with two of its heads against the
+    C chunked oracle (fp32).  The heads are chosen so that their first chunk is not on a slot
+    boundary: their segments start mid-slot, so every segment cut of those heads falls inside
+    a sequence, their first segment runs in a slot shared with the previous head, and the
+    gate-bound skip decides each later segment's start.  The bf16 output is the rounding of
+    the same run's fp32 output."""
+    B, H, T = 4, 10, 32768
+    inp = dgda_inputs(B, H, T, seed=12, device=dev)
+    U = _slot_chunks(B, H, T)
+    nch = T // 64
+    cut = [bh for bh in range(B * H) if (bh * nch) % U != 0]
+    heads = [cut[0], cut[len(cut) // 2]]
+    print(f"\nconfig 2 full run: U={U} heads (b*H+h)={heads}", flush=True)
+    o16, S = _run(inp, out_dtype=torch.bfloat16)
+    o32, S32 = _run(inp)
+    assert torch.equal(o16, o32.to(torch.bfloat16))
+    assert torch.equal(S, S32)
+    f = lambda t: to_np(t).astype(np.float32)  # noqa: E731
+    for bh in heads:
+        b, h = divmod(bh, H)
+        sl = lambda t: t[b:b + 1, h:h + 1]  # noqa: E731
+        eo, eS = dgda_c.dgda_prefill_chunked_c(f(sl(inp["q"])), f(sl(inp["k"])), f(sl(inp["v"])),
+                                               f(sl(inp["log_alpha"])[..., :1]), f(sl(inp["b"])[..., :1]),
+                                               f(sl(inp["w"])[..., :1]), chunk_size=64)
+        assert_close(sl(o32), eo, 2e-3, 2e-3, f"out head {bh}")
+        assert_close(sl(S), eS, 2e-3, 2e-3, f"state head {bh}")
 
 
 def test_chunk_mixed_decay_segments(dev):
@@ -264,3 +307,52 @@ def test_subchunk_path_config2_shape_split_chaining(dev):
            for k, v in inp.items()}
     eo, _ = odgda.dgda_prefill_seq(**oracle_dgda_args(few))
     assert_close(o[:1, :2, :4096], eo, 2e-3, 2e-3, "oracle heads")
+
+
+# ----------------------------------------------------------------------------- config 1
+def _config1_inputs(device):
+    """B=1, H=10, T=2048, d=64, fp32; per-token gates as the op's
+    ``[B,H,T,64]`` stride-0 views, both decay forms given (the reference layer's call)."""
+    inp = dgda_inputs(1, 10, 2048, qkv_dtype=torch.float32, seed=101, device=device)
+    inp["alpha"] = torch.exp(inp["log_alpha"][..., :1]).expand(inp["log_alpha"].shape)
+    return inp
+
+
+def test_config1_fp32_dispatch_vs_oracle(dev):
+    """Config 1 at its shape through the dispatcher, every tensor fp32 (the reference's
+    dtype contract, no mixed dtypes), chunk_size 16 as the layer passes it: rtol = atol =
+    1e-4 against the float64 token recurrence (fp32 inputs, products carried to about 16
+    mantissa bits by the hi/lo MFMA splits)."""
+    from maba_sparse.kernels.dispatcher import dispatch_dgda_prefill
+    inp = _config1_inputs(dev)
+    o, S = dispatch_dgda_prefill(**inp, chunk_size=16)
+    assert o.dtype == torch.float32 and S.dtype == torch.float32 and o.shape == (1, 10, 2048, 64)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    err = max(float(np.abs(to_np(o) - eo).max()), float(np.abs(to_np(S) - eS).max()))
+    print(f"\nconfig 1 fp32: max abs error {err:.3e}", flush=True)
+    assert_close(o, eo, 1e-4, 1e-4, "config 1 out")
+    assert_close(S, eS, 1e-4, 1e-4, "config 1 state")
+
+
+@pytest.mark.parametrize("gates", ["scalar", "channel"])
+def test_growing_decay_contract_hip_vs_reference_backend(dev, gates):
+    """Decays above one (log_alpha = +0.05 on every seventh token), log_alpha alone: the hip
+    backend computes the token recurrence with the gates as given -- the reference's own
+    ``reference`` backend (``ref_dgda_prefill``, common.py:229-268), run here by torch on the
+    same GPU tensors in fp32 -- through the chunked path (per-token gates) and the sub-chunk
+    path (per-channel gates).  The reference's CPU algorithm clamps in-chunk decay ratios to
+    one and so differs for such gates (the ``cpu`` backend mirrors it; pinned in
+    test_cpu_dgda.py)."""
+    from maba_sparse.kernels.dispatcher import get_kernel
+    inp = dgda_inputs(2, 3, 700, seed=17, gates=gates, device=dev, with_state=True)
+    la = inp["log_alpha"][..., :1].clone() if gates == "scalar" else inp["log_alpha"].clone()
+    la[:, :, ::7] = 0.05
+    inp["log_alpha"] = la.expand(inp["log_alpha"].shape) if gates == "scalar" else la
+    o, S = _run(inp)
+    ref = get_kernel("reference", "dgda_prefill")
+    f32 = {k: (v.float() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    ro, rS = ref(**f32)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(ro, eo, 1e-4, 1e-4, "reference backend vs the float64 recurrence")
+    assert_close(o, to_np(ro), 2e-3, 2e-3, f"hip vs reference backend, {gates} gates")
+    assert_close(S, to_np(rS), 2e-3, 2e-3, f"hip vs reference backend state, {gates} gates")

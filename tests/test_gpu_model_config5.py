@@ -17,6 +17,24 @@
   the indexer's picks against oracle decode scores of the centroids it saw, and the fused
   decode against ``oracle.sparse_attn.maba_sa_decode`` with oracle-computed means
   (rtol = atol = 2e-3).
+
+At config 5's own size (B = 16, a 131,072-token prefill of uniform random ids):
+- the captured serving loop (16 tokens) against the eager ``LatentCache`` loop fed the same
+  tokens (both bf16; the 2,100-token test's bound and token rule);
+- prefill of the first 131,071 tokens, then one decode step, against the one-pass prefill's
+  last position.  That is an identity of the reference's semantics: the decode indexer
+  scores the causal prefill row of the last token (query block nb - 1, the zero-padded
+  tail centroid), and the three streams see the same keys.  A split at an arbitrary point
+  (say 65,536) is not one: a continued multi-token prefill scores the new chunk's keys only
+  (reference layers/indexer.py:83-97) and gathers those block numbers from the whole cache
+  (sparse_attention.py:263-266), so its sparse stream differs from a one-pass prefill's;
+- DGDA block 0's fused prefill (prologue in the kernels' staging) over the 131,072 tokens,
+  two heads against the C chunked oracle fed the one-pass prologue's outputs (2e-3);
+- MABA-SA block 3 over the 131,072-token prefill: rows of the causal prefill top-k against
+  oracle prefill scores of the layer's centroids (2,048 of them), rows of the fused prefill
+  in both forms (head space and latent) against the oracle's decode at that position (a
+  prefill row is the decode step of its prefix), and one decode step over the 131,073-row
+  cache against ``oracle.sparse_attn.maba_sa_decode`` with oracle means (2e-3).
 """
 import math
 
@@ -25,7 +43,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from _helpers import assert_close, to_np, topk_agrees
+from _helpers import assert_close, to_np, topk_agrees, topk_is_valid
 from oracle import dgda as odgda
 from oracle import indexer as oidx
 from oracle import sparse_attn as osa
@@ -74,18 +92,25 @@ def _check_tokens(toks, got, ref, min_sure):
     assert torch.equal(toks[sure], ref.argmax(-1)[sure])
 
 
-@pytest.mark.parametrize("graph", [True, False])
-def test_config5_serving_loop_matches_state_passing(model, graph):
-    """bf16 (config 5's dtype), through the captured device-resident step (graph) and the
-    eager LatentCache loop, against the same model's reference-style state passing run in
-    fp32 (the bf16-rounded weights, fed the serving loop's tokens).  The logits are bf16: one
-    ulp is about 0.4 % of their scale, and 20 bf16 blocks round every activation; the
-    measured error is flat over the steps (no drift) at 2-3.5 % of the scale."""
+@pytest.mark.parametrize("path", ["graph", "graph_plain", "eager"])
+def test_config5_serving_loop_matches_state_passing(model, path, monkeypatch):
+    """bf16 (config 5's dtype), through the captured device-resident step (``graph``: every
+    linear a HIP decode linear; ``graph_plain``: the same captured step with torch's GEMMs and
+    the separate norm and SwiGLU kernels, the form ``generate_greedy`` takes when a layer does
+    not fit the decode linear) and the eager LatentCache loop, against the same model's
+    reference-style state passing run in fp32 (the bf16-rounded weights, fed the serving
+    loop's tokens).  The logits are bf16: one ulp is about 0.4 % of their scale, and 20 bf16
+    blocks round every activation; the measured error is flat over the steps (no drift) at
+    2-3.5 % of the scale."""
     import copy
+    from maba_sparse.model import ServingStep
     dev = next(model.parameters()).device
     ids = torch.randint(0, model.config.vocab_size, (BATCH, 2100), generator=torch.Generator().manual_seed(1)).to(dev)
     steps = 60                                                        # positions 2100..2159 cross 2112
-    print(f"\nconfig 5 serving loop vs fp32 state passing: graph={graph}", flush=True)
+    graph = path != "eager"
+    if path == "graph_plain":
+        monkeypatch.setattr(ServingStep, "decode_linear", False)
+    print(f"\nconfig 5 serving loop vs fp32 state passing: {path}", flush=True)
     with torch.no_grad():
         toks, got = model.generate_greedy(ids, steps, return_logits=True, graph=graph)
         ref_model = copy.deepcopy(model).float()
@@ -191,3 +216,177 @@ def test_config5_maba_sa_block_oracle(model):
                              pool=layer.hca_pool_size)
     assert_close(out, exp, 2e-3, 2e-3, "MABA-SA block decode")
     assert math.isfinite(float(out.abs().max()))
+
+
+# ----------------------------------------------------------------------------- full size
+FULL = 131_072
+
+
+@pytest.fixture(scope="module")
+def full_ids(model):
+    dev = next(model.parameters()).device
+    return torch.randint(0, model.config.vocab_size, (BATCH, FULL),
+                         generator=torch.Generator().manual_seed(131)).to(dev)
+
+
+def test_config5_full_serving_graph_vs_eager_loop(model, full_ids):
+    """B=16 after the 131,072-token prefill: 16 tokens of the captured serving loop against
+    the eager ``LatentCache`` loop (``MabaBlock.decode``, torch GEMMs, the ``maba_sa_decode``
+    op) fed the serving loop's tokens.  Logits within 5e-2 of the scale with no growth over
+    the steps, equal tokens wherever a step's top-2 gap exceeds twice that step's difference."""
+    from maba_sparse.layers import LatentCache
+    steps = 16
+    print(f"\nconfig 5 full: graph serving loop, B={BATCH} prefill={FULL} steps={steps}", flush=True)
+    with torch.no_grad():
+        toks, got = model.generate_greedy(full_ids, steps, return_logits=True, graph=True)
+        print("config 5 full: eager LatentCache loop", flush=True)
+        logits, states = model(full_ids, last_only=True)
+        caches = []
+        for layer, (_, _, c_kv) in zip(model.layers, states):
+            cache = None
+            if layer.is_attention:
+                cache = LatentCache(BATCH, FULL + steps, model.config.d_c, pool=model.config.hca_pool_size,
+                                    device=full_ids.device, dtype=c_kv.dtype)
+                cache.append(c_kv)
+            caches.append(cache)
+        ref = [logits[:, -1]]
+        for t in range(steps - 1):
+            x = model.embeddings(toks[:, t:t + 1])
+            for i, layer in enumerate(model.layers):
+                st, cv, _ = states[i]
+                x, nst, ncv = layer.decode(x, state=st, conv_state=cv, cache=caches[i])
+                states[i] = (nst, ncv, None)
+            ref.append(model._logits(x)[:, -1])
+        del caches, states
+    ref = torch.stack(ref, dim=1).float().cpu()
+    got = got.float().cpu()
+    scale = ref.abs().max().item()
+    per_step = (got - ref).abs().amax(dim=(0, 2)) / scale
+    print("per-step error / scale:", [round(x, 4) for x in per_step.tolist()], flush=True)
+    assert per_step[0] <= 1e-3, "the two prefills differ"          # the same prefill, run twice
+    assert per_step.max() <= 5e-2, f"graph and eager loops differ by {per_step.max():.3e} of the scale"
+    assert per_step[-5:].mean() <= 1.5 * per_step[1:6].mean() + 1e-3, "the difference grows over the steps"
+    _check_tokens(toks.cpu(), got, ref, 0.2)
+
+
+def test_config5_full_prefill_then_step_equals_one_pass(model, full_ids):
+    """forward(ids[:, :L-1]) then step(ids[:, L-1]) against forward(ids) at L = 131,072: the
+    decode path's last-position logits (DGDA step from the prefill's state, the decode
+    indexer over the cached keys with the tail centroid, the fused decode streams) equal the
+    prefill's, within the 2,100-token test's bound and token rule."""
+    print(f"\nconfig 5 full: one-pass prefill vs prefill {FULL - 1} + step", flush=True)
+    with torch.no_grad():
+        whole, _ = model(full_ids, last_only=True)
+        head, states = model(full_ids[:, :-1], last_only=True)
+        del head
+        lg, _ = model.step(full_ids[:, -1:], past_states=states)
+        del states
+    a = lg[:, -1].float().cpu()
+    e = whole[:, -1].float().cpu()
+    scale = e.abs().max().item()
+    err = (a - e).abs().max().item()
+    print(f"prefill+step vs one pass: {err / scale:.4f} of the scale", flush=True)
+    assert err <= 5e-2 * scale, f"prefill + step differs from one pass by {err / scale:.3e} of the scale"
+    # one position per sequence: at least two of the 16 must separate (3 do on the boxes measured)
+    _check_tokens(a.argmax(-1)[:, None], a[:, None], e[:, None], 2 / BATCH)
+
+
+def test_config5_full_dgda_block0_vs_c_oracle(model, full_ids):
+    """Block 0's fused prefill over the 131,072 tokens (the prologue in the recurrence kernels'
+    staging, per-channel gates, the sub-chunk path with its segment passes): two heads whose
+    first sub-chunk falls inside a slot, against the C chunked oracle fed the one-pass
+    prologue kernel's outputs (rtol = atol = 2e-3 on the bf16 output and the fp32 state)."""
+    from maba_sparse.kernels import hip_backend as hb
+    from oracle import dgda_c
+    layer = model.layers[0].mixer
+    H = layer.n_heads
+    print(f"\nconfig 5 full: DGDA block 0, T={FULL}", flush=True)
+    with torch.no_grad():
+        x = _block_input(model, full_ids, 0)
+        projs, _ = layer._projections(x, (None, None, None))
+        convs = (layer.conv_q.weight, layer.conv_k.weight, layer.conv_v.weight)
+        o, S, _ = hb.hip_dgda_layer_prefill(projs, convs, None, eps=layer.eps, state_dtype=torch.float32)
+        args, _, _ = layer._fused_op_inputs(x, None, (None, None, None))
+        del x, projs
+    heads = [(0, 1), (BATCH - 1, 3)]
+    f = lambda t: np.ascontiguousarray(t.float().cpu().numpy())  # noqa: E731
+    sel = lambda t: torch.stack([t[b, h] for b, h in heads])[None]  # noqa: E731   [1, 2, T, 64]
+    eo, eS = dgda_c.dgda_prefill_chunked_c(f(sel(args["q"])), f(sel(args["k"])), f(sel(args["v"])),
+                                           f(sel(args["log_alpha"])), f(sel(args["b"])), f(sel(args["w"])),
+                                           chunk_size=64)
+    for n, (b, h) in enumerate(heads):
+        got = o[b, :, 64 * h: 64 * (h + 1)]
+        assert_close(got, eo[0, n], 2e-3, 2e-3, f"block 0 out (b={b}, h={h})")
+        assert_close(S[b, h], eS[0, n], 2e-3, 2e-3, f"block 0 state (b={b}, h={h})")
+
+
+def test_config5_full_maba_sa_block3_vs_oracle(model, full_ids):
+    """MABA-SA block 3 over the 131,072-token prefill, against the oracle:
+    - prefill top-k rows (2,048 centroids; first block, block edges, deep rows) against
+      oracle prefill scores of the layer's centroids: selections bit-exact where the score gap
+      exceeds 1e-4, a valid top-32 up to 1e-4 on every row;
+    - the fused prefill in both forms at the same rows against the oracle's decode at that
+      position with oracle means (rtol = atol = 2e-3);
+    - one decode step over the 131,073-row cache against the oracle decode (2e-3)."""
+    from maba_sparse.kernels.dispatcher import dispatch_maba_sa_decode
+    from maba_sparse.layers import LatentCache
+    dev = full_ids.device
+    blk = 3
+    layer = model.layers[blk].mixer
+    H, dh, K = layer.n_heads, layer.d_head, layer.top_k
+    print(f"\nconfig 5 full: MABA-SA block {blk}, L={FULL}", flush=True)
+    with torch.no_grad():
+        h = _block_input(model, full_ids, blk)
+        layer.reset_cache()
+        c_kv = layer.kv_down_proj(h)
+        qi = layer.indexer.q_idx_proj(h)
+        idx, cent = layer.indexer(h, return_scores=False)
+        q = layer.q_proj(h).view(BATCH, FULL, H, dh).transpose(1, 2)
+        gl = layer.stream_gate(h)
+        forms = {"heads": layer._fused_prefill_heads(h, q, c_kv, idx),
+                 "latent": layer._fused_prefill_latent(h, q, c_kv, idx)}
+        torch.cuda.synchronize()
+    assert idx.shape == (BATCH, FULL, K) and cent.shape[1] == FULL // 64
+    print(f"config 5 full: prefill forms done ({layer._prefill_form(idx)} auto)", flush=True)
+    Wk, Wv = to_np(layer.k_up_proj.weight), to_np(layer.v_up_proj.weight)
+    rows = [0, 62, 63, 64, 2047, 4096 + 17, 65535, FULL - 1]
+    for b in (0, BATCH - 1):
+        sc = oidx.prefill_scores(to_np(qi[b:b + 1, rows]), to_np(cent[b:b + 1]), layer.dist_lambda,
+                                 positions=rows)
+        got_idx = idx[b:b + 1, rows].cpu().numpy()
+        topk_agrees(got_idx, sc, K)
+        topk_is_valid(got_idx, np.where(np.isfinite(sc), sc, -1e30))
+        for t in rows:
+            exp = osa.maba_sa_decode(to_np(q[b:b + 1, :, t]), to_np(c_kv[b:b + 1, : t + 1]), Wk, Wv,
+                                     idx[b:b + 1, t:t + 1].cpu().numpy(), to_np(gl[b:b + 1, t]), L=t + 1,
+                                     window=layer.window_size, n_sink=layer.n_sink_tokens,
+                                     block_size=layer.block_size, pool=layer.hca_pool_size)
+            for name, o in forms.items():
+                assert_close(o[b, :, t][None], exp, 2e-3, 2e-3, f"prefill {name} row (b={b}, t={t})")
+    del forms, q, qi
+    print("config 5 full: decode step over the prefill cache", flush=True)
+    x_tok = torch.randn(BATCH, 1, model.config.dim, generator=torch.Generator().manual_seed(6)).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        _, c_full = layer(h)                                   # seeds the indexer caches
+        cache = LatentCache(BATCH, FULL + 8, layer.d_c, pool=64, device=dev, dtype=torch.bfloat16)
+        cache.append(c_full)
+        del c_full, h
+        qt, c_new, qit, kit, glt = layer._token_projections(x_tok)
+        cache.append(c_new)
+        idt, cent_t = layer.indexer.forward_projected(qit, kit)
+        L = cache.n
+        q_lat = torch.einsum("bhd,hdc->bhc", qt.reshape(BATCH, H, dh).float(),
+                             layer._f32_heads(layer.k_up_proj, "_wk_f32"))
+        z = dispatch_maba_sa_decode(q_lat, cache.c, cache.hca[:, : cache.nh], idt, glt.view(-1, 3), L=L,
+                                    scale=layer.scale, window=layer.window_size, n_sink=layer.n_sink_tokens,
+                                    block_size=layer.block_size, pool=layer.hca_pool_size)
+        out = torch.einsum("bhc,hdc->bhd", z, layer._f32_heads(layer.v_up_proj, "_wv_f32"))
+    assert L == FULL + 1 and cent_t.shape[1] == (L + 63) // 64
+    ref_sc = oidx.decode_scores(to_np(qit), to_np(cent_t), layer.dist_lambda)
+    assert topk_agrees(idt.cpu().numpy(), ref_sc, K) >= BATCH - 2
+    for b in (0, 7, BATCH - 1):
+        exp = osa.maba_sa_decode(to_np(qt.reshape(BATCH, H, dh)[b:b + 1]), to_np(cache.c[b:b + 1, :L]), Wk, Wv,
+                                 idt[b:b + 1].cpu().numpy(), to_np(glt.view(-1, 3)[b:b + 1]), L=L,
+                                 window=layer.window_size, n_sink=layer.n_sink_tokens, block_size=layer.block_size,
+                                 pool=layer.hca_pool_size)
+        assert_close(out[b:b + 1], exp, 2e-3, 2e-3, f"MABA-SA decode at L={L} (b={b})")

@@ -448,6 +448,28 @@ def test_decode_linear_rejects(dev):
     with pytest.raises(Exception, match="16-byte aligned"):
         buf = torch.randn(4, 648, device=dev).to(bf)
         hb.hip_decode_linear(buf[:, 1:641], w)
+    # the output may not overlap the residual input or the residual written in the same launch
+    mo, xo = a.clone(), torch.empty_like(a)
+    with pytest.raises(Exception, match="y may not overlap mo or x_out"):
+        hb.hip_decode_linear(a, w, norm_w=nw, mo=mo, gate=nw, x_out=xo, out=mo[..., :64])
+    with pytest.raises(Exception, match="y may not overlap mo or x_out"):
+        hb.hip_decode_linear(a, w, norm_w=nw, mo=mo, gate=nw, x_out=xo, out=xo[..., 64:128])
+
+
+def test_rmsnorm_and_cache_append_reject_empty_axes(dev):
+    """An empty channel axis for the norm, and an absorbed-query buffer with no heads for the
+    fused append, are argument errors raised before anything launches."""
+    hb = _hb()
+    bf = torch.bfloat16
+    with pytest.raises(ValueError, match="at least 2 channels"):
+        hb.hip_rmsnorm(torch.empty(3, 0, device=dev, dtype=bf), torch.empty(0, device=dev, dtype=bf), 1e-6)
+    B, cap, dc, di = 2, 128, 128, 64
+    z = lambda *s: torch.zeros(*s, device=dev, dtype=bf)  # noqa: E731
+    pos = torch.tensor([5, 6], dtype=torch.long, device=dev)
+    with pytest.raises(ValueError, match="q_lat"):
+        hb.hip_cache_append_heads(z(B, dc), z(B, di), pos[0], z(B, cap, dc), z(B, cap, di), z(B, cap // 64, dc),
+                                  z(B, cap // 64, di), z(B, 640), z(640, dc), z(B, 3), z(3),
+                                  torch.empty(B, 0, dc, device=dev), z(B, 3))
 
 
 def test_decode_linear_gather(dev):

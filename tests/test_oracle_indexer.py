@@ -131,3 +131,17 @@ def test_decode_tail_centroid():
 def test_top_gap():
     assert oidx.top_gap([5.0, 1.0, 3.0, 2.0], 2) == 1.0
     assert oidx.top_gap([1.0, 2.0], 2) == np.inf
+
+
+def test_prefill_scores_at_chosen_positions():
+    """Rows scored at given positions equal those rows of the full causal matrix, including
+    a row in the first block (one live centroid) and rows on block edges."""
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((2, 300, 16))
+    c = rng.standard_normal((2, 5, 16))
+    full = oidx.prefill_scores(q, c, 0.3, block_size=64)
+    rows = np.array([0, 63, 64, 130, 255, 256, 299])
+    part = oidx.prefill_scores(q[:, rows], c, 0.3, block_size=64, positions=rows)
+    assert np.array_equal(np.isinf(part), np.isinf(full[:, rows]))
+    fin = np.isfinite(part)
+    assert np.allclose(part[fin], full[:, rows][fin], rtol=0, atol=1e-12)
