@@ -10,6 +10,8 @@
 // each thread owns one column c and a contiguous run of rows, keeps its slice
 // of S' in registers between the two reductions, and writes S_new once.  The
 // kernel is HBM-bound on the state read + write (8*dk*dv bytes per head).
+#include <initializer_list>
+
 #include "dgda_common.h"
 
 namespace maba {
@@ -104,34 +106,45 @@ struct StepFast {
   const float* gate; int64_t gsb, gsh, gsd;   // log_alpha (use_log) or alpha
   const float* bb; int64_t bsb, bsh, bsd;
   const float* ww; int64_t wsb, wsh, wsd;
-  const void* state; int64_t ssb, ssh, ssr;   // may be null (zero state); fp32 or bf16 (TS)
-  void* nst; int64_t nsb, nsh, nsr;           // same dtype as the state; may alias it
+  const void* state; int64_t ssb, ssh; int ssr32;   // may be null (zero state); fp32 or bf16 (TS)
+  void* nst; int64_t nsb, nsh; int nsr32;           // same dtype as the state; may alias it
   void* out; int odt; int64_t osb, osh, osd;
   int64_t BH;
   int H, use_log;
 };
 
-template <typename T>
-__device__ __forceinline__ float ldf(const void* p, int64_t i);
-template <>
-__device__ __forceinline__ float ldf<float>(const void* p, int64_t i) { return ((const float*)p)[i]; }
-template <>
-__device__ __forceinline__ float ldf<uint16_t>(const void* p, int64_t i) {
-  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
-}
-
 __device__ __forceinline__ float bcast(float x, int r) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), r));
 }
 
+template <typename T>
+__device__ __forceinline__ float cvt(T x);
+template <>
+__device__ __forceinline__ float cvt<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ float cvt<uint16_t>(uint16_t x) { return bf16_bits_to_f32(x); }
+
+// Row offset i of a state slab: rows 64 elements apart (CONTIG, the layout every caller
+// uses: one base address and immediate offsets) or a run-time 32-bit row stride.
+template <bool CONTIG>
+__device__ __forceinline__ int64_t row_at(int i, int rs) { return CONTIG ? (int64_t)(64 * i) : (int64_t)i * rs; }
+
+// The 16 rows of wave w's slab, S[16w + i][lane], from sp = &S[16w][lane] (rs: row stride),
+// as stored (converted by the caller once every load of the step is issued).
+template <typename TS, bool CONTIG>
+__device__ __forceinline__ void load_rows(TS (&s)[16], const TS* sp, int rs) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = sp[row_at<CONTIG>(i, rs)];
+}
+
 // The step on the rows of wave w (lane = column): s[i] holds S[16w + i][lane] on entry;
 // al, bk, kr, qr are the row scalars of row `lane`, vw = w_lane v_lane.  Writes the new state
-// rows (N: element offset of S_new[0][lane], nsr its row stride) and, from wave 0, o[lane].
+// rows through np = &S_new[16w][lane] (row stride nrs) and returns o[lane] (every wave).
 // Every state load of the caller precedes the first store, so S_new may alias S.
-template <typename TS>
+template <typename TS, bool CONTIG>
 __device__ __forceinline__ float step_rows(float (&s)[16], float al, float bk, float kr, float qr, float vw,
-                                           void* nst, int64_t N, int64_t nsr, float (*s_red)[64]) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+                                           TS* np, int nrs, float (*s_red)[64]) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   float pred = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -148,8 +161,8 @@ __device__ __forceinline__ float step_rows(float (&s)[16], float al, float bk, f
   for (int i = 0; i < 16; ++i) {
     const int r = 16 * wave + i;
     const float sn = fmaf(bcast(kr, r), delta, s[i]);
-    if constexpr (sizeof(TS) == 4) ((float*)nst)[N + r * nsr] = sn;
-    else ((uint16_t*)nst)[N + r * nsr] = f32_to_bf16_bits(sn);
+    if constexpr (sizeof(TS) == 4) np[row_at<CONTIG>(i, nrs)] = sn;
+    else np[row_at<CONTIG>(i, nrs)] = f32_to_bf16_bits(sn);
     o = fmaf(bcast(qr, r), sn, o);   // the fp32 state before its rounding, as the generic kernel
   }
   __syncthreads();   // every wave has read s_red before it is reused
@@ -158,31 +171,40 @@ __device__ __forceinline__ float step_rows(float (&s)[16], float al, float bk, f
   return (s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane]);
 }
 
-// T: dtype of q, k, v; TS: dtype of the state in and out (fp32 or bf16).
-template <typename T, typename TS>
+// T: dtype of q, k, v; TS: dtype of the state in and out (fp32 or bf16); HS: a state is
+// given (else zeros); CONTIG: state rows 64 elements apart in and out.  The slab and the row
+// scalars are all loaded before the first wait, so the step waits for one memory round trip
+// (a run-time null test around the slab loads, or 64-bit strided addresses per row, made the
+// compiler wait for the slab before it issued the scalars).
+template <typename T, typename TS, bool HS, bool CONTIG>
 __global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
   __shared__ float s_red[4][64];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t bh = blockIdx.x;
-  const int64_t bi = bh / a.H, hi = bh % a.H;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t bi = blockIdx.y, hi = blockIdx.x;   // grid (H, B): no division
+  TS raw[16];
+  if constexpr (HS)
+    load_rows<TS, CONTIG>(raw, (const TS*)a.state + (bi * a.ssb + hi * a.ssh + row_at<CONTIG>(16 * wave, a.ssr32) + lane),
+                          a.ssr32);
+  // lane r holds the row-r scalars; lane c holds w_c v_c.  The (b, h) base is scalar and the
+  // lane's offset a 32-bit unsigned product (the host checks that 63 * stride fits)
+  const uint32_t l = lane;
+  const T kx = ((const T*)a.k + (bi * a.ksb + hi * a.ksh))[l * (uint32_t)a.ksd];
+  const T qx = ((const T*)a.q + (bi * a.qsb + hi * a.qsh))[l * (uint32_t)a.qsd];
+  const T vx = ((const T*)a.v + (bi * a.vsb + hi * a.vsh))[l * (uint32_t)a.vsd];
+  const float gr = (a.gate + (bi * a.gsb + hi * a.gsh))[l * (uint32_t)a.gsd];
+  const float br = (a.bb + (bi * a.bsb + hi * a.bsh))[l * (uint32_t)a.bsd];
+  const float wc = (a.ww + (bi * a.wsb + hi * a.wsh))[l * (uint32_t)a.wsd];
+  // every load above is issued before the first use waits (with 16-bit state rows the compiler
+  // otherwise converts the first rows, and waits for them, before issuing the rest; with fp32
+  // rows it issues them all and overlaps the first reduction with their arrival)
+  if constexpr (sizeof(TS) == 2) __builtin_amdgcn_sched_barrier(0);
   float s[16];
-  if (a.state) {
-    const int64_t S = bi * a.ssb + hi * a.ssh + lane;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = ldf<TS>(a.state, S + (16 * wave + i) * a.ssr);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
-  }
-  // lane r holds the row-r scalars; lane c holds w_c v_c
-  const float kr = ldf<T>(a.k, bi * a.ksb + hi * a.ksh + lane * a.ksd);
-  const float qr = ldf<T>(a.q, bi * a.qsb + hi * a.qsh + lane * a.qsd);
-  const float vc = ldf<T>(a.v, bi * a.vsb + hi * a.vsh + lane * a.vsd);
-  const float gr = a.gate[bi * a.gsb + hi * a.gsh + lane * a.gsd];
-  const float br = a.bb[bi * a.bsb + hi * a.bsh + lane * a.bsd];
-  const float wc = a.ww[bi * a.wsb + hi * a.wsh + lane * a.wsd];
+  for (int i = 0; i < 16; ++i) s[i] = HS ? cvt<TS>(raw[i]) : 0.f;
+  const float kr = cvt<T>(kx), qr = cvt<T>(qx), vc = cvt<T>(vx);
   const float al = a.use_log ? __expf(gr) : gr;
-  const float o = step_rows<TS>(s, al, br * kr, kr, qr, wc * vc, a.nst, bi * a.nsb + hi * a.nsh + lane, a.nsr, s_red);
+  TS* np = (TS*)a.nst + (bi * a.nsb + hi * a.nsh + row_at<CONTIG>(16 * wave, a.nsr32) + lane);
+  const float o = step_rows<TS, CONTIG>(s, al, br * kr, kr, qr, wc * vc, np, a.nsr32, s_red);
   if (wave == 0) store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
 }
 
@@ -199,47 +221,57 @@ struct LayerStepArgs {
   const void* cw[3]; int cwdt; int64_t cwsc[3], cwst[3];      // conv taps [C, 1, 4]
   const uint16_t* hist[3]; int64_t hsb[3], hsc[3], hst[3];    // bf16 [B, C, 3] or null (zeros)
   uint16_t* nh[3]; int64_t nhsb[3], nhsc[3], nhst[3];         // bf16 new history (may alias hist)
-  const void* state; int64_t ssb, ssh, ssr;                   // [B, H, 64, 64] (TS) or null (zero)
-  void* nst; int64_t nsb, nsh, nsr;                           // may alias state
+  const void* state; int64_t ssb, ssh; int ssr32;             // [B, H, 64, 64] (TS) or null (zero)
+  void* nst; int64_t nsb, nsh; int nsr32;                     // may alias state
   void* out; int odt; int64_t osb, osh, osd;                  // o [B, H, 64]
   int64_t BH;
   int H;
   float eps;
 };
 
-// TW: dtype of the conv taps; HS / HH: a state / a history is given (else zeros).  The
+// TW: dtype of the conv taps; HS / HH: a state / a history is given (else zeros); CONTIG:
+// state rows 64 elements apart (see dgda_step_wave_kernel).  The
 // dtype and the presence of each input are compile-time, so the wave issues every load
 // (state column, projections, taps, history) before it waits for the first: with a
 // run-time dtype switch or a null test around a load, the compiler converts or merges
 // each loaded value inside its branch and waits for that load alone, one memory round
 // trip per tap.
-template <typename TS, typename TW, bool HS, bool HH>
+template <typename TS, typename TW, bool HS, bool HH, bool CONTIG>
 __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
   __shared__ float s_red[4][64];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t bh = blockIdx.x;
-  const int64_t bi = bh / a.H, hi = bh % a.H;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t bi = blockIdx.y, hi = blockIdx.x;   // grid (H, B): no division
   const int64_t c = hi * 64 + lane;   // channel of the projection rows
-  float s[16];
-  if constexpr (HS) {
-    const int64_t S = bi * a.ssb + hi * a.ssh + lane;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = ldf<TS>(a.state, S + (16 * wave + i) * a.ssr);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
-  }
+  TS raw[16];
+  if constexpr (HS)
+    load_rows<TS, CONTIG>(raw, (const TS*)a.state + (bi * a.ssb + hi * a.ssh + row_at<CONTIG>(16 * wave, a.ssr32) + lane),
+                          a.ssr32);
   // ---- prologue (as dgda_prologue_step_kernel); every wave forms all 64 channels
-  float x[6], w[3][4], h[3][3];
+  uint16_t xr[6], hr[3][3];
+  TW wr[3][4];
 #pragma unroll
-  for (int st = 0; st < 6; ++st) x[st] = bf16_bits_to_f32(a.x[st][bi * a.xsb[st] + c]);
+  for (int st = 0; st < 6; ++st) xr[st] = a.x[st][bi * a.xsb[st] + c];
 #pragma unroll
   for (int st = 0; st < 3; ++st) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[st][j] = ldf<TW>(a.cw[st], c * a.cwsc[st] + j * a.cwst[st]);
+    for (int j = 0; j < 4; ++j) wr[st][j] = ((const TW*)a.cw[st])[c * a.cwsc[st] + j * a.cwst[st]];
+    if constexpr (HH) {
 #pragma unroll
-    for (int j = 0; j < 3; ++j)
-      h[st][j] = HH ? bf16_bits_to_f32(a.hist[st][bi * a.hsb[st] + c * a.hsc[st] + j * a.hst[st]]) : 0.f;
+      for (int j = 0; j < 3; ++j) hr[st][j] = a.hist[st][bi * a.hsb[st] + c * a.hsc[st] + j * a.hst[st]];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the first use waits
+  float s[16], x[6], w[3][4], h[3][3];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = HS ? cvt<TS>(raw[i]) : 0.f;
+#pragma unroll
+  for (int st = 0; st < 6; ++st) x[st] = bf16_bits_to_f32(xr[st]);
+#pragma unroll
+  for (int st = 0; st < 3; ++st) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[st][j] = cvt<TW>(wr[st][j]);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) h[st][j] = HH ? bf16_bits_to_f32(hr[st][j]) : 0.f;
   }
   float y[3];
 #pragma unroll
@@ -266,7 +298,8 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
   // overwrites it (in place) after the barriers below.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   const float al = __expf(gr);
-  const float o = step_rows<TS>(s, al, br * kr, kr, qr, wc * vc, a.nst, bi * a.nsb + hi * a.nsh + lane, a.nsr, s_red);
+  TS* np = (TS*)a.nst + (bi * a.nsb + hi * a.nsh + row_at<CONTIG>(16 * wave, a.nsr32) + lane);
+  const float o = step_rows<TS, CONTIG>(s, al, br * kr, kr, qr, wc * vc, np, a.nsr32, s_red);
   if (wave == 0) {
 #pragma unroll
     for (int st = 0; st < 3; ++st) {   // new history: the inputs of tokens -2, -1, 0
@@ -282,6 +315,14 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
 }  // namespace maba
 
 using namespace maba;
+
+// The fast kernel's per-lane offsets of the [B,H,64] operands are 32-bit unsigned products
+// lane * stride (at most 63 * stride elements of up to 4 bytes).
+static bool lane_strides_fit(std::initializer_list<const maba_tensor*> ts) {
+  for (const maba_tensor* t : ts)
+    if (t->stride[2] < 0 || t->stride[2] > ((int64_t)1 << 24)) return false;
+  return true;
+}
 
 extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                                   const maba_tensor* alpha, const maba_tensor* log_alpha,
@@ -331,7 +372,8 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
   const int sdt = new_state->dtype;
   const bool fast = dk == 64 && dv == 64 && qkv_same && gate->dtype == MABA_F32 && b->dtype == MABA_F32 &&
                     w->dtype == MABA_F32 && (sdt == MABA_F32 || sdt == MABA_BF16) && new_state->stride[3] == 1 &&
-                    (!state || (state->dtype == sdt && state->stride[3] == 1));
+                    new_state->stride[2] <= INT32_MAX && B <= 65535 && lane_strides_fit({q, k, v, gate, b, w}) &&
+                    (!state || (state->dtype == sdt && state->stride[3] == 1 && state->stride[2] <= INT32_MAX));
   if (fast) {
     StepFast f;
     f.q = q->data; f.qsb = q->stride[0]; f.qsh = q->stride[1]; f.qsd = q->stride[2];
@@ -341,17 +383,22 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
     f.bb = (const float*)b->data; f.bsb = b->stride[0]; f.bsh = b->stride[1]; f.bsd = b->stride[2];
     f.ww = (const float*)w->data; f.wsb = w->stride[0]; f.wsh = w->stride[1]; f.wsd = w->stride[2];
     f.state = state ? state->data : nullptr;
-    f.ssb = state ? state->stride[0] : 0; f.ssh = state ? state->stride[1] : 0; f.ssr = state ? state->stride[2] : 0;
+    f.ssb = state ? state->stride[0] : 0; f.ssh = state ? state->stride[1] : 0;
+    f.ssr32 = state ? (int)state->stride[2] : 64;
     f.nst = new_state->data; f.nsb = new_state->stride[0]; f.nsh = new_state->stride[1];
-    f.nsr = new_state->stride[2];
+    f.nsr32 = (int)new_state->stride[2];
     f.out = out->data; f.odt = out->dtype; f.osb = out->stride[0]; f.osh = out->stride[1]; f.osd = out->stride[2];
     f.BH = B * H; f.H = (int)H; f.use_log = log_alpha != nullptr;
-    const dim3 g4((unsigned)(B * H));   // one workgroup per (b, h)
-    const bool sbf = sdt == MABA_BF16;
-    if (q->dtype == MABA_BF16 && sbf) hipLaunchKernelGGL((dgda_step_wave_kernel<uint16_t, uint16_t>), g4, dim3(256), 0, s, f);
-    else if (q->dtype == MABA_BF16) hipLaunchKernelGGL((dgda_step_wave_kernel<uint16_t, float>), g4, dim3(256), 0, s, f);
-    else if (sbf) hipLaunchKernelGGL((dgda_step_wave_kernel<float, uint16_t>), g4, dim3(256), 0, s, f);
-    else hipLaunchKernelGGL((dgda_step_wave_kernel<float, float>), g4, dim3(256), 0, s, f);
+    const dim3 g4((unsigned)H, (unsigned)B);   // one workgroup per (b, h)
+    const bool sbf = sdt == MABA_BF16, hs = state != nullptr, contig = f.ssr32 == 64 && f.nsr32 == 64;
+    void (*kern)(StepFast) = nullptr;
+#define MABA_STEP_PICK(T, TS)                                                                          \
+  kern = hs ? (contig ? dgda_step_wave_kernel<T, TS, true, true> : dgda_step_wave_kernel<T, TS, true, false>) \
+            : (contig ? dgda_step_wave_kernel<T, TS, false, true> : dgda_step_wave_kernel<T, TS, false, false>)
+    if (q->dtype == MABA_BF16) { if (sbf) MABA_STEP_PICK(uint16_t, uint16_t); else MABA_STEP_PICK(uint16_t, float); }
+    else { if (sbf) MABA_STEP_PICK(float, uint16_t); else MABA_STEP_PICK(float, float); }
+#undef MABA_STEP_PICK
+    hipLaunchKernelGGL(kern, g4, dim3(256), 0, s, f);
     return check_launch("dgda_step");
   }
   dim3 grid((unsigned)(B * H)), block(256);
@@ -371,7 +418,7 @@ extern "C" int maba_hip_dgda_layer_step(const maba_tensor* const* xs, const maba
   if (out->ndim != 3 || out->shape[2] != 64)
     return fail(MABA_ERR_UNSUPPORTED, "%s: out must be [B,H,64] (64-channel heads)", who);
   const int64_t B = out->shape[0], H = out->shape[1], C = 64 * H;
-  if (H < 1 || H > 16) return fail(MABA_ERR_UNSUPPORTED, "%s: 1 <= H <= 16", who);
+  if (H < 1 || H > 16 || B > 65535) return fail(MABA_ERR_UNSUPPORTED, "%s: 1 <= H <= 16 and B <= 65535", who);
   if (out->dtype != MABA_F32 && out->dtype != MABA_BF16) return fail(MABA_ERR_DTYPE, "%s: out f32 or bf16", who);
   LayerStepArgs a;
   for (int st = 0; st < 6; ++st) {   // [B, C] or [B, 1, C] bf16 rows with unit channel stride
@@ -404,27 +451,31 @@ extern "C" int maba_hip_dgda_layer_step(const maba_tensor* const* xs, const maba
   const int nhist = (int)(a.hist[0] != nullptr) + (a.hist[1] != nullptr) + (a.hist[2] != nullptr);
   if (nhist != 0 && nhist != 3) return fail(MABA_ERR_INVALID, "%s: give all three histories or none", who);
   const int64_t ss4[4] = {B, H, 64, 64};
-  if (!expect_shape(new_state, "new_state", 4, ss4) || new_state->stride[3] != 1 ||
+  if (!expect_shape(new_state, "new_state", 4, ss4) || new_state->stride[3] != 1 || new_state->stride[2] > INT32_MAX ||
       (new_state->dtype != MABA_F32 && new_state->dtype != MABA_BF16))
     return fail(MABA_ERR_INVALID, "%s: new_state must be f32/bf16 [B,H,64,64] with unit column stride", who);
-  if (state && (!expect_shape(state, "state", 4, ss4) || state->stride[3] != 1 || state->dtype != new_state->dtype))
+  if (state && (!expect_shape(state, "state", 4, ss4) || state->stride[3] != 1 || state->stride[2] > INT32_MAX ||
+                state->dtype != new_state->dtype))
     return fail(MABA_ERR_INVALID, "%s: state must match new_state", who);
   a.state = state ? state->data : nullptr;
-  a.ssb = state ? state->stride[0] : 0; a.ssh = state ? state->stride[1] : 0; a.ssr = state ? state->stride[2] : 0;
-  a.nst = new_state->data; a.nsb = new_state->stride[0]; a.nsh = new_state->stride[1]; a.nsr = new_state->stride[2];
+  a.ssb = state ? state->stride[0] : 0; a.ssh = state ? state->stride[1] : 0; a.ssr32 = state ? (int)state->stride[2] : 64;
+  a.nst = new_state->data; a.nsb = new_state->stride[0]; a.nsh = new_state->stride[1]; a.nsr32 = (int)new_state->stride[2];
   a.out = out->data; a.odt = out->dtype; a.osb = out->stride[0]; a.osh = out->stride[1]; a.osd = out->stride[2];
   a.BH = B * H; a.H = (int)H; a.eps = eps;
   if (B == 0) return MABA_OK;
-  const dim3 g4((unsigned)(B * H));   // one workgroup per (b, h)
+  const dim3 g4((unsigned)H, (unsigned)B);   // one workgroup per (b, h)
   hipStream_t s = (hipStream_t)stream;
   const bool sb = new_state->dtype == MABA_BF16, wb = a.cwdt == MABA_BF16, hs = a.state != nullptr, hh = nhist == 3;
+  const bool contig = a.ssr32 == 64 && a.nsr32 == 64;
   void (*k)(LayerStepArgs) = nullptr;
-#define MABA_LS_PICK(TS, TW)                                                                  \
-  k = hs ? (hh ? dgda_layer_step_kernel<TS, TW, true, true> : dgda_layer_step_kernel<TS, TW, true, false>) \
-         : (hh ? dgda_layer_step_kernel<TS, TW, false, true> : dgda_layer_step_kernel<TS, TW, false, false>)
+#define MABA_LS_PICK2(TS, TW, C)                                                                \
+  k = hs ? (hh ? dgda_layer_step_kernel<TS, TW, true, true, C> : dgda_layer_step_kernel<TS, TW, true, false, C>) \
+         : (hh ? dgda_layer_step_kernel<TS, TW, false, true, C> : dgda_layer_step_kernel<TS, TW, false, false, C>)
+#define MABA_LS_PICK(TS, TW) do { if (contig) MABA_LS_PICK2(TS, TW, true); else MABA_LS_PICK2(TS, TW, false); } while (0)
   if (sb) { if (wb) MABA_LS_PICK(uint16_t, uint16_t); else MABA_LS_PICK(uint16_t, float); }
   else { if (wb) MABA_LS_PICK(float, uint16_t); else MABA_LS_PICK(float, float); }
 #undef MABA_LS_PICK
+#undef MABA_LS_PICK2
   hipLaunchKernelGGL(k, g4, dim3(256), 0, s, a);
   return check_launch(who);
 }
