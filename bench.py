@@ -239,18 +239,14 @@ def cpu_anchor_config1(min_seconds: float = 5.0):
 def cpu_row_baselines(min_seconds: float = 2.0):
     """The CPU baselines beside the secondary rows, on the host cores: the package's torch-CPU
     ops (the ``cpu`` backend: chunked DGDA, the reference ops for the indexer and MABA-SA) at
-    the rows' full shapes where that fits a few seconds, otherwise on a stated sample; the
-    float64 oracle where no torch op exists at that shape (the dense prefill attention)."""
-    import numpy as np
+    the rows' full shapes where that fits a few seconds, otherwise on a stated sample (the
+    dense prefill attention: a chunk of queries)."""
     import torch
     import torch.nn.functional as F
     from maba_sparse.kernels import common as C
     from maba_sparse.kernels.cpu_dgda import cpu_dgda_prefill, cpu_dgda_step
-    from oracle import sparse_attn as osa
     out = {}
     nthr = torch.get_num_threads()
-    blas = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    r = np.random.default_rng(7)
     g = torch.Generator().manual_seed(7)
     # DGDA decode step, B=64 H=10 d=64, fp32 (cpu backend's step)
     B, H, d = 64, 10, 64
@@ -309,19 +305,22 @@ def cpu_row_baselines(min_seconds: float = 2.0):
                                             f"{dt:.1f} s, scaled by 16 to the B=4 call; kernels/common.py "
                                             f"ref_dgda_prologue (torch)"}
     del xs
-    # MABA-SA prefill streams: the last 128 of the 32,768 queries of one head, scaled by 256 x 10 heads
-    Lp, dhp, Kp = 32768, 64, 32
-    qp1 = r.standard_normal((1, 1, 128, dhp)); kp1 = r.standard_normal((1, 1, Lp, dhp))
-    vp1 = r.standard_normal((1, 1, Lp, dhp))
-    khp = r.standard_normal((1, 1, Lp // 64, dhp)); vhp = r.standard_normal((1, 1, Lp // 64, dhp))
-    idxp = r.integers(0, Lp // 64, size=(1, 128, Kp))
-    gp = r.standard_normal((1, 128, 3))
-    reps, dt = _timed(lambda: osa.maba_sa_prefill_heads(qp1, kp1, vp1, khp, vhp, None, idxp, gp), min_seconds)
-    out["maba_sa_prefill_32k"] = {"value": dt / reps * 1e3 * (Lp / 128) * 10, "unit": "ms/call", "cores": blas,
+    # MABA-SA prefill streams: the package's torch op (dense masks, fp32, torch's intra-op threads)
+    # on the last 64 of the 32,768 queries of all ten heads, scaled by 512 query chunks
+    Lp, dhp, Kp, Hp, Qp = 32768, 64, 32, 10, 64
+    tg = torch.Generator().manual_seed(7)
+    qp1 = torch.randn(1, Hp, Qp, dhp, generator=tg)
+    kp1, vp1 = torch.randn(1, Hp, Lp, dhp, generator=tg), torch.randn(1, Hp, Lp, dhp, generator=tg)
+    khp, vhp = torch.randn(1, Hp, Lp // 64, dhp, generator=tg), torch.randn(1, Hp, Lp // 64, dhp, generator=tg)
+    idxp = torch.randint(0, Lp // 64, (1, Qp, Kp), generator=tg)
+    gp = torch.randn(1, Qp, 3, generator=tg)
+    reps, dt = _timed(lambda: C.ref_maba_sa_prefill(qp1, kp1, vp1, khp, vhp, None, idxp, gp, scale=0.125), min_seconds)
+    out["maba_sa_prefill_32k"] = {"value": dt / reps * 1e3 * (Lp / Qp), "unit": "ms/call", "cores": nthr,
                                   "kind": "port",
-                                  "sample": f"the last 128 of 32,768 queries of one head, {reps} repeats in "
-                                            f"{dt:.1f} s, scaled by 256 x 10 heads; oracle/sparse_attn.py "
-                                            f"maba_sa_prefill_heads (numpy fp64)"}
+                                  "sample": f"the last {Qp} of 32,768 queries of all {Hp} heads (random top-{Kp} "
+                                            f"rows), {reps} repeats in {dt:.1f} s, scaled by {Lp // Qp} query "
+                                            f"chunks; kernels/common.py ref_maba_sa_prefill (torch fp32)"}
+    del kp1, vp1
     # config 5 on the host: the same 101M stack in fp32 through the dispatcher's torch reference
     # ops (the reference's own CPU path), B=1, a 256-token prefill, then 8 greedy steps
     import torch
