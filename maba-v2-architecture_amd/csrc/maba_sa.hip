@@ -424,7 +424,7 @@ __device__ __forceinline__ SaSeg sa_segment(const SaArgs& a, int sid) {
 struct SaRows {
   const uint16_t* c; int64_t cs;     // latent rows of the sequence, row stride (unit channel stride)
   const uint16_t* hca; int64_t hs;   // block means of the sequence
-  int64_t L;
+  int64_t L, nblk;                   // nblk = ceil(L / bs), formed once per workgroup
   int bs, ns, loc_start, nloc, nc;
 };
 
@@ -433,6 +433,7 @@ __device__ __forceinline__ SaRows sa_rows(const SaArgs& a, int64_t b) {
   r.c = (const uint16_t*)a.c + b * a.csb; r.cs = a.csl;
   r.hca = (const uint16_t*)a.hca + b * a.hsb; r.hs = a.hsn;
   r.L = a.L; r.bs = a.bs; r.ns = a.ns; r.loc_start = a.loc_start; r.nloc = a.nloc; r.nc = a.nc;
+  r.nblk = (a.L + a.bs - 1) / a.bs;
   return r;
 }
 
@@ -452,8 +453,7 @@ __device__ __forceinline__ void sa_load_rows(const SaRows& r, int stream, int64_
   constexpr int TK = 16 * RB;
   const uint16_t* base = stream == 2 ? r.hca : r.c;
   const int rstride = (int)(stream == 2 ? r.hs : r.cs);
-  const int64_t nblk = (r.L + r.bs - 1) / r.bs;
-  const bool blk_ok = blk >= 0 && blk < nblk;
+  const bool blk_ok = blk >= 0 && blk < r.nblk;
   int part = 0;   // the tile's part of its sparse block (block_size <= 64: one part of a 64-key tile)
   if constexpr (RB < 4) part = (int)(tix % ((r.bs + TK - 1) / TK));
   const int first = (int)(stream == 1 ? (blk_ok ? blk * r.bs + part * TK : 0) : tix * TK);
@@ -507,10 +507,10 @@ __device__ __forceinline__ void sa_acc_close(SaAcc<NP>& st, bool head_on) {
 // would wait for the loads).  Loads past the last tile re-read it (in bounds, unused);
 // unconditional loads keep the register pressure at that of straight-line code.  blk_of(t)
 // is the sparse block index of tile t (wave-uniform).
-template <int NP, int RB = 4, class BlkOf>
+template <int NP, int RB = 4, class BlkOf, class Prep>
 __device__ __forceinline__ void sa_stream_tiles(const SaRows& rows, int stream, int64_t t0, int64_t t1, BlkOf blk_of,
                                                 const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile,
-                                                int c16, int g, SaAcc<NP>& st);
+                                                int c16, int g, SaAcc<NP>& st, Prep prep);
 
 // One 64-key tile: scores D[key][head] = C Q^T with the scaled query in bf16 hi + lo (B
 // operand), online softmax, values Z[dim][head] += C^T P with the tile copied row-major into
@@ -606,14 +606,20 @@ __device__ __forceinline__ void sa_tile_step(const s16x8 (&cv)[RB][NP], uint32_t
   }
 }
 
-template <int NP, int RB, class BlkOf>
+// prep() runs once the first tile's loads are issued (or at once when the wave has no tile):
+// the caller's work that waits on earlier loads (the query conversion) then overlaps them.
+template <int NP, int RB, class BlkOf, class Prep>
 __device__ __forceinline__ void sa_stream_tiles(const SaRows& rows, int stream, int64_t t0, int64_t t1, BlkOf blk_of,
                                                 const s16x8 (&qh)[NP], const s16x8 (&ql)[NP], short* tile,
-                                                int c16, int g, SaAcc<NP>& st) {
-  if (t0 >= t1) return;
+                                                int c16, int g, SaAcc<NP>& st, Prep prep) {
+  if (t0 >= t1) {
+    prep();
+    return;
+  }
   s16x8 cvA[RB][NP], cvB[RB][NP];
   uint32_t okA = 0, okB = 0;
   sa_load_rows<NP, RB>(rows, stream, t0, blk_of(t0), c16, g, cvA, okA);
+  prep();
   for (int64_t tix = t0; tix < t1; tix += 2) {
     const int64_t n1 = tix + 1 < t1 ? tix + 1 : tix;
     sa_load_rows<NP, RB>(rows, stream, n1, blk_of(n1), c16, g, cvB, okB);
@@ -625,22 +631,21 @@ __device__ __forceinline__ void sa_stream_tiles(const SaRows& rows, int stream, 
   }
 }
 
-// The lane's query fragment for MFMA column c16 (head c16, dims 32 p + 8 g .. +7) times
-// the score scale, split bf16 hi + lo; heads >= H are zero.  qp: the fp32 query rows of
-// the sequence (head stride qsh, unit channel stride when vec).
-template <int NP>
-__device__ __forceinline__ void sa_query_split(const void* q, int qdt, int64_t qoff, int64_t qsh, int64_t qsd, bool vec,
-                                               int H, float scale, int c16, int g, s16x8 (&qh)[NP], s16x8 (&ql)[NP]) {
-  float qv[NP][8];
-  if (vec) {  // fp32 rows, 16-byte aligned: all of the lane's query loads in flight at once
+// The lane's query fragment for MFMA column c16 (head c16, dims 32 p + 8 g .. +7), loaded as
+// stored (sa_query_load) and then, once the first key tile's loads are in flight, times the
+// score scale and split bf16 hi + lo (sa_query_cvt); heads >= H are zero.  q + qoff: the fp32
+// query rows of the sequence (head stride qsh, unit channel stride when vec).
+template <int NP, bool VEC>
+__device__ __forceinline__ void sa_query_load(const void* q, int qdt, int64_t qoff, int64_t qsh, int64_t qsd,
+                                              int H, int c16, int g, float (&qv)[NP][8]) {
+  if constexpr (VEC) {  // fp32 rows, 16-byte aligned: all of the lane's query loads in flight at once
+    // unconditional loads (columns past H read head H - 1; sa_query_cvt zeroes them), so that
+    // the compiler can count them and later waits need not drain every load
+    const float* qp = (const float*)q + qoff + (c16 < H ? c16 : H - 1) * qsh + 8 * g;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
-      if (c16 < H) {
-        const float* qp = (const float*)q + qoff + c16 * qsh + 32 * p + 8 * g;
-        x0 = *(const f32x4*)qp;
-        x1 = *(const f32x4*)(qp + 4);
-      }
+      const f32x4 x0 = *(const f32x4*)(qp + 32 * p);
+      const f32x4 x1 = *(const f32x4*)(qp + 32 * p + 4);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         qv[p][j] = x0[j];
@@ -654,11 +659,16 @@ __device__ __forceinline__ void sa_query_split(const void* q, int qdt, int64_t q
       for (int j = 0; j < 8; ++j)
         qv[p][j] = (c16 < H) ? load_elem(q, qdt, qoff + c16 * qsh + (32 * p + 8 * g + j) * qsd) : 0.f;
   }
+}
+
+template <int NP>
+__device__ __forceinline__ void sa_query_cvt(const float (&qv)[NP][8], float scale, bool on, s16x8 (&qh)[NP],
+                                             s16x8 (&ql)[NP]) {
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float x = qv[p][j] * scale;   // scores come out scaled
+      const float x = on ? qv[p][j] * scale : 0.f;   // scores come out scaled; heads >= H are zero
       const short h = __builtin_bit_cast(short, (__bf16)x);
       qh[p][j] = h;
       ql[p][j] = __builtin_bit_cast(short, (__bf16)(x - bf16_bits_to_f32((uint16_t)h)));
@@ -666,7 +676,7 @@ __device__ __forceinline__ void sa_query_split(const void* q, int qdt, int64_t q
   }
 }
 
-template <int NP>  // d_c = 32 * NP
+template <int NP, bool QV>  // d_c = 32 * NP; QV: fp32 queries with 16-byte aligned rows
 __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a_in) {
   const SaArgs a = sa_live(a_in);
   constexpr int DC = 32 * NP;
@@ -682,25 +692,26 @@ __global__ __launch_bounds__(256, 2) void maba_sa_mfma_kernel(SaArgs a_in) {
   const int64_t t1 = min(sg.t_end, t0 + tpw);
   short* tile = s_tile[wave];
 
-  // queries times the score scale (B operand of the scores): head c16, split hi/lo
+  // Loads in the order they are needed: the sparse block indices of the wave's tiles (one per
+  // lane), the query rows, then the first tile (which waits for the indices only); the query's
+  // scaling and hi/lo split (the scores' B operand, head c16) wait for it only after that.
+  int64_t blk_l = 0;
+  if (sg.stream == 1 && lane < t1 - t0) blk_l = a.idx[b * a.isb + sg.hs * a.ish + (t0 + lane) * a.isk];
+  float qv[NP][8];
+  sa_query_load<NP, QV>(a.q, a.qdt, b * a.qsb, a.qsh, a.qsd, a.H, c16, g, qv);
   s16x8 qh[NP], ql[NP];
-  sa_query_split<NP>(a.q, a.qdt, b * a.qsb, a.qsh, a.qsd, a.qvec, a.H, a.scale, c16, g, qh, ql);
   const bool head_on = c16 < a.H && (sg.head_only < 0 || sg.head_only == c16);
   SaAcc<NP> st;
   sa_acc_init(st);
   const SaRows rows = sa_rows(a, b);
-
-  // sparse block indices of this wave's tiles, one per lane, fetched up front so that
-  // the tile loads do not wait on a dependent index load
-  int64_t blk_l = 0;
-  if (sg.stream == 1 && lane < t1 - t0) blk_l = a.idx[b * a.isb + sg.hs * a.ish + (t0 + lane) * a.isk];
   auto blk_of = [&](int64_t tix) {   // wave-uniform lane index
     const int src = (int)(tix - t0);
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)blk_l, src);
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)blk_l >> 32), src);
     return (int64_t)(((uint64_t)hi << 32) | lo);
   };
-  sa_stream_tiles<NP>(rows, sg.stream, t0, t1, blk_of, qh, ql, tile, c16, g, st);
+  sa_stream_tiles<NP>(rows, sg.stream, t0, t1, blk_of, qh, ql, tile, c16, g, st,
+                      [&] { sa_query_cvt<NP>(qv, a.scale, c16 < a.H, qh, ql); });
   sa_acc_close(st, head_on);
   const float m_run = st.m, l_run = st.l;
   const f32x4* z = st.z;
@@ -777,7 +788,7 @@ struct PlArgs {
   float scale;
 };
 
-template <int NP>
+template <int NP, bool QV>
 __global__ __launch_bounds__(PL_W * 64, 1) void maba_sa_prefill_latent_kernel(PlArgs a) {
   constexpr int DC = 32 * NP;
   constexpr int TP = DC + 8;
@@ -792,7 +803,7 @@ __global__ __launch_bounds__(PL_W * 64, 1) void maba_sa_prefill_latent_kernel(Pl
   SaRows rows;
   rows.c = a.c + b * a.csb; rows.cs = a.csl;
   rows.hca = a.hca + b * a.hsb; rows.hs = a.hsn;
-  rows.L = L; rows.bs = a.bs;
+  rows.L = L; rows.bs = a.bs; rows.nblk = (L + a.bs - 1) / a.bs;
   const int64_t ns = L < a.n_sink ? L : a.n_sink;
   const int64_t lst = (L - a.window) > ns ? (L - a.window) : ns;
   rows.ns = (int)ns; rows.loc_start = (int)lst; rows.nloc = (int)(ns + (L - lst)); rows.nc = (int)(L / a.pool);
@@ -832,21 +843,25 @@ __global__ __launch_bounds__(PL_W * 64, 1) void maba_sa_prefill_latent_kernel(Pl
   }
   const int64_t t0 = stream == 1 ? u0 * tpb : u0, t1 = stream == 1 ? u1 * tpb : u1;
   short* tile = s_tile[wave];
+  // the wave's sparse slots [u0, u1) (at most 64: K <= 64), one block index per lane, then the
+  // query rows (converted once the first tile's loads are issued)
+  int64_t blk_l = 0;
+  if (stream == 1 && lane < u1 - u0) blk_l = a.idx[b * a.isb + t * a.ist + (u0 + lane) * a.isk];
+  float qv[NP][8];
+  sa_query_load<NP, QV>(a.q, a.qdt, b * a.qsb + t * a.qst, a.qsh, a.qsd, a.H, c16, g, qv);
   s16x8 qh[NP], ql[NP];
-  sa_query_split<NP>(a.q, a.qdt, b * a.qsb + t * a.qst, a.qsh, a.qsd, a.qvec, a.H, a.scale, c16, g, qh, ql);
   const bool head_on = c16 < a.H;
   SaAcc<NP> st;
   sa_acc_init(st);
-  // the wave's sparse slots [u0, u1) (at most 64: K <= 64), one block index per lane
-  int64_t blk_l = 0;
-  if (stream == 1 && lane < u1 - u0) blk_l = a.idx[b * a.isb + t * a.ist + (u0 + lane) * a.isk];
   auto blk_of = [&](int64_t tix) {
     const int src = (int)(tix / tpb - u0);
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)blk_l, src);
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)blk_l >> 32), src);
     return (int64_t)(((uint64_t)hi << 32) | lo);
   };
-  if (stream >= 0) sa_stream_tiles<NP, PL_RB>(rows, stream, t0, t1, blk_of, qh, ql, tile, c16, g, st);
+  if (stream >= 0)
+    sa_stream_tiles<NP, PL_RB>(rows, stream, t0, t1, blk_of, qh, ql, tile, c16, g, st,
+                               [&] { sa_query_cvt<NP>(qv, a.scale, c16 < a.H, qh, ql); });
   sa_acc_close(st, head_on);
   // wave partials to LDS (the tiles are free once every wave is past its loop)
   __syncthreads();
@@ -997,10 +1012,10 @@ static int sa_run(const SaArgs& a, bool seg, hipStream_t s) {
     const dim3 grid(nslot, (unsigned)a.B);
     if (seg) {
       switch (a.dc / 32) {
-        case 1: hipLaunchKernelGGL(maba_sa_mfma_kernel<1>, grid, dim3(256), 0, s, a); break;
-        case 2: hipLaunchKernelGGL(maba_sa_mfma_kernel<2>, grid, dim3(256), 0, s, a); break;
-        case 3: hipLaunchKernelGGL(maba_sa_mfma_kernel<3>, grid, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL(maba_sa_mfma_kernel<4>, grid, dim3(256), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((a.qvec ? maba_sa_mfma_kernel<1, true> : maba_sa_mfma_kernel<1, false>), grid, dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((a.qvec ? maba_sa_mfma_kernel<2, true> : maba_sa_mfma_kernel<2, false>), grid, dim3(256), 0, s, a); break;
+        case 3: hipLaunchKernelGGL((a.qvec ? maba_sa_mfma_kernel<3, true> : maba_sa_mfma_kernel<3, false>), grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL((a.qvec ? maba_sa_mfma_kernel<4, true> : maba_sa_mfma_kernel<4, false>), grid, dim3(256), 0, s, a); break;
       }
     } else {
       hipLaunchKernelGGL(maba_sa_tile_kernel, grid, dim3(256), 0, s, a);
@@ -1198,10 +1213,10 @@ extern "C" int maba_hip_maba_sa_prefill_latent(const maba_tensor* q_lat, const m
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)(B * Lq));
   switch (dc / 32) {
-    case 1: hipLaunchKernelGGL(maba_sa_prefill_latent_kernel<1>, grid, dim3(PL_W * 64), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(maba_sa_prefill_latent_kernel<2>, grid, dim3(PL_W * 64), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(maba_sa_prefill_latent_kernel<3>, grid, dim3(PL_W * 64), 0, s, a); break;
-    default: hipLaunchKernelGGL(maba_sa_prefill_latent_kernel<4>, grid, dim3(PL_W * 64), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((a.qvec ? maba_sa_prefill_latent_kernel<1, true> : maba_sa_prefill_latent_kernel<1, false>), grid, dim3(PL_W * 64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((a.qvec ? maba_sa_prefill_latent_kernel<2, true> : maba_sa_prefill_latent_kernel<2, false>), grid, dim3(PL_W * 64), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((a.qvec ? maba_sa_prefill_latent_kernel<3, true> : maba_sa_prefill_latent_kernel<3, false>), grid, dim3(PL_W * 64), 0, s, a); break;
+    default: hipLaunchKernelGGL((a.qvec ? maba_sa_prefill_latent_kernel<4, true> : maba_sa_prefill_latent_kernel<4, false>), grid, dim3(PL_W * 64), 0, s, a); break;
   }
   return check_launch("maba_sa_prefill_latent");
 }
