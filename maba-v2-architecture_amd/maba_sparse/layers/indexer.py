@@ -98,6 +98,14 @@ class DGIndexer(nn.Module):
         self._keys = None
         self._cents = None
 
+    def restore_cache(self, k_idx: torch.Tensor) -> None:
+        """Set the decode cache to the key rows ``k_idx [B, L, d_idx]`` of a held sequence, as a
+        prefill of those tokens leaves it: the rows, and the centroids of their complete blocks."""
+        self._keys = _Growing(k_idx.detach())
+        full = k_idx.shape[1] // self.block_size
+        self._cents = (_Growing(dispatch_compute_centroids(k_idx[:, : full * self.block_size].detach(),
+                                                           block_size=self.block_size)) if full > 0 else None)
+
     def _centroids(self, ki: torch.Tensor, past_centroids, past_k_idx) -> torch.Tensor:
         b, l, _ = ki.shape
         bs = self.block_size
