@@ -140,14 +140,16 @@ int maba_hip_compute_centroids(const maba_tensor* k_idx, maba_tensor* out, int b
                                void* stream);
 
 /* Causal prefill scoring + top-k.  q_idx: [B,L,d]; centroids: [B,nb,d];
- * out_idx: int64 [B,L,min(top_k,nb)]; out_scores: [B,L,nb] or NULL. */
+ * out_idx: int64 [B,L,min(top_k,nb)]; out_scores: [B,L,nb] or NULL.  Any top_k; above 64 the
+ * rows are sorted whole (at most 16384 blocks, MABA_ERR_UNSUPPORTED beyond). */
 int maba_hip_index_topk(const maba_tensor* q_idx, const maba_tensor* centroids,
                         float lambda_dist, int top_k, int block_size, maba_tensor* out_idx,
                         maba_tensor* out_scores, void* stream);
 
 /* Decode scoring (query block = nb-1, no mask) + top-k for Hq query heads
  * sharing one centroid set.  q: [B,Hq,d]; centroids: [B,nb,d];
- * out_idx: int64 [B,Hq,min(top_k,nb)]; out_scores: f32 [B,Hq,nb] or NULL. */
+ * out_idx: int64 [B,Hq,min(top_k,nb)]; out_scores: f32 [B,Hq,nb] or NULL.  Any top_k; above 64
+ * the rows are sorted whole (at most 16384 blocks, MABA_ERR_UNSUPPORTED beyond; no workspace). */
 size_t maba_hip_index_topk_decode_workspace_size(int64_t B, int64_t Hq, int64_t nb, int top_k);
 int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tensor* centroids,
                                float lambda_dist, int top_k, maba_tensor* out_idx,

@@ -526,6 +526,94 @@ __global__ __launch_bounds__(256) void index_prefill_kernel(PreArgs a) {
   }
 }
 
+// Any top_k (the reference accepts every K, cpu_indexer.py:53-112, layers/indexer.py:101-112):
+// one 256-thread workgroup per query row scores all the row's blocks itself (fp32 dots of the
+// stored inputs, any float dtypes), keeps their keys in LDS and sorts them descending with a
+// bitonic network, then writes the first ak indices.  Decode rows score every block with the
+// distance nb - 1 - n (no mask); prefill rows are causal (blocks n > t / bs score -inf, so they
+// follow every live block, lowest index first, as index_prefill_kernel leaves them).  Rows of
+// at most SORT_MAX_N blocks; the taken path for top_k > 64, where the wave lists above stop.
+constexpr int SORT_MAX_N = 16384;   // 128 KB of keys in LDS
+
+struct SortArgs {
+  const void* q; int qdt; int64_t qsb, qsr, qsd;   // decode: [B, Hq, d]; prefill: [B, L, d]
+  const void* c; int cdt; int64_t csb, csn, csd;   // [B, nb, d]
+  int64_t R, nb, d;          // R: query rows per batch element (Hq or L)
+  int np, ak, bs, prefill;   // np: keys sorted per row (a power of two >= nb)
+  float scale, lam;
+  int64_t* out; int64_t osb, osr, osk;
+  void* scores; int sdt; int64_t ssb, ssr, ssn;    // optional [B, R, nb] score output
+};
+
+__global__ __launch_bounds__(256) void index_sort_topk_kernel(SortArgs a) {
+  extern __shared__ key64 s_key[];   // a.np keys
+  __shared__ float s_q[IDX_MAX_D];
+  const int tid = threadIdx.x;
+  const int64_t bi = blockIdx.y, r = blockIdx.x;
+  for (int64_t c = tid; c < a.d; c += 256) s_q[c] = load_elem(a.q, a.qdt, bi * a.qsb + r * a.qsr + c * a.qsd) * a.scale;
+  __syncthreads();
+  const int64_t qblk = a.prefill ? r / a.bs : a.nb - 1;
+  for (int n = tid; n < a.np; n += 256) {
+    key64 key = KEY_NONE;
+    if (n < a.nb) {
+      float sc = -INFINITY;
+      if (n <= qblk) {
+        float acc = 0.f;
+        const int64_t cb = bi * a.csb + n * a.csn;
+        for (int64_t c = 0; c < a.d; ++c) acc = fmaf(s_q[c], load_elem(a.c, a.cdt, cb + c * a.csd), acc);
+        sc = acc - a.lam * fast_log(1.f + (float)(qblk - n));
+      }
+      if (a.scores) store_elem(a.scores, a.sdt, bi * a.ssb + r * a.ssr + n * a.ssn, sc);
+      key = make_key(sc, (uint32_t)n);
+    }
+    s_key[n] = key;
+  }
+  __syncthreads();
+  for (int k = 2; k <= a.np; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < a.np; i += 256) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const key64 x = s_key[i], y = s_key[ixj];
+          const bool desc = (i & k) == 0;   // descending runs where bit k of i is clear
+          if (desc ? x < y : x > y) {
+            s_key[i] = y;
+            s_key[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = tid; i < a.ak; i += 256) a.out[bi * a.osb + r * a.osr + i * a.osk] = (int64_t)key_index(s_key[i]);
+}
+
+static int launch_sort_topk(const maba_tensor* q, const maba_tensor* centroids, int prefill, int block_size,
+                            float lambda_dist, int ak, maba_tensor* out_idx, maba_tensor* out_scores,
+                            hipStream_t s, const char* who) {
+  const int64_t B = q->shape[0], R = q->shape[1], d = q->shape[2], nb = centroids->shape[1];
+  if (nb > SORT_MAX_N) return fail(MABA_ERR_UNSUPPORTED, "%s: top_k > 64 needs at most %d blocks", who, SORT_MAX_N);
+  if (R > 0xffffffffLL || B > 65535) return fail(MABA_ERR_UNSUPPORTED, "%s: too many query rows", who);
+  SortArgs a;
+  a.q = q->data; a.qdt = q->dtype; a.qsb = q->stride[0]; a.qsr = q->stride[1]; a.qsd = q->stride[2];
+  a.c = centroids->data; a.cdt = centroids->dtype;
+  a.csb = centroids->stride[0]; a.csn = centroids->stride[1]; a.csd = centroids->stride[2];
+  a.R = R; a.nb = nb; a.d = d;
+  int np = 64;
+  while (np < nb) np <<= 1;
+  a.np = np; a.ak = ak; a.bs = block_size; a.prefill = prefill;
+  a.scale = 1.0f / sqrtf((float)d);
+  a.lam = lambda_dist;
+  a.out = (int64_t*)out_idx->data; a.osb = out_idx->stride[0]; a.osr = out_idx->stride[1]; a.osk = out_idx->stride[2];
+  a.scores = out_scores ? out_scores->data : nullptr;
+  a.sdt = out_scores ? out_scores->dtype : MABA_F32;
+  a.ssb = out_scores ? out_scores->stride[0] : 0;
+  a.ssr = out_scores ? out_scores->stride[1] : 0;
+  a.ssn = out_scores ? out_scores->stride[2] : 0;
+  hipLaunchKernelGGL(index_sort_topk_kernel, dim3((unsigned)R, (unsigned)B), dim3(256), (size_t)np * sizeof(key64), s, a);
+  return check_launch(who);
+}
+
 }  // namespace maba
 
 using namespace maba;
@@ -610,7 +698,17 @@ extern "C" int maba_hip_index_topk_decode(const maba_tensor* q, const maba_tenso
   if (!expect_shape(out_idx, "out_idx", 3, so)) return MABA_ERR_INVALID;
   if (out_idx->dtype != MABA_I64) return fail(MABA_ERR_DTYPE, "index_topk_decode: out_idx must be int64");
   if (!expect_float(q, "q") || !expect_float(centroids, "centroids")) return MABA_ERR_DTYPE;
-  if (top_k > 64) return fail(MABA_ERR_UNSUPPORTED, "index_topk_decode: top_k > 64 not supported");
+  if (d > IDX_MAX_D) return fail(MABA_ERR_UNSUPPORTED, "index_topk_decode: d <= %d required", IDX_MAX_D);
+  if (top_k > 64) {   // the general path: per-row scores sorted in LDS (no workspace)
+    if (out_scores) {
+      const int64_t ss[3] = {B, Hq, nb};
+      if (!expect_shape(out_scores, "out_scores", 3, ss)) return MABA_ERR_INVALID;
+      if (out_scores->dtype != MABA_F32) return fail(MABA_ERR_DTYPE, "index_topk_decode: out_scores must be f32");
+    }
+    if (B * Hq == 0 || nb == 0) return MABA_OK;
+    return launch_sort_topk(q, centroids, 0, 64, lambda_dist, (int)ak, out_idx, out_scores, (hipStream_t)stream,
+                            "index_topk_decode");
+  }
   if (Hq > IDX_MAX_HEADS || d > IDX_MAX_D)
     return fail(MABA_ERR_UNSUPPORTED, "index_topk_decode: Hq <= %d and d <= %d required", IDX_MAX_HEADS, IDX_MAX_D);
   if (out_scores) {
@@ -693,7 +791,6 @@ extern "C" int maba_hip_index_topk(const maba_tensor* q_idx, const maba_tensor* 
   if (!expect_shape(out_idx, "out_idx", 3, so)) return MABA_ERR_INVALID;
   if (out_idx->dtype != MABA_I64) return fail(MABA_ERR_DTYPE, "index_topk: out_idx must be int64");
   if (!expect_float(q_idx, "q_idx") || !expect_float(centroids, "centroids")) return MABA_ERR_DTYPE;
-  if (top_k > 64 && nb > 64) return fail(MABA_ERR_UNSUPPORTED, "index_topk: top_k > 64 not supported");
   if (d > IDX_MAX_D) return fail(MABA_ERR_UNSUPPORTED, "index_topk: d <= %d required", IDX_MAX_D);
   if (out_scores) {
     const int64_t ss[3] = {B, L, nb};
@@ -701,6 +798,9 @@ extern "C" int maba_hip_index_topk(const maba_tensor* q_idx, const maba_tensor* 
     if (!expect_float(out_scores, "out_scores")) return MABA_ERR_DTYPE;
   }
   if (B * L == 0 || nb == 0) return MABA_OK;
+  if (top_k > 64 && nb > 64)   // the general path: per-row scores sorted in LDS
+    return launch_sort_topk(q_idx, centroids, 1, block_size, lambda_dist, (int)ak, out_idx, out_scores,
+                            (hipStream_t)stream, "index_topk");
   // MFMA path: bf16 rows with unit channel stride, 16-byte aligned, d a multiple of 32
   const bool mfma = !out_scores && q_idx->dtype == MABA_BF16 && centroids->dtype == MABA_BF16 && d % 32 == 0 &&
                     q_idx->stride[2] == 1 && centroids->stride[2] == 1 && (uintptr_t)q_idx->data % 16 == 0 &&

@@ -127,8 +127,11 @@ def test_index_topk_decode_validation(lib):
     out = _t([2, 4, 32], N.MABA_I64)
     rc = lib.maba_hip_index_topk_decode(q, c, 0.1, 0, out, None, None, 0, None)
     assert rc == N.MABA_ERR_INVALID and b"top_k must be positive" in lib.maba_hip_last_error()
-    rc = lib.maba_hip_index_topk_decode(q, c, 0.1, 65, _t([2, 4, 65], N.MABA_I64), None, None, 0, None)
-    assert rc == N.MABA_ERR_UNSUPPORTED
+    # top_k > 64 takes the general sorted path, which holds at most 16,384 blocks per row; the
+    # refusal comes before anything launches
+    c_long = _t([2, 20000, 128])
+    rc = lib.maba_hip_index_topk_decode(q, c_long, 0.1, 65, _t([2, 4, 65], N.MABA_I64), None, None, 0, None)
+    assert rc == N.MABA_ERR_UNSUPPORTED and b"16384" in lib.maba_hip_last_error()
     rc = lib.maba_hip_index_topk_decode(q, c, 0.1, 32, _t([2, 4, 32], N.MABA_F32), None, None, 0, None)
     assert rc == N.MABA_ERR_DTYPE
     rc = lib.maba_hip_index_topk_decode(q, c, 0.1, 32, out, None, None, 0, None)
@@ -202,7 +205,7 @@ def test_check_maps_status_to_python_exceptions(lib):
     rc = lib.maba_hip_dgda_prefill(q, q, q, None, q, q, q, None, q, q, 64, None, 0, None)
     with pytest.raises(ValueError, match="dgda_prefill"):
         N.check(rc, "dgda_prefill")
-    rc = lib.maba_hip_index_topk_decode(_t([2, 4, 128]), _t([2, 100, 128]), 0.1, 65,
+    rc = lib.maba_hip_index_topk_decode(_t([2, 4, 128]), _t([2, 20000, 128]), 0.1, 65,
                                         _t([2, 4, 65], N.MABA_I64), None, None, 0, None)
     with pytest.raises(NotImplementedError):
         N.check(rc, "index_topk_decode")

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import assert_close, dgda_inputs, oracle_dgda_args, to_np, topk_agrees
+from _helpers import assert_close, dgda_inputs, oracle_dgda_args, to_np, topk_agrees, topk_is_valid
 from oracle import dgda as odgda
 from oracle import indexer as oidx
 from oracle import sparse_attn as osa
@@ -380,3 +380,52 @@ def test_maba_sa_decode_many_segments(dev, L, K, Hi):
     exp = osa.maba_sa_decode(to_np(q), to_np(c), to_np(Wk), to_np(Wv), to_np(idx).astype(np.int64),
                              to_np(gate), means=to_np(hca))
     assert_close(out, exp, 2e-3, 2e-3, "maba_sa")
+
+
+# ----------------------------------------------------------------------------- top_k > 64
+# The reference takes any K (common.py:353-403, cpu_indexer.py:53-112, layers/indexer.py:101-112);
+# past the 64-key wave lists the general path scores each row and sorts it in LDS.
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("nb,k", [(300, 65), (1000, 128), (15625, 256), (200, 200)])
+def test_index_topk_decode_large_k(dev, nb, k, dtype):
+    g = torch.Generator().manual_seed(nb + k)
+    B, Hq, d = 2, 3, 128
+    q = torch.randn(B, Hq, d, generator=g).to(dtype)
+    c = torch.randn(B, nb, d, generator=g).to(dtype)
+    idx, sc = _hip().hip_index_topk_decode(q.to(dev), c.to(dev), lambda_dist=0.1, top_k=k, return_scores=True)
+    ref = oidx.decode_scores(to_np(q), to_np(c), 0.1)
+    assert idx.shape == (B, Hq, min(k, nb))
+    assert_close(sc, ref, 1e-5, 1e-4, "decode scores")
+    assert topk_agrees(idx.cpu().numpy(), ref, k) >= B * Hq - 1
+    topk_is_valid(idx.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("L,k,lam", [(9000, 100, 0.5), (12800, 200, 0.1), (5000, 79, 0.0)])
+def test_index_topk_prefill_large_k(dev, L, k, lam):
+    """Causal prefill with K > 64: rows with fewer live blocks than K fill the remaining slots
+    with the lowest masked blocks; the returned scores are the oracle's (-inf where masked)."""
+    g = torch.Generator().manual_seed(L + k)
+    B, d = 2, 64
+    q = torch.randn(B, L, d, generator=g)
+    keys = torch.randn(B, L, d, generator=g)
+    cent = torch.from_numpy(oidx.compute_centroids(to_np(keys), 64)).float()
+    nb = cent.shape[1]
+    idx, sc = _hip().hip_index_topk(q.to(dev), cent.to(dev), lambda_dist=lam, top_k=k, block_size=64,
+                                    return_scores=True)
+    ref = oidx.prefill_scores(to_np(q), to_np(cent), lam)
+    ak = min(k, nb)
+    assert idx.shape == (B, L, ak)
+    got_sc = sc.double().cpu().numpy()
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got_sc), fin)
+    assert np.allclose(got_sc[fin], ref[fin], rtol=1e-5, atol=1e-4)
+    got = idx.cpu().numpy()
+    rows = [0, 63, 64, 1000, L // 2, L - 1]
+    sub = got[:, rows]
+    assert topk_agrees(sub, ref[:, rows], k) >= 1
+    topk_is_valid(sub, np.where(fin[:, rows], ref[:, rows], -1e30))
+    for t in rows:                                # masked slots: the lowest masked blocks, ascending
+        live = min(t // 64 + 1, nb)
+        if live < ak:
+            assert (got[:, t, live:] == np.arange(live, ak)).all()
