@@ -10,9 +10,10 @@
 //
 //  * the chunked MFMA path (dgda_chunk.hip) for the per-token (scalar) decay
 //    case with dk = dv = 64 and bf16 q/k/v -- the BASELINE configuration;
-//  * the sub-chunk path (dgda_sub.hip) for per-channel gates (the DGDA layer's
-//    layout) with dk = dv = 64 and bf16 or fp32 q/k/v: 16-token sub-chunks with exact
-//    per-channel decay, the state products on MFMA, sequence-parallel like the above.
+//  * the sub-chunk path (dgda_sub.h, dgda_sub*.hip) for per-channel or per-token gates
+//    (the DGDA layer's layout) with dk, dv in {32, 64, 128} and bf16, fp16 or fp32
+//    q/k/v: 16-token sub-chunks with exact per-channel decay, the state products on
+//    MFMA, sequence-parallel like the above.
 #include <algorithm>
 
 #include "maba_common.h"
@@ -120,7 +121,7 @@ int launch_dgda_chunk(const maba_tensor* q, const maba_tensor* k, const maba_ten
 bool dgda_sub_supported(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                         const maba_tensor* gate, const maba_tensor* b, const maba_tensor* w,
                         const maba_tensor* out);
-size_t dgda_sub_workspace(int64_t BH, int64_t L);
+size_t dgda_sub_workspace(int64_t BH, int64_t L, int64_t dk, int64_t dv);
 int launch_dgda_sub(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                     const maba_tensor* gate, int use_log, const maba_tensor* b,
                     const maba_tensor* w, const maba_tensor* s0, maba_tensor* out,
@@ -133,12 +134,14 @@ extern "C" size_t maba_hip_dgda_prefill_workspace_size(const maba_tensor* q, con
                                                       const maba_tensor* gate, const maba_tensor* b) {
   if (!q || q->ndim != 4 || !v || v->ndim != 4 || !gate || !b) return 0;
   // The call picks its path from every operand (k, w and out included), which this query
-  // does not see.  Both workspace sizes depend only on the shape, so whenever q admits a
-  // workspace path the larger of the two is returned: the call's choice always fits.
+  // does not see.  Both workspace sizes depend only on the shapes, so the larger of those
+  // of the paths that q, v and the gates admit is returned: the call's choice always fits.
   const int64_t BH = q->shape[0] * q->shape[1], L = q->shape[2];
-  if (dgda_chunk_supported(q, q, v, gate, b) || dgda_sub_supported(q, q, v, gate, b, nullptr, nullptr))
-    return std::max(dgda_chunk_workspace(BH, L), dgda_sub_workspace(BH, L));
-  return 0;
+  size_t n = 0;
+  if (dgda_chunk_supported(q, q, v, gate, b)) n = dgda_chunk_workspace(BH, L);
+  if (dgda_sub_supported(q, q, v, gate, b, nullptr, nullptr))
+    n = std::max(n, dgda_sub_workspace(BH, L, q->shape[3], v->shape[3]));
+  return n;
 }
 
 extern "C" int maba_hip_dgda_prefill(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
@@ -179,7 +182,7 @@ extern "C" int maba_hip_dgda_prefill(const maba_tensor* q, const maba_tensor* k,
                              workspace, workspace_bytes, s);
   }
   if (dgda_sub_supported(q, k, v, gate, b, w, out)) {
-    const size_t need = dgda_sub_workspace(B * H, L);
+    const size_t need = dgda_sub_workspace(B * H, L, dk, dv);
     if (!workspace || workspace_bytes < need)
       return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace of %zu bytes required", need);
     return launch_dgda_sub(q, k, v, gate, log_alpha != nullptr, b, w, initial_state, out, final_state,

@@ -1,615 +1,9 @@
-// DGDA prefill for per-channel gates (decay, erase and write gates [B,H,L,64] with
-// unit or zero channel stride), dk = dv = 64: the layer's gate layout.
-//
-// Sub-chunks of SC = 16 tokens.  With Lam_i the inclusive cumulative log-decay of
-// token i within the sub-chunk (a 64-vector over key channels) and S the state at the
-// sub-chunk start (reference math: cpu_dgda.py:101-146, common.py:229-268):
-//   L_ij = sum_c (b*k)_ic k_jc e^{Lam_ic - Lam_jc}      i > j
-//   A_ij = sum_c  q_ic    k_jc e^{Lam_ic - Lam_jc}      i >= j
-//   u    = (I + L)^-1 (w*v - (b*k*e^Lam) S)
-//   o    = (q*e^Lam) S + A u
-//   S'   = diag(e^{Lam_15}) S + (k*e^{Lam_15 - Lam})^T u
-// With decay gates a <= 1 every factor above is e^{<= 0}; gates above 1 (growth) are
-// taken as the token recurrence takes them.  L and A are computed as
-// (b*k*e^Lam)(k*e^{-Lam})^T and (q*e^Lam)(k*e^{-Lam})^T on MFMA when |Lam| <= 64 at every
-// token and channel of the sub-chunk (so e^{+-Lam} stay far inside fp32), and pair by
-// pair with exact exponentials on the VALU otherwise.  Products
-// with fp32 operands split them into bf16 hi + lo (three MFMAs), so they carry ~16
-// mantissa bits; the state stays in fp32 registers.
-//
-// MFMA layouts (16x16 tiles, lane (c16, g)): a result lane holds rows 4g..4g+3 of
-// column c16.  The per-token vectors v_e, u and o of a wave's 16 state columns are in
-// that layout (tokens 4g + i, column c16), which is the B-operand layout of the K = 16
-// products T u, A u and (K_C^T) u, so they chain without data movement; the state slab
-// Sr[kt] holds rows 16 kt + 4g + i of column c16 (the layout the segment map uses).
-//
-// Sequence parallelism, passes and modes: as the chunked path in dgda_chunk.hip (slots
-// of U sub-chunks, aggregate [N | M] pass, zero-start and fix-up output passes).
-//
-// Fused layer prologue (PRO, maba_hip_dgda_layer_prefill; reference layers/dgda.py:103-121,
-// 186-207): the kernels read the layer's six bf16 projections instead of q, k, v and the
-// gates, and form the op inputs in the staging step: the causal depthwise conv (kernel 4)
-// + SiLU of q, k, v over [history, projections], the per-head L2 norm of k, the decay
-// max(-softplus, -14) and the sigmoid erase and write gates, all in fp32 and never
-// written back.  A stager lane loads the four conv taps of its token (tokens t-3 .. t,
-// the earlier three mostly L1 hits from its neighbours' loads).  The key norm sums the
-// 64 channels of a token over four waves: each stager wave leaves its partial sums in LDS
-// before the loop-top barrier and the staging after it adds them.
-#include "dgda_common.h"
+// Host side of the sub-chunk DGDA prefill for per-channel gates (kernels and their math
+// in dgda_sub.h): operand checks, workspace sizing, the d_v = 128 split, the kernels for
+// d_k = 64 and the fused layer prologue entry point (maba_hip_dgda_layer_prefill).
+#include "dgda_sub.h"
 
 namespace maba {
-
-constexpr int SC = 16;             // tokens per sub-chunk
-constexpr int SUB_MIN_U = 64;      // sub-chunks per slot at least (1,024 tokens)
-constexpr int SUB_ZERO = 1, SUB_FIX = 2;
-constexpr int FP = 68;             // fp32 row pitch of the [16][64] staging arrays
-constexpr int TP = 20;             // bf16 row pitch of 16-column tiles
-constexpr float SUB_MFMA_RANGE = 64.f;   // largest |Lam| within a sub-chunk on the MFMA path
-
-struct SubArgs {
-  const void* q; int qs0, qs1, qs2;         // [B,H,L,64], channel stride 1 (bf16 or fp32, see F32IN)
-  const void* k; int ks0, ks1, ks2;
-  const void* vp; int vs0, vs1, vs2;
-  const float* gp; int gs0, gs1, gs2, gs3;  // log_alpha (use_log) or alpha, fp32, channel stride 0 or 1
-  const float* bp; int bs0, bs1, bs2, bs3;  // erase gate b, fp32, channel stride 0 or 1
-  const float* wp; int ws0, ws1, ws2, ws3;  // write gate w, fp32, channel stride 0 or 1
-  View4 s0;
-  void* op; int os0, os1, os2;              // output [B,H,L,64], channel stride 1 (bf16 or fp32, see OBF)
-  MView4 sf;
-  float* agg;      // [BH, nseg_max, 64, 128]: [N | M] of segments whose M never vanished, N_k of the others
-  int* zc;         // [BH, nseg_max]: sub-chunks after which the segment's M is exactly zero, -1 if never
-  int64_t U;       // sub-chunks per slot
-  int H, L, BH, nseg_max, nchunks, use_log, has_s0;
-  int mode;        // output kernel: SUB_ZERO or SUB_FIX
-  // fused prologue (PRO): the six bf16 projections [B, L, C] (q, k, v, decay, erase, write;
-  // unit channel stride, head h at channels 64h ..), conv taps [C, 1, 4] (f32/bf16), the
-  // bf16 conv history [B, C, 3] (null: zeros) and the key-norm eps
-  const uint16_t* px[6]; int pxs0[6], pxs1[6];
-  const void* cw[3]; int cwdt; int cwsc[3], cwst[3];
-  const uint16_t* ph[3]; int phs0[3], phs1[3], phs2[3];
-  float eps;
-};
-typedef const __attribute__((address_space(4))) SubArgs KSubArgs;
-
-#define SM_ALIGN_SUB __attribute__((aligned(16)))
-template <bool AGG>
-struct SubSmem {
-  SM_ALIGN_SUB float Q[AGG ? 1 : SC][FP];
-  SM_ALIGN_SUB float K[SC][FP];
-  SM_ALIGN_SUB float BK[SC][FP];            // b * k
-  SM_ALIGN_SUB float WV[SC][FP];            // w * v
-  SM_ALIGN_SUB float LA[SC][FP];            // log decay, then the inclusive prefix Lam
-  SM_ALIGN_SUB short QEh[AGG ? 8 : SC * PITCH], QEl[AGG ? 8 : SC * PITCH];   // q e^Lam
-  SM_ALIGN_SUB short BKEh[SC * PITCH], BKEl[SC * PITCH];                     // b k e^Lam
-  SM_ALIGN_SUB short KIh[SC * PITCH], KIl[SC * PITCH];                       // k e^-Lam
-  SM_ALIGN_SUB short KCh[64 * TP], KCl[64 * TP];                             // (k e^{Lam_15 - Lam})^T
-  SM_ALIGN_SUB short Th[SC * TP], Tl[SC * TP];                               // (I + L)^-1
-  SM_ALIGN_SUB short Ah[AGG ? 8 : SC * TP], Al[AGG ? 8 : SC * TP];           // A (lower, with diagonal)
-  SM_ALIGN_SUB float Lq[SC][4][4];                                            // L[i][p + 4 r] at [i][p][r]
-  SM_ALIGN_SUB float elast[64];                                               // e^{Lam_15}
-  SM_ALIGN_SUB float nrm[2][4][16];   // fused prologue: |k|^2 partials [sub-chunk parity][stager wave][token]
-  SM_ALIGN_SUB float cw[3][4][64];    // fused prologue: the head's conv taps [stream][tap][channel]
-  int big[2];                               // some |Lam| exceeds SUB_MFMA_RANGE (by sub-chunk parity)
-};
-
-// Raw registers of four consecutive row elements (bf16 bits or fp32).  Prefetched rows
-// stay raw until they are staged, so that no conversion waits for the loads.
-template <bool F32IN>
-using Raw4 = std::conditional_t<F32IN, f32x4, i16x4>;
-
-template <bool F32IN>
-__device__ __forceinline__ Raw4<F32IN> load_raw4(const void* base, int64_t off) {
-  if constexpr (F32IN) return *(const f32x4*)((const float*)base + off);
-  else return *(const i16x4*)((const uint16_t*)base + off);
-}
-template <bool F32IN>
-__device__ __forceinline__ f32x4 raw_f32(Raw4<F32IN> r) {
-  if constexpr (F32IN) return r;
-  else return f32x4{bf16_val(r[0]), bf16_val(r[1]), bf16_val(r[2]), bf16_val(r[3])};
-}
-// Four gate values of one token, channels c0 .. c0+3 at channel stride cs (0 or 1):
-// four element loads, the same code for both strides (no branch, so the prefetched
-// registers are not merged across paths, which would wait for the loads).
-__device__ __forceinline__ f32x4 load_gate4(const float* row, int cs, int c0) {
-  return f32x4{row[c0 * cs], row[(c0 + 1) * cs], row[(c0 + 2) * cs], row[(c0 + 3) * cs]};
-}
-
-// Inclusive prefix sum over each 16-lane DPP row (row_shr 1, 2, 4, 8; lanes shifted in
-// from outside the row read zero).
-__device__ __forceinline__ float row16_incl_scan(float x) {
-  auto dpp = [](float v, auto ctrl_c) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl_c)::value, 0xf, 0xf, true));
-  };
-  using std::integral_constant;
-  x += dpp(x, integral_constant<int, 0x111>{});
-  x += dpp(x, integral_constant<int, 0x112>{});
-  x += dpp(x, integral_constant<int, 0x114>{});
-  x += dpp(x, integral_constant<int, 0x118>{});
-  return x;
-}
-
-// One segment: sub-chunks [c_begin, c_end) of sequence bh, segment k of n.
-template <bool AGG, bool F32IN, bool OBF, bool PRO>
-__device__ __forceinline__ void sub_segment(KSubArgs& a, SubSmem<AGG>& sm, int* s_mzero, int tid,
-                                            int bh, int k, int n, int c_begin, int c_end) {
-  const int wave = tid >> 6, lane = tid & 63;
-  const int g = lane >> 4, c16 = lane & 15;
-  const int bi = bh / a.H, hi = bh % a.H;
-  const int64_t sidx = (int64_t)bh * a.nseg_max + k;
-  const bool last = k == n - 1;
-  if (!AGG && a.mode == SUB_ZERO && k > 0 && a.zc[sidx] < 0) return;  // M never vanished: the fix-up runs it
-  if (!AGG && a.mode == SUB_FIX && a.zc[sidx] >= 0) c_end = c_begin + a.zc[sidx];
-  const bool pred_final = !AGG && a.mode == SUB_FIX && (k == 1 || a.zc[sidx - 1] >= 0);
-
-  // ---- start state: Sr[kt][i] = S[16 kt + 4g + i][col0 + c16]
-  f32x4 Sr[4];
-  const int col0 = (wave & 3) * 16;
-  const int col = col0 + c16;
-  const bool is_m = AGG && wave >= 4;   // aggregate pass: M half of [N | M]
-  auto fill = [&](auto load) {
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Sr[kt][i] = load(16 * kt + 4 * g + i);
-  };
-  if (AGG) {
-    fill([&](int r) { return (is_m && r == col) ? 1.f : 0.f; });
-  } else if (k == 0 && a.has_s0) {
-    const int64_t o = bi * a.s0.s0 + hi * a.s0.s1 + col * a.s0.s3, rs = a.s0.s2;
-    if (a.s0.dt == MABA_F32) fill([&](int r) { return ((const float*)a.s0.p)[o + r * rs]; });
-    else if (a.s0.dt == MABA_BF16) fill([&](int r) { return bf16_bits_to_f32(((const uint16_t*)a.s0.p)[o + r * rs]); });
-    else fill([&](int r) { return __half2float(((const __half*)a.s0.p)[o + r * rs]); });
-  } else if (k == 0 || a.mode == SUB_ZERO) {
-    fill([&](int) { return 0.f; });
-  } else if (pred_final) {
-    const float* src = a.agg + (sidx - 1) * 64 * 128 + col;   // S_k = N_{k-1}
-    fill([&](int r) { return src[r * 128]; });
-  } else {
-    // the predecessor's M did not vanish: from the last exact N_j apply the maps of the
-    // segments between
-    const int* zc = a.zc + (int64_t)bh * a.nseg_max;
-    int j = k - 1;
-    while (j > 0 && zc[j] < 0) --j;
-    const float* agg = a.agg + (int64_t)bh * a.nseg_max * 64 * 128;
-    const float* src = agg + (int64_t)j * 64 * 128 + col;
-    fill([&](int r) { return src[r * 128]; });
-    for (int m = j + 1; m < k; ++m) apply_segment_map(agg + (int64_t)m * 64 * 128, Sr, col0, c16, g);
-  }
-  // the slab's loads complete here: inside the loop the compiler would otherwise count
-  // them as pending and wait for every outstanding load (the prefetch) before using it
-#pragma unroll
-  for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(Sr[kt][i]));
-
-  const int64_t qb = (int64_t)bi * a.qs0 + (int64_t)hi * a.qs1;
-  const int64_t kb = (int64_t)bi * a.ks0 + (int64_t)hi * a.ks1;
-  const int64_t vb = (int64_t)bi * a.vs0 + (int64_t)hi * a.vs1;
-  const float* gb = a.gp + (int64_t)bi * a.gs0 + (int64_t)hi * a.gs1;
-  const float* bb = a.bp + (int64_t)bi * a.bs0 + (int64_t)hi * a.bs1;
-  const float* wb = a.wp + (int64_t)bi * a.ws0 + (int64_t)hi * a.ws1;
-  const int64_t obase = (int64_t)bi * a.os0 + (int64_t)hi * a.os1 + col;
-
-  // ---- register prefetch of one sub-chunk's inputs: item (token st, channels c4..c4+3),
-  // tokens along the 16 lanes of a DPP row
-  const bool stager = tid < SC * 16;
-  const int st = tid & 15, c4 = (tid >> 4) * 4;
-  Raw4<F32IN> pq = {}, pk = {}, pv = {};
-  f32x4 pg = {}, pb = {}, pw = {};
-  // fused prologue: conv taps of tokens t-3 .. t (bf16 bits; taps before token 0 are
-  // loaded at token 0 and replaced by the history in the first sub-chunk), the gate
-  // projections and SiLU(conv k) of the staged token.  The head's conv weights go to LDS
-  // once per segment (the previous segment's last reads of them were before its last
-  // post-staging barrier).
-  i16x4 tq[4] = {}, tk[4] = {}, tv[4] = {}, xg[3] = {};
-  f32x4 kc = {};
-  const int ch = hi * 64 + c4;   // the stager's first channel of the projection rows
-  if (PRO) {
-    for (int i = tid; i < 3 * 4 * 64; i += blockDim.x) {
-      const int s = i >> 8, j = (i >> 6) & 3, cl = i & 63;
-      sm.cw[s][j][cl] = load_elem(a.cw[s], a.cwdt, (int64_t)(hi * 64 + cl) * a.cwsc[s] + j * a.cwst[s]);
-    }
-    lds_barrier();
-  }
-  // row tr + st of projection s at the stager's channels: a uniform base pointer plus a
-  // 32-bit lane offset, clamped to row 0 (rows before token 0 are replaced by the history)
-  auto prow = [&](int s, int tr) {
-    const uint16_t* base = a.px[s] + (int64_t)bi * a.pxs0[s];
-    return *(const i16x4*)(base + max(st * a.pxs1[s] + ch + tr * a.pxs1[s], ch));
-  };
-  auto prefetch = [&](int cc) {
-    const int tok = cc * SC + st;
-    if (!stager || tok >= a.L) return;
-    if constexpr (PRO) {
-      const int t0 = cc * SC;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (!AGG) tq[j] = prow(0, t0 - 3 + j);
-        tk[j] = prow(1, t0 - 3 + j);
-        tv[j] = prow(2, t0 - 3 + j);
-      }
-#pragma unroll
-      for (int s = 0; s < 3; ++s) xg[s] = prow(3 + s, t0);
-      return;
-    }
-    pk = load_raw4<F32IN>(a.k, kb + (int64_t)tok * a.ks2 + c4);
-    pv = load_raw4<F32IN>(a.vp, vb + (int64_t)tok * a.vs2 + c4);
-    if (!AGG) pq = load_raw4<F32IN>(a.q, qb + (int64_t)tok * a.qs2 + c4);
-    pg = load_gate4(gb + (int64_t)tok * a.gs2, a.gs3, c4);
-    pb = load_gate4(bb + (int64_t)tok * a.bs2, a.bs3, c4);
-    pw = load_gate4(wb + (int64_t)tok * a.ws2, a.ws3, c4);
-  };
-  prefetch(c_begin);
-
-  // outputs of a sub-chunk are stored during the next one's staging, before its prefetch:
-  // vmcnt counts stores, and a store issued just before the staging's wait for the
-  // prefetched rows would make that wait cover the store's latency
-  f32x4 obuf = {0.f, 0.f, 0.f, 0.f};
-  int ot0 = -1, ont = 0;
-  auto flush = [&]() {
-    if (AGG || ot0 < 0) return;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 4 * g + i;
-      if (t < ont) {
-        const int64_t off = obase + (int64_t)(ot0 + t) * a.os2;
-        if (OBF) ((uint16_t*)a.op)[off] = f32_to_bf16_bits(obuf[i]);
-        else ((float*)a.op)[off] = obuf[i];
-      }
-    }
-  };
-  // fused prologue: SiLU(depthwise conv) of the stager's four channels of stream s from
-  // the taps (oldest first)
-  auto conv4 = [&](int s, const i16x4 (&t)[4]) {
-    f32x4 w[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = *(const f32x4*)&sm.cw[s][j][c4];
-    f32x4 y;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float acc = w[3][e] * bf16_val(t[3][e]);
-      acc = fmaf(w[2][e], bf16_val(t[2][e]), acc);
-      acc = fmaf(w[1][e], bf16_val(t[1][e]), acc);
-      acc = fmaf(w[0][e], bf16_val(t[0][e]), acc);
-      y[e] = pro_silu(acc);
-    }
-    return y;
-  };
-  // taps before token 0 (first sub-chunk of the sequence) come from the history, or are zero
-  auto hist_taps = [&](int s, i16x4 (&t)[4]) {
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      if (st - 3 + j >= 0) continue;
-      i16x4 h = {0, 0, 0, 0};
-      if (a.ph[s]) {
-        const uint16_t* hp = a.ph[s] + (int64_t)bi * a.phs0[s] + (int64_t)ch * a.phs1[s] + (int64_t)(st + j) * a.phs2[s];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = (short)hp[(int64_t)e * a.phs1[s]];
-      }
-      t[j] = h;
-    }
-  };
-  // before the loop-top barrier of sub-chunk cc: SiLU(conv k) of the prefetched taps and the
-  // wave's |k|^2 partial per token (lanes 16 m + st hold channel groups 4 wave + m of token st)
-  auto pre_norm = [&](int cc) {
-    if (!PRO || !stager) return;
-    if (cc == 0) {
-      if (!AGG) hist_taps(0, tq);
-      hist_taps(1, tk);
-      hist_taps(2, tv);
-    }
-    kc = conv4(1, tk);
-    float ss = kc[0] * kc[0] + kc[1] * kc[1] + kc[2] * kc[2] + kc[3] * kc[3];
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
-    if (lane < 16) sm.nrm[cc & 1][wave][lane] = ss;
-  };
-
-  bool idle = false;                     // aggregate pass, M waves: the slab is exactly zero
-  if (AGG && tid < 4) s_mzero[tid] = 0;
-  if (tid == 0) sm.big[c_begin & 1] = 0;   // read after the first loop-top barrier
-  int c_stop = -1;
-
-  for (int c = c_begin; c < c_end; ++c) {
-    const int t0 = c * SC;
-    const int nt = min(SC, a.L - t0);
-    pre_norm(c);
-    lds_barrier();   // the previous sub-chunk is done with the shared buffers
-    if (AGG && s_mzero[0] && s_mzero[1] && s_mzero[2] && s_mzero[3]) {  // workgroup-uniform
-      c_stop = c;
-      break;
-    }
-    // ---- (1) stage and scale.  The 16 lanes of a DPP row hold the 16 tokens of one
-    // four-channel group, so the per-channel prefix Lam over the sub-chunk is a row scan
-    // in registers.  Tokens past the end stage as zeros (no decay, no write).
-    if (stager) {
-      const bool on = st < nt;
-      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-      f32x4 rk, rv, rq, rg, rb, rw;
-      if constexpr (PRO) {
-        const float n2 = (sm.nrm[c & 1][0][st] + sm.nrm[c & 1][1][st]) + (sm.nrm[c & 1][2][st] + sm.nrm[c & 1][3][st]);
-        rk = kc * pro_knorm_inv(n2, a.eps);
-        rv = conv4(2, tv);
-        rq = AGG ? z : conv4(0, tq);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          rg[i] = pro_log_decay(bf16_val(xg[0][i]));
-          rb[i] = pro_sigmoid(bf16_val(xg[1][i]));
-          rw[i] = pro_sigmoid(bf16_val(xg[2][i]));
-        }
-      } else {
-        rk = raw_f32<F32IN>(pk); rv = raw_f32<F32IN>(pv); rq = AGG ? z : raw_f32<F32IN>(pq);
-        rg = pg; rb = pb; rw = pw;
-      }
-      const f32x4 kk = on ? rk : z;
-      f32x4 la, bk, wv, lam, l15;
-      float mx = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float l = a.use_log ? rg[i] : __logf(fmaxf(rg[i], 1e-20f));
-        la[i] = on ? l : 0.f;
-        bk[i] = on ? rb[i] * rk[i] : 0.f;
-        wv[i] = on ? rw[i] * rv[i] : 0.f;
-        lam[i] = row16_incl_scan(la[i]);
-        l15[i] = __shfl(lam[i], lane | 15);
-        mx = fmaxf(mx, fabsf(lam[i]));
-      }
-      if (!(mx <= SUB_MFMA_RANGE)) sm.big[c & 1] = 1;   // benign race: every writer stores 1
-      // fp32 rows for the exact pair-by-pair path
-      *(f32x4*)&sm.K[st][c4] = kk;
-      *(f32x4*)&sm.BK[st][c4] = bk;
-      *(f32x4*)&sm.WV[st][c4] = wv;
-      *(f32x4*)&sm.LA[st][c4] = lam;
-      if (!AGG) *(f32x4*)&sm.Q[st][c4] = on ? rq : z;
-      // scaled operands, split into bf16 hi + lo; e^{-Lam} is used only when |Lam| <= 64
-      f32x4 e, ki, kc, bke;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        e[i] = __expf(lam[i]);
-        ki[i] = kk[i] * __expf(-lam[i]);
-        kc[i] = kk[i] * __expf(l15[i] - lam[i]);
-        bke[i] = bk[i] * e[i];
-      }
-      if (st == SC - 1) *(f32x4*)&sm.elast[c4] = e;
-      i16x4 h, l;
-      split4(bke, h, l);
-      *(i16x4*)(sm.BKEh + st * PITCH + c4) = h;
-      *(i16x4*)(sm.BKEl + st * PITCH + c4) = l;
-      split4(ki, h, l);
-      *(i16x4*)(sm.KIh + st * PITCH + c4) = h;
-      *(i16x4*)(sm.KIl + st * PITCH + c4) = l;
-      if (!AGG) {
-        split4((on ? rq : z) * e, h, l);
-        *(i16x4*)(sm.QEh + st * PITCH + c4) = h;
-        *(i16x4*)(sm.QEl + st * PITCH + c4) = l;
-      }
-      split4(kc, h, l);   // transposed: row = channel, column = token
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sm.KCh[(c4 + i) * TP + st] = h[i];
-        sm.KCl[(c4 + i) * TP + st] = l[i];
-      }
-    }
-    if (tid == 0) sm.big[(c + 1) & 1] = 0;   // last read in the previous sub-chunk
-    flush();
-    if (c + 1 < c_end) prefetch(c + 1);
-    lds_barrier();
-    const bool big = sm.big[c & 1] != 0;   // workgroup-uniform
-
-    // ---- (4) L and its inverse (wave 0), A (wave 1); every wave: v_e and q S for its columns
-    // tile of X (rows i) times KI^T (columns j): lane (c16, g) gets rows 4g + r of column j = c16
-    auto tile_mfma = [&](const short* Xh, const short* Xl) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const i16x8 xh = lds8(Xh, c16, 32 * p + 8 * g, PITCH), xl = lds8(Xl, c16, 32 * p + 8 * g, PITCH);
-        const i16x8 kh = lds8(sm.KIh, c16, 32 * p + 8 * g, PITCH), kl = lds8(sm.KIl, c16, 32 * p + 8 * g, PITCH);
-        acc = mma32(acc, kh, xh);   // D[j][i]: rows of KI as A, rows of X as B
-        acc = mma32(acc, kh, xl);
-        acc = mma32(acc, kl, xh);
-      }
-      return acc;   // lane (c16, g), element r: X_i . KI_j with i = c16, j = 4g + r
-    };
-    if (big) {
-      // strong decay: L and A pair by pair in fp32, exact exponentials (all 256 threads of
-      // the first four waves, pair (i, j) = (t / 16, t % 16))
-      if (tid < SC * SC) {
-        const int i = tid >> 4, j = tid & 15;
-        float lv = 0.f, av = 0.f;
-        if (j <= i) {
-          for (int cc = 0; cc < 64; ++cc) {
-            const float d = __expf(sm.LA[i][cc] - sm.LA[j][cc]) * sm.K[j][cc];
-            lv = fmaf(sm.BK[i][cc], d, lv);
-            if (!AGG) av = fmaf(sm.Q[i][cc], d, av);
-          }
-        }
-        sm.Lq[i][j & 3][j >> 2] = j < i ? lv : 0.f;
-        if (!AGG) {
-          const short hb = bf16_rn(av);
-          sm.Ah[i * TP + j] = hb;
-          sm.Al[i * TP + j] = bf16_rn(av - bf16_val(hb));
-        }
-      }
-      lds_barrier();
-    } else if (wave == 0) {
-      const f32x4 d = tile_mfma(sm.BKEh, sm.BKEl);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sm.Lq[c16][r][g] = (4 * g + r < c16) ? d[r] : 0.f;   // L[c16][4g + r]
-    } else if (!AGG && wave == 1) {
-      const f32x4 d = tile_mfma(sm.QEh, sm.QEl);
-      f32x4 v;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = (4 * g + r <= c16) ? d[r] : 0.f;
-      i16x4 h, l;
-      split4(v, h, l);
-      *(i16x4*)(sm.Ah + c16 * TP + 4 * g) = h;   // row i = c16, columns j = 4g .. 4g + 3
-      *(i16x4*)(sm.Al + c16 * TP + 4 * g) = l;
-    }
-    if (wave == 0) {
-      // T = (I + L)^-1 by forward substitution, x_i = [i == j] - sum_{m<i} L_im x_m for
-      // column j: the four lanes 4j .. 4j+3 split the sum by m mod 4 (lane p keeps x_m for
-      // m = p, p + 4, ...) and add their parts with two quad DPP steps, so a step costs
-      // four FMAs and two DPP adds.  L[i][m] = 0 for m >= i and x_m = 0 until computed,
-      // so the products need no guards.  (Wave 0 reads its own LDS writes above in order.)
-      const int jc = lane >> 2, p = lane & 3;
-      auto qadd = [](float v, auto ctrl_c) {
-        return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl_c)::value,
-                                                              0xf, 0xf, false));
-      };
-      float xm[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < SC; ++i) {
-        const f32x4 lv = *(const f32x4*)&sm.Lq[i][p][0];   // L[i][p + 4 r], r = 0..3
-        float part = (p == 0 && i == jc) ? 1.f : 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) part = fmaf(-lv[r], xm[r], part);
-        part = qadd(part, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
-        part = qadd(part, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
-        if (p == (i & 3)) xm[i >> 2] = part;
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {   // T[p + 4r][jc]
-        const short hb = bf16_rn(xm[r]);
-        sm.Th[(p + 4 * r) * TP + jc] = hb;
-        sm.Tl[(p + 4 * r) * TP + jc] = bf16_rn(xm[r] - bf16_val(hb));
-      }
-    }
-    // v_e = w*v - (b k e^Lam) S and q S: permuted K over the slab's row groups, lane
-    // (c16, g) gets tokens 4g + i of column col
-    i16x4 Sh[4], Sl[4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) split4(Sr[kt], Sh[kt], Sl[kt]);
-    auto state_product = [&](const short* Xh, const short* Xl) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const i16x8 xh = lds4x2(Xh, c16, 32 * p + 4 * g, PITCH), xl = lds4x2(Xl, c16, 32 * p + 4 * g, PITCH);
-        const i16x8 bh8 = cat8(Sh[2 * p], Sh[2 * p + 1]), bl8 = cat8(Sl[2 * p], Sl[2 * p + 1]);
-        acc = mma32(acc, xh, bh8);
-        acc = mma32(acc, xh, bl8);
-        acc = mma32(acc, xl, bh8);
-      }
-      return acc;
-    };
-    f32x4 ve = {0.f, 0.f, 0.f, 0.f}, qs = ve;
-    if (!idle) {
-      ve = state_product(sm.BKEh, sm.BKEl);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ve[i] = (is_m ? 0.f : sm.WV[4 * g + i][col]) - ve[i];
-    }
-    if (!AGG) qs = state_product(sm.QEh, sm.QEl);
-    lds_barrier();   // T (and A) are ready
-
-    // ---- (5) u = T v_e, (6) o = q S + A u, (7) S' = diag(e^{Lam_15}) S + K_C^T u
-    if (idle) continue;
-    i16x4 vh, vl;
-    split4(ve, vh, vl);
-    f32x4 u = {0.f, 0.f, 0.f, 0.f};
-    {
-      const i16x4 th = lds4(sm.Th, c16, 4 * g, TP), tl = lds4(sm.Tl, c16, 4 * g, TP);   // T[c16][4g..]
-      // D[m][n] = sum_k T[m][k] v_e[k][n]: A-operand rows of T, B-operand the v_e fragment
-      u = mma16(u, th, vh);
-      u = mma16(u, th, vl);
-      u = mma16(u, tl, vh);
-    }
-    i16x4 uh, ul;
-    split4(u, uh, ul);
-    if (!AGG) {
-      const i16x4 ah = lds4(sm.Ah, c16, 4 * g, TP), al = lds4(sm.Al, c16, 4 * g, TP);
-      f32x4 o = qs;
-      o = mma16(o, ah, uh);
-      o = mma16(o, ah, ul);
-      o = mma16(o, al, uh);
-      obuf = o;
-      ot0 = t0;
-      ont = nt;
-    }
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const f32x4 el = *(const f32x4*)(sm.elast + 16 * kt + 4 * g);
-      f32x4 acc = Sr[kt] * el;
-      const i16x4 kh = lds4(sm.KCh, 16 * kt + c16, 4 * g, TP), kl = lds4(sm.KCl, 16 * kt + c16, 4 * g, TP);
-      acc = mma16(acc, kh, uh);
-      acc = mma16(acc, kh, ul);
-      acc = mma16(acc, kl, uh);
-      Sr[kt] = acc;
-    }
-    if (AGG && is_m) {
-      bool nz = false;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) nz |= Sr[kt][i] != 0.f;
-      idle = __ballot(nz) == 0ull;
-      if (lane == 0) s_mzero[wave - 4] = idle;   // read after the next loop-top barrier
-    }
-  }
-
-  flush();   // the last sub-chunk's outputs
-  // ---- segment results
-  auto drain = [&](auto put) {
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) put(16 * kt + 4 * g + i, Sr[kt][i]);
-  };
-  if (AGG) {
-    if (tid == 0) a.zc[sidx] = c_stop >= 0 ? c_stop - c_begin : -1;
-    if (c_stop < 0) {  // M never vanished: [N | M] for the fix-up pass
-      float* dst = a.agg + sidx * 64 * 128 + (is_m ? 64 : 0) + col;
-      drain([&](int r, float v) { dst[r * 128] = v; });
-    }
-  } else if (a.mode == SUB_ZERO && !last) {  // N_k for the fix-up pass
-    float* dst = a.agg + sidx * 64 * 128 + col;
-    drain([&](int r, float v) { dst[r * 128] = v; });
-  } else if (last && !(a.mode == SUB_FIX && a.zc[sidx] >= 0)) {
-    const int64_t o = bi * a.sf.s0 + hi * a.sf.s1 + col * a.sf.s3, rs = a.sf.s2;
-    if (a.sf.dt == MABA_F32) drain([&](int r, float v) { ((float*)a.sf.p)[o + r * rs] = v; });
-    else if (a.sf.dt == MABA_BF16)
-      drain([&](int r, float v) { ((uint16_t*)a.sf.p)[o + r * rs] = f32_to_bf16_bits(v); });
-    else drain([&](int r, float v) { ((__half*)a.sf.p)[o + r * rs] = __float2half(v); });
-  }
-}
-
-template <bool AGG, bool F32IN, bool OBF, bool PRO>
-__global__ __launch_bounds__(AGG ? 512 : 256, AGG ? 1 : 2) void dgda_sub_kernel(SubArgs a) {
-  __shared__ SubSmem<AGG> sm;
-  __shared__ int s_mzero[4];
-  // Aggregate and fix-up passes: one workgroup per segment k >= 1.  Output pass: slot
-  // w covers the sub-chunks [U w, U w + U) of the (b,h)-major order, one segment per
-  // sequence it touches.
-  const bool per_segment = AGG || a.mode == SUB_FIX;
-  const int64_t total = (int64_t)a.BH * a.nchunks;
-  int64_t G = per_segment ? 0 : (int64_t)blockIdx.x * a.U;
-  const int64_t Gend = per_segment ? 1 : min(G + a.U, total);
-  while (G < Gend) {
-    int bh, k, n, c0, c1;
-    if (per_segment) {
-      const int per = a.nseg_max - 1;
-      bh = blockIdx.x / per;
-      k = blockIdx.x % per + 1;
-      n = seg_count_of(a.nchunks, a.U, bh);
-      if (k >= n) return;
-      seg_range_of(a.nchunks, a.U, bh, k, n, c0, c1);
-      G = Gend;
-    } else {
-      bh = (int)(G / a.nchunks);
-      const int64_t s = (int64_t)bh * a.nchunks;
-      c0 = (int)(G - s);
-      c1 = (int)(min(Gend, s + a.nchunks) - s);
-      k = c0 == 0 ? 0 : (int)(blockIdx.x - s / a.U);
-      n = seg_count_of(a.nchunks, a.U, bh);
-      G = s + c1;
-    }
-    // the thread index and the argument pointer pass through empty asm statements so
-    // that nothing derived from them is held across the segments
-    int tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    KSubArgs* ap = (KSubArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-    asm volatile("" : "+s"(ap));
-    sub_segment<AGG, F32IN, OBF, PRO>(*ap, sm, s_mzero, tid, bh, k, n, c0, c1);
-  }
-}
 
 // ------------------------------------------------------------------ host side
 
@@ -619,9 +13,10 @@ static bool fits32s(const maba_tensor* t) {
     if (t->stride[d] < 0 || t->stride[d] > INT32_MAX) return false;
   return true;
 }
-// fp32 gate with channel stride 0 (per token) or 1 (per channel, 16-byte aligned rows)
-static bool sub_gate_ok(const maba_tensor* t) {
-  if (!t || t->dtype != MABA_F32 || !fits32s(t)) return false;
+// gate with channel stride 0 (per token) or 1 (per channel, 16-byte aligned rows), fp32 or
+// (16-bit q, k, v) in q's dtype
+static bool sub_gate_ok(const maba_tensor* t, int gdt) {
+  if (!t || t->dtype != gdt || !fits32s(t)) return false;
   if (t->stride[3] == 0) return true;
   if (t->stride[3] != 1 || !al16s(t->data)) return false;
   for (int d = 0; d < 3; ++d)
@@ -629,22 +24,27 @@ static bool sub_gate_ok(const maba_tensor* t) {
   return true;
 }
 
+static bool sub_head_size(int64_t d) { return d == 32 || d == 64 || d == 128; }
+static bool sub_io_dtype(int dt) { return dt == MABA_BF16 || dt == MABA_F16 || dt == MABA_F32; }
+
 bool dgda_sub_supported(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                         const maba_tensor* gate, const maba_tensor* b, const maba_tensor* w,
                         const maba_tensor* out) {
   if (!q || !k || !v || !gate || !b) return false;
-  if (q->shape[3] != 64 || v->shape[3] != 64) return false;
+  if (!sub_head_size(q->shape[3]) || !sub_head_size(v->shape[3])) return false;
   const int dt = q->dtype;
-  if ((dt != MABA_BF16 && dt != MABA_F32) || k->dtype != dt || v->dtype != dt) return false;
+  if (!sub_io_dtype(dt) || k->dtype != dt || v->dtype != dt) return false;
   for (const maba_tensor* t : {q, k, v}) {   // 4-element (8- or 16-byte) loads
     if (t->stride[3] != 1 || !al16s(t->data) || !fits32s(t)) return false;
     for (int d = 0; d < 3; ++d)
       if (t->shape[d] > 1 && t->stride[d] % 4 != 0) return false;
   }
-  if (!sub_gate_ok(gate) || !sub_gate_ok(b)) return false;
-  if (w && !sub_gate_ok(w)) return false;
-  if (out && (out->stride[3] != 1 || !fits32s(out) || (out->dtype != MABA_BF16 && out->dtype != MABA_F32)))
-    return false;
+  // the three gates share one dtype: fp32, or q's 16-bit dtype
+  const int gdt = gate->dtype;
+  if (gdt != MABA_F32 && (gdt != dt || dt == MABA_F32)) return false;
+  if (!sub_gate_ok(gate, gdt) || !sub_gate_ok(b, gdt)) return false;
+  if (w && !sub_gate_ok(w, gdt)) return false;
+  if (out && (out->stride[3] != 1 || !fits32s(out) || !sub_io_dtype(out->dtype))) return false;
   return q->shape[2] <= ((int64_t)1 << 30);
 }
 
@@ -653,32 +53,35 @@ static SlotGeom sub_geom(int64_t BH, int64_t L) {
   return slot_geom(BH, nch, SUB_MIN_U);
 }
 
-size_t dgda_sub_workspace(int64_t BH, int64_t L) {
+// d_v = 128 runs as two d_v = 64 calls, one after the other on the stream, which share
+// the workspace.
+static int64_t sub_dv_call(int64_t dv) { return dv == 128 ? 64 : dv; }
+
+size_t dgda_sub_workspace(int64_t BH, int64_t L, int64_t dk, int64_t dv) {
   const SlotGeom gm = sub_geom(BH, L);
   if (gm.nseg_max <= 1) return 16;
   const int64_t nseg = gm.nseg_max;
-  return (size_t)(BH * nseg * 64 * 128) * sizeof(float) + (size_t)(BH * nseg) * sizeof(int);
+  return (size_t)(BH * nseg * dk * (sub_dv_call(dv) + dk)) * sizeof(float) + (size_t)(BH * nseg) * sizeof(int);
 }
 
-template <bool PRO>
-static int run_sub_passes(SubArgs& a, bool f32in, bool obf, hipStream_t stream);
+static int64_t esz(int dt) { return dt == MABA_F32 ? 4 : 2; }
 
 int launch_dgda_sub(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                     const maba_tensor* gate, int use_log, const maba_tensor* b,
                     const maba_tensor* w, const maba_tensor* s0, maba_tensor* out,
                     maba_tensor* sf, void* ws, size_t ws_bytes, hipStream_t stream) {
-  const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2];
+  const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2], dk = q->shape[3], dv = v->shape[3];
   const int64_t BH = B * H;
   SubArgs a = {};
   // strides fit in int32 (dgda_sub_supported checks every operand)
   a.q = q->data; a.qs0 = (int)q->stride[0]; a.qs1 = (int)q->stride[1]; a.qs2 = (int)q->stride[2];
   a.k = k->data; a.ks0 = (int)k->stride[0]; a.ks1 = (int)k->stride[1]; a.ks2 = (int)k->stride[2];
   a.vp = v->data; a.vs0 = (int)v->stride[0]; a.vs1 = (int)v->stride[1]; a.vs2 = (int)v->stride[2];
-  a.gp = (const float*)gate->data; a.gs0 = (int)gate->stride[0]; a.gs1 = (int)gate->stride[1];
+  a.gp = gate->data; a.gs0 = (int)gate->stride[0]; a.gs1 = (int)gate->stride[1];
   a.gs2 = (int)gate->stride[2]; a.gs3 = (int)gate->stride[3];
-  a.bp = (const float*)b->data; a.bs0 = (int)b->stride[0]; a.bs1 = (int)b->stride[1];
+  a.bp = b->data; a.bs0 = (int)b->stride[0]; a.bs1 = (int)b->stride[1];
   a.bs2 = (int)b->stride[2]; a.bs3 = (int)b->stride[3];
-  a.wp = (const float*)w->data; a.ws0 = (int)w->stride[0]; a.ws1 = (int)w->stride[1];
+  a.wp = w->data; a.ws0 = (int)w->stride[0]; a.ws1 = (int)w->stride[1];
   a.ws2 = (int)w->stride[2]; a.ws3 = (int)w->stride[3];
   a.s0 = view4(s0);
   a.op = out->data; a.os0 = (int)out->stride[0]; a.os1 = (int)out->stride[1]; a.os2 = (int)out->stride[2];
@@ -689,46 +92,38 @@ int launch_dgda_sub(const maba_tensor* q, const maba_tensor* k, const maba_tenso
   a.U = gm.U;
   a.nseg_max = gm.nseg_max;
   a.use_log = use_log; a.has_s0 = s0 != nullptr;
-  const size_t need = dgda_sub_workspace(BH, L);
+  a.f16 = q->dtype == MABA_F16; a.of16 = out->dtype == MABA_F16;
+  const size_t need = dgda_sub_workspace(BH, L, dk, dv);
   if (ws_bytes < need) return fail(MABA_ERR_WORKSPACE, "dgda_prefill: workspace too small");
-  const int64_t nsegs = BH * a.nseg_max;
+  const int64_t nsegs = BH * a.nseg_max, dvc = sub_dv_call(dv);
   a.agg = (float*)ws;
-  a.zc = (int*)(a.agg + nsegs * 64 * 128);
-  return run_sub_passes<false>(a, q->dtype == MABA_F32, out->dtype == MABA_BF16, stream);
+  a.zc = (int*)(a.agg + nsegs * dk * (dvc + dk));
+  const bool f32in = q->dtype == MABA_F32, g16 = gate->dtype != MABA_F32, o16 = out->dtype != MABA_F32;
+  auto run = [&](SubArgs& x) {
+    if (dk == 32) return run_sub_k32(x, (int)dvc, f32in, g16, o16, stream);
+    if (dk == 64) return run_sub_k64(x, (int)dvc, f32in, g16, o16, stream);
+    return run_sub_k128(x, (int)dvc, f32in, g16, o16, stream);
+  };
+  if (dv != 128) return run(a);
+  // the two halves of the value columns: v, w, the output and the states start 64
+  // columns further in the second call
+  for (int half = 0; half < 2; ++half) {
+    SubArgs h = a;
+    const int64_t c = 64 * half;
+    h.vp = (const char*)v->data + c * esz(v->dtype);
+    h.wp = (const char*)w->data + c * w->stride[3] * esz(w->dtype);
+    h.op = (char*)out->data + c * esz(out->dtype);
+    if (s0) h.s0.p = (const char*)s0->data + c * s0->stride[3] * esz(s0->dtype);
+    h.sf.p = (char*)sf->data + c * sf->stride[3] * esz(sf->dtype);
+    const int rc = run(h);
+    if (rc) return rc;
+  }
+  return MABA_OK;
 }
 
-// Workspace slots, then the aggregate, zero-start and fix-up passes (one zero-start pass
-// when every sequence fits one slot).  PRO: the fused-prologue inputs (bf16 projections).
-template <bool PRO>
-static int run_sub_passes(SubArgs& a, bool f32in, bool obf, hipStream_t stream) {
-  auto launch_out = [&](int mode) {
-    a.mode = mode;
-    const dim3 grid(mode == SUB_ZERO ? (unsigned)ceil_div((int64_t)a.BH * a.nchunks, a.U)
-                                     : (unsigned)(a.BH * (a.nseg_max - 1)));
-    if constexpr (PRO) {
-      if (obf) hipLaunchKernelGGL((dgda_sub_kernel<false, false, true, true>), grid, dim3(256), 0, stream, a);
-      else hipLaunchKernelGGL((dgda_sub_kernel<false, false, false, true>), grid, dim3(256), 0, stream, a);
-    } else {
-      if (f32in && obf) hipLaunchKernelGGL((dgda_sub_kernel<false, true, true, false>), grid, dim3(256), 0, stream, a);
-      else if (f32in) hipLaunchKernelGGL((dgda_sub_kernel<false, true, false, false>), grid, dim3(256), 0, stream, a);
-      else if (obf) hipLaunchKernelGGL((dgda_sub_kernel<false, false, true, false>), grid, dim3(256), 0, stream, a);
-      else hipLaunchKernelGGL((dgda_sub_kernel<false, false, false, false>), grid, dim3(256), 0, stream, a);
-    }
-    return check_launch("dgda_prefill/sub-chunk output");
-  };
-  if (a.nseg_max == 1) {
-    a.zc = nullptr;
-    return launch_out(SUB_ZERO);
-  }
-  a.mode = SUB_ZERO;
-  const dim3 agrid((unsigned)(a.BH * (a.nseg_max - 1)));
-  if constexpr (PRO) hipLaunchKernelGGL((dgda_sub_kernel<true, false, true, true>), agrid, dim3(512), 0, stream, a);
-  else if (f32in) hipLaunchKernelGGL((dgda_sub_kernel<true, true, true, false>), agrid, dim3(512), 0, stream, a);
-  else hipLaunchKernelGGL((dgda_sub_kernel<true, false, true, false>), agrid, dim3(512), 0, stream, a);
-  int rc = check_launch("dgda_prefill/sub-chunk aggregate");
-  if (rc) return rc;
-  if ((rc = launch_out(SUB_ZERO))) return rc;
-  return launch_out(SUB_FIX);
+int run_sub_k64(SubArgs& a, int dv, bool f32in, bool g16, bool obf, hipStream_t stream) {
+  return dv == 32 ? run_sub_passes<false, 64, 32>(a, f32in, g16, obf, stream)
+                  : run_sub_passes<false, 64, 64>(a, f32in, g16, obf, stream);
 }
 
 }  // namespace maba
@@ -736,7 +131,7 @@ static int run_sub_passes(SubArgs& a, bool f32in, bool obf, hipStream_t stream) 
 using namespace maba;
 
 extern "C" size_t maba_hip_dgda_layer_prefill_workspace_size(int64_t B, int64_t H, int64_t L) {
-  return dgda_sub_workspace(B * H, L);
+  return dgda_sub_workspace(B * H, L, 64, 64);
 }
 
 extern "C" int maba_hip_dgda_layer_prefill(const maba_tensor* const* xs, const maba_tensor* const* conv_w,
@@ -784,7 +179,7 @@ extern "C" int maba_hip_dgda_layer_prefill(const maba_tensor* const* xs, const m
   if (!expect_float(final_state, "final_state")) return MABA_ERR_DTYPE;
   if (initial_state && (!expect_shape(initial_state, "initial_state", 4, ss) || !expect_float(initial_state, "initial_state")))
     return MABA_ERR_INVALID;
-  const size_t need = dgda_sub_workspace(BH, L);
+  const size_t need = dgda_sub_workspace(BH, L, 64, 64);
   if (!workspace || workspace_bytes < need)
     return fail(MABA_ERR_WORKSPACE, "dgda_layer_prefill: workspace of %zu bytes required", need);
   if (B == 0) return MABA_OK;
@@ -813,7 +208,7 @@ extern "C" int maba_hip_dgda_layer_prefill(const maba_tensor* const* xs, const m
   a.agg = (float*)workspace;
   a.zc = (int*)(a.agg + nsegs * 64 * 128);
   hipStream_t st = (hipStream_t)stream;
-  const int rc = run_sub_passes<true>(a, false, out->dtype == MABA_BF16, st);
+  const int rc = run_sub_passes<true, 64, 64>(a, false, false, out->dtype == MABA_BF16, st);
   if (rc) return rc;
   // after the passes, which read the old history: the new one may overwrite it in place
   return launch_dgda_new_history(xs, hist, new_hist, st);

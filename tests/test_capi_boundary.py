@@ -115,10 +115,23 @@ def test_prefill_workspace_size_at_baseline_shape(lib):
     U, nseg = _slot_geometry(B * H, T // 16, min_u=64)
     assert (U, nseg) == (160, 14)
     assert lib.maba_hip_dgda_prefill_workspace_size(q, q, per_channel, gate) == B * H * nseg * (64 * 128 * 4 + 4)
-    # other head sizes take the sequential kernel, which needs no workspace
+    # d_k = d_v = 32: the sub-chunk path with 32 x 64 segment maps
     q32 = _t([B, H, T, 32])
     pc32 = _t([B, H, T, 32], N.MABA_F32)
-    assert lib.maba_hip_dgda_prefill_workspace_size(q32, q32, pc32, pc32) == 0
+    assert lib.maba_hip_dgda_prefill_workspace_size(q32, q32, pc32, pc32) == B * H * nseg * (32 * 64 * 4 + 4)
+    # d_k = 128, d_v = 128: two calls over the value halves share 128 x (64 + 128) maps
+    q128 = _t([B, H, T, 128])
+    pc128 = _t([B, H, T, 128], N.MABA_F32)
+    assert lib.maba_hip_dgda_prefill_workspace_size(q128, q128, pc128, pc128) == B * H * nseg * (128 * 192 * 4 + 4)
+    # fp16 q with fp16 gates (one dtype, the reference's contract) also takes it
+    qh = _t([B, H, T, 64], N.MABA_F16)
+    gh = _t([B, H, T, 64], N.MABA_F16)
+    assert lib.maba_hip_dgda_prefill_workspace_size(qh, qh, gh, gh) == B * H * nseg * (64 * 128 * 4 + 4)
+    # head sizes outside {32, 64, 128} and bf16 gates with fp32 q take the sequential kernel
+    q48 = _t([B, H, T, 48])
+    assert lib.maba_hip_dgda_prefill_workspace_size(q48, q48, _t([B, H, T, 48], N.MABA_F32), _t([B, H, T, 48], N.MABA_F32)) == 0
+    qf = _t([B, H, T, 64], N.MABA_F32)
+    assert lib.maba_hip_dgda_prefill_workspace_size(qf, qf, _t([B, H, T, 64]), _t([B, H, T, 64])) == 0
 
 
 def test_index_topk_decode_validation(lib):

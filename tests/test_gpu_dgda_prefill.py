@@ -1,4 +1,6 @@
-"""Chunked MFMA DGDA prefill (per-token gates, dk = dv = 64, bf16 q/k/v) vs the oracle.
+"""DGDA prefill on the GPU vs the oracle: the chunked MFMA path (per-token gates, dk = dv
+= 64, bf16 q/k/v) and the sub-chunk MFMA path (per-channel gates, every head size in
+{32, 64, 128}, bf16, fp16 and fp32).
 
 Tolerance: rtol = atol = 2e-3 on fp32 outputs and final states for bf16 inputs
 with fp32 accumulation.  bf16 outputs are checked to be
@@ -39,10 +41,14 @@ def test_chunk_path_is_selected(dev):
     n2 = lib.maba_hip_dgda_prefill_workspace_size(N.desc(inp["q"]), N.desc(inp["v"]), N.desc(inp["log_alpha"]),
                                                   N.desc(inp["b"]))
     assert n2 > 16
-    small = dgda_inputs(1, 2, 4096, dk=32, dv=32, seed=0, device=dev)   # other head sizes -> sequential kernel
+    small = dgda_inputs(1, 2, 4096, dk=32, dv=32, seed=0, device=dev)   # other head sizes -> sub-chunk path
     n3 = lib.maba_hip_dgda_prefill_workspace_size(N.desc(small["q"]), N.desc(small["v"]),
                                                   N.desc(small["log_alpha"]), N.desc(small["b"]))
-    assert n3 == 0
+    assert n3 > 16
+    odd = dgda_inputs(1, 2, 4096, dk=48, dv=48, seed=0, device=dev)     # no MFMA path: sequential kernel
+    n4 = lib.maba_hip_dgda_prefill_workspace_size(N.desc(odd["q"]), N.desc(odd["v"]),
+                                                  N.desc(odd["log_alpha"]), N.desc(odd["b"]))
+    assert n4 == 0
 
 
 @pytest.mark.parametrize("decay", ["baseline", "slow", "none"])
@@ -307,6 +313,86 @@ def test_subchunk_path_config2_shape_split_chaining(dev):
            for k, v in inp.items()}
     eo, _ = odgda.dgda_prefill_seq(**oracle_dgda_args(few))
     assert_close(o[:1, :2, :4096], eo, 2e-3, 2e-3, "oracle heads")
+
+
+# ----------------------------------------------------------------------------- head sizes and dtypes
+# Every head size the reference's GPU prefill takes (d_k, d_v in {32, 64, 128},
+# triton_dgda.py:389-396) runs on the sub-chunk MFMA path; d_v = 128 as two calls over the
+# halves of the value columns.  Each case asserts that path from its workspace size (the
+# sequential kernel takes none) and spans at least two segments, so the aggregate and
+# fix-up passes run: "baseline" decay lets every segment map vanish, "slow" keeps them
+# alive, "strong" adds decays down to e^-30 per token (pair-by-pair sub-chunks).
+
+def _sub_workspace_size(inp):
+    from maba_sparse import _native as N
+    lib = N.load()
+    return lib.maba_hip_dgda_prefill_workspace_size(N.desc(inp["q"]), N.desc(inp["v"]), N.desc(inp["log_alpha"]),
+                                                    N.desc(inp["b"]))
+
+
+def _expected_sub_workspace(B, H, L, dk, dv, cus):
+    """Slots of U = max(64, ceil(B*H*nch / (2 CUs))) sub-chunks of 16 tokens; a sequence of nch
+    > U sub-chunks spans at most ceil((nch - 1) / U) + 1 segments, each holding a d_k x
+    (d_v + d_k) fp32 segment map (d_v of one call: 64 when d_v = 128) and an int32 count."""
+    nch = -(-L // 16)
+    U = max(64, -(-B * H * nch // (2 * cus)))
+    nseg = 1 if nch <= U else -(-(nch - 1) // U) + 1
+    dvc = 64 if dv == 128 else dv
+    return B * H * nseg * (dk * (dvc + dk) * 4 + 4), nseg
+
+
+@pytest.mark.parametrize("dk,dv", [(32, 32), (32, 64), (32, 128), (64, 32), (64, 128), (128, 32), (128, 64),
+                                   (128, 128)])
+@pytest.mark.parametrize("decay,L,qkv", [("baseline", 1100, torch.bfloat16), ("slow", 3000, torch.float32),
+                                         ("strong", 2100, torch.bfloat16)])
+def test_subchunk_head_sizes_vs_oracle(dev, dk, dv, decay, L, qkv):
+    B, H = 1, 2
+    inp = dgda_inputs(B, H, L, dk=dk, dv=dv, seed=dk + 3 * dv + L, decay="baseline" if decay == "strong" else decay,
+                      gates="channel", qkv_dtype=qkv, device=dev, with_state=(decay != "baseline"))
+    if decay == "strong":
+        la = inp["log_alpha"]
+        pick = torch.rand(la.shape, generator=torch.Generator().manual_seed(5)).to(dev) < 0.1
+        inp["log_alpha"] = torch.where(pick, la * 15, la)
+    n = _sub_workspace_size(inp)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    want, nseg = _expected_sub_workspace(B, H, L, dk, dv, cus)
+    assert nseg >= 2 and n == want and n > 16, (n, want, nseg)
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, f"out dk={dk} dv={dv} {decay}")
+    assert_close(S, eS, 2e-3, 2e-3, f"state dk={dk} dv={dv} {decay}")
+
+
+@pytest.mark.parametrize("dk,dv", [(64, 64), (32, 128), (128, 32)])
+def test_subchunk_fp16_same_dtype_contract(dev, dk, dv):
+    """Every tensor fp16 (the reference's contract without mixed dtypes: gates in q's dtype),
+    through the dispatcher with chunk_size 16: fp16 output and state within 2e-3 of the
+    float64 recurrence on the fp16-rounded inputs, and the fp16 output is the rounding of
+    the kernel's fp32 result (fp32 output requested from the same fp16 inputs)."""
+    from maba_sparse.kernels.dispatcher import dispatch_dgda_prefill
+    B, H, L = 1, 3, 1500
+    inp = dgda_inputs(B, H, L, dk=dk, dv=dv, seed=dk * dv, decay="slow", gates="channel", qkv_dtype=torch.float16,
+                      gate_dtype=torch.float16, device=dev, with_state=True)
+    inp["initial_state"] = inp["initial_state"].half()
+    assert _sub_workspace_size(inp) > 16
+    o, S = dispatch_dgda_prefill(**inp, chunk_size=16)
+    assert o.dtype == torch.float16 and S.dtype == torch.float16
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, "fp16 out")
+    assert_close(S, eS, 2e-3, 2e-3, "fp16 state")
+    o32, _ = _hip().hip_dgda_prefill(**inp, out_dtype=torch.float32, state_dtype=torch.float32)
+    assert torch.equal(o, o32.to(torch.float16))
+
+
+def test_subchunk_bf16_gates(dev):
+    """bf16 q, k, v and bf16 gates (16-bit gate loads), per-token and per-channel."""
+    for gates in ("scalar", "channel"):
+        inp = dgda_inputs(2, 2, 1200, seed=77, decay="slow", gates=gates, gate_dtype=torch.bfloat16, device=dev)
+        assert _sub_workspace_size(inp) > 16
+        o, S = _run(inp)
+        eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+        assert_close(o, eo, 2e-3, 2e-3, f"out {gates}")
+        assert_close(S, eS, 2e-3, 2e-3, f"state {gates}")
 
 
 # ----------------------------------------------------------------------------- config 1
