@@ -93,10 +93,11 @@ __global__ __launch_bounds__(256) void dgda_step_kernel(StepArgs a) {
   }
 }
 
-// Fast path for dk = dv = 64 with state rows of unit column stride (fp32 or bf16), q/k/v
-// of one dtype (bf16 or fp32) and fp32 gates: one 256-thread workgroup per (b, h), wave w
-// owning state rows 16w .. 16w+15 and lane c the state column c.  Each lane issues its 16
-// row loads at once and keeps them in registers; the per-row scalars (decay, b*k, k, q) are
+// Fast path for dk, dv in {32, 64, 128} with state rows of unit column stride (fp32 or bf16;
+// contiguous rows unless dk = dv = 64), q/k/v of one dtype (bf16 or fp32) and fp32 gates: one
+// 256-thread workgroup per (b, h), wave w owning state rows (dk/4) w .. (dk/4)(w+1) - 1 and
+// lane c the state column c (and c + 64 when dv = 128).  Each lane issues its row loads at
+// once and keeps them in registers; the per-row scalars (decay, b*k, k, q) are
 // broadcast from the lane that loaded them with readlane, and the two column reductions
 // over the rows (b k^T S' and q^T S_new) are summed per wave, then over the four waves in
 // LDS in a fixed order.
@@ -124,88 +125,166 @@ __device__ __forceinline__ float cvt<float>(float x) { return x; }
 template <>
 __device__ __forceinline__ float cvt<uint16_t>(uint16_t x) { return bf16_bits_to_f32(x); }
 
-// Row offset i of a state slab: rows 64 elements apart (CONTIG, the layout every caller
+// Row offset i of a state slab: rows DV elements apart (CONTIG, the layout every caller
 // uses: one base address and immediate offsets) or a run-time 32-bit row stride.
-template <bool CONTIG>
-__device__ __forceinline__ int64_t row_at(int i, int rs) { return CONTIG ? (int64_t)(64 * i) : (int64_t)i * rs; }
+template <bool CONTIG, int DV = 64>
+__device__ __forceinline__ int64_t row_at(int i, int rs) { return CONTIG ? (int64_t)(DV * i) : (int64_t)i * rs; }
 
-// The 16 rows of wave w's slab, S[16w + i][lane], from sp = &S[16w][lane] (rs: row stride),
-// as stored (converted by the caller once every load of the step is issued).
-template <typename TS, bool CONTIG>
-__device__ __forceinline__ void load_rows(TS (&s)[16], const TS* sp, int rs) {
+// Head sizes of the fast step: d_k / 4 state rows per wave (four waves), step_nc columns per lane
+// (lane c holds columns c and c + 64 when d_v = 128), step_nr row-scalar registers per lane (lane
+// r holds the scalars of rows r and r + 64 when d_k = 128).
+constexpr int step_nc(int dv) { return dv > 64 ? 2 : 1; }
+constexpr int step_nr(int dk) { return dk > 64 ? 2 : 1; }
+
+// The RPW rows of wave w's slab, S[RPW w + i][col + 64 j], from sp = &S[RPW w][col] (rs: row
+// stride), as stored (converted by the caller once every load of the step is issued).
+template <typename TS, bool CONTIG, int DK = 64, int DV = 64>
+__device__ __forceinline__ void load_rows(TS (&s)[step_nc(DV)][DK / 4], const TS* sp, int rs) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = sp[row_at<CONTIG>(i, rs)];
+  for (int j = 0; j < step_nc(DV); ++j)
+#pragma unroll
+    for (int i = 0; i < DK / 4; ++i) s[j][i] = sp[row_at<CONTIG, DV>(i, rs) + 64 * j];
 }
 
-// The step on the rows of wave w (lane = column): s[i] holds S[16w + i][lane] on entry;
-// al, bk, kr, qr are the row scalars of row `lane`, vw = w_lane v_lane.  Writes the new state
-// rows through np = &S_new[16w][lane] (row stride nrs) and returns o[lane] (every wave).
-// Every state load of the caller precedes the first store, so S_new may alias S.
-template <typename TS, bool CONTIG>
-__device__ __forceinline__ float step_rows(float (&s)[16], float al, float bk, float kr, float qr, float vw,
-                                           TS* np, int nrs, float (*s_red)[64]) {
+// Row r's scalar from the lane that holds it (r wave-uniform).
+template <int NR>
+__device__ __forceinline__ float row_scalar(const float (&x)[NR], int r) {
+  if constexpr (NR == 1) return bcast(x[0], r);
+  else return r < 64 ? bcast(x[0], r) : bcast(x[1], r - 64);
+}
+
+// The step on the rows of wave w (lane = column): s[j][i] holds S[RPW w + i][lane + 64 j] on
+// entry; al, bk, kr, qr are the row scalars (register m: row 64 m + lane), vw[j] = w v of
+// column lane + 64 j.  Writes the new state rows through np = &S_new[RPW w][lane] (row stride
+// nrs; columns at or past d_v are not written) and returns o of the lane's columns (every
+// wave).  Every state load of the caller precedes the first store, so S_new may alias S.
+template <typename TS, bool CONTIG, int DK = 64, int DV = 64>
+__device__ __forceinline__ void step_rows(float (&s)[step_nc(DV)][DK / 4],
+                                          const float (&al)[step_nr(DK)],
+                                          const float (&bk)[step_nr(DK)],
+                                          const float (&kr)[step_nr(DK)],
+                                          const float (&qr)[step_nr(DK)],
+                                          const float (&vw)[step_nc(DV)], TS* np, int nrs,
+                                          float (*s_red)[64 * step_nc(DV)],
+                                          float (&o)[step_nc(DV)]) {
+  constexpr int RPW = DK / 4, NC = step_nc(DV), NR = step_nr(DK);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  float pred = 0.f;
+  const bool colok = DV >= 64 || lane < DV;
+  float pred[NC];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int r = 16 * wave + i;
-    s[i] *= bcast(al, r);
-    pred = fmaf(bcast(bk, r), s[i], pred);
+  for (int j = 0; j < NC; ++j) pred[j] = 0.f;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int r = RPW * wave + i;
+    const float a_r = row_scalar<NR>(al, r), b_r = row_scalar<NR>(bk, r);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      s[j][i] *= a_r;
+      pred[j] = fmaf(b_r, s[j][i], pred[j]);
+    }
   }
-  s_red[wave][lane] = pred;
-  __syncthreads();
-  pred = (s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane]);
-  const float delta = vw - pred;
-  float o = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int r = 16 * wave + i;
-    const float sn = fmaf(bcast(kr, r), delta, s[i]);
-    if constexpr (sizeof(TS) == 4) np[row_at<CONTIG>(i, nrs)] = sn;
-    else np[row_at<CONTIG>(i, nrs)] = f32_to_bf16_bits(sn);
-    o = fmaf(bcast(qr, r), sn, o);   // the fp32 state before its rounding, as the generic kernel
+  for (int j = 0; j < NC; ++j) s_red[wave][64 * j + lane] = pred[j];
+  __syncthreads();
+  float delta[NC], oo[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = 64 * j + lane;
+    delta[j] = vw[j] - ((s_red[0][c] + s_red[1][c]) + (s_red[2][c] + s_red[3][c]));
+    oo[j] = 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int r = RPW * wave + i;
+    const float k_r = row_scalar<NR>(kr, r), q_r = row_scalar<NR>(qr, r);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const float sn = fmaf(k_r, delta[j], s[j][i]);
+      if (colok) {
+        if constexpr (sizeof(TS) == 4) np[row_at<CONTIG, DV>(i, nrs) + 64 * j] = sn;
+        else np[row_at<CONTIG, DV>(i, nrs) + 64 * j] = f32_to_bf16_bits(sn);
+      }
+      oo[j] = fmaf(q_r, sn, oo[j]);   // the fp32 state before its rounding, as the generic kernel
+    }
   }
   __syncthreads();   // every wave has read s_red before it is reused
-  s_red[wave][lane] = o;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) s_red[wave][64 * j + lane] = oo[j];
   __syncthreads();
-  return (s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane]);
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = 64 * j + lane;
+    o[j] = (s_red[0][c] + s_red[1][c]) + (s_red[2][c] + s_red[3][c]);
+  }
 }
 
 // T: dtype of q, k, v; TS: dtype of the state in and out (fp32 or bf16); HS: a state is
-// given (else zeros); CONTIG: state rows 64 elements apart in and out.  The slab and the row
-// scalars are all loaded before the first wait, so the step waits for one memory round trip
-// (a run-time null test around the slab loads, or 64-bit strided addresses per row, made the
-// compiler wait for the slab before it issued the scalars).
-template <typename T, typename TS, bool HS, bool CONTIG>
+// given (else zeros); CONTIG: state rows d_v elements apart in and out; DK, DV in {32, 64,
+// 128}.  The slab and the row scalars are all loaded before the first wait, so the step waits
+// for one memory round trip (a run-time null test around the slab loads, or 64-bit strided
+// addresses per row, made the compiler wait for the slab before it issued the scalars).
+// With d_v = 32 the upper 32 lanes load column 31 again and store nothing; with d_k = 32
+// lanes 32 .. 63 load the scalars of row 31 again (never broadcast).
+template <typename T, typename TS, bool HS, bool CONTIG, int DK = 64, int DV = 64>
 __global__ __launch_bounds__(256) void dgda_step_wave_kernel(StepFast a) {
-  __shared__ float s_red[4][64];
+  constexpr int RPW = DK / 4, NC = step_nc(DV), NR = step_nr(DK);
+  __shared__ float s_red[4][64 * NC];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t bi = blockIdx.y, hi = blockIdx.x;   // grid (H, B): no division
-  TS raw[16];
+  const int col = DV >= 64 ? lane : min(lane, DV - 1);
+  TS raw[NC][RPW];
   if constexpr (HS)
-    load_rows<TS, CONTIG>(raw, (const TS*)a.state + (bi * a.ssb + hi * a.ssh + row_at<CONTIG>(16 * wave, a.ssr32) + lane),
-                          a.ssr32);
-  // lane r holds the row-r scalars; lane c holds w_c v_c.  The (b, h) base is scalar and the
-  // lane's offset a 32-bit unsigned product (the host checks that 63 * stride fits)
-  const uint32_t l = lane;
-  const T kx = ((const T*)a.k + (bi * a.ksb + hi * a.ksh))[l * (uint32_t)a.ksd];
-  const T qx = ((const T*)a.q + (bi * a.qsb + hi * a.qsh))[l * (uint32_t)a.qsd];
-  const T vx = ((const T*)a.v + (bi * a.vsb + hi * a.vsh))[l * (uint32_t)a.vsd];
-  const float gr = (a.gate + (bi * a.gsb + hi * a.gsh))[l * (uint32_t)a.gsd];
-  const float br = (a.bb + (bi * a.bsb + hi * a.bsh))[l * (uint32_t)a.bsd];
-  const float wc = (a.ww + (bi * a.wsb + hi * a.wsh))[l * (uint32_t)a.wsd];
+    load_rows<TS, CONTIG, DK, DV>(raw, (const TS*)a.state + (bi * a.ssb + hi * a.ssh +
+                                                               row_at<CONTIG, DV>(RPW * wave, a.ssr32) + col),
+                                  a.ssr32);
+  // lane r holds the row-r scalars (and row r + 64's); lane c holds w_c v_c (and column c +
+  // 64's).  The (b, h) base is scalar and the lane's offset a 32-bit unsigned product (the host
+  // checks that 127 * stride fits)
+  T kx[NR], qx[NR];
+  float gr[NR], br[NR];
+#pragma unroll
+  for (int m = 0; m < NR; ++m) {
+    const uint32_t l = DK >= 64 ? (uint32_t)(lane + 64 * m) : (uint32_t)min(lane, DK - 1);
+    kx[m] = ((const T*)a.k + (bi * a.ksb + hi * a.ksh))[l * (uint32_t)a.ksd];
+    qx[m] = ((const T*)a.q + (bi * a.qsb + hi * a.qsh))[l * (uint32_t)a.qsd];
+    gr[m] = (a.gate + (bi * a.gsb + hi * a.gsh))[l * (uint32_t)a.gsd];
+    br[m] = (a.bb + (bi * a.bsb + hi * a.bsh))[l * (uint32_t)a.bsd];
+  }
+  T vx[NC];
+  float wc[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const uint32_t c = (uint32_t)(col + 64 * j);
+    vx[j] = ((const T*)a.v + (bi * a.vsb + hi * a.vsh))[c * (uint32_t)a.vsd];
+    wc[j] = (a.ww + (bi * a.wsb + hi * a.wsh))[c * (uint32_t)a.wsd];
+  }
   // every load above is issued before the first use waits (with 16-bit state rows the compiler
   // otherwise converts the first rows, and waits for them, before issuing the rest; with fp32
   // rows it issues them all and overlaps the first reduction with their arrival)
   if constexpr (sizeof(TS) == 2) __builtin_amdgcn_sched_barrier(0);
-  float s[16];
+  float s[NC][RPW];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = HS ? cvt<TS>(raw[i]) : 0.f;
-  const float kr = cvt<T>(kx), qr = cvt<T>(qx), vc = cvt<T>(vx);
-  const float al = a.use_log ? __expf(gr) : gr;
-  TS* np = (TS*)a.nst + (bi * a.nsb + hi * a.nsh + row_at<CONTIG>(16 * wave, a.nsr32) + lane);
-  const float o = step_rows<TS, CONTIG>(s, al, br * kr, kr, qr, wc * vc, np, a.nsr32, s_red);
-  if (wave == 0) store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + lane * a.osd, o);
+  for (int j = 0; j < NC; ++j)
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) s[j][i] = HS ? cvt<TS>(raw[j][i]) : 0.f;
+  float kr[NR], qr[NR], al[NR], bk[NR], vw[NC];
+#pragma unroll
+  for (int m = 0; m < NR; ++m) {
+    kr[m] = cvt<T>(kx[m]);
+    qr[m] = cvt<T>(qx[m]);
+    al[m] = a.use_log ? __expf(gr[m]) : gr[m];
+    bk[m] = br[m] * kr[m];
+  }
+#pragma unroll
+  for (int j = 0; j < NC; ++j) vw[j] = wc[j] * cvt<T>(vx[j]);
+  TS* np = (TS*)a.nst + (bi * a.nsb + hi * a.nsh + row_at<CONTIG, DV>(RPW * wave, a.nsr32) + lane);
+  float o[NC];
+  step_rows<TS, CONTIG, DK, DV>(s, al, bk, kr, qr, vw, np, a.nsr32, s_red, o);
+  if (wave == 0) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+      if (lane + 64 * j < DV) store_elem(a.out, a.odt, bi * a.osb + hi * a.osh + (lane + 64 * j) * a.osd, o[j]);
+  }
 }
 
 // One decode token of the DGDA layer after its input projection, in one launch: the
@@ -242,7 +321,7 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t bi = blockIdx.y, hi = blockIdx.x;   // grid (H, B): no division
   const int64_t c = hi * 64 + lane;   // channel of the projection rows
-  TS raw[16];
+  TS raw[1][16];
   if constexpr (HS)
     load_rows<TS, CONTIG>(raw, (const TS*)a.state + (bi * a.ssb + hi * a.ssh + row_at<CONTIG>(16 * wave, a.ssr32) + lane),
                           a.ssr32);
@@ -261,9 +340,9 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
     }
   }
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the first use waits
-  float s[16], x[6], w[3][4], h[3][3];
+  float s[1][16], x[6], w[3][4], h[3][3];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = HS ? cvt<TS>(raw[i]) : 0.f;
+  for (int i = 0; i < 16; ++i) s[0][i] = HS ? cvt<TS>(raw[0][i]) : 0.f;
 #pragma unroll
   for (int st = 0; st < 6; ++st) x[st] = bf16_bits_to_f32(xr[st]);
 #pragma unroll
@@ -297,9 +376,11 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
   // before the step's first barrier, so no wave still reads the history when wave 0
   // overwrites it (in place) after the barriers below.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  const float al = __expf(gr);
+  const float al[1] = {__expf(gr)}, bk[1] = {br * kr}, krr[1] = {kr}, qrr[1] = {qr}, vw[1] = {wc * vc};
   TS* np = (TS*)a.nst + (bi * a.nsb + hi * a.nsh + row_at<CONTIG>(16 * wave, a.nsr32) + lane);
-  const float o = step_rows<TS, CONTIG>(s, al, br * kr, kr, qr, wc * vc, np, a.nsr32, s_red);
+  float ov[1];
+  step_rows<TS, CONTIG>(s, al, bk, krr, qrr, vw, np, a.nsr32, s_red, ov);
+  const float o = ov[0];
   if (wave == 0) {
 #pragma unroll
     for (int st = 0; st < 3; ++st) {   // new history: the inputs of tokens -2, -1, 0
@@ -316,8 +397,31 @@ __global__ __launch_bounds__(256) void dgda_layer_step_kernel(LayerStepArgs a) {
 
 using namespace maba;
 
-// The fast kernel's per-lane offsets of the [B,H,64] operands are 32-bit unsigned products
-// lane * stride (at most 63 * stride elements of up to 4 bytes).
+// The fast kernel for head sizes other than 64 x 64 (contiguous state rows): d_k, d_v in
+// {32, 64, 128}, bf16 or fp32 q/k/v (bq), bf16 or fp32 state (sbf), a state given or not (hs).
+template <int DK, int DV>
+static void (*step_kernel_dims(bool bq, bool sbf, bool hs))(StepFast) {
+#define MABA_STEP_SZ(T, TS) \
+  return hs ? dgda_step_wave_kernel<T, TS, true, true, DK, DV> : dgda_step_wave_kernel<T, TS, false, true, DK, DV>
+  if (bq) { if (sbf) MABA_STEP_SZ(uint16_t, uint16_t); MABA_STEP_SZ(uint16_t, float); }
+  if (sbf) MABA_STEP_SZ(float, uint16_t);
+  MABA_STEP_SZ(float, float);
+#undef MABA_STEP_SZ
+}
+template <int DK>
+static void (*step_kernel_dk(int64_t dv, bool bq, bool sbf, bool hs))(StepFast) {
+  if (dv == 32) return step_kernel_dims<DK, 32>(bq, sbf, hs);
+  if (dv == 64) return step_kernel_dims<DK, 64>(bq, sbf, hs);
+  return step_kernel_dims<DK, 128>(bq, sbf, hs);
+}
+static void (*step_kernel_sized(int64_t dk, int64_t dv, bool bq, bool sbf, bool hs))(StepFast) {
+  if (dk == 32) return step_kernel_dk<32>(dv, bq, sbf, hs);
+  if (dk == 64) return step_kernel_dk<64>(dv, bq, sbf, hs);
+  return step_kernel_dk<128>(dv, bq, sbf, hs);
+}
+
+// The fast kernel's per-lane offsets of the [B,H,d] operands are 32-bit unsigned products
+// lane * stride (at most 127 * stride elements of up to 4 bytes).
 static bool lane_strides_fit(std::initializer_list<const maba_tensor*> ts) {
   for (const maba_tensor* t : ts)
     if (t->stride[2] < 0 || t->stride[2] > ((int64_t)1 << 24)) return false;
@@ -370,7 +474,11 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
   const maba_tensor* gate = log_alpha ? log_alpha : alpha;
   const bool qkv_same = q->dtype == k->dtype && q->dtype == v->dtype && (q->dtype == MABA_BF16 || q->dtype == MABA_F32);
   const int sdt = new_state->dtype;
-  const bool fast = dk == 64 && dv == 64 && qkv_same && gate->dtype == MABA_F32 && b->dtype == MABA_F32 &&
+  auto head_ok = [](int64_t d) { return d == 32 || d == 64 || d == 128; };
+  // other head sizes than 64 take the fast kernel with contiguous state rows only
+  const bool rows_contig = new_state->stride[2] == dv && (!state || state->stride[2] == dv);
+  const bool fast = head_ok(dk) && head_ok(dv) && (dk == 64 && dv == 64 ? true : rows_contig) && qkv_same &&
+                    gate->dtype == MABA_F32 && b->dtype == MABA_F32 &&
                     w->dtype == MABA_F32 && (sdt == MABA_F32 || sdt == MABA_BF16) && new_state->stride[3] == 1 &&
                     new_state->stride[2] <= INT32_MAX && B <= 65535 && lane_strides_fit({q, k, v, gate, b, w}) &&
                     (!state || (state->dtype == sdt && state->stride[3] == 1 && state->stride[2] <= INT32_MAX));
@@ -384,20 +492,24 @@ extern "C" int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, co
     f.ww = (const float*)w->data; f.wsb = w->stride[0]; f.wsh = w->stride[1]; f.wsd = w->stride[2];
     f.state = state ? state->data : nullptr;
     f.ssb = state ? state->stride[0] : 0; f.ssh = state ? state->stride[1] : 0;
-    f.ssr32 = state ? (int)state->stride[2] : 64;
+    f.ssr32 = state ? (int)state->stride[2] : (int)dv;
     f.nst = new_state->data; f.nsb = new_state->stride[0]; f.nsh = new_state->stride[1];
     f.nsr32 = (int)new_state->stride[2];
     f.out = out->data; f.odt = out->dtype; f.osb = out->stride[0]; f.osh = out->stride[1]; f.osd = out->stride[2];
     f.BH = B * H; f.H = (int)H; f.use_log = log_alpha != nullptr;
     const dim3 g4((unsigned)H, (unsigned)B);   // one workgroup per (b, h)
-    const bool sbf = sdt == MABA_BF16, hs = state != nullptr, contig = f.ssr32 == 64 && f.nsr32 == 64;
+    const bool sbf = sdt == MABA_BF16, hs = state != nullptr, contig = f.ssr32 == dv && f.nsr32 == dv;
     void (*kern)(StepFast) = nullptr;
+    if (dk == 64 && dv == 64) {
 #define MABA_STEP_PICK(T, TS)                                                                          \
   kern = hs ? (contig ? dgda_step_wave_kernel<T, TS, true, true> : dgda_step_wave_kernel<T, TS, true, false>) \
             : (contig ? dgda_step_wave_kernel<T, TS, false, true> : dgda_step_wave_kernel<T, TS, false, false>)
-    if (q->dtype == MABA_BF16) { if (sbf) MABA_STEP_PICK(uint16_t, uint16_t); else MABA_STEP_PICK(uint16_t, float); }
-    else { if (sbf) MABA_STEP_PICK(float, uint16_t); else MABA_STEP_PICK(float, float); }
+      if (q->dtype == MABA_BF16) { if (sbf) MABA_STEP_PICK(uint16_t, uint16_t); else MABA_STEP_PICK(uint16_t, float); }
+      else { if (sbf) MABA_STEP_PICK(float, uint16_t); else MABA_STEP_PICK(float, float); }
 #undef MABA_STEP_PICK
+    } else {
+      kern = step_kernel_sized(dk, dv, q->dtype == MABA_BF16, sbf, hs);
+    }
     hipLaunchKernelGGL(kern, g4, dim3(256), 0, s, f);
     return check_launch("dgda_step");
   }

@@ -43,6 +43,39 @@ def test_dgda_step_fp32(dev, B, H, dk, dv):
     assert_close(Sn, eS, 1e-4, 1e-4, "state")
 
 
+@pytest.mark.parametrize("dk", [32, 64, 128])
+@pytest.mark.parametrize("dv", [32, 64, 128])
+@pytest.mark.parametrize("sdt", [torch.float32, torch.bfloat16])
+def test_dgda_step_head_sizes_fast_kernel(dev, dk, dv, sdt):
+    """The four-wave step kernel at every head size of the reference's GPU path (d_k, d_v in
+    {32, 64, 128}, contiguous state rows): bf16 q/k/v, fp32 gates, fp32 or bf16 state updated in
+    place, against the float64 step on the same (rounded) inputs; and with no state."""
+    B, H = 6, 3
+    g = torch.Generator().manual_seed(dk * 7 + dv)
+    q = torch.randn(B, H, dk, generator=g).bfloat16()
+    k = torch.nn.functional.normalize(torch.randn(B, H, dk, generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, H, dv, generator=g).bfloat16()
+    la = -torch.nn.functional.softplus(torch.randn(B, H, dk, generator=g) + 2)
+    b = torch.sigmoid(torch.randn(B, H, dk, generator=g))
+    w = torch.sigmoid(torch.randn(B, H, dv, generator=g))
+    S0 = (torch.randn(B, H, dk, dv, generator=g) * 0.5).to(sdt)
+    S = S0.to(dev)
+    o, Sn = _hip().hip_dgda_step(q.to(dev), k.to(dev), v.to(dev), log_alpha=la.to(dev), b=b.to(dev), w=w.to(dev),
+                                 state=S, new_state=S, out_dtype=torch.float32, state_dtype=sdt,
+                                 allow_mixed_dtypes=True)
+    assert Sn.data_ptr() == S.data_ptr()
+    eo, eS = odgda.dgda_step(to_np(q), to_np(k), to_np(v), alpha=np.exp(to_np(la)), b=to_np(b), w=to_np(w),
+                             state=to_np(S0))
+    tol = 1e-4 if sdt == torch.float32 else 8e-3    # bf16 state: the stored state is rounded to bf16
+    assert_close(o, eo, tol, tol, f"out dk={dk} dv={dv}")
+    assert_close(Sn, eS, tol, tol, f"state dk={dk} dv={dv}")
+    o0, S1 = _hip().hip_dgda_step(q.to(dev), k.to(dev), v.to(dev), log_alpha=la.to(dev), b=b.to(dev), w=w.to(dev),
+                                  out_dtype=torch.float32, state_dtype=torch.float32, allow_mixed_dtypes=True)
+    eo0, eS1 = odgda.dgda_step(to_np(q), to_np(k), to_np(v), alpha=np.exp(to_np(la)), b=to_np(b), w=to_np(w))
+    assert_close(o0, eo0, 1e-4, 1e-4, "out, no state")
+    assert_close(S1, eS1, 1e-4, 1e-4, "state, no state")
+
+
 def test_dgda_step_4d_alpha_no_state(dev):
     g = torch.Generator().manual_seed(7)
     B, H, d = 4, 2, 64
