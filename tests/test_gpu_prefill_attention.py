@@ -80,6 +80,48 @@ def test_maba_sa_prefill_long_against_torch_reference(dev):
     assert_close(out, to_np(ref), 2e-3, 2e-3, "maba_sa_prefill 4k")
 
 
+def test_bench_row_32k_both_kernels_vs_oracle(dev):
+    """The bench row `maba_sa_prefill_32k` at its own shape and inputs: B=1, H=10, d_head 64,
+    d_c 128, 32,768 queries over their own keys, top-32 causal blocks from the HIP prefill
+    top-k (lambda 0.5, recency-biased, about 5 K distinct blocks per 16 queries), 512 means.
+    Both kernels, composed as the bench composes them (the head-space kernel over bf16
+    up-projected keys, values and means, fp32 early rows; the latent kernel over the bf16 latent
+    rows and their means, then W_v,h), at rows spread over the sequence (the first, the last
+    early row, block edges, deep rows), against the oracle's decode at that position
+    (float64, the same bf16 weights), rtol = atol = 2e-3."""
+    hb = _hip()
+    B, H, L, dh, dc, K = 1, 10, 32768, 64, 128, 32
+    g = torch.Generator(device=dev).manual_seed(21)
+    bf = lambda *sh: torch.randn(*sh, device=dev, generator=g, dtype=torch.bfloat16)  # noqa: E731
+    q, c = bf(B, H, L, dh), bf(B, L, dc)
+    Wkb = (torch.randn(H * dh, dc, device=dev, generator=g) * dc ** -0.5).bfloat16()
+    Wvb = (torch.randn(H * dh, dc, device=dev, generator=g) * dc ** -0.5).bfloat16()
+    gate = torch.randn(B, L, 3, device=dev, generator=g)
+    idx = hb.hip_index_topk(bf(B, L, 64), bf(B, L // 64, 64), lambda_dist=0.5, top_k=K, block_size=64)
+    heads = lambda t, n: t.view(B, n, H, dh).transpose(1, 2)  # noqa: E731
+    with torch.no_grad():
+        k, v = heads(c @ Wkb.t(), L), heads(c @ Wvb.t(), L)
+        means = c.reshape(B, L // 64, 64, dc).float().mean(dim=2).bfloat16()
+        kh, vh = heads(means @ Wkb.t(), L // 64), heads(means @ Wvb.t(), L // 64)
+        cnt = torch.arange(1, 64, device=dev, dtype=torch.float32).view(1, -1, 1)
+        # early rows in fp32: at row 0 the output is (up to the gate) this row itself, so a bf16
+        # rounding of it alone would exceed the tolerance
+        early = heads((torch.cumsum(c[:, :63].float(), dim=1) / cnt) @ Wvb.float().t(), 63)
+        o_heads = hb.hip_maba_sa_prefill(q, k, v, kh, vh, early, idx, gate, scale=dh ** -0.5,
+                                         out_dtype=torch.float32)
+        Wk_h, Wv_h = Wkb.float().view(H, dh, dc), Wvb.float().view(H, dh, dc)
+        q_lat = torch.einsum("bhtd,hdc->bthc", q.float(), Wk_h).contiguous()
+        z = hb.hip_maba_sa_prefill_latent(q_lat, c, hb.hip_hca_pool(c, pool=64), idx, gate, scale=dh ** -0.5)
+        o_latent = torch.einsum("bthc,hdc->bhtd", z, Wv_h)
+        torch.cuda.synchronize()
+    Wk, Wv = to_np(Wkb), to_np(Wvb)
+    for t in (0, 62, 63, 64, 4095, 16384 + 33, L - 1):
+        exp = osa.maba_sa_decode(to_np(q[:, :, t]), to_np(c[:, : t + 1]), Wk, Wv, idx[:, t:t + 1].cpu().numpy(),
+                                 to_np(gate[:, t]), L=t + 1)
+        assert_close(o_heads[:, :, t], exp, 2e-3, 2e-3, f"head-space kernel row {t}")
+        assert_close(o_latent[:, :, t], exp, 2e-3, 2e-3, f"latent kernel row {t}")
+
+
 @pytest.mark.parametrize("form", ["latent", "heads", "auto"])
 def test_layer_prefill_fused_matches_dense_path(dev, form):
     """The bf16 MabaSparseAttention prefill through either HIP kernel (the latent form, the
