@@ -114,6 +114,10 @@ int maba_hip_abi_version(void);
  * stride-0 broadcast along the channel axis.  out: [B,H,L,dv],
  * final_state: [B,H,dk,dv]; dtypes f32/f16/bf16 independently per tensor.
  * chunk_size is accepted for signature parity; the result does not depend on it.
+ * dk, dv in {32, 64, 128} with q, k, v of one dtype and the gates fp32 (or in q's
+ * 16-bit dtype) take the sequence-parallel MFMA paths, which need the workspace the
+ * size query returns (it depends on the current device's compute-unit count); every
+ * other shape up to 128 runs a sequential kernel and needs none (the query returns 0).
  */
 size_t maba_hip_dgda_prefill_workspace_size(const maba_tensor* q, const maba_tensor* v,
                                             const maba_tensor* log_alpha_or_alpha,
@@ -126,9 +130,10 @@ int maba_hip_dgda_prefill(const maba_tensor* q, const maba_tensor* k, const maba
                           size_t workspace_bytes, void* stream);
 
 /* DGDA single decode step.  q,k,alpha,log_alpha,b: [B,H,dk]; v,w: [B,H,dv];
- * state / new_state: [B,H,dk,dv] (state NULL = zeros); out: [B,H,dv].  With dk = dv = 64,
- * fp32 gates and an fp32 or bf16 state with unit column stride, new_state may be state
- * itself (the state is updated in place). */
+ * state / new_state: [B,H,dk,dv] (state NULL = zeros); out: [B,H,dv].  new_state may be
+ * state itself (the state is updated in place).  dk, dv in {32, 64, 128}, fp32 gates, q, k,
+ * v of one dtype and an fp32 or bf16 state with unit column stride (rows dv apart unless
+ * dk = dv = 64) take the four-wave kernel; other shapes a generic one. */
 int maba_hip_dgda_step(const maba_tensor* q, const maba_tensor* k, const maba_tensor* v,
                        const maba_tensor* alpha, const maba_tensor* log_alpha,
                        const maba_tensor* b, const maba_tensor* w, const maba_tensor* state,
