@@ -7,7 +7,7 @@
 // the key-side quantities).  q, k, v in bf16, fp16 or fp32.
 //
 // Sub-chunks of SC = 16 tokens.  With Lam_i the inclusive cumulative log-decay of
-// token i within the sub-chunk (a 64-vector over key channels) and S the state at the
+// token i within the sub-chunk (a d_k-vector over key channels) and S the state at the
 // sub-chunk start (reference math: cpu_dgda.py:101-146, common.py:229-268):
 //   L_ij = sum_c (b*k)_ic k_jc e^{Lam_ic - Lam_jc}      i > j
 //   A_ij = sum_c  q_ic    k_jc e^{Lam_ic - Lam_jc}      i >= j
@@ -31,7 +31,7 @@
 // Sequence parallelism, passes and modes: as the chunked path in dgda_chunk.hip (slots
 // of U sub-chunks, aggregate [N | M] pass, zero-start and fix-up output passes).
 //
-// Fused layer prologue (PRO, maba_hip_dgda_layer_prefill; reference layers/dgda.py:103-121,
+// Fused layer prologue (PRO, d_k = d_v = 64; maba_hip_dgda_layer_prefill; reference layers/dgda.py:103-121,
 // 186-207): the kernels read the layer's six bf16 projections instead of q, k, v and the
 // gates, and form the op inputs in the staging step: the causal depthwise conv (kernel 4)
 // + SiLU of q, k, v over [history, projections], the per-head L2 norm of k, the decay
