@@ -363,6 +363,42 @@ def test_subchunk_head_sizes_vs_oracle(dev, dk, dv, decay, L, qkv):
     assert_close(S, eS, 2e-3, 2e-3, f"state dk={dk} dv={dv} {decay}")
 
 
+@pytest.mark.parametrize("dk,dv,L,qkv", [(128, 32, 1, torch.float16), (32, 128, 15, torch.bfloat16),
+                                         (128, 128, 17, torch.float32), (32, 32, 16, torch.float16)])
+def test_subchunk_head_sizes_short_sequences(dev, dk, dv, L, qkv):
+    """One sub-chunk or a partial one (L = 1, 15, 16, 17) at the other head sizes, with an initial
+    state: a single segment, the zero-start pass alone, masked tail tokens."""
+    inp = dgda_inputs(2, 3, L, dk=dk, dv=dv, seed=L + dk, gates="channel", qkv_dtype=qkv, device=dev,
+                      with_state=True)
+    assert _sub_workspace_size(inp) == 16            # one slot per sequence: no aggregate workspace
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, f"out dk={dk} dv={dv} L={L}")
+    assert_close(S, eS, 2e-3, 2e-3, f"state dk={dk} dv={dv} L={L}")
+
+
+@pytest.mark.parametrize("dk,dv", [(128, 128), (32, 64)])
+def test_subchunk_head_sizes_views_and_token_gates(dev, dk, dv):
+    """q/k/v as [B,L,H,d] storage viewed [B,H,L,d] (the layer's layout), per-token gates as stride-0
+    channel views (shared by both value halves at d_v = 128), many segments per sequence."""
+    B, L, H = 2, 5000, 3
+    g = torch.Generator().manual_seed(dk + dv)
+    nrm = lambda t: torch.nn.functional.normalize(t, dim=-1)  # noqa: E731
+    q = nrm(torch.randn(B, L, H, dk, generator=g)).bfloat16().to(dev).transpose(1, 2)
+    k = nrm(torch.randn(B, L, H, dk, generator=g)).bfloat16().to(dev).transpose(1, 2)
+    v = torch.randn(B, L, H, dv, generator=g).bfloat16().to(dev).transpose(1, 2)
+    la = (-torch.nn.functional.softplus(torch.randn(B, H, L, 1, generator=g) + 2) * 0.01).to(dev)
+    be = torch.sigmoid(torch.randn(B, H, L, 1, generator=g)).to(dev)
+    inp = dict(q=q, k=k, v=v, log_alpha=la.expand(B, H, L, dk), b=be.expand(B, H, L, dk),
+               w=be.expand(B, H, L, dv), initial_state=None)
+    if dk != 64 or dv != 64:
+        assert _sub_workspace_size(inp) > 16
+    o, S = _run(inp)
+    eo, eS = odgda.dgda_prefill_seq(**oracle_dgda_args(inp))
+    assert_close(o, eo, 2e-3, 2e-3, "out")
+    assert_close(S, eS, 2e-3, 2e-3, "state")
+
+
 @pytest.mark.parametrize("dk,dv", [(64, 64), (32, 128), (128, 32)])
 def test_subchunk_fp16_same_dtype_contract(dev, dk, dv):
     """Every tensor fp16 (the reference's contract without mixed dtypes: gates in q's dtype),
