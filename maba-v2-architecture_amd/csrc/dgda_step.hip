@@ -136,8 +136,8 @@ __device__ __forceinline__ int64_t row_at(int i, int rs) { return CONTIG ? (int6
 constexpr int step_nc(int dv) { return dv > 64 ? 2 : 1; }
 constexpr int step_nr(int dk) { return dk > 64 ? 2 : 1; }
 
-// The RPW rows of wave w's slab, S[RPW w + i][col + 64 j], from sp = &S[RPW w][col] (rs: row
-// stride), as stored (converted by the caller once every load of the step is issued).
+// The RPW = d_k / 4 rows of wave w's slab, S[RPW w + i][col + 64 j], from sp = &S[RPW w][col]
+// (rs: row stride), as stored (converted by the caller once every load of the step is issued).
 template <typename TS, bool CONTIG, int DK = 64, int DV = 64>
 __device__ __forceinline__ void load_rows(TS (&s)[step_nc(DV)][DK / 4], const TS* sp, int rs) {
 #pragma unroll
